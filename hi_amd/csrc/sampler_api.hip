@@ -1,0 +1,319 @@
+// hi-rocm C ABI: argument checks, workspace carving and kernel launches.
+//
+// The mirrors of the reference launchers (crates/hi-cuda/src/kernels.cu:
+// 14737-14880) keep their argument checks (status 1 for null pointers,
+// non-positive sizes, negative top_k, null stream).  The reference then
+// resolves ranked rows on the host (gpu.rs:15685-15967); here every row is
+// finished on the device by the same kernels as hi_rocm_sample.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "hi_rocm.h"
+#include "sampler_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  g_last_error = std::string(where) + ": " + hipGetErrorString(e);
+  return HI_ROCM_ERR_HIP;
+}
+
+// Library-owned workspace for the workspace-free reference mirrors: one
+// buffer per device, grown on demand, never shrunk.
+struct DeviceWorkspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::unordered_map<int, DeviceWorkspace> g_ws;
+
+int internal_workspace(size_t bytes, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  DeviceWorkspace& ws = g_ws[dev];
+  if (ws.bytes < bytes) {
+    if (ws.ptr) {
+      e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+      e = hipFree(ws.ptr);
+      if (e != hipSuccess) return hip_fail(e, "hipFree");
+      ws.ptr = nullptr;
+      ws.bytes = 0;
+    }
+    e = hipMalloc(&ws.ptr, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(sampler workspace)");
+    ws.bytes = bytes;
+  }
+  *out = ws.ptr;
+  return HI_ROCM_OK;
+}
+
+void carve(hi_rocm::SampleArgs& a, void* ws, const hi_rocm::WorkspaceLayout& L) {
+  char* base = (char*)ws;
+  a.stats = (hi_rocm::ChunkStat*)(base + L.stats);
+  a.cand = (uint64_t*)(base + L.cand);
+  a.ws_s = (float*)(base + L.ws_s);
+  a.ws_w = (float*)(base + L.ws_w);
+  a.ws_list = (uint64_t*)(base + L.ws_list);
+  a.list_stride = L.list_stride;
+  a.n_chunks = L.n_chunks;
+}
+
+int vec_aligned(const void* p, int dtype, int64_t row_stride) {
+  const uintptr_t align = dtype == HI_ROCM_DTYPE_BF16 ? 8 : 16;
+  return ((uintptr_t)p % align == 0) && (row_stride % 4 == 0);
+}
+
+hi_rocm::SampleArgs base_args(const void* logits, int dtype, int B, int V, int64_t row_stride) {
+  hi_rocm::SampleArgs a;
+  memset(&a, 0, sizeof(a));
+  a.logits = logits;
+  a.dtype = dtype;
+  a.B = B;
+  a.V = V;
+  a.row_stride = row_stride;
+  a.vec_ok = vec_aligned(logits, dtype, row_stride);
+  a.mask_words = (V + 31) / 32;
+  return a;
+}
+
+// Run the two sampling kernels with the library workspace.
+int run_with_internal_ws(hi_rocm::SampleArgs& a, hipStream_t stream) {
+  const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(a.B, a.V);
+  void* ws = nullptr;
+  int rc = internal_workspace(L.total, &ws);
+  if (rc != HI_ROCM_OK) return rc;
+  carve(a, ws, L);
+  hipError_t e = hi_rocm::launch_sample(a, stream);
+  if (e != hipSuccess) return hip_fail(e, "sampler launch");
+  return HI_ROCM_OK;
+}
+
+bool vocab_ok(int V) { return V > 0 && (int64_t)V <= (int64_t)hi_rocm::kMaxChunks * hi_rocm::kChunk; }
+
+}  // namespace
+
+extern "C" {
+
+const char* hi_rocm_last_error(void) { return g_last_error.c_str(); }
+
+const char* hi_rocm_version(void) { return "hi-rocm 0.1.0 (gfx950)"; }
+
+int hi_rocm_launch_argmax(const void* logits, void* output_token, int len, void* stream) {
+  if (logits == nullptr || output_token == nullptr || len <= 0 || stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_launch_argmax: invalid arguments");
+  hipError_t e = hi_rocm::launch_argmax((const float*)logits, (uint32_t*)output_token, 1, len, 0,
+                                        len, (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "argmax launch");
+}
+
+int hi_rocm_launch_argmax_last_row(const void* logits, void* output_token, int rows, int cols,
+                                   void* stream) {
+  if (logits == nullptr || output_token == nullptr || rows <= 0 || cols <= 0 || stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_launch_argmax_last_row: invalid arguments");
+  hipError_t e = hi_rocm::launch_argmax((const float*)logits, (uint32_t*)output_token, 1, cols,
+                                        (int64_t)(rows - 1) * cols, cols, (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "argmax launch");
+}
+
+int hi_rocm_launch_argmax_batched_last_token(const void* logits, void* output_tokens,
+                                             int batch_count, int seq_len, int cols,
+                                             void* stream) {
+  if (logits == nullptr || output_tokens == nullptr || batch_count <= 0 || seq_len <= 0 ||
+      cols <= 0 || stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_launch_argmax_batched_last_token: invalid arguments");
+  hipError_t e = hi_rocm::launch_argmax((const float*)logits, (uint32_t*)output_tokens,
+                                        batch_count, (int64_t)seq_len * cols,
+                                        (int64_t)(seq_len - 1) * cols, cols, (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "argmax launch");
+}
+
+int hi_rocm_launch_sample_last_row(const void* logits, void* output_token, int rows, int cols,
+                                   float temperature, float top_p, int top_k, float sample,
+                                   void* stream) {
+  if (logits == nullptr || output_token == nullptr || rows <= 0 || cols <= 0 || top_k < 0 ||
+      stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_launch_sample_last_row: invalid arguments");
+  if (!vocab_ok(cols)) return fail(HI_ROCM_ERR_UNSUPPORTED, "vocabulary too large");
+  const float* row = (const float*)logits + (int64_t)(rows - 1) * cols;
+  hi_rocm::SampleArgs a = base_args(row, HI_ROCM_DTYPE_F32, 1, cols, cols);
+  a.pv.mode = hi_rocm::kParamsUniform;
+  a.pv.T = temperature;
+  a.pv.top_p = top_p;
+  a.pv.top_k = top_k;
+  a.pv.uniforms = nullptr;
+  a.pv.uniform_value = sample;
+  a.pv.greedy_rule = hi_rocm::kGreedyIeee;  // kernels.cu:7990-7993
+  a.out_tokens = (uint32_t*)output_token;
+  return run_with_internal_ws(a, (hipStream_t)stream);
+}
+
+int hi_rocm_launch_sample_batched_last_token(const void* logits, void* output_tokens,
+                                             const void* samples, int batch_count, int seq_len,
+                                             int cols, float temperature, float top_p, int top_k,
+                                             int gpu_ranked, void* stream) {
+  (void)gpu_ranked;
+  if (logits == nullptr || output_tokens == nullptr || samples == nullptr || batch_count <= 0 ||
+      seq_len <= 0 || cols <= 0 || top_k < 0 || stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_launch_sample_batched_last_token: invalid arguments");
+  if (!vocab_ok(cols)) return fail(HI_ROCM_ERR_UNSUPPORTED, "vocabulary too large");
+  const float* first = (const float*)logits + (int64_t)(seq_len - 1) * cols;
+  hi_rocm::SampleArgs a = base_args(first, HI_ROCM_DTYPE_F32, batch_count, cols,
+                                    (int64_t)seq_len * cols);
+  a.pv.mode = hi_rocm::kParamsUniform;
+  a.pv.T = temperature;
+  a.pv.top_p = top_p;
+  a.pv.top_k = top_k;
+  a.pv.uniforms = (const float*)samples;
+  a.pv.greedy_rule = hi_rocm::kGreedyFiniteLane;  // kernels.cu:7803-7808
+  a.out_tokens = (uint32_t*)output_tokens;
+  return run_with_internal_ws(a, (hipStream_t)stream);
+}
+
+int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* output_tokens,
+                                                     const void* samples,
+                                                     const void* temperatures,
+                                                     const void* top_ps, const void* top_ks,
+                                                     int batch_count, int seq_len, int cols,
+                                                     int gpu_ranked, void* stream) {
+  (void)gpu_ranked;
+  if (logits == nullptr || output_tokens == nullptr || samples == nullptr ||
+      temperatures == nullptr || top_ps == nullptr || top_ks == nullptr || batch_count <= 0 ||
+      seq_len <= 0 || cols <= 0 || stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS,
+                "hi_rocm_launch_select_batched_last_token_per_row: invalid arguments");
+  if (!vocab_ok(cols)) return fail(HI_ROCM_ERR_UNSUPPORTED, "vocabulary too large");
+  const float* first = (const float*)logits + (int64_t)(seq_len - 1) * cols;
+  hi_rocm::SampleArgs a = base_args(first, HI_ROCM_DTYPE_F32, batch_count, cols,
+                                    (int64_t)seq_len * cols);
+  a.pv.mode = hi_rocm::kParamsSoA;
+  a.pv.temps = (const float*)temperatures;
+  a.pv.top_ps = (const float*)top_ps;
+  a.pv.top_ks = (const int*)top_ks;
+  a.pv.uniforms = (const float*)samples;
+  a.pv.greedy_rule = hi_rocm::kGreedyIeee;  // kernels.cu:8058-8061
+  a.out_tokens = (uint32_t*)output_tokens;
+  return run_with_internal_ws(a, (hipStream_t)stream);
+}
+
+int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs) {
+  if (max_batch <= 0 || vocab <= 0 || n_logprobs < 0 || n_logprobs > HI_ROCM_MAX_LOGPROBS)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sampler_reserve: invalid arguments");
+  if (!vocab_ok(vocab)) return fail(HI_ROCM_ERR_UNSUPPORTED, "vocabulary too large");
+  void* ws = nullptr;
+  return internal_workspace(hi_rocm::workspace_layout(max_batch, vocab).total, &ws);
+}
+
+int hi_rocm_sampler_workspace_bytes(int max_batch, int vocab, int n_logprobs, size_t* out_bytes) {
+  if (max_batch <= 0 || vocab <= 0 || n_logprobs < 0 || out_bytes == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sampler_workspace_bytes: invalid arguments");
+  if (n_logprobs > HI_ROCM_MAX_LOGPROBS)
+    return fail(HI_ROCM_ERR_UNSUPPORTED, "n_logprobs above HI_ROCM_MAX_LOGPROBS");
+  if (!vocab_ok(vocab)) return fail(HI_ROCM_ERR_UNSUPPORTED, "vocabulary too large");
+  *out_bytes = hi_rocm::workspace_layout(max_batch, vocab).total;
+  return HI_ROCM_OK;
+}
+
+static int check_sample_args(const void* logits, int dtype, int batch, int vocab,
+                             int64_t row_stride, const void* params,
+                             const uint32_t* hist_offsets, const uint32_t* hist_ids,
+                             const uint32_t* hist_counts, const void* out_tokens) {
+  if (logits == nullptr || params == nullptr || out_tokens == nullptr || batch <= 0 ||
+      vocab <= 0 || row_stride < vocab)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm: invalid logits/params/outputs/sizes");
+  if (dtype != HI_ROCM_DTYPE_F32 && dtype != HI_ROCM_DTYPE_BF16)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm: unknown dtype");
+  if ((hist_offsets == nullptr) != (hist_ids == nullptr) ||
+      (hist_offsets == nullptr) != (hist_counts == nullptr))
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm: history needs offsets, ids and counts together");
+  if (!vocab_ok(vocab)) return fail(HI_ROCM_ERR_UNSUPPORTED, "vocabulary too large");
+  return HI_ROCM_OK;
+}
+
+int hi_rocm_sample(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                   const hi_rocm_row_params* params, const float* uniforms,
+                   const uint32_t* hist_offsets, const uint32_t* hist_ids,
+                   const uint32_t* hist_counts, const uint32_t* mask_words,
+                   uint32_t* out_tokens, float* out_logprobs, uint32_t* out_logprob_ids,
+                   float* out_token_logprobs, int n_logprobs, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  int rc = check_sample_args(logits, dtype, batch, vocab, row_stride, params, hist_offsets,
+                             hist_ids, hist_counts, out_tokens);
+  if (rc != HI_ROCM_OK) return rc;
+  if (uniforms == nullptr) return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sample: null uniforms");
+  if (n_logprobs < 0) return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sample: negative n_logprobs");
+  if (n_logprobs > HI_ROCM_MAX_LOGPROBS)
+    return fail(HI_ROCM_ERR_UNSUPPORTED, "n_logprobs above HI_ROCM_MAX_LOGPROBS");
+  if (n_logprobs > 0 && (out_logprobs == nullptr || out_logprob_ids == nullptr))
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sample: logprob outputs missing");
+  const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(batch, vocab);
+  if (workspace == nullptr || workspace_bytes < L.total)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sample: workspace too small");
+  hi_rocm::SampleArgs a = base_args(logits, dtype, batch, vocab, row_stride);
+  a.pv.mode = hi_rocm::kParamsRows;
+  a.pv.rows = params;
+  a.pv.uniforms = uniforms;
+  a.pv.greedy_rule = hi_rocm::kGreedyIeee;
+  a.hoff = hist_offsets;
+  a.hids = hist_ids;
+  a.hcnt = hist_counts;
+  a.mask = mask_words;
+  a.n_lp = n_logprobs;
+  a.need_lse = (n_logprobs > 0 || out_token_logprobs != nullptr) ? 1 : 0;
+  a.out_tokens = out_tokens;
+  a.out_lp = out_logprobs;
+  a.out_lp_ids = out_logprob_ids;
+  a.out_token_lp = out_token_logprobs;
+  carve(a, workspace, L);
+  hipError_t e = hi_rocm::launch_sample(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "sampler launch");
+  return HI_ROCM_OK;
+}
+
+int hi_rocm_debug_distribution(const void* logits, int dtype, int batch, int vocab,
+                               int64_t row_stride, const hi_rocm_row_params* params,
+                               const uint32_t* hist_offsets, const uint32_t* hist_ids,
+                               const uint32_t* hist_counts, const uint32_t* mask_words,
+                               float* out_processed, float* out_probs, void* stream) {
+  int rc = check_sample_args(logits, dtype, batch, vocab, row_stride, params, hist_offsets,
+                             hist_ids, hist_counts, out_processed);
+  if (rc != HI_ROCM_OK) return rc;
+  if (out_probs == nullptr) return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_distribution: null output");
+  hi_rocm::SampleArgs a = base_args(logits, dtype, batch, vocab, row_stride);
+  a.pv.mode = hi_rocm::kParamsRows;
+  a.pv.rows = params;
+  a.hoff = hist_offsets;
+  a.hids = hist_ids;
+  a.hcnt = hist_counts;
+  a.mask = mask_words;
+  const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(batch, vocab);
+  void* ws = nullptr;
+  rc = internal_workspace(L.total, &ws);
+  if (rc != HI_ROCM_OK) return rc;
+  carve(a, ws, L);
+  hipError_t e = hi_rocm::launch_debug_distribution(a, out_processed, out_probs, (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug distribution launch");
+}
+
+int hi_rocm_debug_expf(const float* x, float* y, int64_t n, void* stream) {
+  if (x == nullptr || y == nullptr || n <= 0)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_expf: invalid arguments");
+  hipError_t e = hi_rocm::launch_debug_expf(x, y, n, (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug expf launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+// Shared between the kernels (sampler_kernels.hip) and the host API
+// (sampler_api.hip).  Not part of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hi_rocm.h"
+
+namespace hi_rocm {
+
+constexpr int kScanThreads = 256;                  // scan workgroup (4 waves)
+constexpr int kScanVec = 8;                        // 128-bit loads per thread
+constexpr int kChunk = kScanThreads * kScanVec * 4;  // 8192 logits per chunk
+constexpr int kFast = 1024;                        // candidates kept per chunk (max)
+constexpr int kFinThreads = 1024;                  // finish workgroup (16 waves)
+constexpr int kMaxChunks = 1024;                   // => vocab <= 8,388,608
+constexpr int kLseTop = 16;                        // per-chunk candidates kept for logprobs
+
+enum RowClass : int { kGreedy = 0, kTopK = 1, kTopP = 2, kTempOnly = 3 };
+enum ParamsMode : int { kParamsRows = 0, kParamsSoA = 1, kParamsUniform = 2 };
+// Greedy rows: block_argmax_last (kernels.cu:7153-7186), or the finite-only
+// argmax of sample_last_token_row (kernels.cu:7775-7801), which is what the
+// reference's uniform-config batched kernel returns for temperature <= 0.
+enum GreedyRule : int { kGreedyIeee = 0, kGreedyFiniteLane = 1 };
+
+// Where the per-row parameters come from: the extended API's struct array,
+// the reference per-row launcher's three arrays, or one config for all rows.
+struct ParamsView {
+  const hi_rocm_row_params* rows;
+  const float* temps;
+  const float* top_ps;
+  const int* top_ks;
+  float T, top_p;
+  int top_k;
+  int mode;
+  const float* uniforms;  // device f32[B], or null: uniform_value for every row
+  float uniform_value;
+  int greedy_rule;        // GreedyRule
+};
+
+// Decoded row configuration.
+struct RowCfg {
+  float T, top_p, min_p, rep, freq, pres;
+  int top_k;
+  uint32_t eos, flags;
+  int cls;        // RowClass
+  int k_eff;      // min(top_k, V) for top-k rows
+  float t_eff;    // temperature used for s = l / t_eff (1 for greedy rows)
+  float cutoff;   // clamped top_p (gpu.rs:789-793)
+  bool rep_on;
+  bool wide;      // top-k row with k_eff > kFast
+  int k_sel;      // candidates each chunk keeps
+  bool store_s;   // scaled logits go to the workspace
+};
+
+// Per (row, chunk) statistics written by the scan, merged by the finish.
+struct ChunkStat {
+  float max_s;                    // max of s = l / t_eff (non-finite l -> -inf)
+  float am_ieee_v;                // argmax, IEEE '>' (kernels.cu:7153-7186)
+  uint32_t am_ieee_i;
+  int32_t am_tot_k;               // argmax by total_cmp (gpu.rs:739-751)
+  uint32_t am_tot_i;
+  float am_fin_v;                 // finite argmax, lane rule (kernels.cu:7775-7801)
+  uint32_t am_fin_i;
+  uint32_t any_finite;
+  float lse_m, lse_sum;           // chunk max, sum of exp(s - max) over elements not kept
+  uint32_t n_cand;                // candidates written
+  uint32_t trunc;                 // the chunk had more than k_sel elements
+  uint32_t unkept_key;            // largest scaled-logit key not kept
+  uint32_t pad0;
+  uint64_t min_kept;              // smallest kept candidate key
+};
+static_assert(sizeof(ChunkStat) == 64, "ChunkStat layout");
+
+struct SampleArgs {
+  const void* logits;  // row 0 of the batch
+  int dtype;
+  int B, V;
+  int64_t row_stride;  // elements between rows
+  int vec_ok;          // 128-bit (f32) / 64-bit (bf16) loads are aligned
+  ParamsView pv;
+  const uint32_t* hoff;
+  const uint32_t* hids;
+  const uint32_t* hcnt;
+  const uint32_t* mask;
+  int mask_words;      // ceil(V / 32)
+  int n_lp;
+  int need_lse;
+  int n_chunks;
+  uint32_t* out_tokens;
+  float* out_lp;
+  uint32_t* out_lp_ids;
+  float* out_token_lp;
+  // workspace
+  ChunkStat* stats;    // [B][n_chunks]
+  uint64_t* cand;      // [B][n_chunks][kFast]
+  float* ws_s;         // [B][V]
+  float* ws_w;         // [B][V]
+  uint64_t* ws_list;   // [B][list_stride]
+  int64_t list_stride;
+};
+
+struct WorkspaceLayout {
+  size_t stats, cand, ws_s, ws_w, ws_list, total;
+  int n_chunks;
+  int64_t list_stride;
+};
+
+inline int64_t next_pow2_i64(int64_t x) {
+  int64_t p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+inline WorkspaceLayout workspace_layout(int B, int V) {
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  WorkspaceLayout L;
+  L.n_chunks = (V + kChunk - 1) / kChunk;
+  L.list_stride = next_pow2_i64(V);
+  size_t off = 0;
+  L.stats = off; off = align(off + (size_t)B * L.n_chunks * sizeof(ChunkStat));
+  L.cand = off; off = align(off + (size_t)B * L.n_chunks * kFast * sizeof(uint64_t));
+  L.ws_s = off; off = align(off + (size_t)B * V * sizeof(float));
+  L.ws_w = off; off = align(off + (size_t)B * V * sizeof(float));
+  L.ws_list = off; off = align(off + (size_t)B * L.list_stride * sizeof(uint64_t));
+  L.total = off;
+  return L;
+}
+
+hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
+hipError_t launch_argmax(const float* logits, uint32_t* out, int B, int64_t row_stride,
+                         int64_t row_offset, int cols, hipStream_t stream);
+hipError_t launch_debug_expf(const float* x, float* y, int64_t n, hipStream_t stream);
+hipError_t launch_debug_distribution(const SampleArgs& a, float* out_proc, float* out_probs,
+                                     hipStream_t stream);
+
+}  // namespace hi_rocm

@@ -1,0 +1,187 @@
+/*
+ * hi-rocm: MI355X (gfx950) batched token sampler, C ABI.
+ *
+ * Drop-in for the sampler launchers of the reference's hi-cuda crate
+ * (crates/hi-cuda/src/kernels.cu:14737-14880, bound in Rust at
+ * crates/hi-cuda/src/kernels.rs:1507-1563), plus one extended entry point that
+ * adds the stages the serving path needs (penalties, allowed-token mask,
+ * min-p, logprobs, bf16 logits).
+ *
+ * Conventions shared by every entry point:
+ *   - every pointer argument is caller-owned device memory (HBM) unless the
+ *     comment says otherwise; logits are never copied to the host;
+ *   - work is enqueued on `stream` (a hipStream_t) and is asynchronous;
+ *   - return 0 = launched, 1 = rejected arguments (nothing enqueued),
+ *     2 = unsupported shape or option, 3 = HIP launch/runtime error;
+ *     hi_rocm_last_error() gives a message for the calling thread;
+ *   - no entry point throws or aborts across the ABI;
+ *   - every row is resolved on the device: unlike the reference there is no
+ *     0xFFFFFFFF overflow sentinel and no host re-sampling.
+ */
+#ifndef HI_ROCM_H
+#define HI_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HI_ROCM_OK 0
+#define HI_ROCM_ERR_ARGS 1
+#define HI_ROCM_ERR_UNSUPPORTED 2
+#define HI_ROCM_ERR_HIP 3
+
+#define HI_ROCM_DTYPE_F32 0
+#define HI_ROCM_DTYPE_BF16 1
+
+/* Repetition penalty once per distinct history token instead of once per
+ * occurrence. */
+#define HI_ROCM_FLAG_REP_ONCE 1u
+
+/* Largest n_logprobs accepted by hi_rocm_sample. */
+#define HI_ROCM_MAX_LOGPROBS 1024
+
+/*
+ * Per-row sampling parameters (40 bytes, device array of `batch` entries).
+ * Meaning of the reference fields follows CudaRowSampling
+ * (crates/hi-cuda/src/gpu.rs:55-65) and its device form
+ * (gpu.rs:15861-15884): temperature <= 0 or non-finite is greedy; top_k <= 0
+ * is "unset"; top_p >= 1 or non-finite disables the nucleus cut.
+ * The other fields are extensions the reference's CUDA path lacks:
+ *   min_p               keep tokens with p >= min_p * p_max (<= 0: off)
+ *   repetition_penalty  l < 0 ? l * p : l / p per history occurrence
+ *                       (crates/hi-mlx/src/generate.rs:60-70); off when
+ *                       |p - 1| <= FLT_EPSILON, p <= 0 or non-finite
+ *   frequency_penalty   l -= f * count   (count > 0)
+ *   presence_penalty    l -= presence    (count > 0)
+ *   eos_id              output of a row whose mask allows no finite logit
+ *   flags               HI_ROCM_FLAG_*
+ */
+typedef struct hi_rocm_row_params {
+  float temperature;
+  float top_p;
+  float min_p;
+  float repetition_penalty;
+  float frequency_penalty;
+  float presence_penalty;
+  int32_t top_k;
+  uint32_t eos_id;
+  uint32_t flags;
+  uint32_t reserved;
+} hi_rocm_row_params;
+
+/* ---- drop-in mirrors of the reference launchers (same arguments, same
+ *      argument checks; `stream` must be non-null like the reference) ---- */
+
+/* kernels.cu:14737 hi_cuda_launch_argmax: argmax of `len` f32 logits,
+ * IEEE '>' with ties to the lowest index (kernels.cu:7153-7186). */
+int hi_rocm_launch_argmax(const void* logits, void* output_token, int len, void* stream);
+
+/* kernels.cu:14753 hi_cuda_launch_argmax_last_row: argmax of row rows-1. */
+int hi_rocm_launch_argmax_last_row(const void* logits, void* output_token, int rows, int cols,
+                                   void* stream);
+
+/* kernels.cu:14771 hi_cuda_launch_argmax_batched_last_token: argmax of row
+ * b*seq_len + seq_len-1 for every b. */
+int hi_rocm_launch_argmax_batched_last_token(const void* logits, void* output_tokens,
+                                             int batch_count, int seq_len, int cols,
+                                             void* stream);
+
+/* kernels.cu:14794 hi_cuda_launch_sample_last_row (+ the host ranking of
+ * gpu.rs:15561-15656): one token from row rows-1 with the given config and
+ * uniform `sample`.  Ranked configs follow gpu.rs:753-900 exactly. */
+int hi_rocm_launch_sample_last_row(const void* logits, void* output_token, int rows, int cols,
+                                   float temperature, float top_p, int top_k, float sample,
+                                   void* stream);
+
+/* kernels.cu:14819 hi_cuda_launch_sample_batched_last_token (+ gpu.rs:15685-
+ * 15767): one config for all rows, samples[b] the uniform of row b.
+ * `gpu_ranked` is accepted for ABI compatibility and ignored: ranked rows
+ * are always resolved on the device, bit-exact with the host sampler. */
+int hi_rocm_launch_sample_batched_last_token(const void* logits, void* output_tokens,
+                                             const void* samples, int batch_count, int seq_len,
+                                             int cols, float temperature, float top_p, int top_k,
+                                             int gpu_ranked, void* stream);
+
+/* kernels.cu:14850 hi_cuda_launch_select_batched_last_token_per_row (+ the
+ * host pass of gpu.rs:15810-15967): per-row temperatures (f32[B]), top_ps
+ * (f32[B]), top_ks (i32[B], 0 = unset) and samples (f32[B]). */
+int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* output_tokens,
+                                                     const void* samples,
+                                                     const void* temperatures,
+                                                     const void* top_ps, const void* top_ks,
+                                                     int batch_count, int seq_len, int cols,
+                                                     int gpu_ranked, void* stream);
+
+/* The mirrors above take no workspace, like the reference.  They use a
+ * per-device workspace that the library grows on demand (hipMalloc).  Call
+ * this once, before any stream capture, with the largest shape to be
+ * sampled so that no allocation happens afterwards. No reference
+ * counterpart (the reference pre-warms its buffer pool instead,
+ * crates/hi-cuda/src/runtime.rs:240-262). */
+int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs);
+
+/* ---- extended pipeline (the decode-step API; proposal of the survey's
+ *      boundary section, no single reference counterpart) ---- */
+
+/* Workspace bytes hi_rocm_sample needs for up to max_batch rows of `vocab`. */
+int hi_rocm_sampler_workspace_bytes(int max_batch, int vocab, int n_logprobs,
+                                    size_t* out_bytes);
+
+/*
+ * Sample one token per row.
+ *   logits       [batch][row_stride] elements of `dtype` (f32 or bf16)
+ *   params       hi_rocm_row_params[batch]
+ *   uniforms     f32[batch], one U[0,1) draw per row (clamped like gpu.rs:882-886)
+ *   hist_offsets u32[batch+1] CSR offsets into hist_ids/hist_counts, or NULL
+ *   hist_ids     u32 token ids (ids >= vocab are ignored)
+ *   hist_counts  u32 occurrence counts (repeated ids add up)
+ *   mask_words   u32[batch][ceil(vocab/32)] allowed-token bitmask (bit i%32 of
+ *                word i/32, 1 = allowed), or NULL for no mask
+ *   out_tokens   u32[batch]
+ *   out_logprobs, out_logprob_ids  f32/u32[batch][n_logprobs] (NULL if 0):
+ *                the first n_logprobs tokens in rank order (weight desc,
+ *                index asc) with log-softmax of the processed distribution
+ *   out_token_logprobs f32[batch] log-prob of the sampled token, or NULL
+ *   workspace    >= hi_rocm_sampler_workspace_bytes(batch, vocab, n_logprobs)
+ * No allocation and no host synchronisation: safe to capture in a hipGraph.
+ */
+int hi_rocm_sample(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                   const hi_rocm_row_params* params, const float* uniforms,
+                   const uint32_t* hist_offsets, const uint32_t* hist_ids,
+                   const uint32_t* hist_counts, const uint32_t* mask_words,
+                   uint32_t* out_tokens, float* out_logprobs, uint32_t* out_logprob_ids,
+                   float* out_token_logprobs, int n_logprobs, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/*
+ * Debug export for the 1e-5 numerics check: the processed logits
+ * (mask + penalties, before temperature) and the full-vocabulary
+ * probabilities softmax(l / T) (T = 1 for greedy rows), f32[batch][vocab]
+ * each.  Same inputs as hi_rocm_sample.  No reference counterpart.
+ */
+int hi_rocm_debug_distribution(const void* logits, int dtype, int batch, int vocab,
+                               int64_t row_stride, const hi_rocm_row_params* params,
+                               const uint32_t* hist_offsets, const uint32_t* hist_ids,
+                               const uint32_t* hist_counts, const uint32_t* mask_words,
+                               float* out_processed, float* out_probs, void* stream);
+
+/* Debug export: y[i] = the device weight function exp(x[i]) for n floats
+ * (device arrays).  Bit-identical to host glibc expf.  No reference
+ * counterpart; the reference's closest check is crates/hi-cuda/src/
+ * dsv4_gpu.rs:7332 for its own device expf. */
+int hi_rocm_debug_expf(const float* x, float* y, int64_t n, void* stream);
+
+/* Thread-local message for the last non-zero status. */
+const char* hi_rocm_last_error(void);
+
+/* Library version string. */
+const char* hi_rocm_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HI_ROCM_H */

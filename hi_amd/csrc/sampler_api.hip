@@ -70,7 +70,8 @@ void carve(hi_rocm::SampleArgs& a, void* ws, const hi_rocm::WorkspaceLayout& L) 
   a.ws_w = (float*)(base + L.ws_w);
   a.ws_list = (uint64_t*)(base + L.ws_list);
   a.list_stride = L.list_stride;
-  a.n_chunks = L.n_chunks;
+  a.chunk = hi_rocm::choose_chunk(a.B, a.V);
+  a.n_chunks = (a.V + a.chunk - 1) / a.chunk;
 }
 
 int vec_aligned(const void* p, int dtype, int64_t row_stride) {
@@ -103,7 +104,7 @@ int run_with_internal_ws(hi_rocm::SampleArgs& a, hipStream_t stream) {
   return HI_ROCM_OK;
 }
 
-bool vocab_ok(int V) { return V > 0 && (int64_t)V <= (int64_t)hi_rocm::kMaxChunks * hi_rocm::kChunk; }
+bool vocab_ok(int V) { return V > 0 && V <= hi_rocm::kMaxVocab; }
 
 }  // namespace
 

@@ -8,12 +8,14 @@
 
 namespace hi_rocm {
 
-constexpr int kScanThreads = 256;                  // scan workgroup (4 waves)
-constexpr int kScanVec = 8;                        // 128-bit loads per thread
-constexpr int kChunk = kScanThreads * kScanVec * 4;  // 8192 logits per chunk
+constexpr int kScanThreads = 256;                  // workgroup (4 wave64s)
+constexpr int kVecLarge = 4;                       // float4 loads per thread per tile
+constexpr int kTilesLarge = 4;                     // tiles per chunk
+constexpr int kChunk = kScanThreads * kVecLarge * 4 * kTilesLarge;  // 16384 logits per chunk
+constexpr int kVecSmall = 2;
+constexpr int kChunkSmall = kScanThreads * kVecSmall * 4;  // 2048 (one tile), small batches
 constexpr int kFast = 1024;                        // candidates kept per chunk (max)
-constexpr int kFinThreads = 1024;                  // finish workgroup (16 waves)
-constexpr int kMaxChunks = 1024;                   // => vocab <= 8,388,608
+constexpr int kMaxVocab = 1 << 23;                 // 8,388,608
 constexpr int kLseTop = 16;                        // per-chunk candidates kept for logprobs
 
 enum RowClass : int { kGreedy = 0, kTopK = 1, kTopP = 2, kTempOnly = 3 };
@@ -55,7 +57,8 @@ struct RowCfg {
 
 // Per (row, chunk) statistics written by the scan, merged by the finish.
 struct ChunkStat {
-  float max_s;                    // max of s = l / t_eff (non-finite l -> -inf)
+  float max_l;                    // max finite processed logit l (-inf: none);
+                                  // the debug kernels keep the max of s here
   float am_ieee_v;                // argmax, IEEE '>' (kernels.cu:7153-7186)
   uint32_t am_ieee_i;
   int32_t am_tot_k;               // argmax by total_cmp (gpu.rs:739-751)
@@ -86,6 +89,7 @@ struct SampleArgs {
   int mask_words;      // ceil(V / 32)
   int n_lp;
   int need_lse;
+  int chunk;           // logits per chunk (kChunk or kChunkSmall)
   int n_chunks;
   uint32_t* out_tokens;
   float* out_lp;
@@ -102,9 +106,11 @@ struct SampleArgs {
 
 struct WorkspaceLayout {
   size_t stats, cand, ws_s, ws_w, ws_list, total;
-  int n_chunks;
+  int64_t slots;       // (row, chunk) records reserved
   int64_t list_stride;
 };
+
+int choose_chunk(int B, int V);
 
 inline int64_t next_pow2_i64(int64_t x) {
   int64_t p = 1;
@@ -112,17 +118,23 @@ inline int64_t next_pow2_i64(int64_t x) {
   return p;
 }
 
-inline WorkspaceLayout workspace_layout(int B, int V) {
+// Workspace for any call with up to max_batch rows of V logits.
+inline WorkspaceLayout workspace_layout(int max_batch, int V) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   WorkspaceLayout L;
-  L.n_chunks = (V + kChunk - 1) / kChunk;
+  L.slots = 0;
+  for (int b = 1; b <= max_batch; ++b) {
+    const int ch = choose_chunk(b, V);
+    const int64_t s = (int64_t)b * ((V + ch - 1) / ch);
+    if (s > L.slots) L.slots = s;
+  }
   L.list_stride = next_pow2_i64(V);
   size_t off = 0;
-  L.stats = off; off = align(off + (size_t)B * L.n_chunks * sizeof(ChunkStat));
-  L.cand = off; off = align(off + (size_t)B * L.n_chunks * kFast * sizeof(uint64_t));
-  L.ws_s = off; off = align(off + (size_t)B * V * sizeof(float));
-  L.ws_w = off; off = align(off + (size_t)B * V * sizeof(float));
-  L.ws_list = off; off = align(off + (size_t)B * L.list_stride * sizeof(uint64_t));
+  L.stats = off; off = align(off + (size_t)L.slots * sizeof(ChunkStat));
+  L.cand = off; off = align(off + (size_t)L.slots * kFast * sizeof(uint64_t));
+  L.ws_s = off; off = align(off + (size_t)max_batch * V * sizeof(float));
+  L.ws_w = off; off = align(off + (size_t)max_batch * V * sizeof(float));
+  L.ws_list = off; off = align(off + (size_t)max_batch * L.list_stride * sizeof(uint64_t));
   L.total = off;
   return L;
 }

@@ -1,37 +1,48 @@
 // hi-rocm batched token sampler: CDNA4 (gfx950) kernels.
 //
-// Per decode step the logits [B, V] stay in HBM; two kernels produce one
-// token id (and optional logprobs) per row:
+// Two kernels per decode step.  Logits [B, V] stay in HBM; the scan grid is
+// (chunks per row, B) workgroups of 256 threads (4 wave64s):
 //
-//   scan_chunks   grid (ceil(V/8192), B) x 256 threads.  One streaming pass
-//                 over the row's logits with 128-bit loads: allowed-token
-//                 mask, penalties from an LDS count table built from the
-//                 row's history, temperature, then per-chunk statistics
-//                 (max, three argmax variants, online log-sum-exp) and the
-//                 chunk's exact top-k' candidates (LDS radix select).
-//   finish_rows   grid B x 1024 threads.  Merges the chunk candidates,
-//                 ranks them with the glibc-exact weight function and runs
-//                 the reference's sequential f32 folds and inverse-CDF draw
-//                 (crates/hi-cuda/src/gpu.rs:753-900) on device.
+//   scan   every workgroup streams one chunk of one row exactly once with
+//          128-bit loads, all issued before any use (4 KiB per wave in
+//          flight; 4096-logit chunks, 1024 when the batch is small).  Per element: allowed-token mask, penalties from an LDS
+//          count table built from the row's history, temperature.  The
+//          workgroup then reduces its statistics (max, three argmax
+//          variants) and selects the chunk's exact top-k' by (scaled logit
+//          desc, index asc): a bound from the per-thread maxima pre-filters
+//          the chunk to about 1.3 k' elements, and an 8-bit LDS radix
+//          descent finishes the selection.
+//   finish a second launch, one workgroup per row, merges the chunk
+//          candidates, ranks them with the glibc-exact weight function and
+//          runs the reference's sequential f32 folds and inverse-CDF draw
+//          (crates/hi-cuda/src/gpu.rs:753-900).
 //
 // Rows without top-k (top-p / min-p only, temperature-only) and rows with
-// top_k > 1024 additionally keep their scaled logits in the workspace and are
-// finished from there (several passes, served mostly by L2/MALL).
+// top_k > 1024 also keep their scaled logits in the workspace; their finish
+// re-reads the row from there (served mostly by L2 / MALL).
 //
-// All arithmetic that decides a token mirrors the reference bit for bit:
+// Every operation that decides a token mirrors the reference bit for bit:
 // IEEE f32 division and addition in the reference's order, no contraction
-// (this file is built with -ffp-contract=off), and exact_expf() equal to
-// host glibc expf.  Selections use integer radix histograms only, so results
-// are deterministic run to run.
+// (the library is built with -ffp-contract=off), and exact_expf() equal to
+// host glibc expf.  Selections use integer histograms and prefix scans in a
+// fixed order, so results are deterministic run to run.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <float.h>
+#include <stddef.h>
 
 #include "hi_rocm.h"
 #include "exact_expf.h"
 #include "sampler_internal.h"
 
 namespace hi_rocm {
+
+constexpr int NT = kScanThreads;  // threads of the fused kernel
+constexpr int kBuf = 1024;        // ranked entries held in LDS
+constexpr int kGather = 4096;     // candidates of a row gathered into LDS
+constexpr int kBufCap = 2048;     // running chunk candidates held in LDS
+constexpr int kHashCap = 2048;    // distinct history tokens per chunk held in LDS
+constexpr int kBins = 1024;       // weight histogram of the wide paths (w bits >> 20)
 
 // --------------------------------------------------------------------------
 // small helpers
@@ -42,17 +53,27 @@ __device__ __forceinline__ bool finitef_(float x) {
 
 // Order-preserving unsigned key of a float (NaN never occurs here).
 __device__ __forceinline__ uint32_t okey(float f) {
-  uint32_t u = __float_as_uint(f);
+  const uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 __device__ __forceinline__ float okey_inv(uint32_t k) {
-  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
   return __uint_as_float(u);
+}
+
+// Key of a processed logit: its order key, non-finite values as -inf
+// (gpu.rs:767-777 maps them to -inf before ranking).
+constexpr uint32_t kKeyNegInf = 0x007fffffu;  // okey(-inf)
+__device__ __forceinline__ uint32_t lkey(float l) { return finitef_(l) ? okey(l) : kKeyNegInf; }
+
+// Scaled logit s = l / t_eff of a key (gpu.rs:767-777).
+__device__ __forceinline__ float key_to_s(uint32_t key, float t_eff) {
+  return key == kKeyNegInf ? -__builtin_inff() : okey_inv(key) / t_eff;
 }
 
 // Rust's f32::total_cmp as a signed key (gpu.rs:744).
 __device__ __forceinline__ int32_t total_key(float f) {
-  int32_t i = (int32_t)__float_as_uint(f);
+  const int32_t i = (int32_t)__float_as_uint(f);
   return i ^ (int32_t)(((uint32_t)(i >> 31)) >> 1);
 }
 
@@ -65,16 +86,33 @@ __device__ __forceinline__ uint32_t cand_idx(uint64_t c) { return 0xffffffffu - 
 __device__ __forceinline__ uint32_t cand_skey(uint64_t c) { return (uint32_t)(c >> 32); }
 
 // Rank key of the reference order (weight desc by total_cmp, index asc);
-// weights are >= +0 so their bits order like the floats.
+// weights are >= +0, so their bits order like the floats.
 __device__ __forceinline__ uint64_t rank_key(float w, uint32_t idx) {
   return ((uint64_t)__float_as_uint(w) << 32) | (uint64_t)(0xffffffffu - idx);
+}
+__device__ __forceinline__ float rank_w(uint64_t r) { return __uint_as_float((uint32_t)(r >> 32)); }
+
+// Chunk-local composite (48 bits): key << 16 | (0xffff - local index).
+__device__ __forceinline__ uint64_t local_comp(uint32_t key, uint32_t li) {
+  return ((uint64_t)key << 16) | (uint64_t)(0xffffu - li);
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
+__device__ __forceinline__ float clamp_uniform(float u) {
+  // gpu.rs:882-886
+  return finitef_(u) ? (u < 0.f ? 0.f : (u > 0.99999994f ? 0.99999994f : u)) : 0.f;
+}
+
+__device__ __forceinline__ int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
 // ---- parameters ----------------------------------------------------------
 
-__device__ RowCfg load_cfg(const ParamsView& pv, int row, int V, int n_lp, int need_lse) {
+__device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V, int n_lp, int need_lse) {
   RowCfg c;
   c.min_p = 0.f; c.rep = 1.f; c.freq = 0.f; c.pres = 0.f; c.eos = 0u; c.flags = 0u;
   if (pv.mode == kParamsRows) {
@@ -101,7 +139,7 @@ __device__ RowCfg load_cfg(const ParamsView& pv, int row, int V, int n_lp, int n
   c.pres = finitef_(c.pres) ? c.pres : 0.f;
   c.wide = c.cls == kTopK && c.k_eff > kFast;
   c.k_sel = (c.cls == kTopK && !c.wide) ? max(c.k_eff, n_lp) : n_lp;
-  // Logprobs need the normaliser to ~1e-7 relative: the largest terms are
+  // Logprobs need the normaliser to ~1e-7 relative: its largest terms are
   // summed in double from the candidates, so every chunk keeps a few.
   if (need_lse) c.k_sel = max(c.k_sel, kLseTop);
   if (c.k_sel > V) c.k_sel = V;
@@ -113,7 +151,7 @@ __device__ __forceinline__ float row_uniform(const ParamsView& pv, int row) {
   return pv.uniforms ? pv.uniforms[row] : pv.uniform_value;
 }
 
-// Stage 2 and 3 of the processed logit (the mask is applied by the caller):
+// Stages 2 and 3 of the processed logit (the mask is applied by the caller):
 // repetition penalty per occurrence (crates/hi-mlx/src/generate.rs:60-70),
 // then frequency and presence penalties as separate f32 roundings.
 __device__ __forceinline__ float apply_penalties(float l, uint32_t cnt, const RowCfg& c) {
@@ -128,9 +166,9 @@ __device__ __forceinline__ float apply_penalties(float l, uint32_t cnt, const Ro
   return l;
 }
 
-// ---- block-level reductions ------------------------------------------------
+// ---- block-level reductions (wave64 shuffles, then LDS) -------------------
 
-template <int NT>
+template <int N>
 __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -138,11 +176,11 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
   if (lane == 0) red[wid] = v;
   __syncthreads();
   uint32_t s = 0;
-  for (int i = 0; i < NT / 64; ++i) s += red[i];
+  for (int i = 0; i < N / 64; ++i) s += red[i];
   return s;
 }
 
-template <int NT>
+template <int N>
 __device__ __forceinline__ float block_sum_f32(float v, float* red) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -150,11 +188,11 @@ __device__ __forceinline__ float block_sum_f32(float v, float* red) {
   if (lane == 0) red[wid] = v;
   __syncthreads();
   float s = 0.f;
-  for (int i = 0; i < NT / 64; ++i) s += red[i];
+  for (int i = 0; i < N / 64; ++i) s += red[i];
   return s;
 }
 
-template <int NT>
+template <int N>
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -162,11 +200,11 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
   if (lane == 0) red[wid] = v;
   __syncthreads();
   double s = 0.0;
-  for (int i = 0; i < NT / 64; ++i) s += red[i];
+  for (int i = 0; i < N / 64; ++i) s += red[i];
   return s;
 }
 
-template <int NT>
+template <int N>
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
   for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor(v, o, 64));
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -174,40 +212,50 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
   if (lane == 0) red[wid] = v;
   __syncthreads();
   uint32_t s = 0;
-  for (int i = 0; i < NT / 64; ++i) s = max(s, red[i]);
+  for (int i = 0; i < N / 64; ++i) s = max(s, red[i]);
   return s;
 }
 
-template <int NT>
-__device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* red) {
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int N>
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
   for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t t = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64) << 32) |
-                       (uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
-    if (t < v) v = t;
+    const uint64_t t = shfl_xor_u64(v, o);
+    if (t > v) v = t;
   }
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wid] = v;
   __syncthreads();
   uint64_t s = red[0];
-  for (int i = 1; i < NT / 64; ++i) s = red[i] < s ? red[i] : s;
+  for (int i = 1; i < N / 64; ++i) s = red[i] > s ? red[i] : s;
   return s;
 }
 
+template <int N>
+__device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* red) {
+  return ~block_max_u64<N>(~v, red);
+}
+
 // Exclusive prefix sum over the block in thread order; *total gets the sum.
-template <int NT>
+template <int N>
 __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* red, uint32_t* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   uint32_t inc = v;
   for (int o = 1; o < 64; o <<= 1) {
-    uint32_t t = __shfl_up(inc, o, 64);
+    const uint32_t t = __shfl_up(inc, o, 64);
     if (lane >= o) inc += t;
   }
   __syncthreads();
   if (lane == 63) red[wid] = inc;
   __syncthreads();
   uint32_t before = 0, tot = 0;
-  for (int i = 0; i < NT / 64; ++i) {
+  for (int i = 0; i < N / 64; ++i) {
     if (i < wid) before += red[i];
     tot += red[i];
   }
@@ -215,9 +263,11 @@ __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* re
   return before + inc - v;
 }
 
-// Chunk / row statistics merge (associative, order independent).
+// ---- chunk statistics ------------------------------------------------------
+
+// Associative, order-independent merge of two statistics records.
 __device__ __forceinline__ void stat_merge(ChunkStat& a, const ChunkStat& b) {
-  a.max_s = fmaxf(a.max_s, b.max_s);
+  a.max_l = fmaxf(a.max_l, b.max_l);
   if (b.am_ieee_i != 0xffffffffu &&
       (a.am_ieee_i == 0xffffffffu || b.am_ieee_v > a.am_ieee_v ||
        (b.am_ieee_v == a.am_ieee_v && b.am_ieee_i < a.am_ieee_i))) {
@@ -240,7 +290,7 @@ __device__ __forceinline__ void stat_merge(ChunkStat& a, const ChunkStat& b) {
 }
 
 __device__ __forceinline__ void stat_init(ChunkStat& s) {
-  s.max_s = -__builtin_inff();
+  s.max_l = -__builtin_inff();
   s.am_ieee_v = -__builtin_inff(); s.am_ieee_i = 0xffffffffu;
   s.am_tot_k = 0; s.am_tot_i = 0xffffffffu;
   s.am_fin_v = -__builtin_inff(); s.am_fin_i = 0xffffffffu;
@@ -252,21 +302,20 @@ __device__ __forceinline__ void stat_init(ChunkStat& s) {
 
 __device__ __forceinline__ ChunkStat stat_shfl_xor(const ChunkStat& s, int o) {
   ChunkStat r;
-  r.max_s = __shfl_xor(s.max_s, o, 64);
+  stat_init(r);
+  r.max_l = __shfl_xor(s.max_l, o, 64);
   r.am_ieee_v = __shfl_xor(s.am_ieee_v, o, 64); r.am_ieee_i = __shfl_xor(s.am_ieee_i, o, 64);
   r.am_tot_k = __shfl_xor(s.am_tot_k, o, 64); r.am_tot_i = __shfl_xor(s.am_tot_i, o, 64);
   r.am_fin_v = __shfl_xor(s.am_fin_v, o, 64); r.am_fin_i = __shfl_xor(s.am_fin_i, o, 64);
   r.any_finite = __shfl_xor(s.any_finite, o, 64);
-  r.lse_m = __shfl_xor(s.lse_m, o, 64); r.lse_sum = __shfl_xor(s.lse_sum, o, 64);
-  r.n_cand = 0u; r.trunc = 0u; r.unkept_key = 0u; r.pad0 = 0u; r.min_kept = 0ull;
   return r;
 }
 
-// Reduce a per-thread ChunkStat over the block; the result is valid in all threads.
-template <int NT>
+// Reduce a per-thread statistics record over the block (valid in all threads).
+template <int N>
 __device__ __forceinline__ ChunkStat block_stat(ChunkStat s, ChunkStat* red) {
   for (int o = 32; o > 0; o >>= 1) {
-    ChunkStat t = stat_shfl_xor(s, o);
+    const ChunkStat t = stat_shfl_xor(s, o);
     stat_merge(s, t);
   }
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -274,7 +323,7 @@ __device__ __forceinline__ ChunkStat block_stat(ChunkStat s, ChunkStat* red) {
   if (lane == 0) red[wid] = s;
   __syncthreads();
   ChunkStat r = red[0];
-  for (int i = 1; i < NT / 64; ++i) stat_merge(r, red[i]);
+  for (int i = 1; i < N / 64; ++i) stat_merge(r, red[i]);
   return r;
 }
 
@@ -285,254 +334,53 @@ __device__ __forceinline__ float load_raw(const void* base, int dtype, int64_t o
   return ((const float*)base)[off];
 }
 
-// Processed logit of a single token (mask + penalties), computed by the whole
-// block: the count is reduced over the row's history.  Used off the hot path.
-template <int NT>
-__device__ float processed_single(const SampleArgs& a, int row, const RowCfg& c, uint32_t idx,
+__device__ __forceinline__ bool allowed(const SampleArgs& a, int row, uint32_t idx) {
+  return !a.mask || ((a.mask[(int64_t)row * a.mask_words + (idx >> 5)] >> (idx & 31u)) & 1u);
+}
+
+// Processed logit of one token (mask + penalties), computed by the whole
+// block: its history count is reduced over the row's history list.
+template <int N>
+__device__ __forceinline__ float processed_single(const SampleArgs& a, int row, const RowCfg& c, uint32_t idx,
                                   uint32_t* red) {
   uint32_t cnt = 0;
   if (a.hoff) {
     const uint32_t h0 = a.hoff[row], h1 = a.hoff[row + 1];
-    for (uint32_t h = h0 + threadIdx.x; h < h1; h += NT)
+    for (uint32_t h = h0 + threadIdx.x; h < h1; h += N)
       if (a.hids[h] == idx) cnt += a.hcnt[h];
   }
-  cnt = block_sum_u32<NT>(cnt, red);
-  const int64_t rbase = (int64_t)row * a.row_stride;
-  float l = load_raw(a.logits, a.dtype, rbase + idx);
-  if (a.mask && !((a.mask[(int64_t)row * a.mask_words + (idx >> 5)] >> (idx & 31u)) & 1u))
-    l = -__builtin_inff();
+  cnt = block_sum_u32<N>(cnt, red);
+  float l = load_raw(a.logits, a.dtype, (int64_t)row * a.row_stride + idx);
+  if (!allowed(a, row, idx)) l = -__builtin_inff();
   return apply_penalties(l, cnt, c);
 }
 
-// ==========================================================================
-// Kernel 1: streaming chunk scan
-// ==========================================================================
+// ---- radix selection ------------------------------------------------------
 
-struct ScanShared {
-  uint32_t cnt[kChunk];   // history counts of the chunk (32 KB)
-  uint32_t key[kChunk];   // scaled-logit keys of the chunk (32 KB)
-  uint32_t hist[4096];    // radix histogram (16 KB)
-  ChunkStat red[kScanThreads / 64];
-  uint32_t redu[kScanThreads / 64];
-  uint64_t red64[kScanThreads / 64];
-  float redf[kScanThreads / 64];
-  uint32_t sel_digit, sel_above, sel_cnt, counter;
-};
-
-__global__ void __launch_bounds__(kScanThreads) scan_chunks_kernel(SampleArgs a) {
-  __shared__ ScanShared sh;
-  const int row = blockIdx.y;
-  const int chunk = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int V = a.V;
-  const int c0 = chunk * kChunk;
-  const int c1 = min(c0 + kChunk, V);
-  const int len = c1 - c0;
-  const RowCfg cfg = load_cfg(a.pv, row, V, a.n_lp, a.need_lse);
-
-  // History counts for this chunk, in LDS.
-  bool pen = false;
-  uint32_t h0 = 0, h1 = 0;
-  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; pen = h1 > h0; }
-  if (pen) {
-    for (int i = tid; i < kChunk; i += kScanThreads) sh.cnt[i] = 0u;
-    __syncthreads();
-    for (uint32_t h = h0 + tid; h < h1; h += kScanThreads) {
-      const uint32_t id = a.hids[h];
-      if (id >= (uint32_t)c0 && id < (uint32_t)c1) atomicAdd(&sh.cnt[id - c0], a.hcnt[h]);
-    }
-    __syncthreads();
-  }
-
-  const int64_t rbase = (int64_t)row * a.row_stride;
-  const uint32_t* mrow = a.mask ? a.mask + (int64_t)row * a.mask_words : nullptr;
-  const bool need_keys = cfg.k_sel > 0;
-  float* srow = cfg.store_s ? a.ws_s + (int64_t)row * V : nullptr;
-
-  ChunkStat st;
-  stat_init(st);
-
-  #pragma unroll 1
-  for (int j = 0; j < kScanVec; ++j) {
-    const int e0 = c0 + (j * kScanThreads + tid) * 4;
-    if (e0 >= c1) break;
-    float raw[4];
-    if (a.vec_ok && e0 + 3 < c1) {
-      if (a.dtype == HI_ROCM_DTYPE_BF16) {
-        const uint2 v = *(const uint2*)((const uint16_t*)a.logits + rbase + e0);
-        raw[0] = __uint_as_float(v.x << 16); raw[1] = __uint_as_float(v.x & 0xffff0000u);
-        raw[2] = __uint_as_float(v.y << 16); raw[3] = __uint_as_float(v.y & 0xffff0000u);
-      } else {
-        const float4 v = *(const float4*)((const float*)a.logits + rbase + e0);
-        raw[0] = v.x; raw[1] = v.y; raw[2] = v.z; raw[3] = v.w;
-      }
-    } else {
-      #pragma unroll
-      for (int q = 0; q < 4; ++q) raw[q] = (e0 + q < c1) ? load_raw(a.logits, a.dtype, rbase + e0 + q) : 0.f;
-    }
-    const uint32_t mword = mrow ? mrow[e0 >> 5] : 0xffffffffu;
-    float sv[4];
-    #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = e0 + q;
-      if (e >= c1) { sv[q] = -__builtin_inff(); continue; }
-      float l = raw[q];
-      if (!((mword >> (e & 31)) & 1u)) l = -__builtin_inff();
-      if (pen) l = apply_penalties(l, sh.cnt[e - c0], cfg);
-      const bool fin = finitef_(l);
-      const float s = fin ? l / cfg.t_eff : -__builtin_inff();
-      sv[q] = s;
-      st.max_s = fmaxf(st.max_s, s);
-      if (l > st.am_ieee_v) { st.am_ieee_v = l; st.am_ieee_i = (uint32_t)e; }
-      const int32_t tk = total_key(l);
-      if (st.am_tot_i == 0xffffffffu || tk > st.am_tot_k) { st.am_tot_k = tk; st.am_tot_i = (uint32_t)e; }
-      if (fin) {
-        st.any_finite = 1u;
-        if (st.am_fin_i == 0xffffffffu || l > st.am_fin_v ||
-            (l == st.am_fin_v && ((uint32_t)e & 255u) < (st.am_fin_i & 255u))) {
-          st.am_fin_v = l; st.am_fin_i = (uint32_t)e;
-        }
-      }
-      if (need_keys) sh.key[e - c0] = okey(s);
-    }
-    if (srow) {
-      if (e0 + 3 < c1 && (V & 3) == 0) {
-        *(float4*)(srow + e0) = make_float4(sv[0], sv[1], sv[2], sv[3]);
-      } else {
-        for (int q = 0; q < 4; ++q) if (e0 + q < c1) srow[e0 + q] = sv[q];
-      }
-    }
-  }
-
-  ChunkStat bs = block_stat<kScanThreads>(st, sh.red);
-
-  // Exact top-k' of the chunk by (scaled logit desc, index asc).
-  uint64_t* cand = a.cand + ((int64_t)row * a.n_chunks + chunk) * kFast;
-  if (need_keys) {
-    __syncthreads();
-    const int k = cfg.k_sel;
-    if (len <= k) {
-      for (int i = tid; i < len; i += kScanThreads) cand[i] = cand_key(sh.key[i], (uint32_t)(c0 + i));
-      bs.n_cand = (uint32_t)len; bs.trunc = 0u;
-    } else {
-      // 48-bit composite: key << 16 | (0xffff - local index); unique per item.
-      uint64_t prefix = 0;
-      uint32_t remaining = (uint32_t)k;
-      for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 36 - 12 * pass;
-        for (int b = tid; b < 4096; b += kScanThreads) sh.hist[b] = 0u;
-        __syncthreads();
-        const uint64_t hi_pref = prefix >> (shift + 12);
-        for (int i = tid; i < len; i += kScanThreads) {
-          const uint64_t comp = ((uint64_t)sh.key[i] << 16) | (uint64_t)(0xffffu - (uint32_t)i);
-          if ((comp >> (shift + 12)) == hi_pref) atomicAdd(&sh.hist[(comp >> shift) & 4095u], 1u);
-        }
-        __syncthreads();
-        // thread t owns bins 4095-16t down to 4080-16t
-        uint32_t loc[16];
-        uint32_t lsum = 0;
-        #pragma unroll
-        for (int q = 0; q < 16; ++q) { loc[q] = sh.hist[4095 - 16 * tid - q]; lsum += loc[q]; }
-        uint32_t tot;
-        const uint32_t above = block_excl_scan_u32<kScanThreads>(lsum, sh.redu, &tot);
-        if (above < remaining && remaining <= above + lsum) {
-          uint32_t acc = above;
-          for (int q = 0; q < 16; ++q) {
-            if (remaining <= acc + loc[q]) {
-              sh.sel_digit = 4095u - 16u * tid - q; sh.sel_above = acc; sh.sel_cnt = loc[q];
-              break;
-            }
-            acc += loc[q];
-          }
-        }
-        __syncthreads();
-        prefix |= (uint64_t)sh.sel_digit << shift;
-        remaining -= sh.sel_above;
-        const bool done = sh.sel_cnt == remaining;
-        __syncthreads();
-        if (done) break;
-      }
-      const uint64_t thr = prefix;
-      if (tid == 0) sh.counter = 0u;
-      __syncthreads();
-      uint32_t unkept = 0u;
-      uint64_t minkept = ~0ull;
-      float rest = 0.f;  // sum of exp(s - chunk max) over elements not kept
-      const bool rest_on = a.need_lse && finitef_(bs.max_s);
-      for (int i = tid; i < len; i += kScanThreads) {
-        const uint32_t kk = sh.key[i];
-        const uint64_t comp = ((uint64_t)kk << 16) | (uint64_t)(0xffffu - (uint32_t)i);
-        if (comp >= thr) {
-          const uint32_t pos = atomicAdd(&sh.counter, 1u);
-          const uint64_t ck = cand_key(kk, (uint32_t)(c0 + i));
-          if (pos < (uint32_t)kFast) cand[pos] = ck;
-          if (ck < minkept) minkept = ck;
-        } else {
-          unkept = max(unkept, kk);
-          if (rest_on) rest += __expf(okey_inv(kk) - bs.max_s);
-        }
-      }
-      bs.lse_m = bs.max_s;
-      bs.lse_sum = block_sum_f32<kScanThreads>(rest, sh.redf);
-      const uint64_t mk = block_min_u64<kScanThreads>(minkept, sh.red64);
-      const uint32_t um = block_max_u32<kScanThreads>(unkept, sh.redu);
-      bs.n_cand = (uint32_t)k;
-      bs.trunc = 1u;
-      bs.unkept_key = um;
-      bs.min_kept = mk;
-    }
-  }
-  if (tid == 0) a.stats[(int64_t)row * a.n_chunks + chunk] = bs;
-}
-
-// ==========================================================================
-// Kernel 2: per-row finish
-// ==========================================================================
-
-constexpr int kFinBuf = 8192;  // u64 LDS entries
-
-struct FinShared {
-  uint64_t buf[kFinBuf];       // 64 KB: candidates / rank keys / tiles
-  uint32_t hist[4096];         // 16 KB
-  uint64_t mass[2048];         // 16 KB (top-p path)
-  uint32_t aux[2048];          //  8 KB (fill counters, per-thread sums)
-  float fa[kFast];             //  4 KB: weights in rank order
-  float fb[kFast];             //  4 KB: q = w / total
-  uint32_t pay[kFast];         //  4 KB: scaled-logit keys riding with sh.buf
-  ChunkStat red[kFinThreads / 64];
-  uint32_t redu[kFinThreads / 64];
-  double redd[kFinThreads / 64];
-  uint32_t sel_digit, sel_above, sel_cnt, counter, n_ext, token, flag;
-  float fval0, fval1;
-  uint64_t thr;
-};
-
-// Top-`k` threshold over a set of unique 64-bit keys produced by get(j)
-// for j < n (invalid slots return 0 and are never selected because k never
-// exceeds the number of valid non-zero keys).  Returns T with exactly k keys
-// >= T.  8-bit MSD radix descent with early exit.
-template <typename Get>
-__device__ uint64_t block_select64(FinShared& sh, int n, uint32_t k, Get get) {
+// Threshold T such that exactly k of the block's items (unique keys of
+// `bits` bits, a multiple of 8) are >= T.  for_each(cb) calls cb(key) for
+// every item the calling thread owns.  8-bit MSD descent with early exit;
+// hist has 256 entries, sel 3.
+template <typename ForEach>
+__device__ __forceinline__ uint64_t radix_select_top(uint32_t* hist, uint32_t* sel, uint32_t k, int bits,
+                                     ForEach for_each) {
   const int tid = threadIdx.x;
   uint64_t prefix = 0;
   uint32_t remaining = k;
-  for (int pass = 0; pass < 8; ++pass) {
-    const int shift = 56 - 8 * pass;
-    for (int b = tid; b < 256; b += kFinThreads) sh.hist[b] = 0u;
+  for (int shift = bits - 8; shift >= 0; shift -= 8) {
+    for (int b = tid; b < 256; b += NT) hist[b] = 0u;
     __syncthreads();
-    for (int j = tid; j < n; j += kFinThreads) {
-      bool valid;
-      const uint64_t x = get(j, valid);
-      if (!valid) continue;
-      if (pass == 0 || (x >> (shift + 8)) == (prefix >> (shift + 8)))
-        atomicAdd(&sh.hist[(x >> shift) & 255u], 1u);
-    }
+    const int hs = shift + 8;
+    const uint64_t hp = hs >= 64 ? 0ull : (prefix >> hs);
+    for_each([&](uint64_t x) {
+      if (hs >= 64 || (x >> hs) == hp) atomicAdd(&hist[(uint32_t)(x >> shift) & 255u], 1u);
+    });
     __syncthreads();
     if (tid < 64) {
-      // each lane of wave 0 owns 4 bins, highest bins first
+      // lane l owns bins 255-4l .. 252-4l (descending)
       uint32_t loc[4], lsum = 0;
       #pragma unroll
-      for (int q = 0; q < 4; ++q) { loc[q] = sh.hist[255 - 4 * tid - q]; lsum += loc[q]; }
+      for (int q = 0; q < 4; ++q) { loc[q] = hist[255 - 4 * tid - q]; lsum += loc[q]; }
       uint32_t inc = lsum;
       for (int o = 1; o < 64; o <<= 1) {
         const uint32_t t = __shfl_up(inc, o, 64);
@@ -541,38 +389,118 @@ __device__ uint64_t block_select64(FinShared& sh, int n, uint32_t k, Get get) {
       const uint32_t above = inc - lsum;
       if (above < remaining && remaining <= above + lsum) {
         uint32_t acc = above;
+        #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (remaining <= acc + loc[q]) {
-            sh.sel_digit = 255u - 4u * tid - q; sh.sel_above = acc; sh.sel_cnt = loc[q];
-            break;
+          if (remaining <= acc + loc[q] && acc < remaining) {
+            sel[0] = 255u - 4u * tid - q; sel[1] = acc; sel[2] = loc[q];
           }
           acc += loc[q];
         }
       }
     }
     __syncthreads();
-    prefix |= (uint64_t)sh.sel_digit << shift;
-    remaining -= sh.sel_above;
-    const bool done = sh.sel_cnt == remaining;
+    prefix |= (uint64_t)sel[0] << shift;
+    remaining -= sel[1];
+    const bool done = sel[2] == remaining;
     __syncthreads();
     if (done) break;
   }
   return prefix;
 }
 
-// Bitonic sort of sh.buf[0..n2) in descending order, carrying sh.pay along
-// (n2 a power of two <= kFast).
-__device__ void lds_sort_desc(FinShared& sh, int n2) {
+// ==========================================================================
+// LDS layouts
+// ==========================================================================
+
+struct ScanLds {
+  uint64_t cbuf[kBufCap];     // running candidates (48-bit local composites)
+  uint32_t U[kBuf];           // per-thread top-j keys of the first tile
+  uint32_t hist[256];
+  ChunkStat red[NT / 64];
+  uint32_t redu[NT / 64];
+  uint64_t red64[NT / 64];
+  float redf[NT / 64];
+  uint32_t sel[4];
+  uint32_t bound, count, hovf;
+  // when the batch has histories: bitmap[chunk / 32], hash keys[kHashCap],
+  // hash counts[kHashCap] follow
+};
+
+struct FinLds {
+  uint64_t cbig[kGather];     // gathered candidates (32 KiB) -- also a fold tile
+  uint64_t buf[kBuf];         // selected candidates / rank keys
+  uint32_t pay[kBuf];         // scaled-logit keys riding with buf
+  float fa[kBuf];             // weights in rank order
+  float fb[kBuf];             // w / total
+  uint32_t hist[kBins];
+  uint64_t mass[kBins];
+  uint32_t aux[kBins];
+  ChunkStat red[NT / 64];
+  uint32_t redu[NT / 64];
+  double redd[NT / 64];
+  uint64_t red64[NT / 64];
+  uint32_t sel[4];
+  uint32_t counter, n_ext, token, flag;
+  float fval0, fval1;
+};
+constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
+
+size_t scan_lds_bytes(int chunk, bool hist) {
+  return sizeof(ScanLds) + (hist ? (size_t)chunk / 8 + 2 * kHashCap * sizeof(uint32_t) : 0);
+}
+
+// ==========================================================================
+// Finish phase (one workgroup per row)
+// ==========================================================================
+
+// Candidates of `row` (written by the chunks): visit every (chunk, slot).
+// Chunk c kept min(k_sel, its length) candidates, so the slots are known
+// without reading the chunk records; one flat parallel loop.
+template <typename F>
+__device__ __forceinline__ void for_each_candidate(const SampleArgs& a, int row, int k_sel, F f) {
+  const int nch = a.n_chunks;
+  const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
+  const int last_len = a.V - (nch - 1) * a.chunk;
+  const int n_full = min(k_sel, a.chunk);
+  const int n_last = min(k_sel, last_len);
+  const int span = (nch - 1) * n_full + n_last;
+  for (int j = threadIdx.x; j < span; j += NT) {
+    const int c = n_full > 0 ? j / n_full : 0;
+    const int s = j - c * n_full;
+    f(cand[(int64_t)c * kFast + s]);
+  }
+}
+
+// Descending sort of fs.buf[0..n) carrying fs.pay; n <= kBuf.
+__device__ __forceinline__ void sort_ranked(FinLds& fs, int n) {
+  const int tid = threadIdx.x;
+  if (n <= NT) {
+    // rank by counting (keys are unique), then scatter
+    uint64_t x = 0;
+    uint32_t p = 0, r = 0;
+    if (tid < n) {
+      x = fs.buf[tid];
+      p = fs.pay[tid];
+      for (int j = 0; j < n; ++j) r += fs.buf[j] > x;
+    }
+    __syncthreads();
+    if (tid < n) { fs.buf[r] = x; fs.pay[r] = p; }
+    __syncthreads();
+    return;
+  }
+  const int n2 = next_pow2(n);
+  for (int i = n + tid; i < n2; i += NT) { fs.buf[i] = 0ull; fs.pay[i] = 0u; }
+  __syncthreads();
   for (int k = 2; k <= n2; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < n2; i += kFinThreads) {
+      for (int i = tid; i < n2; i += NT) {
         const int ixj = i ^ j;
         if (ixj > i) {
-          const uint64_t x = sh.buf[i], y = sh.buf[ixj];
+          const uint64_t x = fs.buf[i], y = fs.buf[ixj];
           const bool desc = (i & k) == 0;
           if (desc ? (x < y) : (x > y)) {
-            sh.buf[i] = y; sh.buf[ixj] = x;
-            const uint32_t t = sh.pay[i]; sh.pay[i] = sh.pay[ixj]; sh.pay[ixj] = t;
+            fs.buf[i] = y; fs.buf[ixj] = x;
+            const uint32_t t = fs.pay[i]; fs.pay[i] = fs.pay[ixj]; fs.pay[ixj] = t;
           }
         }
       }
@@ -581,11 +509,290 @@ __device__ void lds_sort_desc(FinShared& sh, int n2) {
   }
 }
 
-// Bitonic sort of a global array (descending), used by the wide paths.
-__device__ void global_sort_desc(uint64_t* g, int n2) {
+// Number of candidates the chunks of `row` wrote: chunk c keeps
+// min(k_sel, its length), so it is known without reading the records.
+__device__ __forceinline__ int candidate_count(const SampleArgs& a, int k_sel) {
+  const int last_len = a.V - (a.n_chunks - 1) * a.chunk;
+  return (a.n_chunks - 1) * min(k_sel, a.chunk) + min(k_sel, last_len);
+}
+
+// The exact first `kk` entries of the reference rank order (weight desc,
+// index asc) of `row`.  On return fs.buf[0..kk) holds rank keys in order and
+// fs.pay[0..kk) the scaled-logit keys; returns kk.  M is the row max of s.
+// When lse_part is not null, it receives this thread's share of
+// sum(exp(s - M)) over every candidate (double).
+__device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg,
+                               int kk_req, float M, double* lse_part) {
+  const int tid = threadIdx.x;
+  const int nch = a.n_chunks;
+  const ChunkStat* stats = a.stats + (int64_t)row * nch;
+  const int n_total = candidate_count(a, cfg.k_sel);
+  const int kk = min(kk_req, n_total);
+  if (kk <= 0) return 0;
+  auto s_of = [&](uint64_t x) { return key_to_s(cand_skey(x), cfg.t_eff); };
+  double part = 0.0;
+  // 1. candidates into LDS: all of them when they fit, else those at or above
+  //    t0, the largest chunk cut (the kk-th composite is at least every
+  //    truncated chunk's smallest kept composite)
+  uint64_t t0 = 0;
+  uint64_t below_max = 0;  // largest candidate left out of LDS
+  int n_u;
+  bool in_lds = true;
+  if (n_total <= kGather) {
+    int j = 0;
+    for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+      fs.cbig[tid + j * NT] = x;
+      ++j;
+      if (lse_part) part += exp((double)s_of(x) - (double)M);
+    });
+    n_u = n_total;
+  } else {
+    for (int c = tid; c < nch; c += NT)
+      if (stats[c].trunc && stats[c].min_kept > t0) t0 = stats[c].min_kept;
+    t0 = block_max_u64<NT>(t0, fs.red64);
+    uint32_t nu = 0;
+    for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+      nu += x >= t0;
+      if (x < t0 && x > below_max) below_max = x;
+      if (lse_part) part += exp((double)s_of(x) - (double)M);
+    });
+    n_u = (int)block_sum_u32<NT>(nu, fs.redu);
+    below_max = block_max_u64<NT>(below_max, fs.red64);
+    in_lds = n_u <= kGather;
+    if (in_lds) {
+      if (tid == 0) fs.counter = 0u;
+      __syncthreads();
+      for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+        if (x >= t0) fs.cbig[atomicAdd(&fs.counter, 1u)] = x;
+      });
+    }
+  }
+  __syncthreads();
+  if (lse_part) *lse_part = part;
+  // 2. the kk largest
+  uint64_t thr = 0;
+  if (in_lds) {
+    if (n_u > kk) {
+      thr = radix_select_top(fs.hist, fs.sel, (uint32_t)kk, 64, [&](auto cb) {
+        for (int i = tid; i < n_u; i += NT) cb(fs.cbig[i]);
+      });
+    }
+    uint64_t umax = 0;  // largest unselected
+    if (tid == 0) fs.counter = 0u;
+    __syncthreads();
+    for (int i = tid; i < n_u; i += NT) {
+      const uint64_t x = fs.cbig[i];
+      if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
+      else if (x > umax) umax = x;
+    }
+    below_max = max(below_max, block_max_u64<NT>(umax, fs.red64));
+  } else {
+    // rare: more than kGather candidates above t0; select over global memory
+    thr = radix_select_top(fs.hist, fs.sel, (uint32_t)kk, 64, [&](auto cb) {
+      for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) { if (x >= t0) cb(x); });
+    });
+    if (tid == 0) fs.counter = 0u;
+    __syncthreads();
+    uint64_t umax = 0;
+    for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+      if (x >= thr && x >= t0) {
+        const uint32_t p = atomicAdd(&fs.counter, 1u);
+        if (p < (uint32_t)kBuf) fs.buf[p] = x;
+      } else if (x > umax) {
+        umax = x;
+      }
+    });
+    below_max = max(below_max, block_max_u64<NT>(umax, fs.red64));
+  }
+  thr = thr > t0 ? thr : t0;
+  // 3. weights; the smallest selected weight is w_b
+  uint32_t wmin_bits = 0xffffffffu;
+  for (int i = tid; i < kk; i += NT) {
+    const uint64_t x = fs.buf[i];
+    const float sx = s_of(x);
+    const float w = exact_expf(sx - M);
+    fs.buf[i] = rank_key(w, cand_idx(x));
+    fs.pay[i] = okey(sx);
+    wmin_bits = min(wmin_bits, __float_as_uint(w));
+  }
+  const float w_b = __uint_as_float(~block_max_u32<NT>(~wmin_bits, fs.redu));
+  // 4. tie extension: elements outside the selection with weight w_b can
+  //    still belong to the first kk of the rank order (lower index)
+  if (tid == 0) fs.n_ext = 0u;
+  __syncthreads();
+  uint64_t* ext = a.ws_list + (int64_t)row * a.list_stride;
+  uint32_t* ext_aux = reinterpret_cast<uint32_t*>(a.ws_w + (int64_t)row * a.V);
+  const int64_t ext_cap = a.V;
+  auto add_ext = [&](float w, uint32_t idx, float sx) {
+    const uint32_t p = atomicAdd(&fs.n_ext, 1u);
+    if (p < ext_cap) { ext[p] = rank_key(w, idx); ext_aux[p] = okey(sx); }
+  };
+  if (w_b > 0.f) {
+    // (a) unselected candidates: weights are monotone in the key, so only if
+    //     the largest of them ties
+    if (below_max != 0 && exact_expf(s_of(below_max) - M) == w_b) {
+      if (in_lds) {
+        for (int i = tid; i < n_u; i += NT) {
+          const uint64_t x = fs.cbig[i];
+          if (x >= thr) continue;
+          const float sx = s_of(x);
+          const float w = exact_expf(sx - M);
+          if (w == w_b) add_ext(w, cand_idx(x), sx);
+        }
+      }
+      if (!in_lds || t0 != 0) {
+        for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+          if (x >= thr || (in_lds && x >= t0)) return;  // selected, or seen in LDS
+          const float sx = s_of(x);
+          const float w = exact_expf(sx - M);
+          if (w == w_b) add_ext(w, cand_idx(x), sx);
+        });
+      }
+    }
+    // (b) elements a truncated chunk did not keep (rare: recompute the
+    //     chunk); chunks are checked NT at a time
+    for (int cb = 0; cb < nch; cb += NT) {
+      if (tid == 0) fs.counter = 0u;
+      __syncthreads();
+      {
+        const int c = cb + tid;
+        if (c < nch) {
+          const ChunkStat cs = stats[c];
+          if (cs.trunc && exact_expf(key_to_s(cs.unkept_key, cfg.t_eff) - M) == w_b)
+            fs.aux[atomicAdd(&fs.counter, 1u)] = (uint32_t)c;
+        }
+      }
+      __syncthreads();
+      const uint32_t n_flag = fs.counter;
+      for (uint32_t f = 0; f < n_flag; ++f) {
+        const int c = (int)fs.aux[f];
+        const ChunkStat cs = stats[c];
+        const int c0 = c * a.chunk, c1 = min(c0 + a.chunk, a.V);
+        const int64_t rbase = (int64_t)row * a.row_stride;
+        uint32_t h0 = 0, h1 = 0;
+        if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; }
+        for (int e = c0 + tid; e < c1; e += NT) {
+          float l = load_raw(a.logits, a.dtype, rbase + e);
+          if (!allowed(a, row, (uint32_t)e)) l = -__builtin_inff();
+          uint32_t cnt = 0;
+          for (uint32_t h = h0; h < h1; ++h) if (a.hids[h] == (uint32_t)e) cnt += a.hcnt[h];
+          l = apply_penalties(l, cnt, cfg);
+          const uint32_t kl = lkey(l);
+          if (cand_key(kl, (uint32_t)e) >= cs.min_kept) continue;  // already a candidate
+          const float sx = key_to_s(kl, cfg.t_eff);
+          const float w = exact_expf(sx - M);
+          if (w == w_b) add_ext(w, (uint32_t)e, sx);
+        }
+      }
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  const uint32_t n_ext = min(fs.n_ext, (uint32_t)(ext_cap - kk));
+  if (n_ext > 0) {
+    // union of selection and extension, then its first kk by rank key
+    const int n_all = kk + (int)n_ext;
+    for (int i = tid; i < kk; i += NT) { ext[n_ext + i] = fs.buf[i]; ext_aux[n_ext + i] = fs.pay[i]; }
+    __syncthreads();
+    const uint64_t t2 = radix_select_top(fs.hist, fs.sel, (uint32_t)kk, 64, [&](auto cb) {
+      for (int j = tid; j < n_all; j += NT) cb(ext[j]);
+    });
+    if (tid == 0) fs.counter = 0u;
+    __syncthreads();
+    for (int j = tid; j < n_all; j += NT) {
+      const uint64_t x = ext[j];
+      if (x >= t2) {
+        const uint32_t p = atomicAdd(&fs.counter, 1u);
+        if (p < (uint32_t)kBuf) { fs.buf[p] = x; fs.pay[p] = ext_aux[j]; }
+      }
+    }
+    __syncthreads();
+  }
+  sort_ranked(fs, kk);
+  return kk;
+}
+
+// Reference steps 7-10 (gpu.rs:831-899) over the first k entries of the rank
+// order in fs.buf (top-k rows).  Returns the token, or 0xffffffff for "fall
+// back to argmax_host".
+__device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int k, float u) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < k; i += NT) {
+    const float w = rank_w(fs.buf[i]);
+    fs.fa[i] = (w < cfg.min_p) ? 0.f : w;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float total = -0.0f;  // gpu.rs:834-836: kept mass in rank order
+    for (int i = 0; i < k; ++i) total += fs.fa[i];
+    fs.fval0 = total;
+  }
+  __syncthreads();
+  const float total = fs.fval0;
+  if (total <= 0.f || !finitef_(total)) return 0xffffffffu;
+  for (int i = tid; i < k; i += NT) fs.fb[i] = fs.fa[i] / total;
+  __syncthreads();
+  if (tid == 0) {
+    float cum_p = 0.f;
+    int m_end = 0;  // candidates: positive weights in [0, m_end)
+    bool any = false;
+    for (int i = 0; i < k; ++i) {
+      if (fs.fa[i] <= 0.f) continue;
+      any = true;
+      m_end = i + 1;
+      cum_p += fs.fb[i];
+      if (cfg.cutoff < 1.f && cum_p >= cfg.cutoff) break;
+    }
+    uint32_t tok = 0xffffffffu;
+    if (any) {
+      float ct = -0.0f;
+      for (int i = 0; i < m_end; ++i) if (fs.fa[i] > 0.f) ct += fs.fa[i];
+      if (ct > 0.f && finitef_(ct)) {
+        const float target = clamp_uniform(u) * ct;
+        float cum = 0.f;
+        int last = -1, pick = -1;
+        for (int i = 0; i < m_end; ++i) {
+          if (fs.fa[i] <= 0.f) continue;
+          last = i;
+          cum += fs.fa[i];
+          if (target < cum) { pick = i; break; }
+        }
+        if (pick < 0) pick = last;
+        tok = cand_idx(fs.buf[pick]);
+      }
+    }
+    fs.token = tok;
+  }
+  __syncthreads();
+  return fs.token;
+}
+
+// Serial f32 fold of a global float array in index order (Rust's Sum: a fold
+// from -0.0), by thread 0, staged through LDS tiles.  Valid in all threads.
+__device__ __forceinline__ float fold_global(FinLds& fs, const float* x, int n) {
+  float* tile = reinterpret_cast<float*>(fs.cbig);
+  float acc = -0.0f;  // meaningful in thread 0 only
+  for (int t0 = 0; t0 < n; t0 += kTileFloats) {
+    const int m = min(kTileFloats, n - t0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < m; i += NT) tile[i] = x[t0 + i];
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int i = 0; i < m; ++i) acc += tile[i];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) fs.fval0 = acc;
+  __syncthreads();
+  const float r = fs.fval0;
+  __syncthreads();
+  return r;
+}
+
+// Bitonic sort of a global array (descending) by one workgroup.
+__device__ __forceinline__ void global_sort_desc(uint64_t* g, int n2) {
   for (int k = 2; k <= n2; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < n2; i += kFinThreads) {
+      for (int i = threadIdx.x; i < n2; i += NT) {
         const int ixj = i ^ j;
         if (ixj > i) {
           const uint64_t x = g[i], y = g[ixj];
@@ -598,399 +805,135 @@ __device__ void global_sort_desc(uint64_t* g, int n2) {
   }
 }
 
-__device__ __forceinline__ int next_pow2(int x) {
-  int p = 1;
-  while (p < x) p <<= 1;
-  return p;
-}
-
-// Merge the chunk candidates of `row` into the exact first `kk` entries of
-// the reference rank order (weight desc, index asc).  On return (all
-// threads): sh.buf[0..kk) holds rank keys in order, sh.pay[0..kk) the
-// matching scaled-logit keys, and the function returns kk (0 if the row max
-// is not finite).  M is the row max of s.
-__device__ int rank_candidates(FinShared& sh, const SampleArgs& a, int row, const RowCfg& cfg,
-                               int kk_req, float M) {
-  const int tid = threadIdx.x;
-  const int nch = a.n_chunks;
-  const ChunkStat* stats = a.stats + (int64_t)row * nch;
-  const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
-  if (!finitef_(M) || kk_req <= 0) return 0;
-  int n_total = 0;
-  for (int c = 0; c < nch; ++c) n_total += (int)stats[c].n_cand;
-  const int kk = min(kk_req, n_total);
-  // 1. select top-kk candidates by (key desc, index asc)
-  const int span = nch * kFast;
-  auto get_cand = [&](int j, bool& valid) -> uint64_t {
-    const int c = j / kFast, s = j - c * kFast;
-    valid = (uint32_t)s < stats[c].n_cand;
-    return valid ? cand[j] : 0ull;
-  };
-  uint64_t thr = 0;
-  if (kk < n_total) thr = block_select64(sh, span, (uint32_t)kk, get_cand);
-  if (tid == 0) sh.counter = 0u;
-  __syncthreads();
-  for (int j = tid; j < span; j += kFinThreads) {
-    bool valid;
-    const uint64_t x = get_cand(j, valid);
-    if (valid && x >= thr) {
-      const uint32_t p = atomicAdd(&sh.counter, 1u);
-      if (p < (uint32_t)kFast) sh.buf[p] = x;
-    }
-  }
-  __syncthreads();
-  // 2. weights; the smallest selected weight (the kk-th) is w_b
-  uint32_t wmin_bits = 0xffffffffu;
-  for (int i = tid; i < kk; i += kFinThreads) {
-    const uint64_t x = sh.buf[i];
-    const float s = okey_inv(cand_skey(x));
-    const float w = exact_expf(s - M);
-    const uint32_t idx = cand_idx(x);
-    sh.buf[i] = rank_key(w, idx);
-    sh.pay[i] = cand_skey(x);
-    wmin_bits = min(wmin_bits, __float_as_uint(w));
-  }
-  // block min via max of complement
-  const uint32_t wb_bits = ~block_max_u32<kFinThreads>(~wmin_bits, sh.redu);
-  const float w_b = __uint_as_float(wb_bits);
-  // 3. tie extension: elements outside the selection with the same weight
-  if (tid == 0) sh.n_ext = 0u;
-  __syncthreads();
-  uint64_t* ext = a.ws_list + (int64_t)row * a.list_stride;
-  uint32_t* ext_aux = (uint32_t*)(a.ws_w + (int64_t)row * a.V);
-  const int64_t ext_cap = a.V;
-  if (w_b > 0.f) {
-    // (a) candidates not selected
-    if (kk < n_total) {
-      for (int j = tid; j < span; j += kFinThreads) {
-        bool valid;
-        const uint64_t x = get_cand(j, valid);
-        if (!valid || x >= thr) continue;
-        const float w = exact_expf(okey_inv(cand_skey(x)) - M);
-        if (w == w_b) {
-          const uint32_t p = atomicAdd(&sh.n_ext, 1u);
-          if (p < ext_cap) { ext[p] = rank_key(w, cand_idx(x)); ext_aux[p] = cand_skey(x); }
-        }
-      }
-    }
-    // (b) elements a chunk did not keep
-    for (int c = 0; c < nch; ++c) {
-      const ChunkStat cs = stats[c];
-      if (!cs.trunc) continue;
-      if (exact_expf(okey_inv(cs.unkept_key) - M) != w_b) continue;
-      // Recompute the chunk's scaled logits (rare path).
-      const int c0 = c * kChunk, c1 = min(c0 + kChunk, a.V);
-      uint32_t* cnt = (uint32_t*)sh.hist;  // 4096 u32 reused as two halves below
-      // counts for the chunk, two 4096-element halves
-      for (int half = 0; half < 2; ++half) {
-        const int b0 = c0 + half * 4096, b1 = min(b0 + 4096, c1);
-        if (b0 >= b1) break;
-        __syncthreads();
-        for (int i = tid; i < 4096; i += kFinThreads) cnt[i] = 0u;
-        __syncthreads();
-        if (a.hoff) {
-          const uint32_t h0 = a.hoff[row], h1 = a.hoff[row + 1];
-          for (uint32_t h = h0 + tid; h < h1; h += kFinThreads) {
-            const uint32_t id = a.hids[h];
-            if (id >= (uint32_t)b0 && id < (uint32_t)b1) atomicAdd(&cnt[id - b0], a.hcnt[h]);
-          }
-        }
-        __syncthreads();
-        const int64_t rbase = (int64_t)row * a.row_stride;
-        for (int e = b0 + tid; e < b1; e += kFinThreads) {
-          float l = load_raw(a.logits, a.dtype, rbase + e);
-          if (a.mask && !((a.mask[(int64_t)row * a.mask_words + (e >> 5)] >> (e & 31)) & 1u))
-            l = -__builtin_inff();
-          l = apply_penalties(l, cnt[e - b0], cfg);
-          const float s = finitef_(l) ? l / cfg.t_eff : -__builtin_inff();
-          const uint64_t ck = cand_key(okey(s), (uint32_t)e);
-          if (ck >= cs.min_kept) continue;  // kept by the chunk: already a candidate
-          const float w = exact_expf(s - M);
-          if (w == w_b) {
-            const uint32_t p = atomicAdd(&sh.n_ext, 1u);
-            if (p < ext_cap) { ext[p] = rank_key(w, (uint32_t)e); ext_aux[p] = okey(s); }
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-  __syncthreads();
-  const uint32_t n_ext = min(sh.n_ext, (uint32_t)(ext_cap - kk));
-  if (n_ext > 0) {
-    // Union of selection and extension, then the top-kk by rank key.
-    const int n_all = kk + (int)n_ext;
-    // move the selection behind the extension in the global list
-    for (int i = tid; i < kk; i += kFinThreads) { ext[n_ext + i] = sh.buf[i]; ext_aux[n_ext + i] = sh.pay[i]; }
-    __syncthreads();
-    auto get_ext = [&](int j, bool& valid) -> uint64_t { valid = true; return ext[j]; };
-    const uint64_t t2 = block_select64(sh, n_all, (uint32_t)kk, get_ext);
-    if (tid == 0) sh.counter = 0u;
-    __syncthreads();
-    for (int j = tid; j < n_all; j += kFinThreads) {
-      const uint64_t x = ext[j];
-      if (x >= t2) {
-        const uint32_t p = atomicAdd(&sh.counter, 1u);
-        if (p < (uint32_t)kFast) {
-          sh.buf[p] = x;
-          sh.pay[p] = ext_aux[j];
-        }
-      }
-    }
-    __syncthreads();
-  }
-  // 4. sort the kk rank keys (pad with 0, which sorts last)
-  const int n2 = next_pow2(kk);
-  for (int i = kk + tid; i < n2; i += kFinThreads) sh.buf[i] = 0ull;
-  __syncthreads();
-  lds_sort_desc(sh, n2);
-  return kk;
-}
-
-__device__ __forceinline__ float clamp_uniform(float u) {
-  // gpu.rs:882-886
-  return finitef_(u) ? (u < 0.f ? 0.f : (u > 0.99999994f ? 0.99999994f : u)) : 0.f;
-}
-
-// Reference steps 7-10 (gpu.rs:831-899) over the first `k` entries of the rank
-// order held in sh.buf (top-k rows).  Returns the token or 0xffffffff for
-// "fall back to argmax_host".
-__device__ uint32_t draw_topk(FinShared& sh, const RowCfg& cfg, int k, float u) {
-  const int tid = threadIdx.x;
-  for (int i = tid; i < k; i += kFinThreads) {
-    const float w = __uint_as_float((uint32_t)(sh.buf[i] >> 32));
-    sh.fa[i] = (w < cfg.min_p) ? 0.f : w;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float total = -0.0f;
-    for (int i = 0; i < k; ++i) total += sh.fa[i];
-    sh.fval0 = total;
-  }
-  __syncthreads();
-  const float total = sh.fval0;
-  if (total <= 0.f || !finitef_(total)) return 0xffffffffu;
-  for (int i = tid; i < k; i += kFinThreads) sh.fb[i] = sh.fa[i] / total;
-  __syncthreads();
-  if (tid == 0) {
-    float cum_p = 0.f;
-    int m_end = 0;  // candidates are entries [0, m_end) with positive weight
-    bool any = false;
-    for (int i = 0; i < k; ++i) {
-      if (sh.fa[i] <= 0.f) continue;
-      any = true;
-      m_end = i + 1;
-      cum_p += sh.fb[i];
-      if (cfg.cutoff < 1.f && cum_p >= cfg.cutoff) break;
-    }
-    uint32_t tok = 0xffffffffu;
-    if (any) {
-      float ct = -0.0f;
-      for (int i = 0; i < m_end; ++i) if (sh.fa[i] > 0.f) ct += sh.fa[i];
-      if (ct > 0.f && finitef_(ct)) {
-        const float target = clamp_uniform(u) * ct;
-        float cum = 0.f;
-        int last = -1, pick = -1;
-        for (int i = 0; i < m_end; ++i) {
-          if (sh.fa[i] <= 0.f) continue;
-          last = i;
-          cum += sh.fa[i];
-          if (target < cum) { pick = i; break; }
-        }
-        if (pick < 0) pick = last;
-        tok = 0xffffffffu - (uint32_t)sh.buf[pick];
-      }
-    }
-    sh.token = tok;
-  }
-  __syncthreads();
-  return sh.token;
-}
-
-// Serial f32 fold of a global float array in index order (Rust's Sum: a
-// fold from -0.0), by thread 0, staged through LDS tiles.  Result valid in
-// all threads.
-__device__ float fold_global(FinShared& sh, const float* x, int n) {
-  float* tile = (float*)sh.buf;
-  const int T = kFinBuf * 2;  // floats per tile
-  float acc = -0.0f;          // meaningful in thread 0 only
-  for (int t0 = 0; t0 < n; t0 += T) {
-    const int m = min(T, n - t0);
-    __syncthreads();
-    for (int i = threadIdx.x; i < m; i += kFinThreads) tile[i] = x[t0 + i];
-    __syncthreads();
-    if (threadIdx.x == 0)
-      for (int i = 0; i < m; ++i) acc += tile[i];
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) sh.fval0 = acc;
-  __syncthreads();
-  const float r = sh.fval0;
-  __syncthreads();
-  return r;
-}
-
-// Rows without top-k (or with top_k > 1024): the whole distribution is
-// re-read from the workspace (ws_s holds the scaled logits).
-__device__ uint32_t draw_wide(FinShared& sh, const SampleArgs& a, int row, const RowCfg& cfg,
+// Rows without top-k (or with top_k > 1024): the distribution is re-read from
+// the workspace (ws_s holds the scaled logits).  Returns the token or
+// 0xffffffff for the argmax fallback.
+__device__ __forceinline__ uint32_t draw_wide(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg,
                               float M, float u) {
   const int tid = threadIdx.x;
   const int V = a.V;
   const float* srow = a.ws_s + (int64_t)row * V;
   float* wrow = a.ws_w + (int64_t)row * V;
   uint64_t* list = a.ws_list + (int64_t)row * a.list_stride;
-  // weights (min-p applied), histogram of positive weights over 2048 bins
-  for (int b = tid; b < 2048; b += kFinThreads) { sh.hist[b] = 0u; sh.mass[b] = 0ull; }
+  for (int b = tid; b < kBins; b += NT) { fs.hist[b] = 0u; fs.mass[b] = 0ull; }
   __syncthreads();
-  for (int i = tid; i < V; i += kFinThreads) {
+  for (int i = tid; i < V; i += NT) {
     float w = exact_expf(srow[i] - M);
     if (w < cfg.min_p) w = 0.f;
     wrow[i] = w;
     if (w > 0.f) {
-      const uint32_t b = __float_as_uint(w) >> 19;
-      atomicAdd(&sh.hist[b], 1u);
-      atomicAdd((unsigned long long*)&sh.mass[b], (unsigned long long)((double)w * 1099511627776.0));
+      const uint32_t b = __float_as_uint(w) >> 20;
+      atomicAdd(&fs.hist[b], 1u);
+      atomicAdd((unsigned long long*)&fs.mass[b], (unsigned long long)((double)w * 1099511627776.0));
     }
   }
   __syncthreads();
   const bool wide_k = cfg.cls == kTopK;
   float total = 0.f;
   if (!wide_k) {
-    total = fold_global(sh, wrow, V);  // gpu.rs:837: vocab-order sum
+    total = fold_global(fs, wrow, V);  // gpu.rs:837: vocab-order sum
     if (total <= 0.f || !finitef_(total)) return 0xffffffffu;
   }
-  // boundary bin of the superset
   if (tid == 0) {
     uint64_t all_mass = 0;
-    uint32_t all_cnt = 0;
-    for (int b = 0; b < 2048; ++b) { all_mass += sh.mass[b]; all_cnt += sh.hist[b]; }
+    for (int b = 0; b < kBins; ++b) all_mass += fs.mass[b];
     int bstar = 0;
     if (wide_k) {
       uint32_t c = 0;
-      for (int b = 2047; b >= 0; --b) { c += sh.hist[b]; if (c >= (uint32_t)cfg.k_eff) { bstar = b; break; } }
+      for (int b = kBins - 1; b >= 0; --b) { c += fs.hist[b]; if (c >= (uint32_t)cfg.k_eff) { bstar = b; break; } }
     } else if (cfg.cutoff < 1.f) {
+      // superset holding the nucleus with margin (verified below)
       const double need = fmin(1.0, (double)cfg.cutoff + 0.02) * (double)all_mass;
       uint64_t c = 0;
-      for (int b = 2047; b >= 0; --b) { c += sh.mass[b]; if ((double)c >= need) { bstar = b; break; } }
+      for (int b = kBins - 1; b >= 0; --b) { c += fs.mass[b]; if ((double)c >= need) { bstar = b; break; } }
     }
-    sh.flag = (uint32_t)bstar;
-    (void)all_cnt;
+    fs.flag = (uint32_t)bstar;
   }
   __syncthreads();
-  int bstar = (int)sh.flag;
+  int bstar = (int)fs.flag;
   uint32_t tok = 0xffffffffu;
   for (int attempt = 0; attempt < 2; ++attempt) {
-    // offsets of bins >= bstar in descending bin order
     __syncthreads();
     if (tid == 0) {
       uint32_t off = 0;
-      for (int b = 2047; b >= 0; --b) {
-        sh.aux[b] = off;
-        if (b >= bstar) off += sh.hist[b];
+      for (int b = kBins - 1; b >= 0; --b) {
+        fs.aux[b] = off;
+        if (b >= bstar) off += fs.hist[b];
       }
-      sh.counter = off;
+      fs.counter = off;
     }
     __syncthreads();
-    const int n_sup = (int)sh.counter;
-    for (int i = tid; i < V; i += kFinThreads) {
+    const int n_sup = (int)fs.counter;
+    for (int i = tid; i < V; i += NT) {
       const float w = wrow[i];
       if (w > 0.f) {
-        const int b = (int)(__float_as_uint(w) >> 19);
-        if (b >= bstar) list[atomicAdd(&sh.aux[b], 1u)] = rank_key(w, (uint32_t)i);
+        const int b = (int)(__float_as_uint(w) >> 20);
+        if (b >= bstar) list[atomicAdd(&fs.aux[b], 1u)] = rank_key(w, (uint32_t)i);
       }
     }
     __syncthreads();
     const int n2 = next_pow2(max(n_sup, 1));
-    for (int i = n_sup + tid; i < n2; i += kFinThreads) list[i] = 0ull;
+    for (int i = n_sup + tid; i < n2; i += NT) list[i] = 0ull;
     __syncthreads();
     global_sort_desc(list, n2);
-    // serial walk over the sorted superset (thread 0), tiles through LDS
-    if (wide_k) {
-      const int k = min(cfg.k_eff, n_sup);  // zero-weight entries add nothing
-      if (tid == 0) {
+    if (tid == 0) {
+      int k = n_sup;
+      if (wide_k) {
+        k = min(cfg.k_eff, n_sup);  // zero-weight entries add nothing
         float t = -0.0f;
-        for (int i = 0; i < k; ++i) t += __uint_as_float((uint32_t)(list[i] >> 32));
-        sh.fval0 = t;
+        for (int i = 0; i < k; ++i) t += rank_w(list[i]);
+        total = t;
       }
-      __syncthreads();
-      total = sh.fval0;
-      if (total <= 0.f || !finitef_(total)) return 0xffffffffu;
-      if (tid == 0) {
+      uint32_t r = 0xffffffffu;
+      uint32_t flag = 1u;
+      if (total > 0.f && finitef_(total)) {
         float cum_p = 0.f;
         int m_end = 0;
+        bool reached = false;
         for (int i = 0; i < k; ++i) {
-          const float w = __uint_as_float((uint32_t)(list[i] >> 32));
           m_end = i + 1;
-          cum_p += w / total;
-          if (cfg.cutoff < 1.f && cum_p >= cfg.cutoff) break;
+          cum_p += rank_w(list[i]) / total;
+          if (cfg.cutoff < 1.f && cum_p >= cfg.cutoff) { reached = true; break; }
         }
-        float ct = -0.0f;
-        for (int i = 0; i < m_end; ++i) ct += __uint_as_float((uint32_t)(list[i] >> 32));
-        uint32_t r = 0xffffffffu;
-        if (m_end > 0 && ct > 0.f && finitef_(ct)) {
-          const float target = clamp_uniform(u) * ct;
-          float cum = 0.f;
-          int pick = m_end - 1;
-          for (int i = 0; i < m_end; ++i) {
-            cum += __uint_as_float((uint32_t)(list[i] >> 32));
-            if (target < cum) { pick = i; break; }
+        if (!wide_k && !reached && bstar != 0) {
+          flag = 0xffffffffu;  // superset too small: retry with every positive weight
+        } else {
+          float ct = -0.0f;
+          for (int i = 0; i < m_end; ++i) ct += rank_w(list[i]);
+          if (m_end > 0 && ct > 0.f && finitef_(ct)) {
+            const float target = clamp_uniform(u) * ct;
+            float cum = 0.f;
+            int pick = m_end - 1;
+            for (int i = 0; i < m_end; ++i) {
+              cum += rank_w(list[i]);
+              if (target < cum) { pick = i; break; }
+            }
+            r = cand_idx(list[pick]);
           }
-          r = 0xffffffffu - (uint32_t)list[pick];
         }
-        sh.token = r;
-        sh.flag = 1u;
       }
-      __syncthreads();
-      return sh.token;
-    }
-    if (tid == 0) {
-      float cum_p = 0.f;
-      int m_end = 0;
-      bool reached = false;
-      for (int i = 0; i < n_sup; ++i) {
-        const float w = __uint_as_float((uint32_t)(list[i] >> 32));
-        m_end = i + 1;
-        cum_p += w / total;
-        if (cfg.cutoff < 1.f && cum_p >= cfg.cutoff) { reached = true; break; }
-      }
-      const bool complete = bstar == 0;
-      if (!reached && !complete) {
-        sh.flag = 0xffffffffu;  // superset too small: retry with every positive weight
-      } else {
-        float ct = -0.0f;
-        for (int i = 0; i < m_end; ++i) ct += __uint_as_float((uint32_t)(list[i] >> 32));
-        uint32_t r = 0xffffffffu;
-        if (m_end > 0 && ct > 0.f && finitef_(ct)) {
-          const float target = clamp_uniform(u) * ct;
-          float cum = 0.f;
-          int pick = m_end - 1;
-          for (int i = 0; i < m_end; ++i) {
-            cum += __uint_as_float((uint32_t)(list[i] >> 32));
-            if (target < cum) { pick = i; break; }
-          }
-          r = 0xffffffffu - (uint32_t)list[pick];
-        }
-        sh.token = r;
-        sh.flag = 1u;
-      }
+      fs.token = r;
+      fs.flag = flag;
     }
     __syncthreads();
-    if (sh.flag != 0xffffffffu) { tok = sh.token; break; }
+    if (fs.flag != 0xffffffffu) { tok = fs.token; break; }
     bstar = 0;
   }
   return tok;
 }
 
 // Temperature-only rows: kernels.cu:7803-7867 with the exact weight function.
-__device__ uint32_t draw_temp_only(FinShared& sh, const SampleArgs& a, int row, float M, float u,
+// 256 contiguous chunks, one per thread of the (256-thread) workgroup.
+__device__ __forceinline__ uint32_t draw_temp_only(FinLds& fs, const SampleArgs& a, int row, float M, float u,
                                    uint32_t argmax_fin) {
+  static_assert(NT == 256, "the reference's temperature-only path uses 256 chunks");
   const int tid = threadIdx.x;
   const int V = a.V;
   const float* srow = a.ws_s + (int64_t)row * V;
   const int chunk = (V + 255) / 256;
-  float* csum = sh.fa;       // 256 used
-  float* prefix = sh.fb;     // 256 used
-  if (tid < 256) {
+  float* csum = fs.fa;
+  float* prefix = fs.fb;
+  {
     const int start = tid * chunk, end = min(start + chunk, V);
     float s = 0.f;
     for (int i = start; i < end; ++i) s += exact_expf(srow[i] - M);
@@ -1000,15 +943,15 @@ __device__ uint32_t draw_temp_only(FinShared& sh, const SampleArgs& a, int row, 
   if (tid == 0) {
     float acc = 0.f;
     for (int j = 0; j < 256; ++j) { prefix[j] = acc; acc += csum[j]; }
-    sh.fval0 = acc;
-    sh.token = 0xffffffffu;
+    fs.fval0 = acc;
+    fs.token = 0xffffffffu;
   }
   __syncthreads();
-  const float total = sh.fval0;
+  const float total = fs.fval0;
   if (total <= 0.f || !finitef_(total)) return argmax_fin;
   const float uu = finitef_(u) ? fminf(fmaxf(u, 0.f), 0.99999994f) : 0.f;
   const float target = uu * total;
-  if (tid < 256) {
+  {
     const int start = tid * chunk, end = min(start + chunk, V);
     const float lo = prefix[tid];
     const float hi = lo + csum[tid];
@@ -1022,118 +965,590 @@ __device__ uint32_t draw_temp_only(FinShared& sh, const SampleArgs& a, int row, 
         cum += w;
         if (target < cum) break;
       }
-      if (chosen >= 0) atomicMin(&sh.token, (uint32_t)chosen);
+      if (chosen >= 0) atomicMin(&fs.token, (uint32_t)chosen);
     }
   }
   __syncthreads();
-  return sh.token != 0xffffffffu ? sh.token : argmax_fin;
+  return fs.token != 0xffffffffu ? fs.token : argmax_fin;
 }
 
-__global__ void __launch_bounds__(kFinThreads) finish_rows_kernel(SampleArgs a) {
-  __shared__ FinShared sh;
-  const int row = blockIdx.x;
+// argmax_host (gpu.rs:739-751, total_cmp, lowest index) over the processed
+// logits of the row.  Only needed when no scaled logit is finite (or l / T
+// overflows), so the row is re-read here, 4096 logits at a time, with an LDS
+// count table for the penalties.
+__device__ __forceinline__ uint32_t row_argmax_total(FinLds& fs, const SampleArgs& a, int row,
+                                                     const RowCfg& cfg) {
   const int tid = threadIdx.x;
   const int V = a.V;
-  const RowCfg cfg = load_cfg(a.pv, row, V, a.n_lp, a.need_lse);
+  constexpr int T = 4096;
+  static_assert(kGather * 2 >= T, "count table fits cbig");
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(fs.cbig);
+  uint32_t h0 = 0, h1 = 0;
+  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; }
+  const int64_t rbase = (int64_t)row * a.row_stride;
+  uint64_t best = 0ull;  // (total key biased) << 32 | (0xffffffff - index)
+  for (int t0 = 0; t0 < V; t0 += T) {
+    const int t1 = min(t0 + T, V);
+    __syncthreads();
+    for (int i = tid; i < T; i += NT) cnt[i] = 0u;
+    __syncthreads();
+    for (uint32_t h = h0 + tid; h < h1; h += NT) {
+      const uint32_t id = a.hids[h];
+      if (id >= (uint32_t)t0 && id < (uint32_t)t1) atomicAdd(&cnt[id - t0], a.hcnt[h]);
+    }
+    __syncthreads();
+    for (int e = t0 + tid; e < t1; e += NT) {
+      float l = load_raw(a.logits, a.dtype, rbase + e);
+      if (!allowed(a, row, (uint32_t)e)) l = -__builtin_inff();
+      l = apply_penalties(l, cnt[e - t0], cfg);
+      const uint64_t v = ((uint64_t)((uint32_t)total_key(l) ^ 0x80000000u) << 32) |
+                         (uint64_t)(0xffffffffu - (uint32_t)e);
+      best = v > best ? v : best;
+    }
+  }
+  best = block_max_u64<NT>(best, fs.red64);
+  return 0xffffffffu - (uint32_t)best;
+}
 
-  // Row statistics from the chunk statistics.
+__device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg) {
+  const int tid = threadIdx.x;
+  const int V = a.V;
   ChunkStat st;
   stat_init(st);
-  for (int c = tid; c < a.n_chunks; c += kFinThreads) stat_merge(st, a.stats[(int64_t)row * a.n_chunks + c]);
-  const ChunkStat rs = block_stat<kFinThreads>(st, sh.red);
-  const float M = rs.max_s;
+  for (int c = tid; c < a.n_chunks; c += NT) stat_merge(st, a.stats[(int64_t)row * a.n_chunks + c]);
+  const ChunkStat rs = block_stat<NT>(st, fs.red);
+  // row max of s = l / T: division is monotone, so it is max(l) / T
+  const float M = finitef_(rs.max_l) ? rs.max_l / cfg.t_eff : -__builtin_inff();
   const uint32_t am_ieee = rs.am_ieee_i == 0xffffffffu ? 0u : rs.am_ieee_i;
-  const uint32_t am_tot = rs.am_tot_i == 0xffffffffu ? 0u : rs.am_tot_i;
   const uint32_t am_fin = rs.am_fin_i == 0xffffffffu ? 0u : rs.am_fin_i;
   const float u = row_uniform(a.pv, row);
 
   const bool eos = a.mask && !rs.any_finite;
   uint32_t token;
-  int ranked_k = 0;  // entries of sh.buf that are in rank order
+  int ranked_k = 0;  // entries of fs.buf in rank order
+  double lse_part = 0.0;  // this thread's share of sum(exp(s - M)) over the candidates
+  bool have_part = false;
   if (eos) {
     token = cfg.eos;
   } else if (cfg.cls == kGreedy) {
     token = a.pv.greedy_rule == kGreedyFiniteLane ? am_fin : am_ieee;
+  } else if (!finitef_(M)) {
+    token = cfg.cls == kTempOnly ? am_fin : row_argmax_total(fs, a, row, cfg);
   } else if (cfg.cls == kTopK && !cfg.wide) {
-    if (!finitef_(M)) {
-      token = am_tot;
-    } else {
-      ranked_k = rank_candidates(sh, a, row, cfg, cfg.k_sel, M);
-      token = draw_topk(sh, cfg, cfg.k_eff, u);
-      if (token == 0xffffffffu) token = am_tot;
-    }
+    ranked_k = rank_candidates(fs, a, row, cfg, cfg.k_sel, M, a.need_lse ? &lse_part : nullptr);
+    have_part = a.need_lse != 0;
+    token = draw_topk(fs, cfg, cfg.k_eff, u);
+    if (token == 0xffffffffu) token = row_argmax_total(fs, a, row, cfg);
   } else if (cfg.cls == kTempOnly) {
-    token = finitef_(M) ? draw_temp_only(sh, a, row, M, u, am_fin) : am_fin;
+    token = draw_temp_only(fs, a, row, M, u, am_fin);
   } else {
-    if (!finitef_(M)) {
-      token = am_tot;
-    } else {
-      token = draw_wide(sh, a, row, cfg, M, u);
-      if (token == 0xffffffffu) token = am_tot;
-    }
+    token = draw_wide(fs, a, row, cfg, M, u);
+    if (token == 0xffffffffu) token = row_argmax_total(fs, a, row, cfg);
   }
   if (tid == 0) a.out_tokens[row] = token;
+  if (a.n_lp <= 0 && !a.out_token_lp) return;
 
   // Logprobs of the processed distribution (extension).
-  if (a.n_lp > 0 || a.out_token_lp) {
+  __syncthreads();
+  const int N = a.n_lp;
+  if (eos || !finitef_(M)) {
+    for (int j = tid; j < N; j += NT) {
+      a.out_lp[(int64_t)row * N + j] = -__builtin_inff();
+      a.out_lp_ids[(int64_t)row * N + j] = 0xffffffffu;
+    }
+    if (tid == 0 && a.out_token_lp) a.out_token_lp[row] = eos ? 0.f : -__builtin_inff();
+    return;
+  }
+  if (N > 0 && ranked_k < N) {
+    ranked_k = rank_candidates(fs, a, row, cfg, N, M, have_part ? nullptr : &lse_part);
+    have_part = true;
+  }
+  // log of the normaliser relative to M: the kept candidates of every chunk
+  // in double, the rest from each chunk's sum over the elements it dropped
+  if (!have_part) {
+    for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+      lse_part += exp((double)key_to_s(cand_skey(x), cfg.t_eff) - (double)M);
+    });
+  }
+  double part = lse_part;
+  for (int c = tid; c < a.n_chunks; c += NT) {
+    const ChunkStat cs = a.stats[(int64_t)row * a.n_chunks + c];
+    if (cs.lse_sum > 0.f) part += (double)cs.lse_sum * exp((double)cs.lse_m - (double)M);
+  }
+  const double log_sum = log(block_sum_f64<NT>(part, fs.redd));
+  for (int j = tid; j < N; j += NT) {
+    float lp = -__builtin_inff();
+    uint32_t id = 0xffffffffu;
+    if (j < ranked_k) {
+      id = cand_idx(fs.buf[j]);
+      lp = (float)(((double)okey_inv(fs.pay[j]) - (double)M) - log_sum);
+    }
+    a.out_lp_ids[(int64_t)row * N + j] = id;
+    a.out_lp[(int64_t)row * N + j] = lp;
+  }
+  if (a.out_token_lp) {
+    if (tid == 0) fs.flag = 0u;
     __syncthreads();
-    const int N = a.n_lp;
-    if (eos || !finitef_(M)) {
-      for (int j = tid; j < N; j += kFinThreads) {
-        a.out_lp[(int64_t)row * N + j] = -__builtin_inff();
-        a.out_lp_ids[(int64_t)row * N + j] = 0xffffffffu;
-      }
-      if (tid == 0 && a.out_token_lp) a.out_token_lp[row] = eos ? 0.f : -__builtin_inff();
-      return;
+    for (int j = tid; j < ranked_k; j += NT)
+      if (cand_idx(fs.buf[j]) == token) { fs.flag = 1u; fs.fval1 = okey_inv(fs.pay[j]); }
+    __syncthreads();
+    float s;
+    if (fs.flag) {
+      s = fs.fval1;
+    } else {
+      const float l = processed_single<NT>(a, row, cfg, token < (uint32_t)V ? token : 0u, fs.redu);
+      s = finitef_(l) ? l / cfg.t_eff : -__builtin_inff();
     }
-    if (N > 0 && ranked_k < N) ranked_k = rank_candidates(sh, a, row, cfg, N, M);
-    // log of the normaliser relative to M (lse = M + log_sum): the kept
-    // candidates of every chunk in double, the rest from each chunk's sum.
-    double part = 0.0;
-    {
-      const int nch = a.n_chunks;
-      const ChunkStat* stats = a.stats + (int64_t)row * nch;
-      const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
-      for (int c = 0; c < nch; ++c) {
-        const uint32_t nc = stats[c].n_cand;
-        for (uint32_t j = tid; j < nc; j += kFinThreads)
-          part += exp((double)okey_inv(cand_skey(cand[(int64_t)c * kFast + j])) - (double)M);
-      }
-      for (int c = tid; c < nch; c += kFinThreads) {
-        const ChunkStat cs = stats[c];
-        if (cs.lse_sum > 0.f) part += (double)cs.lse_sum * exp((double)cs.lse_m - (double)M);
-      }
-    }
-    const double log_sum = log(block_sum_f64<kFinThreads>(part, sh.redd));
-    for (int j = tid; j < N; j += kFinThreads) {
-      float lp = -__builtin_inff();
-      uint32_t id = 0xffffffffu;
-      if (j < ranked_k) {
-        id = 0xffffffffu - (uint32_t)sh.buf[j];
-        const float s = okey_inv(sh.pay[j]);
-        lp = (float)(((double)s - (double)M) - log_sum);
-      }
-      a.out_lp_ids[(int64_t)row * N + j] = id;
-      a.out_lp[(int64_t)row * N + j] = lp;
-    }
-    if (a.out_token_lp) {
-      if (tid == 0) sh.flag = 0u;
-      __syncthreads();
-      for (int j = tid; j < ranked_k; j += kFinThreads) {
-        if (0xffffffffu - (uint32_t)sh.buf[j] == token) { sh.flag = 1u; sh.fval1 = okey_inv(sh.pay[j]); }
-      }
-      __syncthreads();
-      float s;
-      if (sh.flag) {
-        s = sh.fval1;
-      } else {
-        const float l = processed_single<kFinThreads>(a, row, cfg, token < (uint32_t)V ? token : 0u, sh.redu);
-        s = finitef_(l) ? l / cfg.t_eff : -__builtin_inff();
-      }
-      if (tid == 0)
-        a.out_token_lp[row] = token < (uint32_t)V ? (float)(((double)s - (double)M) - log_sum) : -__builtin_inff();
+    if (tid == 0)
+      a.out_token_lp[row] = token < (uint32_t)V ? (float)(((double)s - (double)M) - log_sum) : -__builtin_inff();
+  }
+}
+
+// ==========================================================================
+// The scan kernel: one pass over the logits
+// ==========================================================================
+
+// Online sum of exp(s - m) with a running maximum m (for the log-sum-exp of
+// the elements a chunk does not keep).
+struct RestAcc {
+  float m, sum;
+  __device__ __forceinline__ void init() { m = -__builtin_inff(); sum = 0.f; }
+  __device__ __forceinline__ void add(float s) {
+    if (!finitef_(s)) return;
+    if (sum == 0.f) { m = s; sum = 1.f; }
+    else if (s > m) { sum = sum * __expf(m - s) + 1.f; m = s; }
+    else sum += __expf(s - m);
+  }
+};
+
+// Per-chunk running selection state (kept in registers, uniform over the
+// workgroup): tau is a 48-bit local composite below which no element can be
+// among the chunk's top k.
+struct SelState {
+  uint64_t tau;
+  uint32_t unkept;  // largest key known not to be kept
+  RestAcc rest;
+  bool rest_on;
+  float t_eff;
+};
+
+__device__ __forceinline__ void reject_key(SelState& ss, uint32_t key) {
+  ss.unkept = max(ss.unkept, key);
+  if (ss.rest_on) ss.rest.add(key_to_s(key, ss.t_eff));
+}
+__device__ __forceinline__ void reject(SelState& ss, uint64_t comp) {
+  reject_key(ss, (uint32_t)(comp >> 16));
+}
+
+// Keep the k largest composites of the LDS buffer; raises tau and rejects
+// the others.  All threads call it.
+__device__ __forceinline__ void compact_buffer(ScanLds& sh, SelState& ss, uint32_t k) {
+  const int tid = threadIdx.x;
+  const uint32_t n = sh.count;
+  if (n <= k) return;
+  const uint64_t thr = radix_select_top(sh.hist, sh.sel, k, 48, [&](auto cb) {
+    for (uint32_t i = tid; i < n; i += NT) cb(sh.cbuf[i]);
+  });
+  constexpr int PER = kBufCap / NT;
+  uint64_t v[PER];
+  uint32_t keep = 0;
+  #pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const uint32_t i = r * NT + tid;
+    v[r] = i < n ? sh.cbuf[i] : 0ull;
+    if (i < n) {
+      if (v[r] >= thr) ++keep;
+      else reject(ss, v[r]);
     }
   }
+  uint32_t total;
+  uint32_t pos = block_excl_scan_u32<NT>(keep, sh.redu, &total);  // has barriers
+  #pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const uint32_t i = r * NT + tid;
+    if (i < n && v[r] >= thr) sh.cbuf[pos++] = v[r];
+  }
+  if (thr > ss.tau) ss.tau = thr;
+  __syncthreads();
+  if (tid == 0) sh.count = total;
+  __syncthreads();
+}
+
+// Append NI items per thread to the running selection.  Item i has scaled-
+// logit key key[i] (0 = no item) and local index li_of(i).  Items below tau
+// are rejected, the rest go to the LDS buffer.  The caller guarantees that
+// NI * NT <= kBufCap - k, so after one compaction (which leaves at most k
+// entries) every batch fits.
+template <int NI, typename LiOf>
+__device__ __forceinline__ void append_batch(ScanLds& sh, SelState& ss, uint32_t k,
+                                             const uint32_t (&key)[NI], LiOf li_of) {
+  static_assert(NI * NT + kFast <= kBufCap, "a batch must fit after compaction");
+  uint32_t mine = 0;
+  #pragma unroll
+  for (int i = 0; i < NI; ++i) mine += key[i] != 0u && local_comp(key[i], li_of(i)) >= ss.tau;
+  uint32_t total;
+  uint32_t off = block_excl_scan_u32<NT>(mine, sh.redu, &total);
+  if (sh.count + total > (uint32_t)kBufCap) {
+    compact_buffer(sh, ss, k);
+    mine = 0;
+    #pragma unroll
+    for (int i = 0; i < NI; ++i) mine += key[i] != 0u && local_comp(key[i], li_of(i)) >= ss.tau;
+    off = block_excl_scan_u32<NT>(mine, sh.redu, &total);
+  }
+  const uint32_t base = sh.count;
+  #pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    if (key[i] == 0u) continue;
+    const uint64_t c = local_comp(key[i], li_of(i));
+    if (c >= ss.tau) sh.cbuf[base + off++] = c;
+    else reject(ss, c);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) sh.count = base + total;
+  __syncthreads();
+}
+
+template <int VEC>
+__device__ __forceinline__ void load_tile(const SampleArgs& a, int64_t rbase, int tb, int c1,
+                                          float (&raw)[VEC * 4]) {
+  const int tid = threadIdx.x;
+  if (a.dtype == HI_ROCM_DTYPE_BF16) {
+    #pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e0 = tb + (j * NT + tid) * 4;
+      if (a.vec_ok && e0 + 3 < c1) {
+        const uint2 v = *(const uint2*)((const uint16_t*)a.logits + rbase + e0);
+        raw[4 * j + 0] = __uint_as_float(v.x << 16); raw[4 * j + 1] = __uint_as_float(v.x & 0xffff0000u);
+        raw[4 * j + 2] = __uint_as_float(v.y << 16); raw[4 * j + 3] = __uint_as_float(v.y & 0xffff0000u);
+      } else {
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) raw[4 * j + q] = (e0 + q < c1) ? load_raw(a.logits, a.dtype, rbase + e0 + q) : 0.f;
+      }
+    }
+  } else {
+    #pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e0 = tb + (j * NT + tid) * 4;
+      if (a.vec_ok && e0 + 3 < c1) {
+        const float4 v = *(const float4*)((const float*)a.logits + rbase + e0);
+        raw[4 * j + 0] = v.x; raw[4 * j + 1] = v.y; raw[4 * j + 2] = v.z; raw[4 * j + 3] = v.w;
+      } else {
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) raw[4 * j + q] = (e0 + q < c1) ? load_raw(a.logits, a.dtype, rbase + e0 + q) : 0.f;
+      }
+    }
+  }
+}
+
+// Which statistics a row needs from the scan (uniform per row).
+struct StatNeeds {
+  bool ieee;  // greedy rows: block_argmax_last
+  bool fin;   // temperature-only rows and the finite-lane greedy rule
+};
+
+__device__ __forceinline__ StatNeeds stat_needs(const RowCfg& c, const ParamsView& pv) {
+  StatNeeds n;
+  n.ieee = c.cls == kGreedy && pv.greedy_rule == kGreedyIeee;
+  n.fin = c.cls == kTempOnly || (c.cls == kGreedy && pv.greedy_rule == kGreedyFiniteLane);
+  return n;
+}
+
+// Statistics update for one processed logit l at index e.  The maximum is
+// tracked on the order key of l (non-finite l maps to the key of -inf),
+// which also tells whether any finite value exists.
+__device__ __forceinline__ void stat_add(ChunkStat& st, const StatNeeds& nd, uint32_t& maxkey,
+                                         float l, uint32_t kl, uint32_t e) {
+  maxkey = max(maxkey, kl);
+  if (nd.ieee && l > st.am_ieee_v) { st.am_ieee_v = l; st.am_ieee_i = e; }
+  if (nd.fin && finitef_(l) &&
+      (st.am_fin_i == 0xffffffffu || l > st.am_fin_v ||
+       (l == st.am_fin_v && (e & 255u) < (st.am_fin_i & 255u)))) {
+    st.am_fin_v = l; st.am_fin_i = e;
+  }
+}
+
+
+// History count of token `id` from the chunk's LDS hash (linear probing);
+// `found` is false when the hash overflowed before the token was inserted.
+__device__ __forceinline__ uint32_t hash_count(const uint32_t* hkey, const uint32_t* hcnt,
+                                               uint32_t id, bool& found) {
+  uint32_t slot = (id * 2654435761u) & (kHashCap - 1);
+  for (int p = 0; p < kHashCap; ++p) {
+    const uint32_t kk = hkey[slot];
+    if (kk == id) { found = true; return hcnt[slot]; }
+    if (kk == 0xffffffffu) break;
+    slot = (slot + 1) & (kHashCap - 1);
+  }
+  found = false;
+  return 0u;
+}
+
+// Block reduction of (min u64, max u32, f32 sum): the chunk's smallest kept
+// candidate, largest dropped key and dropped log-sum-exp mass.
+__device__ __forceinline__ void block_tail3(uint64_t& mn, uint32_t& mx, float& sum, ScanLds& sh) {
+  uint64_t a = ~mn;
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t t = shfl_xor_u64(a, o);
+    a = t > a ? t : a;
+    mx = max(mx, (uint32_t)__shfl_xor(mx, o, 64));
+    sum += __shfl_xor(sum, o, 64);
+  }
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) { sh.red64[wid] = a; sh.redu[wid] = mx; sh.redf[wid] = sum; }
+  __syncthreads();
+  a = sh.red64[0]; mx = sh.redu[0]; sum = sh.redf[0];
+  for (int i = 1; i < NT / 64; ++i) {
+    a = sh.red64[i] > a ? sh.red64[i] : a;
+    mx = max(mx, sh.redu[i]);
+    sum += sh.redf[i];
+  }
+  mn = ~a;
+}
+
+// Each workgroup streams one chunk of TILES tiles of NT*VEC*4 logits; the
+// next tile's 128-bit loads are in flight while the current one is
+// processed.  Tokens present in the row's history are marked in an LDS
+// bitmap; the lanes holding one look their count up in an LDS hash.
+template <int VEC, int TILES>
+__global__ void __launch_bounds__(NT) scan_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  ScanLds& sh = *reinterpret_cast<ScanLds*>(lds_raw);
+  constexpr int TILE = NT * VEC * 4;
+  constexpr int CH = TILE * TILES;
+  constexpr int E = VEC * 4;
+  static_assert(CH <= 65536, "local indices are 16-bit");
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds_raw + sizeof(ScanLds));
+  uint32_t* hkey = bitmap + CH / 32;
+  uint32_t* hcnt = hkey + kHashCap;
+
+  const int row = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int V = a.V;
+  const int c0 = chunk * CH;
+  const int c1 = min(c0 + CH, V);
+  const int len = c1 - c0;
+  const RowCfg cfg = load_cfg(a.pv, row, V, a.n_lp, a.need_lse);
+  const int64_t rbase = (int64_t)row * a.row_stride;
+  const uint32_t* mrow = a.mask ? a.mask + (int64_t)row * a.mask_words : nullptr;
+  float* srow = cfg.store_s ? a.ws_s + (int64_t)row * V : nullptr;
+  const uint32_t k = (uint32_t)cfg.k_sel;
+
+  float cur[E];
+  load_tile<VEC>(a, rbase, c0, c1, cur);
+
+  // history tokens of this chunk: bitmap + (id -> count) hash
+  bool pen = false;
+  uint32_t h0 = 0, h1 = 0;
+  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; pen = h1 > h0; }
+  if (tid == 0) { sh.count = 0u; sh.hovf = 0u; }
+  if (pen) {
+    for (int i = tid; i < CH / 32; i += NT) bitmap[i] = 0u;
+    for (int i = tid; i < kHashCap; i += NT) { hkey[i] = 0xffffffffu; hcnt[i] = 0u; }
+    __syncthreads();
+    for (uint32_t hb = h0; hb < h1; hb += NT * 8) {
+      uint32_t ids[8], cnts[8];
+      #pragma unroll
+      for (int r = 0; r < 8; ++r) {  // independent loads first
+        const uint32_t h = hb + r * NT + tid;
+        ids[r] = h < h1 ? a.hids[h] : 0xffffffffu;
+        cnts[r] = h < h1 ? a.hcnt[h] : 0u;
+      }
+      #pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const uint32_t id = ids[r];
+        if (id < (uint32_t)c0 || id >= (uint32_t)c1) continue;
+        const uint32_t li = id - (uint32_t)c0;
+        atomicOr(&bitmap[li >> 5], 1u << (li & 31u));
+        uint32_t slot = (id * 2654435761u) & (kHashCap - 1);
+        bool done = false;
+        for (int probe = 0; probe < kHashCap && !done; ++probe) {
+          const uint32_t prev = atomicCAS(&hkey[slot], 0xffffffffu, id);
+          if (prev == 0xffffffffu || prev == id) {
+            atomicAdd(&hcnt[slot], cnts[r]);
+            done = true;
+          } else {
+            slot = (slot + 1) & (kHashCap - 1);
+          }
+        }
+        if (!done) sh.hovf = 1u;
+      }
+    }
+  }
+  __syncthreads();
+
+  SelState ss;
+  ss.tau = 0ull;
+  ss.unkept = 0u;
+  ss.rest.init();
+  ss.rest_on = a.need_lse != 0;
+  ss.t_eff = cfg.t_eff;
+  ChunkStat st;
+  stat_init(st);
+  const StatNeeds nd = stat_needs(cfg, a.pv);
+  uint32_t maxkey = 0u;
+
+  #pragma unroll 1
+  for (int t = 0; t < TILES; ++t) {
+    const int tb = c0 + t * TILE;
+    if (tb >= c1) break;
+    float nxt[E];
+    if (t + 1 < TILES && tb + TILE < c1) load_tile<VEC>(a, rbase, tb + TILE, c1, nxt);
+    uint32_t key[E];  // 0: no element (past the end)
+    #pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e0 = tb + (j * NT + tid) * 4;
+      const uint32_t mword = (mrow && e0 < c1) ? mrow[e0 >> 5] : 0xffffffffu;
+      uint32_t flags = 0u;
+      if (pen && e0 < c1) flags = (bitmap[(e0 - c0) >> 5] >> ((e0 - c0) & 31)) & 15u;
+      #pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = e0 + q;
+        float l = cur[4 * j + q];
+        if (!((mword >> (e & 31)) & 1u)) l = -__builtin_inff();
+        if ((flags >> q) & 1u) {
+          bool found;
+          uint32_t cnt = hash_count(hkey, hcnt, (uint32_t)e, found);
+          if (!found) {  // the hash overflowed: count from the global list (slow)
+            cnt = 0u;
+            for (uint32_t h = h0; h < h1; ++h) if (a.hids[h] == (uint32_t)e) cnt += a.hcnt[h];
+          }
+          l = apply_penalties(l, cnt, cfg);
+        }
+        const uint32_t kl = lkey(l);
+        const bool in = e < c1;
+        if (in) stat_add(st, nd, maxkey, l, kl, (uint32_t)e);
+        key[4 * j + q] = in ? kl : 0u;
+      }
+      if (srow) {
+        float sv[4];
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) sv[q] = key[4 * j + q] ? key_to_s(key[4 * j + q], cfg.t_eff) : -__builtin_inff();
+        if (e0 + 3 < c1 && (V & 3) == 0) {
+          *(float4*)(srow + e0) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+        } else {
+          for (int q = 0; q < 4; ++q) if (e0 + q < c1) srow[e0 + q] = sv[q];
+        }
+      }
+    }
+    if (k > 0) {
+      if (t == 0 && len > (int)k) {
+        // bound from the first tile: the k-th largest of the per-thread
+        // top-j keys, rounded down to 16 bits (k or more real elements are
+        // at or above it)
+        const int jt = ((int)k + NT - 1) / NT;  // 1..4
+        uint32_t t4[4] = {0u, 0u, 0u, 0u};
+        #pragma unroll
+        for (int i = 0; i < E; ++i) {
+          uint32_t x = key[i];
+          #pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t hi = max(t4[r], x);
+            x = min(t4[r], x);
+            t4[r] = hi;
+          }
+        }
+        for (int r = 0; r < jt; ++r) sh.U[r * NT + tid] = t4[r];
+        __syncthreads();
+        if (tid < 64) {
+          const int nr = jt * NT / 64;
+          uint32_t prefix = 0u;
+          for (int bit = 31; bit >= 16; --bit) {
+            const uint32_t probe = prefix | (1u << bit);
+            uint32_t c = 0;
+            for (int r = 0; r < nr; ++r) c += (uint32_t)__popcll(__ballot(sh.U[r * 64 + tid] >= probe));
+            if (c >= k) prefix = probe;
+          }
+          if (tid == 0) sh.bound = prefix;
+        }
+        __syncthreads();
+        ss.tau = (uint64_t)sh.bound << 16;
+      }
+      const uint32_t li0 = (uint32_t)(tb - c0);
+      auto li_of = [&](int i) { return li0 + (uint32_t)(((i >> 2) * NT + tid) * 4 + (i & 3)); };
+      // fast path: the whole tile's survivors fit the buffer (one scan).
+      // Survivors are compared on the key alone (a superset of the
+      // composite test; the extra entries are dropped at compaction).
+      const uint32_t tk = (uint32_t)(ss.tau >> 16);
+      uint32_t mine = 0;
+      #pragma unroll
+      for (int i = 0; i < E; ++i) mine += key[i] >= tk && key[i] != 0u;
+      uint32_t total;
+      uint32_t off = block_excl_scan_u32<NT>(mine, sh.redu, &total);
+      if (sh.count + total <= (uint32_t)kBufCap) {
+        const uint32_t base = sh.count;
+        #pragma unroll
+        for (int i = 0; i < E; ++i) {
+          if (key[i] == 0u) continue;
+          if (key[i] >= tk) sh.cbuf[base + off++] = local_comp(key[i], li_of(i));
+          else reject_key(ss, key[i]);
+        }
+        __syncthreads();
+        if (tid == 0) sh.count = base + total;
+        __syncthreads();
+      } else {
+        // one float4 column (NT * 4 items) at a time, so each batch fits
+        #pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const uint32_t kj[4] = {key[4 * j], key[4 * j + 1], key[4 * j + 2], key[4 * j + 3]};
+          const uint32_t lij = li0 + (uint32_t)((j * NT + tid) * 4);
+          append_batch<4>(sh, ss, k, kj, [&](int q) { return lij + (uint32_t)q; });
+        }
+      }
+    }
+    #pragma unroll
+    for (int i = 0; i < E; ++i) cur[i] = nxt[i];
+  }
+
+  st.max_l = maxkey > kKeyNegInf ? okey_inv(maxkey) : -__builtin_inff();
+  st.any_finite = maxkey > kKeyNegInf ? 1u : 0u;
+  ChunkStat bs = block_stat<NT>(st, sh.red);
+  uint64_t* cand = a.cand + ((int64_t)row * a.n_chunks + chunk) * kFast;
+  if (k > 0) {
+    // the chunk's exact top-k: select in the buffer, emit in thread order
+    compact_buffer(sh, ss, k);
+    const uint32_t n = sh.count;
+    constexpr int PER = kBufCap / NT;
+    uint32_t mine = 0;
+    #pragma unroll
+    for (int r = 0; r < PER; ++r) mine += (uint32_t)(r * NT + tid) < n;
+    uint32_t total;
+    uint32_t pos = block_excl_scan_u32<NT>(mine, sh.redu, &total);
+    uint64_t minkept = ~0ull;
+    #pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const uint32_t i = r * NT + tid;
+      if (i >= n) continue;
+      const uint64_t v = sh.cbuf[i];
+      const uint32_t li = 0xffffu - (uint32_t)(v & 0xffffu);
+      const uint64_t ck = cand_key((uint32_t)(v >> 16), (uint32_t)c0 + li);
+      if (pos < (uint32_t)kFast) cand[pos] = ck;
+      ++pos;
+      minkept = ck < minkept ? ck : minkept;
+    }
+    const float mc = finitef_(bs.max_l) ? bs.max_l / cfg.t_eff : -__builtin_inff();
+    float part = (ss.rest_on && ss.rest.sum > 0.f && finitef_(mc)) ? ss.rest.sum * __expf(ss.rest.m - mc) : 0.f;
+    uint32_t unkept = ss.unkept;
+    block_tail3(minkept, unkept, part, sh);
+    bs.n_cand = min(total, (uint32_t)kFast);
+    bs.trunc = len > (int)k ? 1u : 0u;
+    bs.min_kept = minkept;
+    bs.unkept_key = unkept;
+    bs.lse_m = mc;
+    bs.lse_sum = part;
+  }
+  if (tid == 0) a.stats[(int64_t)row * a.n_chunks + chunk] = bs;
+}
+
+// One workgroup per row: merge the row's chunk results and draw.  A separate
+// launch: the kernel boundary makes every chunk's results visible to the
+// finishing workgroup on any XCD without a device-scope fence per chunk.
+__global__ void __launch_bounds__(NT) finish_kernel(SampleArgs a) {
+  __shared__ FinLds fs;
+  const int row = blockIdx.x;
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  finish_row(fs, a, row, cfg);
 }
 
 // ==========================================================================
@@ -1190,10 +1605,11 @@ __global__ void debug_expf_kernel(const float* x, float* y, int64_t n) {
   if (i < n) y[i] = exact_expf(x[i]);
 }
 
-// Processed logits and per-chunk max of s (stats[.].max_s) for the debug export.
-__global__ void __launch_bounds__(kScanThreads) debug_processed_kernel(SampleArgs a, float* out_proc) {
+// Processed logits and per-chunk max of s (kept in stats[.].max_l) for the
+// debug export.
+__global__ void __launch_bounds__(NT) debug_processed_kernel(SampleArgs a, float* out_proc) {
   __shared__ uint32_t cnt[kChunk];
-  __shared__ ChunkStat red[kScanThreads / 64];
+  __shared__ ChunkStat red[NT / 64];
   const int row = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x;
   const int V = a.V, c0 = chunk * kChunk, c1 = min(c0 + kChunk, V);
   const RowCfg cfg = load_cfg(a.pv, row, V, 0, 0);
@@ -1201,9 +1617,9 @@ __global__ void __launch_bounds__(kScanThreads) debug_processed_kernel(SampleArg
   uint32_t h0 = 0, h1 = 0;
   if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; pen = h1 > h0; }
   if (pen) {
-    for (int i = tid; i < kChunk; i += kScanThreads) cnt[i] = 0u;
+    for (int i = tid; i < kChunk; i += NT) cnt[i] = 0u;
     __syncthreads();
-    for (uint32_t h = h0 + tid; h < h1; h += kScanThreads) {
+    for (uint32_t h = h0 + tid; h < h1; h += NT) {
       const uint32_t id = a.hids[h];
       if (id >= (uint32_t)c0 && id < (uint32_t)c1) atomicAdd(&cnt[id - c0], a.hcnt[h]);
     }
@@ -1212,15 +1628,15 @@ __global__ void __launch_bounds__(kScanThreads) debug_processed_kernel(SampleArg
   ChunkStat st;
   stat_init(st);
   const int64_t rbase = (int64_t)row * a.row_stride;
-  for (int e = c0 + tid; e < c1; e += kScanThreads) {
+  for (int e = c0 + tid; e < c1; e += NT) {
     float l = load_raw(a.logits, a.dtype, rbase + e);
-    if (a.mask && !((a.mask[(int64_t)row * a.mask_words + (e >> 5)] >> (e & 31)) & 1u)) l = -__builtin_inff();
+    if (!allowed(a, row, (uint32_t)e)) l = -__builtin_inff();
     if (pen) l = apply_penalties(l, cnt[e - c0], cfg);
     out_proc[(int64_t)row * V + e] = l;
     const float s = finitef_(l) ? l / cfg.t_eff : -__builtin_inff();
-    st.max_s = fmaxf(st.max_s, s);
+    st.max_l = fmaxf(st.max_l, s);
   }
-  const ChunkStat bs = block_stat<kScanThreads>(st, red);
+  const ChunkStat bs = block_stat<NT>(st, red);
   if (tid == 0) a.stats[(int64_t)row * a.n_chunks + chunk] = bs;
 }
 
@@ -1230,7 +1646,7 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
   const int row = blockIdx.x, tid = threadIdx.x, V = a.V;
   const RowCfg cfg = load_cfg(a.pv, row, V, 0, 0);
   float M = -__builtin_inff();
-  for (int c = tid; c < a.n_chunks; c += 1024) M = fmaxf(M, a.stats[(int64_t)row * a.n_chunks + c].max_s);
+  for (int c = tid; c < a.n_chunks; c += 1024) M = fmaxf(M, a.stats[(int64_t)row * a.n_chunks + c].max_l);
   for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
   if ((tid & 63) == 0) fred[tid >> 6] = M;
   __syncthreads();
@@ -1260,12 +1676,26 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
 // --------------------------------------------------------------------------
 // launch wrappers (called from the host API)
 
+int choose_chunk(int B, int V) {
+  // fewer, larger chunks when the batch alone fills the GPU; otherwise
+  // smaller chunks so that a small batch still spreads over many CUs
+  const long wg_large = (long)B * ((V + kChunk - 1) / kChunk);
+  return wg_large >= 512 ? kChunk : kChunkSmall;
+}
+
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
-  dim3 g1(a.n_chunks, a.B);
-  hipLaunchKernelGGL(scan_chunks_kernel, g1, dim3(kScanThreads), 0, stream, a);
+  const bool hist = a.hoff != nullptr;
+  dim3 grid(a.n_chunks, a.B);
+  if (a.chunk == kChunk) {
+    hipLaunchKernelGGL((scan_kernel<kVecLarge, kTilesLarge>), grid, dim3(NT),
+                       scan_lds_bytes(kChunk, hist), stream, a);
+  } else {
+    hipLaunchKernelGGL((scan_kernel<kVecSmall, 1>), grid, dim3(NT),
+                       scan_lds_bytes(kChunkSmall, hist), stream, a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(finish_rows_kernel, dim3(a.B), dim3(kFinThreads), 0, stream, a);
+  hipLaunchKernelGGL(finish_kernel, dim3(a.B), dim3(NT), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -1285,11 +1715,13 @@ hipError_t launch_debug_expf(const float* x, float* y, int64_t n, hipStream_t st
 
 hipError_t launch_debug_distribution(const SampleArgs& a, float* out_proc, float* out_probs,
                                      hipStream_t stream) {
-  dim3 g1(a.n_chunks, a.B);
-  hipLaunchKernelGGL(debug_processed_kernel, g1, dim3(kScanThreads), 0, stream, a, out_proc);
+  dim3 g1((a.V + kChunk - 1) / kChunk, a.B);
+  SampleArgs b = a;
+  b.n_chunks = (int)g1.x;
+  hipLaunchKernelGGL(debug_processed_kernel, g1, dim3(NT), 0, stream, b, out_proc);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(debug_probs_kernel, dim3(a.B), dim3(1024), 0, stream, a, (const float*)out_proc, out_probs);
+  hipLaunchKernelGGL(debug_probs_kernel, dim3(a.B), dim3(1024), 0, stream, b, (const float*)out_proc, out_probs);
   return hipGetLastError();
 }
 

@@ -182,7 +182,7 @@ class Sampler:
         nbytes = ctypes.c_size_t()
         check(lib.hi_rocm_sampler_workspace_bytes(max_batch, vocab, n_logprobs, ctypes.byref(nbytes)))
         self.max_batch, self.vocab, self.n_logprobs = max_batch, vocab, n_logprobs
-        self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=device)
+        self.workspace = torch.zeros(nbytes.value, dtype=torch.uint8, device=device)
 
     def sample(self, logits: torch.Tensor, params: torch.Tensor, uniforms: torch.Tensor,
                hist_offsets: Optional[torch.Tensor] = None, hist_ids: Optional[torch.Tensor] = None,

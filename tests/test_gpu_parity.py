@@ -344,3 +344,57 @@ def test_host_layer_error_messages(hip):
         select_batched_last_token_per_row(x, 4, 1, [RowSampling.Greedy()], [0.1] * 4)
     with pytest.raises(SamplerError, match="do not match batch"):
         select_batched_last_token_per_row(x, 2, 1, [RowSampling.Greedy()] * 2, [0.1] * 2)
+
+
+def test_graph_replays_match_eager(hip, oracle):
+    """The step has no allocation and no host sync, so it can be captured in
+    a graph; every replay (with new uniforms and eager work in between) must
+    match the oracle."""
+    torch = _torch()
+    from hi_amd import sampler as S
+    w = CONFIGS[1]()
+    logits = dev(w.logits)
+    params = S.params_to_device(w.params)
+    unif = dev(w.uniforms)
+    hist = [dev(w.hist_offsets), dev(w.hist_ids), dev(w.hist_counts)]
+    smp = S.Sampler(1, w.vocab, w.n_logprobs)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        out = smp.sample(logits, params, unif, *hist, n_logprobs=w.n_logprobs, stream=stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        smp.sample(logits, params, unif, *hist, n_logprobs=w.n_logprobs, out=out, stream=stream)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(99)
+    for rep in range(6):
+        u = rng.random(1).astype(F32)
+        unif.copy_(torch.from_numpy(u))
+        junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        want = oracle.sample_rows(w.logits, w.params, u, w.hist_offsets, w.hist_ids, w.hist_counts,
+                                  None, w.n_logprobs)
+        got_tok = out["tokens"].cpu().numpy().view(np.uint32)
+        assert got_tok[0] == want["tokens"][0], (rep, got_tok, want["tokens"])
+        assert np.array_equal(out["logprob_ids"].cpu().numpy().view(np.uint32), want["logprob_ids"])
+        del junk
+
+
+def test_workspace_reuse_across_batch_sizes(hip, oracle):
+    """One workspace, successive calls with different batch sizes (the chunk
+    size and the per-row tickets change between calls)."""
+    torch = _torch()
+    from hi_amd import sampler as S
+    full = CONFIGS[3](B=64)
+    smp = S.Sampler(64, full.vocab, 0)
+    for B in (64, 1, 3, 64, 2):
+        sel = slice(0, B)
+        w = Workload("c3-slice", full.logits[sel], full.params[sel], full.uniforms[sel],
+                     full.hist_offsets[:B + 1], full.hist_ids[:full.hist_offsets[B]],
+                     full.hist_counts[:full.hist_offsets[B]])
+        out = smp.sample(dev(w.logits), S.params_to_device(w.params), dev(w.uniforms),
+                         dev(w.hist_offsets), dev(w.hist_ids), dev(w.hist_counts))
+        torch.cuda.synchronize()
+        want = run_oracle(oracle, w)
+        assert np.array_equal(out["tokens"].cpu().numpy().view(np.uint32), want["tokens"]), B

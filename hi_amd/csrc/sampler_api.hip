@@ -70,7 +70,7 @@ void carve(hi_rocm::SampleArgs& a, void* ws, const hi_rocm::WorkspaceLayout& L) 
   a.ws_w = (float*)(base + L.ws_w);
   a.ws_list = (uint64_t*)(base + L.ws_list);
   a.list_stride = L.list_stride;
-  a.chunk = hi_rocm::choose_chunk(a.B, a.V);
+  a.chunk = hi_rocm::choose_chunk(a.B, a.V, a.n_lp, a.vec_ok, a.hoff != nullptr);
   a.n_chunks = (a.V + a.chunk - 1) / a.chunk;
 }
 

@@ -15,6 +15,7 @@ constexpr int kChunk = kScanThreads * kVecLarge * 4 * kTilesLarge;  // 16384 log
 constexpr int kVecSmall = 2;
 constexpr int kChunkSmall = kScanThreads * kVecSmall * 4;  // 2048 (one tile), small batches
 constexpr int kFast = 1024;                        // candidates kept per chunk (max)
+constexpr int kLeanK = 256;                        // largest top-k of the streaming selection
 constexpr int kMaxVocab = 1 << 23;                 // 8,388,608
 constexpr int kLseTop = 16;                        // per-chunk candidates kept for logprobs
 
@@ -50,7 +51,7 @@ struct RowCfg {
   float t_eff;    // temperature used for s = l / t_eff (1 for greedy rows)
   float cutoff;   // clamped top_p (gpu.rs:789-793)
   bool rep_on;
-  bool wide;      // top-k row with k_eff > kFast
+  bool wide;      // top-k row with k_eff > kLeanK
   int k_sel;      // candidates each chunk keeps
   bool store_s;   // scaled logits go to the workspace
 };
@@ -110,7 +111,7 @@ struct WorkspaceLayout {
   int64_t list_stride;
 };
 
-int choose_chunk(int B, int V);
+int choose_chunk(int B, int V, int n_lp, int vec_ok, bool hist);
 
 inline int64_t next_pow2_i64(int64_t x) {
   int64_t p = 1;
@@ -124,7 +125,7 @@ inline WorkspaceLayout workspace_layout(int max_batch, int V) {
   WorkspaceLayout L;
   L.slots = 0;
   for (int b = 1; b <= max_batch; ++b) {
-    const int ch = choose_chunk(b, V);
+    const int ch = choose_chunk(b, V, kLeanK + 1, 1, true);  // the chunked layout needs the most records
     const int64_t s = (int64_t)b * ((V + ch - 1) / ch);
     if (s > L.slots) L.slots = s;
   }

@@ -41,7 +41,7 @@ constexpr int NT = kScanThreads;  // threads of the fused kernel
 constexpr int kBuf = 1024;        // ranked entries held in LDS
 constexpr int kGather = 4096;     // candidates of a row gathered into LDS
 constexpr int kBufCap = 2048;     // running chunk candidates held in LDS
-constexpr int kHashCap = 2048;    // distinct history tokens per chunk held in LDS
+constexpr int kHashCap = 1024;    // distinct history tokens per chunk held in LDS
 constexpr int kBins = 1024;       // weight histogram of the wide paths (w bits >> 20)
 
 // --------------------------------------------------------------------------
@@ -66,9 +66,10 @@ __device__ __forceinline__ float okey_inv(uint32_t k) {
 constexpr uint32_t kKeyNegInf = 0x007fffffu;  // okey(-inf)
 __device__ __forceinline__ uint32_t lkey(float l) { return finitef_(l) ? okey(l) : kKeyNegInf; }
 
-// Scaled logit s = l / t_eff of a key (gpu.rs:767-777).
+// Scaled logit s = l / t_eff of a key (gpu.rs:767-777); the key of -inf
+// decodes to -inf and t_eff is positive, so no case needs a branch.
 __device__ __forceinline__ float key_to_s(uint32_t key, float t_eff) {
-  return key == kKeyNegInf ? -__builtin_inff() : okey_inv(key) / t_eff;
+  return okey_inv(key) / t_eff;
 }
 
 // Rust's f32::total_cmp as a signed key (gpu.rs:744).
@@ -137,7 +138,7 @@ __device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V,
   c.rep_on = finitef_(c.rep) && c.rep > 0.f && fabsf(c.rep - 1.f) > FLT_EPSILON;
   c.freq = finitef_(c.freq) ? c.freq : 0.f;
   c.pres = finitef_(c.pres) ? c.pres : 0.f;
-  c.wide = c.cls == kTopK && c.k_eff > kFast;
+  c.wide = c.cls == kTopK && c.k_eff > kLeanK;
   c.k_sel = (c.cls == kTopK && !c.wide) ? max(c.k_eff, n_lp) : n_lp;
   // Logprobs need the normaliser to ~1e-7 relative: its largest terms are
   // summed in double from the candidates, so every chunk keeps a few.
@@ -445,9 +446,6 @@ struct FinLds {
 };
 constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
 
-size_t scan_lds_bytes(int chunk, bool hist) {
-  return sizeof(ScanLds) + (hist ? (size_t)chunk / 8 + 2 * kHashCap * sizeof(uint32_t) : 0);
-}
 
 // ==========================================================================
 // Finish phase (one workgroup per row)
@@ -1306,76 +1304,832 @@ __device__ __forceinline__ void block_tail3(uint64_t& mn, uint32_t& mx, float& s
   mn = ~a;
 }
 
-// Each workgroup streams one chunk of TILES tiles of NT*VEC*4 logits; the
-// next tile's 128-bit loads are in flight while the current one is
-// processed.  Tokens present in the row's history are marked in an LDS
-// bitmap; the lanes holding one look their count up in an LDS hash.
-template <int VEC, int TILES>
-__global__ void __launch_bounds__(NT) scan_kernel(SampleArgs a) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  ScanLds& sh = *reinterpret_cast<ScanLds*>(lds_raw);
-  constexpr int TILE = NT * VEC * 4;
-  constexpr int CH = TILE * TILES;
-  constexpr int E = VEC * 4;
-  static_assert(CH <= 65536, "local indices are 16-bit");
-  uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds_raw + sizeof(ScanLds));
-  uint32_t* hkey = bitmap + CH / 32;
-  uint32_t* hcnt = hkey + kHashCap;
+// ==========================================================================
+// Lean scan path (every row class when at most kLeanK logprobs are asked)
+// ==========================================================================
+//
+// Every wave keeps its own running top-(k+1) of the elements it streams, in
+// its own LDS buffer, with a wave-uniform threshold: an element below the
+// threshold costs a compare, survivors are appended with ballot/mbcnt, and a
+// buffer that passes its limit is compacted by a wave-level radix select.
+// No workgroup barrier runs inside the tile loop.  At the end wave 0 merges
+// the four per-wave sets into the range's top k.  Selection entries are the
+// 64-bit candidate keys (scaled-logit key, inverted index).
 
-  const int row = blockIdx.y;
-  const int chunk = blockIdx.x;
+constexpr int kLeanVec = 2;                     // float4 loads per thread per tile
+constexpr int kWaveCap = 1024;                  // per-wave buffer entries
+constexpr int kWaveMaxLim = kWaveCap - kLeanVec * 4 * 64;  // a tile's survivors fit above the limit
+static_assert(kLeanK + 1 <= kWaveMaxLim, "a compacted buffer is below the limit");
+constexpr uint32_t kChunkHistCap = 1024;        // distinct history tokens counted in LDS per chunk
+constexpr uint32_t kRowHistCap = 4096;          // ... per row (row kernel)
+
+template <int NW>
+struct LeanLds {
+  uint64_t wbuf[NW][kWaveCap];
+  uint32_t whist[NW][256];
+  uint32_t wcount[NW];
+  uint32_t wmax[NW];
+  float wbv[NW];
+  uint32_t wbi[NW];
+  float wrest[NW];
+  float wlref[NW];
+  float wfv[NW];
+  uint32_t wfi[NW];
+};
+
+// Orders this wave's LDS accesses (a wave executes its LDS operations in
+// order; this keeps the compiler from moving them across the point).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Number of set bits of m below the calling lane.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Up to NS LDS arrays of candidate keys, read as one list.
+template <int NS>
+struct Segs {
+  const uint64_t* p[NS];
+  uint32_t n[NS];
+  int ns;
+};
+
+// Threshold T such that exactly `need` of the listed entries (unique keys)
+// are >= T, for 1 <= need <= the number of entries.  8-bit MSD descent with
+// early exit over a 256-bin LDS histogram owned by the wave.
+template <int NS>
+__device__ __forceinline__ uint64_t wave_select(const Segs<NS>& sg, uint32_t need, uint32_t* hist) {
+  const uint32_t lane = threadIdx.x & 63u;
+  uint64_t prefix = 0;
+  uint32_t remaining = need;
+  #pragma unroll 1
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    wave_lds_sync();
+    *reinterpret_cast<uint4*>(hist + 4 * lane) = make_uint4(0u, 0u, 0u, 0u);
+    wave_lds_sync();
+    const int hs = shift + 8;
+    const uint64_t hp = hs >= 64 ? 0ull : (prefix >> hs);
+    #pragma unroll
+    for (int sgi = 0; sgi < NS; ++sgi) {
+      if (sgi >= sg.ns) break;
+      const uint64_t* p = sg.p[sgi];
+      const uint32_t n = sg.n[sgi];
+      #pragma unroll 2
+      for (uint32_t i = lane; i < n; i += 64u) {
+        const uint64_t x = p[i];
+        if (hs >= 64 || (x >> hs) == hp) atomicAdd(&hist[(uint32_t)(x >> shift) & 255u], 1u);
+      }
+    }
+    wave_lds_sync();
+    // lane l owns bins 255-4l, 254-4l, 253-4l, 252-4l (descending)
+    const uint4 h = *reinterpret_cast<const uint4*>(hist + 252 - 4 * lane);
+    const uint32_t cs[4] = {h.w, h.z, h.y, h.x};
+    const uint32_t lsum = cs[0] + cs[1] + cs[2] + cs[3];
+    uint32_t inc = lsum;
+    #pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t t = (uint32_t)__shfl_up((int)inc, o, 64);
+      if (lane >= (uint32_t)o) inc += t;
+    }
+    uint32_t acc = inc - lsum, d = 0, da = 0, dc = 0;
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (acc < remaining && remaining <= acc + cs[q]) { d = 255u - 4u * lane - (uint32_t)q; da = acc; dc = cs[q]; }
+      acc += cs[q];
+    }
+    const uint64_t who = __ballot(inc - lsum < remaining && remaining <= inc);
+    const int src = __ffsll((unsigned long long)who) - 1;
+    d = (uint32_t)__builtin_amdgcn_readlane((int)d, src);
+    da = (uint32_t)__builtin_amdgcn_readlane((int)da, src);
+    dc = (uint32_t)__builtin_amdgcn_readlane((int)dc, src);
+    prefix |= (uint64_t)d << shift;
+    remaining -= da;
+    if (dc == remaining) break;
+  }
+  return prefix;
+}
+
+// Rest of the normaliser over the elements a range does not keep, per lane:
+// sum of 2^((l - lref) * a2) with a2 = log2(e) / T and a wave-uniform
+// reference lref that only grows (the value of the current threshold key).
+struct LseRest {
+  float sum, lref, a2;
+  __device__ __forceinline__ void add(float l) { sum += exp2f((l - lref) * a2); }
+  __device__ __forceinline__ void add_key(uint32_t key) {
+    if (key > kKeyNegInf) add(okey_inv(key));
+  }
+  __device__ __forceinline__ void move_ref(uint32_t tk) {
+    if (tk <= kKeyNegInf) return;
+    const float nl = okey_inv(tk);
+    if (finitef_(lref)) sum *= exp2f((lref - nl) * a2);
+    else sum = 0.f;
+    lref = nl;
+  }
+};
+
+// Running per-wave selection of the top k1 candidate keys.
+struct WaveSel {
+  uint64_t* buf;
+  uint32_t* hist;
+  uint32_t count;   // entries in buf (wave-uniform)
+  uint32_t k1;      // entries a compaction keeps
+  uint32_t lim;     // compaction trigger
+  uint64_t tau;     // keys below tau are not among the wave's top k1
+  uint32_t tk;      // scaled-logit key threshold: max(1, tau >> 32)
+};
+
+// Compact the wave's buffer to its top k1 (in place, in order) and raise
+// the threshold.
+__device__ __forceinline__ void wave_compact(WaveSel& ws, LseRest& rest, bool lse) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t n = ws.count;
+  if (n <= ws.k1) return;
+  Segs<1> sg;
+  sg.p[0] = ws.buf;
+  sg.n[0] = n;
+  sg.ns = 1;
+  const uint64_t thr = wave_select(sg, ws.k1, ws.hist);
+  if (thr > ws.tau) ws.tau = thr;
+  ws.tk = max(1u, (uint32_t)(ws.tau >> 32));
+  if (lse) rest.move_ref(ws.tk);
+  wave_lds_sync();
+  uint32_t pos = 0;
+  // entry i moves to a position <= i, and a block of 64 is read before any
+  // of its writes, so the compaction can run in place
+  #pragma unroll 1
+  for (uint32_t b = 0; b < n; b += 64u) {
+    const uint32_t i = b + lane;
+    const bool valid = i < n;
+    const uint64_t x = valid ? ws.buf[i] : 0ull;
+    const bool keep = valid && x >= thr;
+    const uint64_t m = __ballot(keep);
+    if (keep) ws.buf[pos + lanes_below(m)] = x;
+    else if (lse && valid) rest.add_key(cand_skey(x));
+    pos += (uint32_t)__popcll(m);
+  }
+  ws.count = pos;
+}
+
+// History tokens of [base, base + len) as seen by the lean path: bit li of
+// `bitmap` marks token base + li, prefix[w] counts the marked tokens of the
+// words below w, and cnts[r] is the summed count of the marked token of rank
+// r (for r < cap; higher ranks are counted from the global list).
+struct HistView {
+  const uint32_t* bitmap;
+  const uint32_t* prefix;
+  uint32_t* cnts;         // counts by rank; the lean pass then keeps keys there
+  const uint32_t* ids;    // ids[r]: the marked token of rank r (r < min(distinct, cap))
+  uint32_t cap;
+  uint32_t distinct;      // marked tokens
+  uint32_t h0, h1;
+  bool on;
+  bool ovf;               // more marked tokens than cap
+};
+
+// LDS bytes of a HistView over `len` tokens with `cap` counted tokens
+// (bitmap, prefix, counts + a zero slot, ids, 16 reduction words).
+__host__ __device__ constexpr size_t hist_lds_bytes(int len, uint32_t cap) {
+  return (size_t)2 * ((len + 31) / 32) * 4 + (size_t)(2 * cap + 1) * 4 + 64;
+}
+
+// Builds the HistView of row `row` over [base, base + len) in `mem`.  All
+// NTH threads of the workgroup call it.
+template <int NTH>
+__device__ __forceinline__ HistView stage_history_rank(const SampleArgs& a, int row, int base, int len,
+                                                       uint32_t cap, uint32_t* mem) {
+  const int tid = threadIdx.x;
+  const int W = (len + 31) / 32;
+  uint32_t* bitmap = mem;
+  uint32_t* prefix = mem + W;
+  uint32_t* cnts = mem + 2 * W;   // cap counts, then a zero slot at cnts[cap]
+  uint32_t* ids = cnts + cap + 1;
+  uint32_t* red = ids + cap;
+  HistView hv;
+  hv.bitmap = bitmap; hv.prefix = prefix; hv.cnts = cnts; hv.ids = ids; hv.cap = cap;
+  hv.distinct = 0u;
+  hv.h0 = a.hoff[row];
+  hv.h1 = a.hoff[row + 1];
+  hv.on = hv.h1 > hv.h0;
+  hv.ovf = false;
+  if (!hv.on) return hv;
+  const uint32_t h0 = hv.h0, h1 = hv.h1;
+  for (int i = tid; i < W; i += NTH) bitmap[i] = 0u;
+  __syncthreads();
+  constexpr int PER = 8;
+  const bool one = h1 - h0 <= (uint32_t)(NTH * PER);
+  uint32_t hid[PER], cs[PER];
+  for (uint32_t hb = h0; hb < h1; hb += NTH * PER) {
+    #pragma unroll
+    for (int r = 0; r < PER; ++r) {  // independent loads first
+      const uint32_t h = hb + r * NTH + tid;
+      hid[r] = h < h1 ? a.hids[h] : 0xffffffffu;
+      cs[r] = h < h1 ? a.hcnt[h] : 0u;
+    }
+    #pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const uint32_t li = hid[r] - (uint32_t)base;
+      if (hid[r] >= (uint32_t)base && li < (uint32_t)len) atomicOr(&bitmap[li >> 5], 1u << (li & 31u));
+    }
+  }
+  __syncthreads();
+  // exclusive prefix of the per-word popcounts
+  const int PW = (W + NTH - 1) / NTH;
+  uint32_t loc = 0;
+  for (int i = 0; i < PW; ++i) {
+    const int w = tid * PW + i;
+    if (w < W) loc += (uint32_t)__popc(bitmap[w]);
+  }
+  uint32_t total;
+  uint32_t run = block_excl_scan_u32<NTH>(loc, red, &total);
+  for (int i = 0; i < PW; ++i) {
+    const int w = tid * PW + i;
+    if (w < W) { prefix[w] = run; run += (uint32_t)__popc(bitmap[w]); }
+  }
+  const uint32_t nz = min(total, cap);
+  hv.ovf = total > cap;
+  hv.distinct = total;
+  for (uint32_t i = tid; i < nz; i += NTH) cnts[i] = 0u;
+  if (tid == 0) cnts[cap] = 0u;
+  __syncthreads();
+  for (uint32_t hb = h0; hb < h1; hb += NTH * PER) {
+    if (!one) {
+      #pragma unroll
+      for (int r = 0; r < PER; ++r) {
+        const uint32_t h = hb + r * NTH + tid;
+        hid[r] = h < h1 ? a.hids[h] : 0xffffffffu;
+        cs[r] = h < h1 ? a.hcnt[h] : 0u;
+      }
+    }
+    #pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const uint32_t li = hid[r] - (uint32_t)base;
+      if (hid[r] >= (uint32_t)base && li < (uint32_t)len) {
+        const uint32_t w = li >> 5;
+        const uint32_t rank = prefix[w] + (uint32_t)__popc(bitmap[w] & ((1u << (li & 31u)) - 1u));
+        if (rank < cap) {
+          atomicAdd(&cnts[rank], cs[r]);
+          ids[rank] = (uint32_t)base + li;  // every occurrence writes the same id
+        }
+      }
+    }
+  }
+  __syncthreads();
+  return hv;
+}
+
+// History count of the marked token e of rank `rank`.  OVF: the table may
+// not hold every marked token; the others are counted from the global list.
+template <bool OVF>
+__device__ __forceinline__ uint32_t hist_count(const SampleArgs& a, const HistView& hv, uint32_t e,
+                                               uint32_t rank) {
+  if (!OVF || rank < hv.cap) return hv.cnts[rank];
+  uint32_t cnt = 0u;
+  for (uint32_t h = hv.h0; h < hv.h1; ++h) if (a.hids[h] == e) cnt += a.hcnt[h];
+  return cnt;
+}
+
+// f(x) with x - lref <= 0 relevant only where `use` holds (0 elsewhere).
+__device__ __forceinline__ float masked_exp2(bool use, float v) { return use ? exp2f(v) : 0.f; }
+
+// Range-checked loads of one row (byte offsets at or past the range read
+// as zero; nothing faults).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+constexpr int kBufferConfig = 0x00020000;  // raw buffer, 32-bit data (gfx9 family)
+
+struct RowBuf {
+  __amdgpu_buffer_rsrc_t logits, mask;
+};
+
+// Range [c0, c1) of `row` (c0 a multiple of 32).
+template <int DT, bool MASK>
+__device__ __forceinline__ RowBuf row_buf(const SampleArgs& a, int row, int c0, int c1) {
+  RowBuf rb;
+  const int esize = DT == HI_ROCM_DTYPE_BF16 ? 2 : 4;
+  const char* base = (const char*)a.logits + ((int64_t)row * a.row_stride + c0) * esize;
+  rb.logits = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (c1 - c0) * esize, kBufferConfig);
+  if (MASK)
+    rb.mask = __builtin_amdgcn_make_buffer_rsrc((void*)(a.mask + (int64_t)row * a.mask_words + (c0 >> 5)),
+                                                (short)0, ((c1 - c0 + 31) >> 5) * 4, kBufferConfig);
+  return rb;
+}
+
+// One tile at offset tr from the range start (element tr + (j * NTH + tid)
+// * 4 + q in x[4 * j + q]); needs 16-byte (f32) or 8-byte (bf16) aligned
+// rows.
+template <int NTH, int VEC, int DT, bool MASK>
+__device__ __forceinline__ void buf_load(const RowBuf& rb, int tr, float (&x)[VEC * 4], uint32_t (&mw)[VEC]) {
+  const int tid = threadIdx.x;
+  #pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const int e0 = tr + (j * NTH + tid) * 4;
+    if (DT == HI_ROCM_DTYPE_BF16) {
+      const i32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rb.logits, e0 * 2, 0, 0);
+      x[4 * j + 0] = __uint_as_float((uint32_t)v.x << 16); x[4 * j + 1] = __uint_as_float((uint32_t)v.x & 0xffff0000u);
+      x[4 * j + 2] = __uint_as_float((uint32_t)v.y << 16); x[4 * j + 3] = __uint_as_float((uint32_t)v.y & 0xffff0000u);
+    } else {
+      const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb.logits, e0 * 4, 0, 0);
+      x[4 * j + 0] = __int_as_float(v.x); x[4 * j + 1] = __int_as_float(v.y);
+      x[4 * j + 2] = __int_as_float(v.z); x[4 * j + 3] = __int_as_float(v.w);
+    }
+    if (MASK) mw[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb.mask, (e0 >> 5) * 4, 0, 0);
+  }
+}
+
+// Argmax merges: IEEE '>' with ties to the lower index (kernels.cu:7153-7186),
+// and the finite-lane rule of kernels.cu:7775-7801 (ties to the lower
+// index modulo 256, then the lower index).
+__device__ __forceinline__ void merge_ieee(float& v, uint32_t& i, float ov, uint32_t oi) {
+  if (oi != 0xffffffffu && (i == 0xffffffffu || ov > v || (ov == v && oi < i))) { v = ov; i = oi; }
+}
+__device__ __forceinline__ void merge_fin(float& v, uint32_t& i, float ov, uint32_t oi) {
+  if (oi == 0xffffffffu) return;
+  bool take = i == 0xffffffffu || ov > v;
+  if (!take && ov == v) {
+    const uint32_t ra = i & 255u, rb = oi & 255u;
+    take = rb < ra || (rb == ra && oi < i);
+  }
+  if (take) { v = ov; i = oi; }
+}
+
+// Per-wave results written before the workgroup barrier of the merge.
+struct WaveOut {
+  uint32_t count, maxkey;
+  float bv;
+  uint32_t bi;
+  float fv;
+  uint32_t fi;
+  float rest, lref;
+};
+
+template <int NW>
+__device__ __forceinline__ void wave_results(LeanLds<NW>& L, int wid, WaveOut o, bool ieee, bool fin,
+                                             bool lse) {
+  #pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    o.maxkey = max(o.maxkey, (uint32_t)__shfl_xor((int)o.maxkey, s, 64));
+    if (ieee) merge_ieee(o.bv, o.bi, __shfl_xor(o.bv, s, 64), (uint32_t)__shfl_xor((int)o.bi, s, 64));
+    if (fin) merge_fin(o.fv, o.fi, __shfl_xor(o.fv, s, 64), (uint32_t)__shfl_xor((int)o.fi, s, 64));
+    if (lse) o.rest += __shfl_xor(o.rest, s, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    L.wcount[wid] = o.count;
+    L.wmax[wid] = o.maxkey;
+    L.wbv[wid] = o.bv;
+    L.wbi[wid] = o.bi;
+    L.wfv[wid] = o.fv;
+    L.wfi[wid] = o.fi;
+    L.wrest[wid] = o.rest;
+    L.wlref[wid] = o.lref;
+  }
+}
+
+// Per-wave state of the lean pass.
+struct LeanState {
+  WaveSel ws;
+  LseRest rest;
+  uint32_t maxkey;
+  float bv, fv;
+  uint32_t bi, fi;
+};
+
+// Constant context of the lean pass over [c0, c1) of `row`.
+struct LeanCtx {
+  const SampleArgs* a;
+  const RowCfg* cfg;
+  const HistView* hv;
+  float* srow;      // scaled logits for the finish, or null
+  int c0, c1, len;
+  uint32_t k;       // candidates to keep (k_sel)
+  bool ieee, fin, lse, rep_once;
+};
+
+// One tile of the lean pass: mask, penalties, keys, statistics, survivors.
+// cur holds the tile's logits (element tb + (j * NTH + tid) * 4 + q in
+// cur[4 * j + q]); first: the range's first tile.
+template <int NTH, int VEC, bool MASK, bool OVF>
+__device__ __forceinline__ void lean_tile(const LeanCtx& x, LeanState& st, float (&cur)[VEC * 4],
+                                          const uint32_t (&mw)[VEC], int tb, bool first) {
+  constexpr int TILE = NTH * VEC * 4;
+  constexpr int E = VEC * 4;
+  const SampleArgs& a = *x.a;
+  const RowCfg& cfg = *x.cfg;
+  const HistView& hv = *x.hv;
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const int c0 = x.c0, c1 = x.c1;
+  const bool full = tb + TILE <= c1;
+  WaveSel& ws = st.ws;
+  if (MASK) {
+    #pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e0 = tb + (j * NTH + tid) * 4;
+      const uint32_t nib = mw[j] >> (e0 & 31);
+      #pragma unroll
+      for (int q = 0; q < 4; ++q) if (!((nib >> q) & 1u)) cur[4 * j + q] = -__builtin_inff();
+    }
+  }
+  // elements this tile does not stream: past the range, and (without OVF)
+  // history tokens, which the lean pass handles on their own
+  uint32_t drop[VEC];
+  bool anyd = false;
+  #pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const int e0 = tb + (j * NTH + tid) * 4;
+    drop[j] = full ? 0u : (e0 + 3 < c1 ? 0u : (0xfu << max(0, min(4, c1 - e0))) & 0xfu);
+  }
+  if (hv.on) {
+    uint32_t wb[VEC];
+    bool anyf = false;
+    #pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const uint32_t li0 = (uint32_t)(tb - c0 + (j * NTH + tid) * 4);
+      wb[j] = li0 < (uint32_t)x.len ? hv.bitmap[li0 >> 5] : 0u;
+      anyf |= ((wb[j] >> (li0 & 31u)) & 15u) != 0u;
+    }
+    if (!OVF) {
+      #pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const uint32_t li0 = (uint32_t)(tb - c0 + (j * NTH + tid) * 4);
+        drop[j] |= (wb[j] >> (li0 & 31u)) & 15u;
+      }
+    } else if (__ballot(anyf) != 0ull) {
+      // counts of the marked elements; the others read the zero slot
+      // cnts[cap] (tokens of rank >= cap count from the global list)
+      const uint32_t W = (uint32_t)(x.len + 31) >> 5;
+      uint32_t cnt[E];
+      uint32_t most = 0u;
+      #pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const uint32_t li0 = (uint32_t)(tb - c0 + (j * NTH + tid) * 4);
+        const uint32_t sh = li0 & 31u;
+        const uint32_t nib = (wb[j] >> sh) & 15u;
+        const uint32_t base = hv.prefix[min(li0 >> 5, W - 1u)] + (uint32_t)__popc(wb[j] & ((1u << sh) - 1u));
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const bool m = (nib >> q) & 1u;
+          const uint32_t r = base + (uint32_t)__popc(nib & ((1u << q) - 1u));
+          cnt[4 * j + q] = m ? hist_count<true>(a, hv, (uint32_t)c0 + li0 + (uint32_t)q, r) : 0u;
+          most = max(most, cnt[4 * j + q]);
+        }
+      }
+      // repetition penalty once per occurrence (or once), then the
+      // frequency and presence penalties (apply_penalties, element-wise)
+      if (cfg.rep_on) {
+        const uint32_t reps = x.rep_once ? min(most, 1u) : most;
+        #pragma unroll 1
+        for (uint32_t rr = 0; rr < reps; ++rr) {
+          #pragma unroll
+          for (int i = 0; i < E; ++i) {
+            const uint32_t ci = x.rep_once ? min(cnt[i], 1u) : cnt[i];
+            const float y = cur[i] < 0.f ? cur[i] * cfg.rep : cur[i] / cfg.rep;
+            cur[i] = rr < ci ? y : cur[i];
+          }
+        }
+      }
+      #pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const float fc = cfg.freq * (float)cnt[i];
+        const float y = (cur[i] - fc) - cfg.pres;
+        cur[i] = cnt[i] != 0u ? y : cur[i];
+      }
+    }
+  }
+  #pragma unroll
+  for (int j = 0; j < VEC; ++j) anyd |= drop[j] != 0u;
+  uint32_t key[E];
+  #pragma unroll
+  for (int i = 0; i < E; ++i) key[i] = lkey(cur[i]);
+  if (__ballot(anyd) != 0ull) {
+    #pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const bool dr = (drop[i >> 2] >> (i & 3)) & 1u;
+      key[i] = dr ? 0u : key[i];
+      cur[i] = dr ? -__builtin_inff() : cur[i];
+    }
+  }
+  #pragma unroll
+  for (int i = 0; i < E; ++i) st.maxkey = max(st.maxkey, key[i]);
+  if (x.ieee) {
+    #pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const bool g = cur[i] > st.bv;
+      st.bv = g ? cur[i] : st.bv;
+      st.bi = g ? (uint32_t)(tb + ((i >> 2) * NTH + tid) * 4 + (i & 3)) : st.bi;
+    }
+  }
+  if (x.fin) {
+    // within a lane indices grow, so a tie keeps the earlier index unless
+    // the new one has the smaller residue modulo 256
+    #pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const uint32_t e = (uint32_t)(tb + ((i >> 2) * NTH + tid) * 4 + (i & 3));
+      const bool g = finitef_(cur[i]) &&
+                     (st.fi == 0xffffffffu || cur[i] > st.fv || (cur[i] == st.fv && (e & 255u) < (st.fi & 255u)));
+      st.fv = g ? cur[i] : st.fv;
+      st.fi = g ? e : st.fi;
+    }
+  }
+  if (x.srow) {
+    // scaled logits s = l / T for the finish (non-finite -> -inf)
+    #pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int e0 = tb + (j * NTH + tid) * 4;
+      float sv[4];
+      #pragma unroll
+      for (int q = 0; q < 4; ++q) sv[q] = key_to_s(key[4 * j + q] ? key[4 * j + q] : kKeyNegInf, cfg.t_eff);
+      if (full && (a.V & 3) == 0) {
+        *(float4*)(x.srow + e0) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+      } else {
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) if (e0 + q < c1) x.srow[e0 + q] = sv[q];
+      }
+    }
+  }
+  if (x.k == 0u) return;
+  if (first && ws.k1 <= 256u) {
+    // bound from this wave's first tile: the k1-th largest of the per-lane
+    // top-jt keys, rounded down to 16 bits (at least k1 of the wave's
+    // elements are at or above it)
+    const int jt = (int)((ws.k1 + 63u) >> 6);
+    uint32_t t4[4] = {0u, 0u, 0u, 0u};
+    if (jt == 1) {
+      #pragma unroll
+      for (int i = 0; i < E; ++i) t4[0] = max(t4[0], key[i]);
+    } else {
+      #pragma unroll
+      for (int i = 0; i < E; ++i) {
+        uint32_t v = key[i];
+        #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t hi = max(t4[r], v);
+          v = min(t4[r], v);
+          t4[r] = hi;
+        }
+      }
+    }
+    uint32_t prefix = 0u;
+    #pragma unroll 1
+    for (int bit = 31; bit >= 16; --bit) {
+      const uint32_t probe = prefix | (1u << bit);
+      uint32_t c = 0u;
+      #pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (r < jt) c += (uint32_t)__popcll(__ballot(t4[r] >= probe));
+      if (c >= ws.k1) prefix = probe;
+    }
+    if (prefix > 1u) {
+      ws.tau = (uint64_t)prefix << 32;
+      ws.tk = prefix;
+      if (x.lse) st.rest.move_ref(ws.tk);
+    }
+  }
+  // survivors of the tile (<= 64 * E entries: count <= lim before, so they
+  // fit); compact when the buffer passes its limit
+  uint64_t m[E];
+  uint64_t any = 0ull;
+  #pragma unroll
+  for (int i = 0; i < E; ++i) { m[i] = __ballot(key[i] >= ws.tk); any |= m[i]; }
+  if (x.lse) {
+    // the elements below the threshold leave the selection here
+    float add = 0.f;
+    #pragma unroll
+    for (int i = 0; i < E; ++i)
+      add += masked_exp2(key[i] < ws.tk && key[i] > kKeyNegInf, (cur[i] - st.rest.lref) * st.rest.a2);
+    st.rest.sum += add;
+  }
+  if (any != 0ull) {
+    #pragma unroll
+    for (int i = 0; i < E; ++i) {
+      if (key[i] >= ws.tk)
+        ws.buf[ws.count + lanes_below(m[i])] = cand_key(key[i], (uint32_t)(tb + ((i >> 2) * NTH + tid) * 4 + (i & 3)));
+      ws.count += (uint32_t)__popcll(m[i]);
+    }
+    if (ws.count > ws.lim) wave_compact(ws, st.rest, x.lse);
+  }
+}
+
+// Tiles t0 + d .. t0 + D - 1 of one pipeline round: process buffer d, then
+// load tile t0 + d + D into it (past the range the loads read zeros).
+template <int d, int NTH, int VEC, int D, int DT, bool MASK, bool OVF>
+__device__ __forceinline__ void lean_round(const LeanCtx& x, LeanState& st, const RowBuf& rb,
+                                           float (&tl)[D][VEC * 4], uint32_t (&tmw)[D][VEC], int t0) {
+  constexpr int TILE = NTH * VEC * 4;
+  const int tb = x.c0 + (t0 + d) * TILE;
+  lean_tile<NTH, VEC, MASK, OVF>(x, st, tl[d], tmw[d], tb, d == 0 && t0 == 0);
+  buf_load<NTH, VEC, DT, MASK>(rb, tb - x.c0 + D * TILE, tl[d], tmw[d]);
+  if constexpr (d + 1 < D) lean_round<d + 1, NTH, VEC, D, DT, MASK, OVF>(x, st, rb, tl, tmw, t0);
+}
+
+// Streams [c0, c1) of `row` in tiles of NTH * VEC * 4 logits with D tiles of
+// loads in flight per thread: tl[d] holds tile d on entry (the caller issues
+// those loads first).  Writes the range's record to stats[slot] and its
+// candidates to cand[slot * kFast ...].  Every thread returns after the
+// workgroup barrier.
+template <int NTH, int VEC, int D, int DT, bool MASK, bool OVF>
+__device__ __forceinline__ void scan_lean(const SampleArgs& a, const RowCfg& cfg, LeanLds<NTH / 64>& L,
+                                          const RowBuf& rb,
+                                          float (&tl)[D][VEC * 4], uint32_t (&tmw)[D][VEC],
+                                          const HistView& hv, int row, int64_t slot, int c0, int c1) {
+  constexpr int TILE = NTH * VEC * 4;
+  constexpr int NW = NTH / 64;
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const int wid = tid >> 6;
+  LeanCtx x;
+  x.a = &a; x.cfg = &cfg; x.hv = &hv;
+  x.srow = cfg.store_s ? a.ws_s + (int64_t)row * a.V : nullptr;
+  x.c0 = c0; x.c1 = c1; x.len = c1 - c0;
+  x.k = (uint32_t)cfg.k_sel;
+  x.ieee = cfg.cls == kGreedy && a.pv.greedy_rule == kGreedyIeee;
+  x.fin = cfg.cls == kTempOnly || (cfg.cls == kGreedy && a.pv.greedy_rule == kGreedyFiniteLane);
+  x.lse = a.need_lse != 0;
+  x.rep_once = (cfg.flags & HI_ROCM_FLAG_REP_ONCE) != 0u;
+  const uint32_t k = x.k;
+  const bool ieee = x.ieee, fin = x.fin;
+  const int len = x.len;
+  const int ntiles = (len + TILE - 1) / TILE;
+
+  LeanState st;
+  WaveSel& ws = st.ws;
+  ws.buf = L.wbuf[wid];
+  ws.hist = L.whist[wid];
+  ws.count = 0u;
+  ws.k1 = k + 1u;
+  ws.lim = min((uint32_t)kWaveMaxLim, ws.k1 + max(ws.k1, 192u));
+  ws.tau = 0ull;
+  ws.tk = 1u;
+  LseRest& rest = st.rest;
+  rest.sum = 0.f;
+  rest.lref = -__builtin_inff();
+  rest.a2 = 1.4426950408889634f / cfg.t_eff;
+  st.maxkey = 0u;
+  st.bv = -__builtin_inff(); st.fv = -__builtin_inff();
+  st.bi = 0xffffffffu; st.fi = 0xffffffffu;
+
+  // history tokens (without OVF the tiles skip them): gather each marked
+  // token's logit, apply the mask and the penalties exactly, and enter it
+  // like a streamed element; its key replaces its count in hv.cnts
+  float pbv = -__builtin_inff(), pfv = -__builtin_inff();
+  uint32_t pbi = 0xffffffffu, pfi = 0xffffffffu;
+  if (!OVF && hv.on) {
+    const uint32_t nd = hv.distinct;
+    #pragma unroll 1
+    for (uint32_t r0 = (uint32_t)wid * 64u; r0 < nd; r0 += NTH) {
+      const uint32_t r = r0 + lane;
+      const bool v = r < nd;
+      const uint32_t e = v ? hv.ids[r] : (uint32_t)c0;
+      const uint32_t off = e - (uint32_t)c0;
+      float l;
+      if (DT == HI_ROCM_DTYPE_BF16)
+        l = __uint_as_float((uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rb.logits, off * 2, 0, 0) << 16);
+      else
+        l = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb.logits, off * 4, 0, 0));
+      if (MASK) {
+        const uint32_t w = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb.mask, (off >> 5) * 4, 0, 0);
+        if (!((w >> (off & 31u)) & 1u)) l = -__builtin_inff();
+      }
+      l = apply_penalties(l, v ? hv.cnts[r] : 0u, cfg);
+      const uint32_t key = v ? lkey(l) : 0u;
+      if (v) hv.cnts[r] = key;
+      l = v ? l : -__builtin_inff();
+      st.maxkey = max(st.maxkey, key);
+      if (ieee && l > -__builtin_inff()) merge_ieee(pbv, pbi, l, e);
+      if (fin && finitef_(l)) merge_fin(pfv, pfi, l, e);
+      if (k > 0u) {
+        const uint64_t m = __ballot(key >= ws.tk);
+        if (key >= ws.tk) ws.buf[ws.count + lanes_below(m)] = cand_key(key, e);
+        ws.count += (uint32_t)__popcll(m);
+        if (ws.count > ws.lim) wave_compact(ws, rest, x.lse);
+      }
+    }
+  }
+
+  #pragma unroll 1
+  for (int t0 = 0; t0 < ntiles; t0 += D) lean_round<0, NTH, VEC, D, DT, MASK, OVF>(x, st, rb, tl, tmw, t0);
+
+  uint32_t maxkey = st.maxkey;
+  float bv = st.bv, fv = st.fv;
+  uint32_t bi = st.bi, fi = st.fi;
+  merge_ieee(bv, bi, pbv, pbi);
+  merge_fin(fv, fi, pfv, pfi);
+  if (k > 0u) wave_compact(ws, rest, x.lse);
+  {
+    WaveOut o;
+    o.count = ws.count; o.maxkey = maxkey; o.bv = bv; o.bi = bi; o.fv = fv; o.fi = fi;
+    o.rest = rest.sum; o.lref = rest.lref;
+    wave_results(L, wid, o, ieee, fin, x.lse);
+  }
+  __syncthreads();
+  if (!OVF && hv.on && x.srow) {
+    // the tiles stored -inf for the history tokens; store their s now
+    for (uint32_t r = (uint32_t)tid; r < hv.distinct; r += NTH) x.srow[hv.ids[r]] = key_to_s(hv.cnts[r], cfg.t_eff);
+  }
+  if (wid != 0) return;
+
+  // wave 0: merge the per-wave sets into the range's top k
+  ChunkStat bs;
+  stat_init(bs);
+  maxkey = 0u;
+  #pragma unroll
+  for (int w = 0; w < NW; ++w) maxkey = max(maxkey, L.wmax[w]);
+  bs.max_l = maxkey > kKeyNegInf ? okey_inv(maxkey) : -__builtin_inff();
+  bs.any_finite = maxkey > kKeyNegInf ? 1u : 0u;
+  if (ieee) {
+    #pragma unroll
+    for (int w = 0; w < NW; ++w) merge_ieee(bs.am_ieee_v, bs.am_ieee_i, L.wbv[w], L.wbi[w]);
+  }
+  if (fin) {
+    #pragma unroll
+    for (int w = 0; w < NW; ++w) merge_fin(bs.am_fin_v, bs.am_fin_i, L.wfv[w], L.wfi[w]);
+  }
+  if (k > 0u) {
+    Segs<NW> sg;
+    uint32_t total = 0u;
+    #pragma unroll
+    for (int w = 0; w < NW; ++w) { sg.p[w] = L.wbuf[w]; sg.n[w] = L.wcount[w]; total += sg.n[w]; }
+    sg.ns = NW;
+    uint64_t thr = 0ull;
+    if (total > k) thr = wave_select(sg, k, L.whist[0]);
+    // the dropped mass relative to the range max
+    const float lmax = bs.max_l;
+    float part = 0.f;
+    const bool LSE = x.lse;
+    if (LSE && finitef_(lmax)) {
+      #pragma unroll
+      for (int w = 0; w < NW; ++w)
+        if (L.wrest[w] > 0.f && finitef_(L.wlref[w]))
+          part += L.wrest[w] * exp2f((L.wlref[w] - lmax) * rest.a2);
+    }
+    float lane_part = 0.f;
+    uint64_t* cand = a.cand + slot * kFast;
+    uint32_t pos = 0u, unkept = 0u;
+    uint64_t minkept = ~0ull;
+    #pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t n = sg.n[w];
+      #pragma unroll 1
+      for (uint32_t b = 0; b < n; b += 64u) {
+        const uint32_t i = b + lane;
+        const bool valid = i < n;
+        const uint64_t x = valid ? sg.p[w][i] : 0ull;
+        const bool keep = valid && x >= thr;
+        const uint64_t m = __ballot(keep);
+        if (keep) {
+          cand[pos + lanes_below(m)] = x;
+          minkept = x < minkept ? x : minkept;
+        } else if (valid) {
+          const uint32_t kv = cand_skey(x);
+          unkept = max(unkept, kv);
+          if (LSE && finitef_(lmax) && kv > kKeyNegInf) lane_part += exp2f((okey_inv(kv) - lmax) * rest.a2);
+        }
+        pos += (uint32_t)__popcll(m);
+      }
+    }
+    #pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t t = shfl_xor_u64(minkept, o);
+      minkept = t < minkept ? t : minkept;
+      unkept = max(unkept, (uint32_t)__shfl_xor((int)unkept, o, 64));
+      if (LSE) lane_part += __shfl_xor(lane_part, o, 64);
+    }
+    bs.n_cand = pos;
+    bs.trunc = len > (int)k ? 1u : 0u;
+    bs.min_kept = minkept;
+    bs.unkept_key = unkept;
+    bs.lse_m = finitef_(lmax) ? lmax / cfg.t_eff : -__builtin_inff();
+    bs.lse_sum = LSE ? part + lane_part : 0.f;
+  }
+  if (lane == 0u) a.stats[slot] = bs;
+}
+
+// The general per-chunk pass (top-p, min-p, temperature-only and wide rows,
+// the finite-lane greedy rule, large logprob counts): block-level running
+// selection, scaled logits stored for the finish.
+template <int VEC, int TILES>
+__device__ __forceinline__ void scan_generic(const SampleArgs& a, const RowCfg& cfg, ScanLds& sh,
+                                             const float (&tile0)[VEC * 4],
+                                             const uint32_t* bitmap, const uint32_t* hkey,
+                                             const uint32_t* hcnt, bool pen, uint32_t h0, uint32_t h1,
+                                             int row, int chunk, int c0, int c1) {
+  constexpr int TILE = NT * VEC * 4;
+  constexpr int E = VEC * 4;
   const int tid = threadIdx.x;
   const int V = a.V;
-  const int c0 = chunk * CH;
-  const int c1 = min(c0 + CH, V);
   const int len = c1 - c0;
-  const RowCfg cfg = load_cfg(a.pv, row, V, a.n_lp, a.need_lse);
   const int64_t rbase = (int64_t)row * a.row_stride;
   const uint32_t* mrow = a.mask ? a.mask + (int64_t)row * a.mask_words : nullptr;
   float* srow = cfg.store_s ? a.ws_s + (int64_t)row * V : nullptr;
   const uint32_t k = (uint32_t)cfg.k_sel;
 
   float cur[E];
-  load_tile<VEC>(a, rbase, c0, c1, cur);
-
-  // history tokens of this chunk: bitmap + (id -> count) hash
-  bool pen = false;
-  uint32_t h0 = 0, h1 = 0;
-  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; pen = h1 > h0; }
-  if (tid == 0) { sh.count = 0u; sh.hovf = 0u; }
-  if (pen) {
-    for (int i = tid; i < CH / 32; i += NT) bitmap[i] = 0u;
-    for (int i = tid; i < kHashCap; i += NT) { hkey[i] = 0xffffffffu; hcnt[i] = 0u; }
-    __syncthreads();
-    for (uint32_t hb = h0; hb < h1; hb += NT * 8) {
-      uint32_t ids[8], cnts[8];
-      #pragma unroll
-      for (int r = 0; r < 8; ++r) {  // independent loads first
-        const uint32_t h = hb + r * NT + tid;
-        ids[r] = h < h1 ? a.hids[h] : 0xffffffffu;
-        cnts[r] = h < h1 ? a.hcnt[h] : 0u;
-      }
-      #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const uint32_t id = ids[r];
-        if (id < (uint32_t)c0 || id >= (uint32_t)c1) continue;
-        const uint32_t li = id - (uint32_t)c0;
-        atomicOr(&bitmap[li >> 5], 1u << (li & 31u));
-        uint32_t slot = (id * 2654435761u) & (kHashCap - 1);
-        bool done = false;
-        for (int probe = 0; probe < kHashCap && !done; ++probe) {
-          const uint32_t prev = atomicCAS(&hkey[slot], 0xffffffffu, id);
-          if (prev == 0xffffffffu || prev == id) {
-            atomicAdd(&hcnt[slot], cnts[r]);
-            done = true;
-          } else {
-            slot = (slot + 1) & (kHashCap - 1);
-          }
-        }
-        if (!done) sh.hovf = 1u;
-      }
-    }
-  }
+  #pragma unroll
+  for (int i = 0; i < E; ++i) cur[i] = tile0[i];
+  if (tid == 0) sh.count = 0u;
   __syncthreads();
 
   SelState ss;
@@ -1541,6 +2295,156 @@ __global__ void __launch_bounds__(NT) scan_kernel(SampleArgs a) {
   if (tid == 0) a.stats[(int64_t)row * a.n_chunks + chunk] = bs;
 }
 
+// History tokens of the chunk [c0, c1) for the general pass: an LDS bitmap
+// of the tokens present and an (id -> summed count) hash with linear
+// probing.  All threads call it.
+template <int CH>
+__device__ __forceinline__ void stage_history_hash(const SampleArgs& a, uint32_t h0, uint32_t h1, int c0,
+                                                   int c1, uint32_t* bitmap, uint32_t* hkey, uint32_t* hcnt) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < CH / 32; i += NT) bitmap[i] = 0u;
+  for (int i = tid; i < kHashCap; i += NT) { hkey[i] = 0xffffffffu; hcnt[i] = 0u; }
+  __syncthreads();
+  for (uint32_t hb = h0; hb < h1; hb += NT * 8) {
+    uint32_t ids[8], cnts[8];
+    #pragma unroll
+    for (int r = 0; r < 8; ++r) {  // independent loads first
+      const uint32_t h = hb + r * NT + tid;
+      ids[r] = h < h1 ? a.hids[h] : 0xffffffffu;
+      cnts[r] = h < h1 ? a.hcnt[h] : 0u;
+    }
+    #pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const uint32_t id = ids[r];
+      if (id < (uint32_t)c0 || id >= (uint32_t)c1) continue;
+      const uint32_t li = id - (uint32_t)c0;
+      atomicOr(&bitmap[li >> 5], 1u << (li & 31u));
+      // a token that finds no free slot is counted from the global list
+      // when it is looked up (hash_count reports it as not found)
+      uint32_t slot = (id * 2654435761u) & (kHashCap - 1);
+      for (int probe = 0; probe < kHashCap; ++probe) {
+        const uint32_t prev = atomicCAS(&hkey[slot], 0xffffffffu, id);
+        if (prev == 0xffffffffu || prev == id) {
+          atomicAdd(&hcnt[slot], cnts[r]);
+          break;
+        }
+        slot = (slot + 1) & (kHashCap - 1);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// LDS of the scan kernels.
+constexpr int kRowThreads = 512;  // row kernel: 8 waves stream, the first 4 finish
+size_t lean_chunk_lds_bytes(int chunk, bool hist) {
+  return ((sizeof(LeanLds<NT / 64>) + 15) & ~(size_t)15) + (hist ? hist_lds_bytes(chunk, kChunkHistCap) : 0);
+}
+size_t generic_chunk_lds_bytes(int chunk, bool hist) {
+  return ((sizeof(ScanLds) + 15) & ~(size_t)15) +
+         (hist ? (size_t)chunk / 8 + 2 * kHashCap * sizeof(uint32_t) : 0);
+}
+constexpr size_t kRowUnionBytes =
+    ((sizeof(FinLds) > sizeof(LeanLds<kRowThreads / 64>) ? sizeof(FinLds) : sizeof(LeanLds<kRowThreads / 64>)) + 15) &
+    ~(size_t)15;
+size_t row_lds_bytes(int V, bool hist) {
+  return kRowUnionBytes + (hist ? hist_lds_bytes(V, kRowHistCap) : 0);
+}
+constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
+
+template <int NTH, int VEC, int D, int DT, bool MASK>
+__device__ __forceinline__ void scan_lean_dispatch(const SampleArgs& a, const RowCfg& cfg, LeanLds<NTH / 64>& L,
+                                                   const RowBuf& rb, float (&tl)[D][VEC * 4],
+                                                   uint32_t (&tmw)[D][VEC], const HistView& hv, int row,
+                                                   int64_t slot, int c0, int c1) {
+  if (hv.on && hv.ovf) scan_lean<NTH, VEC, D, DT, MASK, true>(a, cfg, L, rb, tl, tmw, hv, row, slot, c0, c1);
+  else scan_lean<NTH, VEC, D, DT, MASK, false>(a, cfg, L, rb, tl, tmw, hv, row, slot, c0, c1);
+}
+
+// One workgroup per (chunk, row): the lean pass over a chunk, finished by
+// finish_kernel.  Used when a row's history table does not fit the row
+// kernel's LDS.
+template <int VEC, int TILES, int DT, bool MASK>
+__global__ void __launch_bounds__(NT) scan_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  constexpr int CH = NT * VEC * 4 * TILES;
+  static_assert(CH <= 65536, "chunk");
+  const int row = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int c0 = chunk * CH;
+  const int c1 = min(c0 + CH, a.V);
+  // every load of the chunk is issued first, so that the parameter and
+  // history reads below overlap them
+  const RowBuf rb = row_buf<DT, MASK>(a, row, c0, c1);
+  float tl[TILES][VEC * 4];
+  uint32_t tmw[TILES][VEC];
+  #pragma unroll
+  for (int t = 0; t < TILES; ++t) buf_load<NT, VEC, DT, MASK>(rb, t * NT * VEC * 4, tl[t], tmw[t]);
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  HistView hv;
+  hv.on = false;
+  hv.ovf = false;
+  if (a.hoff)
+    hv = stage_history_rank<NT>(a, row, c0, c1 - c0, kChunkHistCap,
+                                reinterpret_cast<uint32_t*>(lds_raw + ((sizeof(LeanLds<NT / 64>) + 15) & ~(size_t)15)));
+  scan_lean_dispatch<NT, VEC, TILES, DT, MASK>(a, cfg, *reinterpret_cast<LeanLds<NT / 64>*>(lds_raw), rb, tl, tmw,
+                                               hv, row, (int64_t)row * a.n_chunks + chunk, c0, c1);
+}
+
+// One workgroup per row: kRowThreads threads stream the whole row with D
+// tiles of loads in flight per thread; then the waves past the first four
+// end (a barrier waits only for the waves still running) and the first four
+// finish the row in place (the row is one chunk for the finish code).
+template <int VEC, int D, int DT, bool MASK>
+__global__ void __launch_bounds__(kRowThreads) row_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  constexpr int NTH = kRowThreads;
+  constexpr int TILE = NTH * VEC * 4;
+  const int row = blockIdx.x;
+  const int V = a.V;
+  const RowBuf rb = row_buf<DT, MASK>(a, row, 0, V);
+  float tl[D][VEC * 4];
+  uint32_t tmw[D][VEC];
+  #pragma unroll
+  for (int t = 0; t < D; ++t) buf_load<NTH, VEC, DT, MASK>(rb, t * TILE, tl[t], tmw[t]);
+  const RowCfg cfg = load_cfg(a.pv, row, V, a.n_lp, a.need_lse);
+  HistView hv;
+  hv.on = false;
+  hv.ovf = false;
+  if (a.hoff)
+    hv = stage_history_rank<NTH>(a, row, 0, V, kRowHistCap, reinterpret_cast<uint32_t*>(lds_raw + kRowUnionBytes));
+  scan_lean_dispatch<NTH, VEC, D, DT, MASK>(a, cfg, *reinterpret_cast<LeanLds<NTH / 64>*>(lds_raw), rb, tl, tmw,
+                                            hv, row, row, 0, V);
+  if (threadIdx.x >= NT) return;
+  __syncthreads();  // the row's record and candidates are visible to the workgroup
+  finish_row(*reinterpret_cast<FinLds*>(lds_raw), a, row, cfg);
+}
+
+// The general pass with a block-level running selection of up to kFast
+// candidates per chunk: used when more than kLeanK logprobs are requested.
+template <int VEC, int TILES>
+__global__ void __launch_bounds__(NT) scan_generic_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  constexpr int CH = NT * VEC * 4 * TILES;
+  static_assert(CH <= 65536, "local indices are 16-bit");
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds_raw + ((sizeof(ScanLds) + 15) & ~(size_t)15));
+  uint32_t* hkey = bitmap + CH / 32;
+  uint32_t* hcnt = hkey + kHashCap;
+  const int row = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int c0 = chunk * CH;
+  const int c1 = min(c0 + CH, a.V);
+  float tile0[VEC * 4];
+  load_tile<VEC>(a, (int64_t)row * a.row_stride, c0, c1, tile0);
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  bool pen = false;
+  uint32_t h0 = 0, h1 = 0;
+  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; pen = h1 > h0; }
+  if (pen) stage_history_hash<CH>(a, h0, h1, c0, c1, bitmap, hkey, hcnt);
+  scan_generic<VEC, TILES>(a, cfg, *reinterpret_cast<ScanLds*>(lds_raw), tile0, bitmap, hkey, hcnt,
+                           pen, h0, h1, row, chunk, c0, c1);
+}
+
 // One workgroup per row: merge the row's chunk results and draw.  A separate
 // launch: the kernel boundary makes every chunk's results visible to the
 // finishing workgroup on any XCD without a device-scope fence per chunk.
@@ -1676,27 +2580,80 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
 // --------------------------------------------------------------------------
 // launch wrappers (called from the host API)
 
-int choose_chunk(int B, int V) {
-  // fewer, larger chunks when the batch alone fills the GPU; otherwise
-  // smaller chunks so that a small batch still spreads over many CUs
+bool row_mode(int V, int n_lp, int vec_ok, bool hist) {
+  return n_lp <= kLeanK && vec_ok && row_lds_bytes(V, hist) <= kMaxLds;
+}
+
+int choose_chunk(int B, int V, int n_lp, int vec_ok, bool hist) {
+  // one workgroup per row when the row fits the row kernel's LDS;
+  // otherwise chunks: fewer, larger ones when the batch alone fills the GPU
+  if (row_mode(V, n_lp, vec_ok, hist)) return V;
   const long wg_large = (long)B * ((V + kChunk - 1) / kChunk);
   return wg_large >= 512 ? kChunk : kChunkSmall;
 }
 
-hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
+// Dynamic LDS above 64 KiB needs the kernel's attribute raised once.
+template <typename K>
+hipError_t allow_lds(K kernel, size_t bytes) {
+  if (bytes <= 65536) return hipSuccess;
+  return hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+hipError_t launch_chunked(const SampleArgs& a, hipStream_t stream) {
   const bool hist = a.hoff != nullptr;
+  const bool large = a.chunk == kChunk;
   dim3 grid(a.n_chunks, a.B);
-  if (a.chunk == kChunk) {
-    hipLaunchKernelGGL((scan_kernel<kVecLarge, kTilesLarge>), grid, dim3(NT),
-                       scan_lds_bytes(kChunk, hist), stream, a);
+  if (a.n_lp > kLeanK || !a.vec_ok) {
+    if (large)
+      hipLaunchKernelGGL((scan_generic_kernel<kVecLarge, kTilesLarge>), grid, dim3(NT),
+                         generic_chunk_lds_bytes(kChunk, hist), stream, a);
+    else
+      hipLaunchKernelGGL((scan_generic_kernel<kVecSmall, 1>), grid, dim3(NT),
+                         generic_chunk_lds_bytes(kChunkSmall, hist), stream, a);
   } else {
-    hipLaunchKernelGGL((scan_kernel<kVecSmall, 1>), grid, dim3(NT),
-                       scan_lds_bytes(kChunkSmall, hist), stream, a);
+    constexpr int TL = kChunk / (NT * kLeanVec * 4);
+    constexpr int TS = kChunkSmall / (NT * kLeanVec * 4);
+    static_assert(TL * NT * kLeanVec * 4 == kChunk && TS * NT * kLeanVec * 4 == kChunkSmall, "chunk sizes");
+    const size_t lds = lean_chunk_lds_bytes(large ? kChunk : kChunkSmall, hist);
+#define HI_ROCM_LAUNCH_LEAN(DT, M)                                                                   \
+  do {                                                                                              \
+    if (large) hipLaunchKernelGGL((scan_kernel<kLeanVec, TL, DT, M>), grid, dim3(NT), lds, stream, a); \
+    else hipLaunchKernelGGL((scan_kernel<kLeanVec, TS, DT, M>), grid, dim3(NT), lds, stream, a);       \
+  } while (0)
+    if (a.dtype == HI_ROCM_DTYPE_BF16) {
+      if (a.mask) HI_ROCM_LAUNCH_LEAN(HI_ROCM_DTYPE_BF16, true);
+      else HI_ROCM_LAUNCH_LEAN(HI_ROCM_DTYPE_BF16, false);
+    } else {
+      if (a.mask) HI_ROCM_LAUNCH_LEAN(HI_ROCM_DTYPE_F32, true);
+      else HI_ROCM_LAUNCH_LEAN(HI_ROCM_DTYPE_F32, false);
+    }
+#undef HI_ROCM_LAUNCH_LEAN
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(finish_kernel, dim3(a.B), dim3(NT), 0, stream, a);
   return hipGetLastError();
+}
+
+constexpr int kRowDepth = 4;  // tiles of loads in flight per thread
+
+template <int DT, bool MASK>
+hipError_t launch_row_t(const SampleArgs& a, hipStream_t stream) {
+  const size_t lds = row_lds_bytes(a.V, a.hoff != nullptr);
+  auto kern = row_kernel<kLeanVec, kRowDepth, DT, MASK>;
+  hipError_t e = allow_lds(kern, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(a.B), dim3(kRowThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
+  if (a.n_chunks == 1 && a.chunk == a.V && row_mode(a.V, a.n_lp, a.vec_ok, a.hoff != nullptr)) {
+    if (a.dtype == HI_ROCM_DTYPE_BF16)
+      return a.mask ? launch_row_t<HI_ROCM_DTYPE_BF16, true>(a, stream) : launch_row_t<HI_ROCM_DTYPE_BF16, false>(a, stream);
+    return a.mask ? launch_row_t<HI_ROCM_DTYPE_F32, true>(a, stream) : launch_row_t<HI_ROCM_DTYPE_F32, false>(a, stream);
+  }
+  return launch_chunked(a, stream);
 }
 
 hipError_t launch_argmax(const float* logits, uint32_t* out, int B, int64_t row_stride,

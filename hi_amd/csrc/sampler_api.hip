@@ -74,9 +74,10 @@ void carve(hi_rocm::SampleArgs& a, void* ws, const hi_rocm::WorkspaceLayout& L) 
   a.n_chunks = (a.V + a.chunk - 1) / a.chunk;
 }
 
+// Rows that start on 16 bytes take the streaming pass's 16-byte loads.
 int vec_aligned(const void* p, int dtype, int64_t row_stride) {
-  const uintptr_t align = dtype == HI_ROCM_DTYPE_BF16 ? 8 : 16;
-  return ((uintptr_t)p % align == 0) && (row_stride % 4 == 0);
+  const int64_t esize = dtype == HI_ROCM_DTYPE_BF16 ? 2 : 4;
+  return ((uintptr_t)p % 16 == 0) && ((row_stride * esize) % 16 == 0);
 }
 
 hi_rocm::SampleArgs base_args(const void* logits, int dtype, int B, int V, int64_t row_stride) {

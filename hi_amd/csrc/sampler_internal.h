@@ -62,17 +62,17 @@ struct ChunkStat {
                                   // the debug kernels keep the max of s here
   float am_ieee_v;                // argmax, IEEE '>' (kernels.cu:7153-7186)
   uint32_t am_ieee_i;
-  int32_t am_tot_k;               // argmax by total_cmp (gpu.rs:739-751)
-  uint32_t am_tot_i;
   float am_fin_v;                 // finite argmax, lane rule (kernels.cu:7775-7801)
   uint32_t am_fin_i;
   uint32_t any_finite;
-  float lse_m, lse_sum;           // chunk max, sum of exp(s - max) over elements not kept
+  float lse_m;                    // scaled-logit reference of the masses below
+  float lse_sum;                  // sum of exp(s - lse_m) over the logits not written as candidates
   uint32_t n_cand;                // candidates written
-  uint32_t trunc;                 // the chunk had more than k_sel elements
-  uint32_t unkept_key;            // largest scaled-logit key not kept
+  uint32_t trunc;                 // the chunk has logits that are not candidates
+  uint32_t unkept_key;            // bound on the keys of those logits
   uint32_t pad0;
-  uint64_t min_kept;              // smallest kept candidate key
+  uint64_t min_kept;              // smallest candidate key
+  uint64_t pad1;
 };
 static_assert(sizeof(ChunkStat) == 64, "ChunkStat layout");
 
@@ -125,9 +125,12 @@ inline WorkspaceLayout workspace_layout(int max_batch, int V) {
   WorkspaceLayout L;
   L.slots = 0;
   for (int b = 1; b <= max_batch; ++b) {
-    const int ch = choose_chunk(b, V, kLeanK + 1, 1, true);  // the chunked layout needs the most records
-    const int64_t s = (int64_t)b * ((V + ch - 1) / ch);
-    if (s > L.slots) L.slots = s;
+    // records of either pass (streaming select or general scan) at b rows
+    for (int n_lp : {0, kLeanK + 1}) {
+      const int ch = choose_chunk(b, V, n_lp, 1, true);
+      const int64_t s = (int64_t)b * ((V + ch - 1) / ch);
+      if (s > L.slots) L.slots = s;
+    }
   }
   L.list_stride = next_pow2_i64(V);
   size_t off = 0;

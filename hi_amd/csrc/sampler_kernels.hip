@@ -223,6 +223,33 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Wave-wide reductions (every lane gets the result).
+__device__ __forceinline__ float wave_max_f32(float v) {
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { const uint64_t t = shfl_xor_u64(v, o); v = t > v ? t : v; }
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { const uint64_t t = shfl_xor_u64(v, o); v = t < v ? t : v; }
+  return v;
+}
+
 template <int N>
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
   for (int o = 32; o > 0; o >>= 1) {
@@ -274,11 +301,6 @@ __device__ __forceinline__ void stat_merge(ChunkStat& a, const ChunkStat& b) {
        (b.am_ieee_v == a.am_ieee_v && b.am_ieee_i < a.am_ieee_i))) {
     a.am_ieee_v = b.am_ieee_v; a.am_ieee_i = b.am_ieee_i;
   }
-  if (b.am_tot_i != 0xffffffffu &&
-      (a.am_tot_i == 0xffffffffu || b.am_tot_k > a.am_tot_k ||
-       (b.am_tot_k == a.am_tot_k && b.am_tot_i < a.am_tot_i))) {
-    a.am_tot_k = b.am_tot_k; a.am_tot_i = b.am_tot_i;
-  }
   if (b.am_fin_i != 0xffffffffu) {
     bool take = a.am_fin_i == 0xffffffffu || b.am_fin_v > a.am_fin_v;
     if (!take && b.am_fin_v == a.am_fin_v) {
@@ -293,12 +315,12 @@ __device__ __forceinline__ void stat_merge(ChunkStat& a, const ChunkStat& b) {
 __device__ __forceinline__ void stat_init(ChunkStat& s) {
   s.max_l = -__builtin_inff();
   s.am_ieee_v = -__builtin_inff(); s.am_ieee_i = 0xffffffffu;
-  s.am_tot_k = 0; s.am_tot_i = 0xffffffffu;
   s.am_fin_v = -__builtin_inff(); s.am_fin_i = 0xffffffffu;
   s.any_finite = 0u;
   s.lse_m = -__builtin_inff(); s.lse_sum = 0.f;
   s.n_cand = 0u; s.trunc = 0u; s.unkept_key = 0u; s.pad0 = 0u;
   s.min_kept = 0ull;
+  s.pad1 = 0ull;
 }
 
 __device__ __forceinline__ ChunkStat stat_shfl_xor(const ChunkStat& s, int o) {
@@ -306,7 +328,6 @@ __device__ __forceinline__ ChunkStat stat_shfl_xor(const ChunkStat& s, int o) {
   stat_init(r);
   r.max_l = __shfl_xor(s.max_l, o, 64);
   r.am_ieee_v = __shfl_xor(s.am_ieee_v, o, 64); r.am_ieee_i = __shfl_xor(s.am_ieee_i, o, 64);
-  r.am_tot_k = __shfl_xor(s.am_tot_k, o, 64); r.am_tot_i = __shfl_xor(s.am_tot_i, o, 64);
   r.am_fin_v = __shfl_xor(s.am_fin_v, o, 64); r.am_fin_i = __shfl_xor(s.am_fin_i, o, 64);
   r.any_finite = __shfl_xor(s.any_finite, o, 64);
   return r;
@@ -421,6 +442,7 @@ struct ScanLds {
   uint32_t redu[NT / 64];
   uint64_t red64[NT / 64];
   float redf[NT / 64];
+  double redd[NT / 64];
   uint32_t sel[4];
   uint32_t bound, count, hovf;
   // when the batch has histories: bitmap[chunk / 32], hash keys[kHashCap],
@@ -440,6 +462,7 @@ struct FinLds {
   uint32_t redu[NT / 64];
   double redd[NT / 64];
   uint64_t red64[NT / 64];
+  uint64_t red64b[NT / 64];
   uint32_t sel[4];
   uint32_t counter, n_ext, token, flag;
   float fval0, fval1;
@@ -451,21 +474,19 @@ constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
 // Finish phase (one workgroup per row)
 // ==========================================================================
 
-// Candidates of `row` (written by the chunks): visit every (chunk, slot).
-// Chunk c kept min(k_sel, its length) candidates, so the slots are known
-// without reading the chunk records; one flat parallel loop.
+// Candidates of `row` (written by the chunks): chunk c wrote
+// stats[c].n_cand of them at the start of its kFast slots.  f(x, pos) gets
+// each candidate and its position in the chunk-major concatenation.
 template <typename F>
-__device__ __forceinline__ void for_each_candidate(const SampleArgs& a, int row, int k_sel, F f) {
+__device__ __forceinline__ void for_each_candidate(const SampleArgs& a, int row, F f) {
   const int nch = a.n_chunks;
+  const ChunkStat* stats = a.stats + (int64_t)row * nch;
   const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
-  const int last_len = a.V - (nch - 1) * a.chunk;
-  const int n_full = min(k_sel, a.chunk);
-  const int n_last = min(k_sel, last_len);
-  const int span = (nch - 1) * n_full + n_last;
-  for (int j = threadIdx.x; j < span; j += NT) {
-    const int c = n_full > 0 ? j / n_full : 0;
-    const int s = j - c * n_full;
-    f(cand[(int64_t)c * kFast + s]);
+  int off = 0;
+  for (int c = 0; c < nch; ++c) {
+    const int n = (int)stats[c].n_cand;
+    for (int s = threadIdx.x; s < n; s += NT) f(cand[(int64_t)c * kFast + s], off + s);
+    off += n;
   }
 }
 
@@ -507,28 +528,26 @@ __device__ __forceinline__ void sort_ranked(FinLds& fs, int n) {
   }
 }
 
-// Number of candidates the chunks of `row` wrote: chunk c keeps
-// min(k_sel, its length), so it is known without reading the records.
-__device__ __forceinline__ int candidate_count(const SampleArgs& a, int k_sel) {
-  const int last_len = a.V - (a.n_chunks - 1) * a.chunk;
-  return (a.n_chunks - 1) * min(k_sel, a.chunk) + min(k_sel, last_len);
+// Number of candidates the chunks of `row` wrote.
+__device__ __forceinline__ int candidate_count(const SampleArgs& a, int row) {
+  const ChunkStat* stats = a.stats + (int64_t)row * a.n_chunks;
+  int n = 0;
+  for (int c = 0; c < a.n_chunks; ++c) n += (int)stats[c].n_cand;
+  return n;
 }
 
 // The exact first `kk` entries of the reference rank order (weight desc,
 // index asc) of `row`.  On return fs.buf[0..kk) holds rank keys in order and
 // fs.pay[0..kk) the scaled-logit keys; returns kk.  M is the row max of s.
-// When lse_part is not null, it receives this thread's share of
-// sum(exp(s - M)) over every candidate (double).
 __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg,
-                               int kk_req, float M, double* lse_part) {
+                               int kk_req, float M) {
   const int tid = threadIdx.x;
   const int nch = a.n_chunks;
   const ChunkStat* stats = a.stats + (int64_t)row * nch;
-  const int n_total = candidate_count(a, cfg.k_sel);
+  const int n_total = candidate_count(a, row);
   const int kk = min(kk_req, n_total);
   if (kk <= 0) return 0;
   auto s_of = [&](uint64_t x) { return key_to_s(cand_skey(x), cfg.t_eff); };
-  double part = 0.0;
   // 1. candidates into LDS: all of them when they fit, else those at or above
   //    t0, the largest chunk cut (the kk-th composite is at least every
   //    truncated chunk's smallest kept composite)
@@ -537,22 +556,16 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
   int n_u;
   bool in_lds = true;
   if (n_total <= kGather) {
-    int j = 0;
-    for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
-      fs.cbig[tid + j * NT] = x;
-      ++j;
-      if (lse_part) part += exp((double)s_of(x) - (double)M);
-    });
+    for_each_candidate(a, row, [&](uint64_t x, int pos) { fs.cbig[pos] = x; });
     n_u = n_total;
   } else {
     for (int c = tid; c < nch; c += NT)
       if (stats[c].trunc && stats[c].min_kept > t0) t0 = stats[c].min_kept;
     t0 = block_max_u64<NT>(t0, fs.red64);
     uint32_t nu = 0;
-    for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+    for_each_candidate(a, row, [&](uint64_t x, int) {
       nu += x >= t0;
       if (x < t0 && x > below_max) below_max = x;
-      if (lse_part) part += exp((double)s_of(x) - (double)M);
     });
     n_u = (int)block_sum_u32<NT>(nu, fs.redu);
     below_max = block_max_u64<NT>(below_max, fs.red64);
@@ -560,13 +573,12 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
     if (in_lds) {
       if (tid == 0) fs.counter = 0u;
       __syncthreads();
-      for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+      for_each_candidate(a, row, [&](uint64_t x, int) {
         if (x >= t0) fs.cbig[atomicAdd(&fs.counter, 1u)] = x;
       });
     }
   }
   __syncthreads();
-  if (lse_part) *lse_part = part;
   // 2. the kk largest
   uint64_t thr = 0;
   if (in_lds) {
@@ -587,12 +599,12 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
   } else {
     // rare: more than kGather candidates above t0; select over global memory
     thr = radix_select_top(fs.hist, fs.sel, (uint32_t)kk, 64, [&](auto cb) {
-      for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) { if (x >= t0) cb(x); });
+      for_each_candidate(a, row, [&](uint64_t x, int) { if (x >= t0) cb(x); });
     });
     if (tid == 0) fs.counter = 0u;
     __syncthreads();
     uint64_t umax = 0;
-    for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+    for_each_candidate(a, row, [&](uint64_t x, int) {
       if (x >= thr && x >= t0) {
         const uint32_t p = atomicAdd(&fs.counter, 1u);
         if (p < (uint32_t)kBuf) fs.buf[p] = x;
@@ -639,7 +651,7 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
         }
       }
       if (!in_lds || t0 != 0) {
-        for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
+        for_each_candidate(a, row, [&](uint64_t x, int) {
           if (x >= thr || (in_lds && x >= t0)) return;  // selected, or seen in LDS
           const float sx = s_of(x);
           const float w = exact_expf(sx - M);
@@ -1024,8 +1036,6 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
   const bool eos = a.mask && !rs.any_finite;
   uint32_t token;
   int ranked_k = 0;  // entries of fs.buf in rank order
-  double lse_part = 0.0;  // this thread's share of sum(exp(s - M)) over the candidates
-  bool have_part = false;
   if (eos) {
     token = cfg.eos;
   } else if (cfg.cls == kGreedy) {
@@ -1033,8 +1043,7 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
   } else if (!finitef_(M)) {
     token = cfg.cls == kTempOnly ? am_fin : row_argmax_total(fs, a, row, cfg);
   } else if (cfg.cls == kTopK && !cfg.wide) {
-    ranked_k = rank_candidates(fs, a, row, cfg, cfg.k_sel, M, a.need_lse ? &lse_part : nullptr);
-    have_part = a.need_lse != 0;
+    ranked_k = rank_candidates(fs, a, row, cfg, cfg.k_sel, M);
     token = draw_topk(fs, cfg, cfg.k_eff, u);
     if (token == 0xffffffffu) token = row_argmax_total(fs, a, row, cfg);
   } else if (cfg.cls == kTempOnly) {
@@ -1057,18 +1066,13 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
     if (tid == 0 && a.out_token_lp) a.out_token_lp[row] = eos ? 0.f : -__builtin_inff();
     return;
   }
-  if (N > 0 && ranked_k < N) {
-    ranked_k = rank_candidates(fs, a, row, cfg, N, M, have_part ? nullptr : &lse_part);
-    have_part = true;
-  }
-  // log of the normaliser relative to M: the kept candidates of every chunk
-  // in double, the rest from each chunk's sum over the elements it dropped
-  if (!have_part) {
-    for_each_candidate(a, row, cfg.k_sel, [&](uint64_t x) {
-      lse_part += exp((double)key_to_s(cand_skey(x), cfg.t_eff) - (double)M);
-    });
-  }
-  double part = lse_part;
+  if (N > 0 && ranked_k < N) ranked_k = rank_candidates(fs, a, row, cfg, N, M);
+  // log of the normaliser relative to M: the candidates of every chunk in
+  // double, the other logits from each chunk's mass
+  double part = 0.0;
+  for_each_candidate(a, row, [&](uint64_t x, int) {
+    if (cand_skey(x) > kKeyNegInf) part += exp((double)key_to_s(cand_skey(x), cfg.t_eff) - (double)M);
+  });
   for (int c = tid; c < a.n_chunks; c += NT) {
     const ChunkStat cs = a.stats[(int64_t)row * a.n_chunks + c];
     if (cs.lse_sum > 0.f) part += (double)cs.lse_sum * exp((double)cs.lse_m - (double)M);
@@ -1100,6 +1104,352 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
     if (tid == 0)
       a.out_token_lp[row] = token < (uint32_t)V ? (float)(((double)s - (double)M) - log_sum) : -__builtin_inff();
   }
+}
+
+// ==========================================================================
+// Lean finish (greedy rows; top-k rows with k_eff <= kLeanK)
+// ==========================================================================
+//
+// The common case of the finish without its general machinery: every wave
+// merges the chunk records on its own (no barrier), the candidates are
+// gathered into LDS, a radix select that starts below their common high
+// bits keeps the top k_sel, each thread ranks one of them by counting, and
+// every wave runs the reference's sequential f32 folds from registers
+// (readlane), so the draw is computed without a barrier either.  A row
+// whose k_sel-th weight could tie with a logit outside the candidates, or
+// whose fold hits the reference's argmax fallback, returns false and takes
+// finish_row.
+
+constexpr int kFinPer = kGather / NT;  // candidates each thread gathers
+
+// Threshold T such that exactly k of items[0, n) (unique keys, LDS) are
+// >= T, 1 <= k <= n: an 8-bit MSD radix select over the workgroup that
+// starts below the items' common high bits.  All threads call it.
+__device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int n, uint32_t k, uint32_t* hist,
+                                                      uint32_t* sel, uint64_t* reda, uint64_t* redb) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  uint64_t mn = ~0ull, mx = 0ull;
+  for (int i = tid; i < n; i += NT) {
+    const uint64_t x = items[i];
+    mn = x < mn ? x : mn;
+    mx = x > mx ? x : mx;
+  }
+  mn = wave_min_u64(mn);
+  mx = wave_max_u64(mx);
+  if (lane == 0) { reda[wid] = mn; redb[wid] = mx; }
+  __syncthreads();
+  mn = reda[0];
+  mx = redb[0];
+  #pragma unroll
+  for (int w = 1; w < NT / 64; ++w) { mn = reda[w] < mn ? reda[w] : mn; mx = redb[w] > mx ? redb[w] : mx; }
+  if (mn == mx) return mx;
+  int hi = 64 - __clzll(mn ^ mx);
+  uint64_t prefix = hi >= 64 ? 0ull : (mx >> hi) << hi;
+  uint32_t remaining = k;
+  #pragma unroll 1
+  while (hi > 0) {
+    const int db = hi >= 8 ? 8 : hi;
+    const int lo = hi - db;
+    const uint64_t hp = hi >= 64 ? 0ull : (prefix >> hi);
+    for (int b = tid; b < 256; b += NT) hist[b] = 0u;
+    __syncthreads();
+    for (int i = tid; i < n; i += NT) {
+      const uint64_t x = items[i];
+      if (hi >= 64 || (x >> hi) == hp) atomicAdd(&hist[(uint32_t)(x >> lo) & ((1u << db) - 1u)], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // lane l owns bins 255-4l .. 252-4l (descending)
+      uint32_t loc[4], lsum = 0;
+      #pragma unroll
+      for (int q = 0; q < 4; ++q) { loc[q] = hist[255 - 4 * tid - q]; lsum += loc[q]; }
+      uint32_t inc = lsum;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(inc, o, 64);
+        if (tid >= o) inc += t;
+      }
+      const uint32_t above = inc - lsum;
+      if (above < remaining && remaining <= above + lsum) {
+        uint32_t acc = above;
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (remaining <= acc + loc[q] && acc < remaining) {
+            sel[0] = 255u - 4u * tid - q; sel[1] = acc; sel[2] = loc[q];
+          }
+          acc += loc[q];
+        }
+      }
+    }
+    __syncthreads();
+    prefix |= (uint64_t)sel[0] << lo;
+    remaining -= sel[1];
+    const bool done = sel[2] == remaining;
+    hi = lo;
+    if (done) break;
+  }
+  return prefix;
+}
+
+constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
+
+__device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg) {
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const bool want_lp = a.n_lp > 0 || a.out_token_lp != nullptr;
+  if (cfg.cls == kGreedy) {
+    if (want_lp) return false;
+  } else if (cfg.cls != kTopK || cfg.wide) {
+    return false;
+  }
+  const int nch = a.n_chunks;
+  if (nch > kLeanChunks) return false;
+  const ChunkStat* stats = a.stats + (int64_t)row * nch;
+  const int k_sel = cfg.k_sel;
+
+  // 1. the chunk records, merged by every wave on its own; candidate counts
+  //    and their chunk-major offsets
+  constexpr int CQ = kLeanChunks / 64;
+  float mx = -__builtin_inff();
+  uint32_t anyf = 0u;
+  float iv = -__builtin_inff(), fv = -__builtin_inff();
+  uint32_t ii = 0xffffffffu, fi = 0xffffffffu;
+  uint32_t cnt[CQ];
+  #pragma unroll
+  for (int q = 0; q < CQ; ++q) {
+    const int c = q * 64 + (int)lane;
+    cnt[q] = 0u;
+    if (c >= nch) continue;
+    const ChunkStat& cs = stats[c];
+    cnt[q] = cs.n_cand;
+    mx = fmaxf(mx, cs.max_l);
+    anyf |= cs.any_finite;
+    if (cs.am_ieee_i != 0xffffffffu &&
+        (ii == 0xffffffffu || cs.am_ieee_v > iv || (cs.am_ieee_v == iv && cs.am_ieee_i < ii))) {
+      iv = cs.am_ieee_v; ii = cs.am_ieee_i;
+    }
+    if (cs.am_fin_i != 0xffffffffu) {
+      bool take = fi == 0xffffffffu || cs.am_fin_v > fv;
+      if (!take && cs.am_fin_v == fv) {
+        const uint32_t ra = fi & 255u, rb = cs.am_fin_i & 255u;
+        take = rb < ra || (rb == ra && cs.am_fin_i < fi);
+      }
+      if (take) { fv = cs.am_fin_v; fi = cs.am_fin_i; }
+    }
+  }
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    anyf |= (uint32_t)__shfl_xor((int)anyf, o, 64);
+    const float ov = __shfl_xor(iv, o, 64);
+    const uint32_t oi = (uint32_t)__shfl_xor((int)ii, o, 64);
+    if (oi != 0xffffffffu && (ii == 0xffffffffu || ov > iv || (ov == iv && oi < ii))) { iv = ov; ii = oi; }
+    const float pv = __shfl_xor(fv, o, 64);
+    const uint32_t pi = (uint32_t)__shfl_xor((int)fi, o, 64);
+    if (pi != 0xffffffffu) {
+      bool take = fi == 0xffffffffu || pv > fv;
+      if (!take && pv == fv) {
+        const uint32_t ra = fi & 255u, rb = pi & 255u;
+        take = rb < ra || (rb == ra && pi < fi);
+      }
+      if (take) { fv = pv; fi = pi; }
+    }
+  }
+  const bool eos = a.mask && !anyf;
+  if (cfg.cls == kGreedy) {
+    if (tid == 0) {
+      const uint32_t am = a.pv.greedy_rule == kGreedyFiniteLane ? fi : ii;
+      a.out_tokens[row] = eos ? cfg.eos : (am == 0xffffffffu ? 0u : am);
+    }
+    return true;
+  }
+  const float M = finitef_(mx) ? mx / cfg.t_eff : -__builtin_inff();
+  if (eos || !finitef_(M)) return false;
+  uint32_t offq[CQ];  // exclusive offset of chunk q * 64 + lane
+  uint32_t n_total = 0u;
+  #pragma unroll
+  for (int q = 0; q < CQ; ++q) {
+    uint32_t incl = cnt[q];
+    #pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t t = (uint32_t)__shfl_up((int)incl, o, 64);
+      if (lane >= (uint32_t)o) incl += t;
+    }
+    offq[q] = n_total + incl - cnt[q];
+    n_total += (uint32_t)__shfl((int)incl, 63, 64);
+  }
+  if (n_total > (uint32_t)kGather || n_total == 0u) return false;
+  if (tid < 64) {
+    #pragma unroll
+    for (int q = 0; q < CQ; ++q) if (q * 64 + (int)lane < nch) fs.aux[q * 64 + lane] = offq[q];
+    if (lane == 0u) fs.aux[nch] = n_total;
+  }
+  __syncthreads();
+
+  // 2. the candidates into LDS (chunk-major): all loads first
+  uint64_t cr[kFinPer];
+  {
+    const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
+    int c = 0;
+    #pragma unroll
+    for (int r = 0; r < kFinPer; ++r) {
+      const uint32_t j = (uint32_t)(tid + r * NT);
+      cr[r] = 0ull;
+      if (j < n_total) {
+        while (fs.aux[c + 1] <= j) ++c;
+        cr[r] = cand[(int64_t)c * kFast + (j - fs.aux[c])];
+      }
+    }
+    #pragma unroll
+    for (int r = 0; r < kFinPer; ++r) {
+      const uint32_t j = (uint32_t)(tid + r * NT);
+      if (j < n_total) fs.cbig[j] = cr[r];
+    }
+  }
+  __syncthreads();
+  double part = 0.0;  // the candidates' share of the logprob normaliser
+  if (want_lp) {
+    #pragma unroll
+    for (int r = 0; r < kFinPer; ++r) {
+      const uint32_t j = (uint32_t)(tid + r * NT);
+      if (j < n_total && cand_skey(cr[r]) > kKeyNegInf)
+        part += exp((double)key_to_s(cand_skey(cr[r]), cfg.t_eff) - (double)M);
+    }
+  }
+
+  // 4. the top kk by (processed logit desc, index asc)
+  const int kk = min(k_sel, (int)n_total);
+  uint64_t thr = 0ull;
+  if ((int)n_total > kk) thr = block_select_skip(fs.cbig, (int)n_total, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b);
+  if (tid == 0) fs.counter = 0u;
+  __syncthreads();
+  uint64_t below = 0ull;  // largest candidate left out
+  for (int j = tid; j < (int)n_total; j += NT) {
+    const uint64_t x = fs.cbig[j];
+    if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
+    else below = x > below ? x : below;
+  }
+  below = block_max_u64<NT>(below, fs.red64);  // has barriers: fs.buf is complete
+
+  // 5. weights in rank order keys; the smallest selected weight w_b
+  uint64_t rk = 0ull;
+  uint32_t pk = 0u;
+  uint32_t wbits = 0xffffffffu;
+  if (tid < kk) {
+    const uint64_t x = fs.buf[tid];
+    const float sx = key_to_s(cand_skey(x), cfg.t_eff);
+    const float w = exact_expf(sx - M);
+    rk = rank_key(w, cand_idx(x));
+    pk = okey(sx);
+    wbits = __float_as_uint(w);
+  }
+  const float w_b = __uint_as_float(~block_max_u32<NT>(~wbits, fs.redu));
+  // 6. could a logit outside the candidates tie with w_b?  (finish_row
+  //    resolves those rows exactly)
+  uint32_t tie = 0u;
+  if (w_b > 0.f) {
+    if (tid == 0 && below != 0ull && exact_expf(key_to_s(cand_skey(below), cfg.t_eff) - M) == w_b) tie = 1u;
+    for (int c = tid; c < nch; c += NT) {
+      const ChunkStat& cs = stats[c];
+      if (cs.trunc && exact_expf(key_to_s(cs.unkept_key, cfg.t_eff) - M) == w_b) tie = 1u;
+    }
+  }
+  if (tid < kk) fs.buf[tid] = rk;
+  if (block_max_u32<NT>(tie, fs.redu)) return false;  // has barriers: rank keys are visible
+
+  // 7. rank order by counting (kk <= NT: one entry per thread)
+  if (tid < kk) {
+    uint32_t r = 0u;
+    for (int j = 0; j < kk; ++j) r += fs.buf[j] > rk;
+    fs.cbig[r] = rk;
+    fs.aux[r] = pk;
+  }
+  __syncthreads();
+
+  // 8. the draw, by every wave from registers (gpu.rs:831-899)
+  const int k = min(cfg.k_eff, kk);
+  constexpr int DM = kLeanK / 64;
+  float fa[DM], pa[DM];
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const float w = i < k ? rank_w(fs.cbig[i]) : 0.f;
+    fa[m] = w < cfg.min_p ? 0.f : w;
+    pa[m] = 0.f;
+  }
+  // P_i: the sequential f32 sum of fa[0..i] (gpu.rs:834-836 total, and the
+  // candidate total and CDF walk of gpu.rs:874-896 at positive entries; the
+  // zero entries of min-p sit at the end of the rank order)
+  float P = -0.0f;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int cnt = min(64, k - m * 64);
+    for (int l = 0; l < cnt; ++l) {
+      P = P + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa[m]), l));
+      pa[m] = lane == (uint32_t)l ? P : pa[m];
+    }
+  }
+  const float total = P;
+  if (!(total > 0.f) || !finitef_(total)) return false;  // argmax_host fallback
+  // the nucleus: cum_p over w / total in rank order (gpu.rs:843-856)
+  float fb[DM];
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) fb[m] = fa[m] / total;
+  float Q = 0.f;
+  int m_end = 0;
+  bool stop = false;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int cnt = stop ? 0 : min(64, k - m * 64);
+    for (int l = 0; l < cnt; ++l) {
+      if (!(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa[m]), l)) > 0.f)) continue;
+      m_end = m * 64 + l + 1;
+      Q += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb[m]), l));
+      if (cfg.cutoff < 1.f && Q >= cfg.cutoff) { stop = true; break; }
+    }
+  }
+  if (m_end == 0) return false;  // no candidate: argmax_host fallback
+  const int me = m_end - 1;
+  float ct = 0.f;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m)
+    if ((me >> 6) == m) ct = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pa[m]), me & 63));
+  if (!(ct > 0.f) || !finitef_(ct)) return false;
+  // inverse CDF: the first candidate whose cumulative weight passes target
+  const float target = clamp_uniform(row_uniform(a.pv, row)) * ct;
+  int pick = -1;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const uint64_t hit = __ballot(i < m_end && target < pa[m]);
+    if (pick < 0 && hit != 0ull) pick = m * 64 + __ffsll((unsigned long long)hit) - 1;
+  }
+  if (pick < 0) pick = me;
+  const uint32_t token = cand_idx(fs.cbig[pick]);
+  if (tid == 0) a.out_tokens[row] = token;
+  if (!want_lp) return true;
+
+  // 9. logprobs of the processed distribution (extension): the normaliser
+  //    from the candidates (above) and each chunk's other logits
+  for (int c = tid; c < nch; c += NT) {
+    const ChunkStat& cs = stats[c];
+    if (cs.lse_sum > 0.f) part += (double)cs.lse_sum * exp((double)cs.lse_m - (double)M);
+  }
+  const double log_sum = log(block_sum_f64<NT>(part, fs.redd));
+  const int N = a.n_lp;
+  for (int j = tid; j < N; j += NT) {
+    float lp = -__builtin_inff();
+    uint32_t id = 0xffffffffu;
+    if (j < kk) {
+      id = cand_idx(fs.cbig[j]);
+      lp = (float)(((double)okey_inv(fs.aux[j]) - (double)M) - log_sum);
+    }
+    a.out_lp_ids[(int64_t)row * N + j] = id;
+    a.out_lp[(int64_t)row * N + j] = lp;
+  }
+  if (a.out_token_lp && tid == 0)
+    a.out_token_lp[row] = (float)(((double)okey_inv(fs.aux[pick]) - (double)M) - log_sum);
+  return true;
 }
 
 // ==========================================================================
@@ -1305,37 +1655,8 @@ __device__ __forceinline__ void block_tail3(uint64_t& mn, uint32_t& mx, float& s
 }
 
 // ==========================================================================
-// Lean scan path (every row class when at most kLeanK logprobs are asked)
+// Wave-level helpers
 // ==========================================================================
-//
-// Every wave keeps its own running top-(k+1) of the elements it streams, in
-// its own LDS buffer, with a wave-uniform threshold: an element below the
-// threshold costs a compare, survivors are appended with ballot/mbcnt, and a
-// buffer that passes its limit is compacted by a wave-level radix select.
-// No workgroup barrier runs inside the tile loop.  At the end wave 0 merges
-// the four per-wave sets into the range's top k.  Selection entries are the
-// 64-bit candidate keys (scaled-logit key, inverted index).
-
-constexpr int kLeanVec = 2;                     // float4 loads per thread per tile
-constexpr int kWaveCap = 1024;                  // per-wave buffer entries
-constexpr int kWaveMaxLim = kWaveCap - kLeanVec * 4 * 64;  // a tile's survivors fit above the limit
-static_assert(kLeanK + 1 <= kWaveMaxLim, "a compacted buffer is below the limit");
-constexpr uint32_t kChunkHistCap = 1024;        // distinct history tokens counted in LDS per chunk
-constexpr uint32_t kRowHistCap = 4096;          // ... per row (row kernel)
-
-template <int NW>
-struct LeanLds {
-  uint64_t wbuf[NW][kWaveCap];
-  uint32_t whist[NW][256];
-  uint32_t wcount[NW];
-  uint32_t wmax[NW];
-  float wbv[NW];
-  uint32_t wbi[NW];
-  float wrest[NW];
-  float wlref[NW];
-  float wfv[NW];
-  uint32_t wfi[NW];
-};
 
 // Orders this wave's LDS accesses (a wave executes its LDS operations in
 // order; this keeps the compiler from moving them across the point).
@@ -1413,188 +1734,6 @@ __device__ __forceinline__ uint64_t wave_select(const Segs<NS>& sg, uint32_t nee
   return prefix;
 }
 
-// Rest of the normaliser over the elements a range does not keep, per lane:
-// sum of 2^((l - lref) * a2) with a2 = log2(e) / T and a wave-uniform
-// reference lref that only grows (the value of the current threshold key).
-struct LseRest {
-  float sum, lref, a2;
-  __device__ __forceinline__ void add(float l) { sum += exp2f((l - lref) * a2); }
-  __device__ __forceinline__ void add_key(uint32_t key) {
-    if (key > kKeyNegInf) add(okey_inv(key));
-  }
-  __device__ __forceinline__ void move_ref(uint32_t tk) {
-    if (tk <= kKeyNegInf) return;
-    const float nl = okey_inv(tk);
-    if (finitef_(lref)) sum *= exp2f((lref - nl) * a2);
-    else sum = 0.f;
-    lref = nl;
-  }
-};
-
-// Running per-wave selection of the top k1 candidate keys.
-struct WaveSel {
-  uint64_t* buf;
-  uint32_t* hist;
-  uint32_t count;   // entries in buf (wave-uniform)
-  uint32_t k1;      // entries a compaction keeps
-  uint32_t lim;     // compaction trigger
-  uint64_t tau;     // keys below tau are not among the wave's top k1
-  uint32_t tk;      // scaled-logit key threshold: max(1, tau >> 32)
-};
-
-// Compact the wave's buffer to its top k1 (in place, in order) and raise
-// the threshold.
-__device__ __forceinline__ void wave_compact(WaveSel& ws, LseRest& rest, bool lse) {
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t n = ws.count;
-  if (n <= ws.k1) return;
-  Segs<1> sg;
-  sg.p[0] = ws.buf;
-  sg.n[0] = n;
-  sg.ns = 1;
-  const uint64_t thr = wave_select(sg, ws.k1, ws.hist);
-  if (thr > ws.tau) ws.tau = thr;
-  ws.tk = max(1u, (uint32_t)(ws.tau >> 32));
-  if (lse) rest.move_ref(ws.tk);
-  wave_lds_sync();
-  uint32_t pos = 0;
-  // entry i moves to a position <= i, and a block of 64 is read before any
-  // of its writes, so the compaction can run in place
-  #pragma unroll 1
-  for (uint32_t b = 0; b < n; b += 64u) {
-    const uint32_t i = b + lane;
-    const bool valid = i < n;
-    const uint64_t x = valid ? ws.buf[i] : 0ull;
-    const bool keep = valid && x >= thr;
-    const uint64_t m = __ballot(keep);
-    if (keep) ws.buf[pos + lanes_below(m)] = x;
-    else if (lse && valid) rest.add_key(cand_skey(x));
-    pos += (uint32_t)__popcll(m);
-  }
-  ws.count = pos;
-}
-
-// History tokens of [base, base + len) as seen by the lean path: bit li of
-// `bitmap` marks token base + li, prefix[w] counts the marked tokens of the
-// words below w, and cnts[r] is the summed count of the marked token of rank
-// r (for r < cap; higher ranks are counted from the global list).
-struct HistView {
-  const uint32_t* bitmap;
-  const uint32_t* prefix;
-  uint32_t* cnts;         // counts by rank; the lean pass then keeps keys there
-  const uint32_t* ids;    // ids[r]: the marked token of rank r (r < min(distinct, cap))
-  uint32_t cap;
-  uint32_t distinct;      // marked tokens
-  uint32_t h0, h1;
-  bool on;
-  bool ovf;               // more marked tokens than cap
-};
-
-// LDS bytes of a HistView over `len` tokens with `cap` counted tokens
-// (bitmap, prefix, counts + a zero slot, ids, 16 reduction words).
-__host__ __device__ constexpr size_t hist_lds_bytes(int len, uint32_t cap) {
-  return (size_t)2 * ((len + 31) / 32) * 4 + (size_t)(2 * cap + 1) * 4 + 64;
-}
-
-// Builds the HistView of row `row` over [base, base + len) in `mem`.  All
-// NTH threads of the workgroup call it.
-template <int NTH>
-__device__ __forceinline__ HistView stage_history_rank(const SampleArgs& a, int row, int base, int len,
-                                                       uint32_t cap, uint32_t* mem) {
-  const int tid = threadIdx.x;
-  const int W = (len + 31) / 32;
-  uint32_t* bitmap = mem;
-  uint32_t* prefix = mem + W;
-  uint32_t* cnts = mem + 2 * W;   // cap counts, then a zero slot at cnts[cap]
-  uint32_t* ids = cnts + cap + 1;
-  uint32_t* red = ids + cap;
-  HistView hv;
-  hv.bitmap = bitmap; hv.prefix = prefix; hv.cnts = cnts; hv.ids = ids; hv.cap = cap;
-  hv.distinct = 0u;
-  hv.h0 = a.hoff[row];
-  hv.h1 = a.hoff[row + 1];
-  hv.on = hv.h1 > hv.h0;
-  hv.ovf = false;
-  if (!hv.on) return hv;
-  const uint32_t h0 = hv.h0, h1 = hv.h1;
-  for (int i = tid; i < W; i += NTH) bitmap[i] = 0u;
-  __syncthreads();
-  constexpr int PER = 8;
-  const bool one = h1 - h0 <= (uint32_t)(NTH * PER);
-  uint32_t hid[PER], cs[PER];
-  for (uint32_t hb = h0; hb < h1; hb += NTH * PER) {
-    #pragma unroll
-    for (int r = 0; r < PER; ++r) {  // independent loads first
-      const uint32_t h = hb + r * NTH + tid;
-      hid[r] = h < h1 ? a.hids[h] : 0xffffffffu;
-      cs[r] = h < h1 ? a.hcnt[h] : 0u;
-    }
-    #pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const uint32_t li = hid[r] - (uint32_t)base;
-      if (hid[r] >= (uint32_t)base && li < (uint32_t)len) atomicOr(&bitmap[li >> 5], 1u << (li & 31u));
-    }
-  }
-  __syncthreads();
-  // exclusive prefix of the per-word popcounts
-  const int PW = (W + NTH - 1) / NTH;
-  uint32_t loc = 0;
-  for (int i = 0; i < PW; ++i) {
-    const int w = tid * PW + i;
-    if (w < W) loc += (uint32_t)__popc(bitmap[w]);
-  }
-  uint32_t total;
-  uint32_t run = block_excl_scan_u32<NTH>(loc, red, &total);
-  for (int i = 0; i < PW; ++i) {
-    const int w = tid * PW + i;
-    if (w < W) { prefix[w] = run; run += (uint32_t)__popc(bitmap[w]); }
-  }
-  const uint32_t nz = min(total, cap);
-  hv.ovf = total > cap;
-  hv.distinct = total;
-  for (uint32_t i = tid; i < nz; i += NTH) cnts[i] = 0u;
-  if (tid == 0) cnts[cap] = 0u;
-  __syncthreads();
-  for (uint32_t hb = h0; hb < h1; hb += NTH * PER) {
-    if (!one) {
-      #pragma unroll
-      for (int r = 0; r < PER; ++r) {
-        const uint32_t h = hb + r * NTH + tid;
-        hid[r] = h < h1 ? a.hids[h] : 0xffffffffu;
-        cs[r] = h < h1 ? a.hcnt[h] : 0u;
-      }
-    }
-    #pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const uint32_t li = hid[r] - (uint32_t)base;
-      if (hid[r] >= (uint32_t)base && li < (uint32_t)len) {
-        const uint32_t w = li >> 5;
-        const uint32_t rank = prefix[w] + (uint32_t)__popc(bitmap[w] & ((1u << (li & 31u)) - 1u));
-        if (rank < cap) {
-          atomicAdd(&cnts[rank], cs[r]);
-          ids[rank] = (uint32_t)base + li;  // every occurrence writes the same id
-        }
-      }
-    }
-  }
-  __syncthreads();
-  return hv;
-}
-
-// History count of the marked token e of rank `rank`.  OVF: the table may
-// not hold every marked token; the others are counted from the global list.
-template <bool OVF>
-__device__ __forceinline__ uint32_t hist_count(const SampleArgs& a, const HistView& hv, uint32_t e,
-                                               uint32_t rank) {
-  if (!OVF || rank < hv.cap) return hv.cnts[rank];
-  uint32_t cnt = 0u;
-  for (uint32_t h = hv.h0; h < hv.h1; ++h) if (a.hids[h] == e) cnt += a.hcnt[h];
-  return cnt;
-}
-
-// f(x) with x - lref <= 0 relevant only where `use` holds (0 elsewhere).
-__device__ __forceinline__ float masked_exp2(bool use, float v) { return use ? exp2f(v) : 0.f; }
-
 // Range-checked loads of one row (byte offsets at or past the range read
 // as zero; nothing faults).
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -1616,495 +1755,6 @@ __device__ __forceinline__ RowBuf row_buf(const SampleArgs& a, int row, int c0, 
     rb.mask = __builtin_amdgcn_make_buffer_rsrc((void*)(a.mask + (int64_t)row * a.mask_words + (c0 >> 5)),
                                                 (short)0, ((c1 - c0 + 31) >> 5) * 4, kBufferConfig);
   return rb;
-}
-
-// One tile at offset tr from the range start (element tr + (j * NTH + tid)
-// * 4 + q in x[4 * j + q]); needs 16-byte (f32) or 8-byte (bf16) aligned
-// rows.
-template <int NTH, int VEC, int DT, bool MASK>
-__device__ __forceinline__ void buf_load(const RowBuf& rb, int tr, float (&x)[VEC * 4], uint32_t (&mw)[VEC]) {
-  const int tid = threadIdx.x;
-  #pragma unroll
-  for (int j = 0; j < VEC; ++j) {
-    const int e0 = tr + (j * NTH + tid) * 4;
-    if (DT == HI_ROCM_DTYPE_BF16) {
-      const i32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rb.logits, e0 * 2, 0, 0);
-      x[4 * j + 0] = __uint_as_float((uint32_t)v.x << 16); x[4 * j + 1] = __uint_as_float((uint32_t)v.x & 0xffff0000u);
-      x[4 * j + 2] = __uint_as_float((uint32_t)v.y << 16); x[4 * j + 3] = __uint_as_float((uint32_t)v.y & 0xffff0000u);
-    } else {
-      const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb.logits, e0 * 4, 0, 0);
-      x[4 * j + 0] = __int_as_float(v.x); x[4 * j + 1] = __int_as_float(v.y);
-      x[4 * j + 2] = __int_as_float(v.z); x[4 * j + 3] = __int_as_float(v.w);
-    }
-    if (MASK) mw[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb.mask, (e0 >> 5) * 4, 0, 0);
-  }
-}
-
-// Argmax merges: IEEE '>' with ties to the lower index (kernels.cu:7153-7186),
-// and the finite-lane rule of kernels.cu:7775-7801 (ties to the lower
-// index modulo 256, then the lower index).
-__device__ __forceinline__ void merge_ieee(float& v, uint32_t& i, float ov, uint32_t oi) {
-  if (oi != 0xffffffffu && (i == 0xffffffffu || ov > v || (ov == v && oi < i))) { v = ov; i = oi; }
-}
-__device__ __forceinline__ void merge_fin(float& v, uint32_t& i, float ov, uint32_t oi) {
-  if (oi == 0xffffffffu) return;
-  bool take = i == 0xffffffffu || ov > v;
-  if (!take && ov == v) {
-    const uint32_t ra = i & 255u, rb = oi & 255u;
-    take = rb < ra || (rb == ra && oi < i);
-  }
-  if (take) { v = ov; i = oi; }
-}
-
-// Per-wave results written before the workgroup barrier of the merge.
-struct WaveOut {
-  uint32_t count, maxkey;
-  float bv;
-  uint32_t bi;
-  float fv;
-  uint32_t fi;
-  float rest, lref;
-};
-
-template <int NW>
-__device__ __forceinline__ void wave_results(LeanLds<NW>& L, int wid, WaveOut o, bool ieee, bool fin,
-                                             bool lse) {
-  #pragma unroll
-  for (int s = 32; s > 0; s >>= 1) {
-    o.maxkey = max(o.maxkey, (uint32_t)__shfl_xor((int)o.maxkey, s, 64));
-    if (ieee) merge_ieee(o.bv, o.bi, __shfl_xor(o.bv, s, 64), (uint32_t)__shfl_xor((int)o.bi, s, 64));
-    if (fin) merge_fin(o.fv, o.fi, __shfl_xor(o.fv, s, 64), (uint32_t)__shfl_xor((int)o.fi, s, 64));
-    if (lse) o.rest += __shfl_xor(o.rest, s, 64);
-  }
-  if ((threadIdx.x & 63) == 0) {
-    L.wcount[wid] = o.count;
-    L.wmax[wid] = o.maxkey;
-    L.wbv[wid] = o.bv;
-    L.wbi[wid] = o.bi;
-    L.wfv[wid] = o.fv;
-    L.wfi[wid] = o.fi;
-    L.wrest[wid] = o.rest;
-    L.wlref[wid] = o.lref;
-  }
-}
-
-// Per-wave state of the lean pass.
-struct LeanState {
-  WaveSel ws;
-  LseRest rest;
-  uint32_t maxkey;
-  float bv, fv;
-  uint32_t bi, fi;
-};
-
-// Constant context of the lean pass over [c0, c1) of `row`.
-struct LeanCtx {
-  const SampleArgs* a;
-  const RowCfg* cfg;
-  const HistView* hv;
-  float* srow;      // scaled logits for the finish, or null
-  int c0, c1, len;
-  uint32_t k;       // candidates to keep (k_sel)
-  bool ieee, fin, lse, rep_once;
-};
-
-// One tile of the lean pass: mask, penalties, keys, statistics, survivors.
-// cur holds the tile's logits (element tb + (j * NTH + tid) * 4 + q in
-// cur[4 * j + q]); first: the range's first tile.
-template <int NTH, int VEC, bool MASK, bool OVF>
-__device__ __forceinline__ void lean_tile(const LeanCtx& x, LeanState& st, float (&cur)[VEC * 4],
-                                          const uint32_t (&mw)[VEC], int tb, bool first) {
-  constexpr int TILE = NTH * VEC * 4;
-  constexpr int E = VEC * 4;
-  const SampleArgs& a = *x.a;
-  const RowCfg& cfg = *x.cfg;
-  const HistView& hv = *x.hv;
-  const int tid = threadIdx.x;
-  const uint32_t lane = (uint32_t)tid & 63u;
-  const int c0 = x.c0, c1 = x.c1;
-  const bool full = tb + TILE <= c1;
-  WaveSel& ws = st.ws;
-  if (MASK) {
-    #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const int e0 = tb + (j * NTH + tid) * 4;
-      const uint32_t nib = mw[j] >> (e0 & 31);
-      #pragma unroll
-      for (int q = 0; q < 4; ++q) if (!((nib >> q) & 1u)) cur[4 * j + q] = -__builtin_inff();
-    }
-  }
-  // elements this tile does not stream: past the range, and (without OVF)
-  // history tokens, which the lean pass handles on their own
-  uint32_t drop[VEC];
-  bool anyd = false;
-  #pragma unroll
-  for (int j = 0; j < VEC; ++j) {
-    const int e0 = tb + (j * NTH + tid) * 4;
-    drop[j] = full ? 0u : (e0 + 3 < c1 ? 0u : (0xfu << max(0, min(4, c1 - e0))) & 0xfu);
-  }
-  if (hv.on) {
-    uint32_t wb[VEC];
-    bool anyf = false;
-    #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const uint32_t li0 = (uint32_t)(tb - c0 + (j * NTH + tid) * 4);
-      wb[j] = li0 < (uint32_t)x.len ? hv.bitmap[li0 >> 5] : 0u;
-      anyf |= ((wb[j] >> (li0 & 31u)) & 15u) != 0u;
-    }
-    if (!OVF) {
-      #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const uint32_t li0 = (uint32_t)(tb - c0 + (j * NTH + tid) * 4);
-        drop[j] |= (wb[j] >> (li0 & 31u)) & 15u;
-      }
-    } else if (__ballot(anyf) != 0ull) {
-      // counts of the marked elements; the others read the zero slot
-      // cnts[cap] (tokens of rank >= cap count from the global list)
-      const uint32_t W = (uint32_t)(x.len + 31) >> 5;
-      uint32_t cnt[E];
-      uint32_t most = 0u;
-      #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const uint32_t li0 = (uint32_t)(tb - c0 + (j * NTH + tid) * 4);
-        const uint32_t sh = li0 & 31u;
-        const uint32_t nib = (wb[j] >> sh) & 15u;
-        const uint32_t base = hv.prefix[min(li0 >> 5, W - 1u)] + (uint32_t)__popc(wb[j] & ((1u << sh) - 1u));
-        #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const bool m = (nib >> q) & 1u;
-          const uint32_t r = base + (uint32_t)__popc(nib & ((1u << q) - 1u));
-          cnt[4 * j + q] = m ? hist_count<true>(a, hv, (uint32_t)c0 + li0 + (uint32_t)q, r) : 0u;
-          most = max(most, cnt[4 * j + q]);
-        }
-      }
-      // repetition penalty once per occurrence (or once), then the
-      // frequency and presence penalties (apply_penalties, element-wise)
-      if (cfg.rep_on) {
-        const uint32_t reps = x.rep_once ? min(most, 1u) : most;
-        #pragma unroll 1
-        for (uint32_t rr = 0; rr < reps; ++rr) {
-          #pragma unroll
-          for (int i = 0; i < E; ++i) {
-            const uint32_t ci = x.rep_once ? min(cnt[i], 1u) : cnt[i];
-            const float y = cur[i] < 0.f ? cur[i] * cfg.rep : cur[i] / cfg.rep;
-            cur[i] = rr < ci ? y : cur[i];
-          }
-        }
-      }
-      #pragma unroll
-      for (int i = 0; i < E; ++i) {
-        const float fc = cfg.freq * (float)cnt[i];
-        const float y = (cur[i] - fc) - cfg.pres;
-        cur[i] = cnt[i] != 0u ? y : cur[i];
-      }
-    }
-  }
-  #pragma unroll
-  for (int j = 0; j < VEC; ++j) anyd |= drop[j] != 0u;
-  uint32_t key[E];
-  #pragma unroll
-  for (int i = 0; i < E; ++i) key[i] = lkey(cur[i]);
-  if (__ballot(anyd) != 0ull) {
-    #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const bool dr = (drop[i >> 2] >> (i & 3)) & 1u;
-      key[i] = dr ? 0u : key[i];
-      cur[i] = dr ? -__builtin_inff() : cur[i];
-    }
-  }
-  #pragma unroll
-  for (int i = 0; i < E; ++i) st.maxkey = max(st.maxkey, key[i]);
-  if (x.ieee) {
-    #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const bool g = cur[i] > st.bv;
-      st.bv = g ? cur[i] : st.bv;
-      st.bi = g ? (uint32_t)(tb + ((i >> 2) * NTH + tid) * 4 + (i & 3)) : st.bi;
-    }
-  }
-  if (x.fin) {
-    // within a lane indices grow, so a tie keeps the earlier index unless
-    // the new one has the smaller residue modulo 256
-    #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const uint32_t e = (uint32_t)(tb + ((i >> 2) * NTH + tid) * 4 + (i & 3));
-      const bool g = finitef_(cur[i]) &&
-                     (st.fi == 0xffffffffu || cur[i] > st.fv || (cur[i] == st.fv && (e & 255u) < (st.fi & 255u)));
-      st.fv = g ? cur[i] : st.fv;
-      st.fi = g ? e : st.fi;
-    }
-  }
-  if (x.srow) {
-    // scaled logits s = l / T for the finish (non-finite -> -inf)
-    #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const int e0 = tb + (j * NTH + tid) * 4;
-      float sv[4];
-      #pragma unroll
-      for (int q = 0; q < 4; ++q) sv[q] = key_to_s(key[4 * j + q] ? key[4 * j + q] : kKeyNegInf, cfg.t_eff);
-      if (full && (a.V & 3) == 0) {
-        *(float4*)(x.srow + e0) = make_float4(sv[0], sv[1], sv[2], sv[3]);
-      } else {
-        #pragma unroll
-        for (int q = 0; q < 4; ++q) if (e0 + q < c1) x.srow[e0 + q] = sv[q];
-      }
-    }
-  }
-  if (x.k == 0u) return;
-  if (first && ws.k1 <= 256u) {
-    // bound from this wave's first tile: the k1-th largest of the per-lane
-    // top-jt keys, rounded down to 16 bits (at least k1 of the wave's
-    // elements are at or above it)
-    const int jt = (int)((ws.k1 + 63u) >> 6);
-    uint32_t t4[4] = {0u, 0u, 0u, 0u};
-    if (jt == 1) {
-      #pragma unroll
-      for (int i = 0; i < E; ++i) t4[0] = max(t4[0], key[i]);
-    } else {
-      #pragma unroll
-      for (int i = 0; i < E; ++i) {
-        uint32_t v = key[i];
-        #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t hi = max(t4[r], v);
-          v = min(t4[r], v);
-          t4[r] = hi;
-        }
-      }
-    }
-    uint32_t prefix = 0u;
-    #pragma unroll 1
-    for (int bit = 31; bit >= 16; --bit) {
-      const uint32_t probe = prefix | (1u << bit);
-      uint32_t c = 0u;
-      #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (r < jt) c += (uint32_t)__popcll(__ballot(t4[r] >= probe));
-      if (c >= ws.k1) prefix = probe;
-    }
-    if (prefix > 1u) {
-      ws.tau = (uint64_t)prefix << 32;
-      ws.tk = prefix;
-      if (x.lse) st.rest.move_ref(ws.tk);
-    }
-  }
-  // survivors of the tile (<= 64 * E entries: count <= lim before, so they
-  // fit); compact when the buffer passes its limit
-  uint64_t m[E];
-  uint64_t any = 0ull;
-  #pragma unroll
-  for (int i = 0; i < E; ++i) { m[i] = __ballot(key[i] >= ws.tk); any |= m[i]; }
-  if (x.lse) {
-    // the elements below the threshold leave the selection here
-    float add = 0.f;
-    #pragma unroll
-    for (int i = 0; i < E; ++i)
-      add += masked_exp2(key[i] < ws.tk && key[i] > kKeyNegInf, (cur[i] - st.rest.lref) * st.rest.a2);
-    st.rest.sum += add;
-  }
-  if (any != 0ull) {
-    #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      if (key[i] >= ws.tk)
-        ws.buf[ws.count + lanes_below(m[i])] = cand_key(key[i], (uint32_t)(tb + ((i >> 2) * NTH + tid) * 4 + (i & 3)));
-      ws.count += (uint32_t)__popcll(m[i]);
-    }
-    if (ws.count > ws.lim) wave_compact(ws, st.rest, x.lse);
-  }
-}
-
-// Tiles t0 + d .. t0 + D - 1 of one pipeline round: process buffer d, then
-// load tile t0 + d + D into it (past the range the loads read zeros).
-template <int d, int NTH, int VEC, int D, int DT, bool MASK, bool OVF>
-__device__ __forceinline__ void lean_round(const LeanCtx& x, LeanState& st, const RowBuf& rb,
-                                           float (&tl)[D][VEC * 4], uint32_t (&tmw)[D][VEC], int t0) {
-  constexpr int TILE = NTH * VEC * 4;
-  const int tb = x.c0 + (t0 + d) * TILE;
-  lean_tile<NTH, VEC, MASK, OVF>(x, st, tl[d], tmw[d], tb, d == 0 && t0 == 0);
-  buf_load<NTH, VEC, DT, MASK>(rb, tb - x.c0 + D * TILE, tl[d], tmw[d]);
-  if constexpr (d + 1 < D) lean_round<d + 1, NTH, VEC, D, DT, MASK, OVF>(x, st, rb, tl, tmw, t0);
-}
-
-// Streams [c0, c1) of `row` in tiles of NTH * VEC * 4 logits with D tiles of
-// loads in flight per thread: tl[d] holds tile d on entry (the caller issues
-// those loads first).  Writes the range's record to stats[slot] and its
-// candidates to cand[slot * kFast ...].  Every thread returns after the
-// workgroup barrier.
-template <int NTH, int VEC, int D, int DT, bool MASK, bool OVF>
-__device__ __forceinline__ void scan_lean(const SampleArgs& a, const RowCfg& cfg, LeanLds<NTH / 64>& L,
-                                          const RowBuf& rb,
-                                          float (&tl)[D][VEC * 4], uint32_t (&tmw)[D][VEC],
-                                          const HistView& hv, int row, int64_t slot, int c0, int c1) {
-  constexpr int TILE = NTH * VEC * 4;
-  constexpr int NW = NTH / 64;
-  const int tid = threadIdx.x;
-  const uint32_t lane = (uint32_t)tid & 63u;
-  const int wid = tid >> 6;
-  LeanCtx x;
-  x.a = &a; x.cfg = &cfg; x.hv = &hv;
-  x.srow = cfg.store_s ? a.ws_s + (int64_t)row * a.V : nullptr;
-  x.c0 = c0; x.c1 = c1; x.len = c1 - c0;
-  x.k = (uint32_t)cfg.k_sel;
-  x.ieee = cfg.cls == kGreedy && a.pv.greedy_rule == kGreedyIeee;
-  x.fin = cfg.cls == kTempOnly || (cfg.cls == kGreedy && a.pv.greedy_rule == kGreedyFiniteLane);
-  x.lse = a.need_lse != 0;
-  x.rep_once = (cfg.flags & HI_ROCM_FLAG_REP_ONCE) != 0u;
-  const uint32_t k = x.k;
-  const bool ieee = x.ieee, fin = x.fin;
-  const int len = x.len;
-  const int ntiles = (len + TILE - 1) / TILE;
-
-  LeanState st;
-  WaveSel& ws = st.ws;
-  ws.buf = L.wbuf[wid];
-  ws.hist = L.whist[wid];
-  ws.count = 0u;
-  ws.k1 = k + 1u;
-  ws.lim = min((uint32_t)kWaveMaxLim, ws.k1 + max(ws.k1, 192u));
-  ws.tau = 0ull;
-  ws.tk = 1u;
-  LseRest& rest = st.rest;
-  rest.sum = 0.f;
-  rest.lref = -__builtin_inff();
-  rest.a2 = 1.4426950408889634f / cfg.t_eff;
-  st.maxkey = 0u;
-  st.bv = -__builtin_inff(); st.fv = -__builtin_inff();
-  st.bi = 0xffffffffu; st.fi = 0xffffffffu;
-
-  // history tokens (without OVF the tiles skip them): gather each marked
-  // token's logit, apply the mask and the penalties exactly, and enter it
-  // like a streamed element; its key replaces its count in hv.cnts
-  float pbv = -__builtin_inff(), pfv = -__builtin_inff();
-  uint32_t pbi = 0xffffffffu, pfi = 0xffffffffu;
-  if (!OVF && hv.on) {
-    const uint32_t nd = hv.distinct;
-    #pragma unroll 1
-    for (uint32_t r0 = (uint32_t)wid * 64u; r0 < nd; r0 += NTH) {
-      const uint32_t r = r0 + lane;
-      const bool v = r < nd;
-      const uint32_t e = v ? hv.ids[r] : (uint32_t)c0;
-      const uint32_t off = e - (uint32_t)c0;
-      float l;
-      if (DT == HI_ROCM_DTYPE_BF16)
-        l = __uint_as_float((uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rb.logits, off * 2, 0, 0) << 16);
-      else
-        l = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb.logits, off * 4, 0, 0));
-      if (MASK) {
-        const uint32_t w = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb.mask, (off >> 5) * 4, 0, 0);
-        if (!((w >> (off & 31u)) & 1u)) l = -__builtin_inff();
-      }
-      l = apply_penalties(l, v ? hv.cnts[r] : 0u, cfg);
-      const uint32_t key = v ? lkey(l) : 0u;
-      if (v) hv.cnts[r] = key;
-      l = v ? l : -__builtin_inff();
-      st.maxkey = max(st.maxkey, key);
-      if (ieee && l > -__builtin_inff()) merge_ieee(pbv, pbi, l, e);
-      if (fin && finitef_(l)) merge_fin(pfv, pfi, l, e);
-      if (k > 0u) {
-        const uint64_t m = __ballot(key >= ws.tk);
-        if (key >= ws.tk) ws.buf[ws.count + lanes_below(m)] = cand_key(key, e);
-        ws.count += (uint32_t)__popcll(m);
-        if (ws.count > ws.lim) wave_compact(ws, rest, x.lse);
-      }
-    }
-  }
-
-  #pragma unroll 1
-  for (int t0 = 0; t0 < ntiles; t0 += D) lean_round<0, NTH, VEC, D, DT, MASK, OVF>(x, st, rb, tl, tmw, t0);
-
-  uint32_t maxkey = st.maxkey;
-  float bv = st.bv, fv = st.fv;
-  uint32_t bi = st.bi, fi = st.fi;
-  merge_ieee(bv, bi, pbv, pbi);
-  merge_fin(fv, fi, pfv, pfi);
-  if (k > 0u) wave_compact(ws, rest, x.lse);
-  {
-    WaveOut o;
-    o.count = ws.count; o.maxkey = maxkey; o.bv = bv; o.bi = bi; o.fv = fv; o.fi = fi;
-    o.rest = rest.sum; o.lref = rest.lref;
-    wave_results(L, wid, o, ieee, fin, x.lse);
-  }
-  __syncthreads();
-  if (!OVF && hv.on && x.srow) {
-    // the tiles stored -inf for the history tokens; store their s now
-    for (uint32_t r = (uint32_t)tid; r < hv.distinct; r += NTH) x.srow[hv.ids[r]] = key_to_s(hv.cnts[r], cfg.t_eff);
-  }
-  if (wid != 0) return;
-
-  // wave 0: merge the per-wave sets into the range's top k
-  ChunkStat bs;
-  stat_init(bs);
-  maxkey = 0u;
-  #pragma unroll
-  for (int w = 0; w < NW; ++w) maxkey = max(maxkey, L.wmax[w]);
-  bs.max_l = maxkey > kKeyNegInf ? okey_inv(maxkey) : -__builtin_inff();
-  bs.any_finite = maxkey > kKeyNegInf ? 1u : 0u;
-  if (ieee) {
-    #pragma unroll
-    for (int w = 0; w < NW; ++w) merge_ieee(bs.am_ieee_v, bs.am_ieee_i, L.wbv[w], L.wbi[w]);
-  }
-  if (fin) {
-    #pragma unroll
-    for (int w = 0; w < NW; ++w) merge_fin(bs.am_fin_v, bs.am_fin_i, L.wfv[w], L.wfi[w]);
-  }
-  if (k > 0u) {
-    Segs<NW> sg;
-    uint32_t total = 0u;
-    #pragma unroll
-    for (int w = 0; w < NW; ++w) { sg.p[w] = L.wbuf[w]; sg.n[w] = L.wcount[w]; total += sg.n[w]; }
-    sg.ns = NW;
-    uint64_t thr = 0ull;
-    if (total > k) thr = wave_select(sg, k, L.whist[0]);
-    // the dropped mass relative to the range max
-    const float lmax = bs.max_l;
-    float part = 0.f;
-    const bool LSE = x.lse;
-    if (LSE && finitef_(lmax)) {
-      #pragma unroll
-      for (int w = 0; w < NW; ++w)
-        if (L.wrest[w] > 0.f && finitef_(L.wlref[w]))
-          part += L.wrest[w] * exp2f((L.wlref[w] - lmax) * rest.a2);
-    }
-    float lane_part = 0.f;
-    uint64_t* cand = a.cand + slot * kFast;
-    uint32_t pos = 0u, unkept = 0u;
-    uint64_t minkept = ~0ull;
-    #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const uint32_t n = sg.n[w];
-      #pragma unroll 1
-      for (uint32_t b = 0; b < n; b += 64u) {
-        const uint32_t i = b + lane;
-        const bool valid = i < n;
-        const uint64_t x = valid ? sg.p[w][i] : 0ull;
-        const bool keep = valid && x >= thr;
-        const uint64_t m = __ballot(keep);
-        if (keep) {
-          cand[pos + lanes_below(m)] = x;
-          minkept = x < minkept ? x : minkept;
-        } else if (valid) {
-          const uint32_t kv = cand_skey(x);
-          unkept = max(unkept, kv);
-          if (LSE && finitef_(lmax) && kv > kKeyNegInf) lane_part += exp2f((okey_inv(kv) - lmax) * rest.a2);
-        }
-        pos += (uint32_t)__popcll(m);
-      }
-    }
-    #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const uint64_t t = shfl_xor_u64(minkept, o);
-      minkept = t < minkept ? t : minkept;
-      unkept = max(unkept, (uint32_t)__shfl_xor((int)unkept, o, 64));
-      if (LSE) lane_part += __shfl_xor(lane_part, o, 64);
-    }
-    bs.n_cand = pos;
-    bs.trunc = len > (int)k ? 1u : 0u;
-    bs.min_kept = minkept;
-    bs.unkept_key = unkept;
-    bs.lse_m = finitef_(lmax) ? lmax / cfg.t_eff : -__builtin_inff();
-    bs.lse_sum = LSE ? part + lane_part : 0.f;
-  }
-  if (lane == 0u) a.stats[slot] = bs;
 }
 
 // The general per-chunk pass (top-p, min-p, temperature-only and wide rows,
@@ -2270,6 +1920,7 @@ __device__ __forceinline__ void scan_generic(const SampleArgs& a, const RowCfg& 
     uint32_t total;
     uint32_t pos = block_excl_scan_u32<NT>(mine, sh.redu, &total);
     uint64_t minkept = ~0ull;
+    const float mc = finitef_(bs.max_l) ? bs.max_l / cfg.t_eff : -__builtin_inff();
     #pragma unroll
     for (int r = 0; r < PER; ++r) {
       const uint32_t i = r * NT + tid;
@@ -2281,7 +1932,6 @@ __device__ __forceinline__ void scan_generic(const SampleArgs& a, const RowCfg& 
       ++pos;
       minkept = ck < minkept ? ck : minkept;
     }
-    const float mc = finitef_(bs.max_l) ? bs.max_l / cfg.t_eff : -__builtin_inff();
     float part = (ss.rest_on && ss.rest.sum > 0.f && finitef_(mc)) ? ss.rest.sum * __expf(ss.rest.m - mc) : 0.f;
     uint32_t unkept = ss.unkept;
     block_tail3(minkept, unkept, part, sh);
@@ -2335,93 +1985,931 @@ __device__ __forceinline__ void stage_history_hash(const SampleArgs& a, uint32_t
   __syncthreads();
 }
 
-// LDS of the scan kernels.
-constexpr int kRowThreads = 512;  // row kernel: 8 waves stream, the first 4 finish
-size_t lean_chunk_lds_bytes(int chunk, bool hist) {
-  return ((sizeof(LeanLds<NT / 64>) + 15) & ~(size_t)15) + (hist ? hist_lds_bytes(chunk, kChunkHistCap) : 0);
+// ==========================================================================
+// Streaming select pass
+// ==========================================================================
+//
+// One workgroup of NT threads per (chunk, row).  A chunk is NT * E logits;
+// thread tid owns the EPL logits of each 16-byte load j at local index
+// (j * NT + tid) * EPL, so every load instruction of a wave covers 1 KiB of
+// consecutive HBM.  The row's history list and then every load of the chunk
+// are issued before anything waits on them.  The row's class picks the path
+// (uniform per workgroup):
+//
+// select_lean   greedy rows and top-k rows that keep no scaled logits.
+//   phase A   per-lane maxima of 4 groups of E/4 logits (allowed-token mask
+//             as -inf; history tokens keep their raw logit here);
+//   bound     each wave binary-searches, with ballots and popcounts, the
+//             largest key t_w such that at least ceil(k/4) + h_w of its
+//             group maxima are >= t_w, h_w being the history tokens among
+//             the wave's logits: at least ceil(k/4) of those maxima are then
+//             distinct non-history logits, so the workgroup bound
+//             t = min t_w has at least k logits >= t;
+//   phase B   one compare per logit builds a per-lane survivor bitmask; a
+//             short per-lane loop re-reads the few survivors (L2 hits),
+//             skipping history tokens, whose penalised values were computed
+//             out of band;
+//   select    wave 0 runs an 8-bit radix select that starts below the
+//             survivors' common key prefix and keeps the chunk's exact top
+//             k_sel by (processed logit desc, index asc).
+//
+// select_wide   rows that keep their scaled logits (top-p / min-p only,
+//             temperature-only, top-k above kLeanK): history tokens are
+//             marked absent in the stream, the scaled logits are stored, and
+//             candidates (for logprobs) come from wave-private survivor lists.
+//
+// Chunks with +inf, no finite logit, a zero maximum on an argmax row, a
+// failed bound or too many survivors take select_exact(), which reads the
+// chunk again and recomputes everything element by element with integer
+// keys.  Every path writes the same record and candidates.
+
+constexpr int kSurvCap = 640;              // survivors per wave
+constexpr uint32_t kSelHistCap = 1024;     // distinct history tokens per chunk held in LDS
+constexpr int kSelHistPer = 8;             // history entries each thread loads up front
+constexpr int kSelOb = (int)kSelHistCap / NT;  // out-of-band history items per thread
+constexpr int kLaneSurv = 6;               // streamed survivors a lane takes per round (lean path)
+
+struct SelLds {
+  uint64_t surv[NT / 64][kSurvCap];
+  uint32_t hist[256];
+  uint32_t sel[4];
+  uint32_t hw[NT / 64];       // history tokens among each wave's logits
+  uint32_t wcnt[NT / 64];
+  uint32_t wkept[NT / 64];
+  uint32_t wflag[NT / 64];
+  uint32_t wkey[NT / 64];
+  float wmax[NT / 64];
+  uint64_t red64[NT / 64];
+  uint64_t red64b[NT / 64];
+  uint64_t red64c[NT / 64];
+  uint32_t redu[NT / 64];
+  uint32_t redu2[NT / 64];
+  float redf[NT / 64];
+  double redd[NT / 64];
+  ChunkStat red[NT / 64];
+};
+constexpr size_t kSelHead = (sizeof(SelLds) + 15) & ~(size_t)15;
+
+// History tokens of the chunk: bit li of `bitmap` marks token c0 + li,
+// prefix[w] counts the marked tokens of the words below w, and the token of
+// rank r (r < kSelHistCap) has id ids[r] and summed count cnts[r].
+struct SelHist {
+  const uint32_t* bitmap;
+  const uint32_t* prefix;
+  const uint32_t* cnts;
+  const uint32_t* ids;
+  uint32_t distinct;
+  uint32_t h0, h1;
+  bool on;
+  bool ovf;  // more marked tokens than kSelHistCap
+};
+
+__host__ __device__ constexpr size_t sel_hist_bytes(int len) {
+  return (size_t)2 * ((len + 31) / 32) * 4 + (size_t)2 * kSelHistCap * 4 + 64;
 }
+
+// Builds the SelHist of [c0, c0 + len) in `mem` from the history entries
+// each thread loaded (hid/hcs: entry h0 + r * NT + tid); entries past those
+// are read here.  hw[w] counts the entries that fall on wave w's logits
+// (logit li belongs to wave ((li / epl) % NT) / 64).  All threads call it.
+__device__ __forceinline__ SelHist stage_history_sel(const SampleArgs& a, int c0, int len, int epl, uint32_t* mem,
+                                                     uint32_t* hw, const uint32_t (&hid)[kSelHistPer],
+                                                     const uint32_t (&hcs)[kSelHistPer], uint32_t h0,
+                                                     uint32_t h1) {
+  const int tid = threadIdx.x;
+  const int W = (len + 31) >> 5;
+  uint32_t* bitmap = mem;
+  uint32_t* prefix = mem + W;
+  uint32_t* cnts = prefix + W;
+  uint32_t* ids = cnts + kSelHistCap;
+  uint32_t* red = ids + kSelHistCap;
+  SelHist hv;
+  hv.bitmap = bitmap; hv.prefix = prefix; hv.cnts = cnts; hv.ids = ids;
+  hv.distinct = 0u; hv.h0 = h0; hv.h1 = h1;
+  hv.on = h1 > h0;
+  hv.ovf = false;
+  if (tid < NT / 64) hw[tid] = 0u;
+  if (!hv.on) {
+    __syncthreads();
+    return hv;
+  }
+  constexpr uint32_t kFirst = (uint32_t)(kSelHistPer * NT);
+  for (int i = tid; i < W; i += NT) bitmap[i] = 0u;
+  __syncthreads();
+  auto mark = [&](uint32_t id) {
+    const uint32_t li = id - (uint32_t)c0;
+    if (id >= (uint32_t)c0 && li < (uint32_t)len) {
+      atomicOr(&bitmap[li >> 5], 1u << (li & 31u));
+      atomicAdd(&hw[((li / (uint32_t)epl) % (uint32_t)NT) >> 6], 1u);
+    }
+  };
+  #pragma unroll
+  for (int r = 0; r < kSelHistPer; ++r) mark(hid[r]);
+  for (uint32_t h = h0 + kFirst + tid; h < h1; h += NT) mark(a.hids[h]);
+  __syncthreads();
+  const int PW = (W + NT - 1) / NT;
+  uint32_t loc = 0;
+  for (int i = 0; i < PW; ++i) {
+    const int w = tid * PW + i;
+    if (w < W) loc += (uint32_t)__popc(bitmap[w]);
+  }
+  uint32_t total;
+  uint32_t run = block_excl_scan_u32<NT>(loc, red, &total);
+  for (int i = 0; i < PW; ++i) {
+    const int w = tid * PW + i;
+    if (w < W) { prefix[w] = run; run += (uint32_t)__popc(bitmap[w]); }
+  }
+  const uint32_t nz = min(total, kSelHistCap);
+  for (uint32_t i = tid; i < nz; i += NT) cnts[i] = 0u;
+  __syncthreads();
+  auto add = [&](uint32_t id, uint32_t c) {
+    const uint32_t li = id - (uint32_t)c0;
+    if (id >= (uint32_t)c0 && li < (uint32_t)len) {
+      const uint32_t w = li >> 5;
+      const uint32_t rank = prefix[w] + (uint32_t)__popc(bitmap[w] & ((1u << (li & 31u)) - 1u));
+      if (rank < kSelHistCap) {
+        atomicAdd(&cnts[rank], c);
+        ids[rank] = id;  // every occurrence writes the same id
+      }
+    }
+  };
+  #pragma unroll
+  for (int r = 0; r < kSelHistPer; ++r) add(hid[r], hcs[r]);
+  for (uint32_t h = h0 + kFirst + tid; h < h1; h += NT) add(a.hids[h], a.hcnt[h]);
+  __syncthreads();
+  hv.distinct = total;
+  hv.ovf = total > kSelHistCap;
+  return hv;
+}
+
+__device__ __forceinline__ bool hist_marked(const SelHist& hv, uint32_t li) {
+  return hv.on && ((hv.bitmap[li >> 5] >> (li & 31u)) & 1u);
+}
+
+// Summed history count of token e (local index li) for the exact path.
+__device__ __forceinline__ uint32_t sel_hist_count(const SampleArgs& a, const SelHist& hv, int c0, uint32_t li,
+                                                   bool& marked) {
+  const uint32_t w = li >> 5;
+  marked = hist_marked(hv, li);
+  if (!marked) return 0u;
+  const uint32_t rank = hv.prefix[w] + (uint32_t)__popc(hv.bitmap[w] & ((1u << (li & 31u)) - 1u));
+  if (rank < kSelHistCap) return hv.cnts[rank];
+  const uint32_t e = (uint32_t)c0 + li;
+  uint32_t c = 0u;
+  for (uint32_t h = hv.h0; h < hv.h1; ++h) if (a.hids[h] == e) c += a.hcnt[h];
+  return c;
+}
+
+// Threshold T such that exactly `need` of the listed entries (unique keys)
+// are >= T, 1 <= need <= entries.  Like wave_select, but the first digit
+// starts just below the entries' common high bits, and the last digit may be
+// narrower than 8 bits.  Called by one whole wave.
+template <int NS>
+__device__ __forceinline__ uint64_t wave_select_skip(const Segs<NS>& sg, uint32_t need, uint32_t* hist) {
+  const uint32_t lane = threadIdx.x & 63u;
+  uint64_t mn = ~0ull, mx = 0ull;
+  #pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    if (s >= sg.ns) break;
+    for (uint32_t i = lane; i < sg.n[s]; i += 64u) {
+      const uint64_t x = sg.p[s][i];
+      mn = x < mn ? x : mn;
+      mx = x > mx ? x : mx;
+    }
+  }
+  mn = wave_min_u64(mn);
+  mx = wave_max_u64(mx);
+  if (mn == mx) return mx;
+  int hi = 64 - __clzll(mn ^ mx);  // bits [0, hi) still undecided
+  uint64_t prefix = hi >= 64 ? 0ull : (mx >> hi) << hi;
+  uint32_t remaining = need;
+  #pragma unroll 1
+  while (hi > 0) {
+    const int db = hi >= 8 ? 8 : hi;
+    const int lo = hi - db;
+    const uint64_t hp = hi >= 64 ? 0ull : (prefix >> hi);
+    wave_lds_sync();
+    *reinterpret_cast<uint4*>(hist + 4 * lane) = make_uint4(0u, 0u, 0u, 0u);
+    wave_lds_sync();
+    #pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (s >= sg.ns) break;
+      for (uint32_t i = lane; i < sg.n[s]; i += 64u) {
+        const uint64_t x = sg.p[s][i];
+        if (hi >= 64 || (x >> hi) == hp) atomicAdd(&hist[(uint32_t)(x >> lo) & ((1u << db) - 1u)], 1u);
+      }
+    }
+    wave_lds_sync();
+    // lane l owns bins 255-4l .. 252-4l (descending)
+    const uint4 h = *reinterpret_cast<const uint4*>(hist + 252 - 4 * lane);
+    const uint32_t cs[4] = {h.w, h.z, h.y, h.x};
+    const uint32_t lsum = cs[0] + cs[1] + cs[2] + cs[3];
+    uint32_t inc = lsum;
+    #pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t t = (uint32_t)__shfl_up((int)inc, o, 64);
+      if (lane >= (uint32_t)o) inc += t;
+    }
+    uint32_t acc = inc - lsum, d = 0, da = 0, dc = 0;
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (acc < remaining && remaining <= acc + cs[q]) { d = 255u - 4u * lane - (uint32_t)q; da = acc; dc = cs[q]; }
+      acc += cs[q];
+    }
+    const uint64_t who = __ballot(inc - lsum < remaining && remaining <= inc);
+    const int src = __ffsll((unsigned long long)who) - 1;
+    d = (uint32_t)__builtin_amdgcn_readlane((int)d, src);
+    da = (uint32_t)__builtin_amdgcn_readlane((int)da, src);
+    dc = (uint32_t)__builtin_amdgcn_readlane((int)dc, src);
+    prefix |= (uint64_t)d << lo;
+    remaining -= da;
+    hi = lo;
+    if (dc == remaining) break;
+  }
+  return prefix;
+}
+
+// What a row needs from the pass (uniform per row).
+struct SelNeeds {
+  bool ieee, fin;   // argmax rules (greedy rows, temperature-only rows)
+  bool sel;         // candidates (k_sel > 0)
+  bool surv;        // a survivor list at all (sel or an argmax)
+  bool lse;         // normaliser rest for logprobs
+};
+
+__device__ __forceinline__ SelNeeds sel_needs(const SampleArgs& a, const RowCfg& cfg) {
+  SelNeeds n;
+  n.ieee = cfg.cls == kGreedy && a.pv.greedy_rule == kGreedyIeee;
+  n.fin = cfg.cls == kTempOnly || (cfg.cls == kGreedy && a.pv.greedy_rule == kGreedyFiniteLane);
+  n.sel = cfg.k_sel > 0;
+  n.surv = n.sel || n.ieee || n.fin;
+  n.lse = a.need_lse != 0;
+  return n;
+}
+
+// Exact pass over the chunk from global memory, element by element.  Used
+// for the rare chunks the fast paths do not take.  All threads call it.
+__device__ __forceinline__ void select_exact(SelLds& L, const SampleArgs& a, const RowCfg& cfg, const SelHist& hv,
+                                             const SelNeeds& nd, int row, int c0, int len, int64_t slot) {
+  const int tid = threadIdx.x;
+  const int64_t rbase = (int64_t)row * a.row_stride;
+  auto proc = [&](int li) -> float {
+    const uint32_t e = (uint32_t)(c0 + li);
+    float l = load_raw(a.logits, a.dtype, rbase + e);
+    if (!allowed(a, row, e)) l = -__builtin_inff();
+    bool marked;
+    const uint32_t cnt = sel_hist_count(a, hv, c0, (uint32_t)li, marked);
+    return marked ? apply_penalties(l, cnt, cfg) : l;
+  };
+  // statistics (per thread in increasing index order, then merged)
+  ChunkStat st;
+  stat_init(st);
+  uint32_t maxkey = 0u;
+  for (int li = tid; li < len; li += NT) {
+    const float l = proc(li);
+    const uint32_t e = (uint32_t)(c0 + li);
+    maxkey = max(maxkey, lkey(l));
+    if (nd.ieee && l > st.am_ieee_v) { st.am_ieee_v = l; st.am_ieee_i = e; }
+    if (nd.fin && finitef_(l) &&
+        (st.am_fin_i == 0xffffffffu || l > st.am_fin_v ||
+         (l == st.am_fin_v && (e & 255u) < (st.am_fin_i & 255u)))) {
+      st.am_fin_v = l; st.am_fin_i = e;
+    }
+  }
+  st.max_l = maxkey > kKeyNegInf ? okey_inv(maxkey) : -__builtin_inff();
+  st.any_finite = maxkey > kKeyNegInf ? 1u : 0u;
+  ChunkStat bs = block_stat<NT>(st, L.red);
+  const float lmax = bs.max_l;
+  const float a2 = 1.4426950408889634f / cfg.t_eff;
+  if (nd.sel) {
+    const uint32_t k = (uint32_t)cfg.k_sel;
+    uint64_t thr = 0ull;
+    if ((uint32_t)len > k)
+      thr = radix_select_top(L.hist, L.sel, k, 64, [&](auto cb) {
+        for (int li = tid; li < len; li += NT) cb(cand_key(lkey(proc(li)), (uint32_t)(c0 + li)));
+      });
+    uint32_t mine = 0u;
+    for (int li = tid; li < len; li += NT) mine += cand_key(lkey(proc(li)), (uint32_t)(c0 + li)) >= thr;
+    uint32_t total;
+    uint32_t pos = block_excl_scan_u32<NT>(mine, L.redu, &total);
+    uint64_t* cand = a.cand + slot * kFast;
+    uint64_t minkept = ~0ull;
+    uint32_t unkept = 0u;
+    float rest = 0.f;
+    const float lm = finitef_(lmax) ? lmax / cfg.t_eff : -__builtin_inff();
+    for (int li = tid; li < len; li += NT) {
+      const float l = proc(li);
+      const uint32_t kl = lkey(l);
+      const uint64_t ck = cand_key(kl, (uint32_t)(c0 + li));
+      const bool live = nd.lse && finitef_(lmax) && kl > kKeyNegInf;
+      if (ck >= thr) {
+        cand[pos++] = ck;
+        minkept = ck < minkept ? ck : minkept;
+      } else {
+        unkept = max(unkept, kl);
+        if (live) rest += exp2f((l - lmax) * a2);
+      }
+    }
+    minkept = ~block_max_u64<NT>(~minkept, L.red64);
+    unkept = block_max_u32<NT>(unkept, L.redu);
+    rest = block_sum_f32<NT>(rest, L.redf);
+    bs.n_cand = total;
+    bs.trunc = (uint32_t)len > k ? 1u : 0u;
+    bs.min_kept = minkept;
+    bs.unkept_key = unkept;
+    bs.lse_m = lm;
+    bs.lse_sum = nd.lse ? rest : 0.f;
+  }
+  if (cfg.store_s) {
+    float* srow = a.ws_s + (int64_t)row * a.V + c0;
+    for (int li = tid; li < len; li += NT) srow[li] = key_to_s(lkey(proc(li)), cfg.t_eff);
+  }
+  if (tid == 0) a.stats[slot] = bs;
+}
+
+// Raw logits of load j as floats.
+template <int DT, int EPL>
+__device__ __forceinline__ void unpack16(const i32x4_t& r, float (&v)[EPL]) {
+  if constexpr (DT == HI_ROCM_DTYPE_BF16) {
+    #pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      v[2 * w] = __uint_as_float((uint32_t)r[w] << 16);
+      v[2 * w + 1] = __uint_as_float((uint32_t)r[w] & 0xffff0000u);
+    }
+  } else {
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = __int_as_float(r[q]);
+  }
+}
+
+// One raw logit of the chunk (local index li), range-checked.
+template <int DT>
+__device__ __forceinline__ float load_one(const RowBuf& rb, uint32_t li) {
+  if constexpr (DT == HI_ROCM_DTYPE_BF16)
+    return __uint_as_float((uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rb.logits, li * 2, 0, 0) << 16);
+  else
+    return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb.logits, li * 4, 0, 0));
+}
+
+// Inputs every path of the select pass shares.
+template <int NL>
+struct SelIn {
+  i32x4_t raw[NL];            // the chunk's logits, load j
+  uint32_t mw[NL];            // mask word of load j
+  float ob[kSelOb];           // processed logits of the chunk's history tokens
+  uint32_t obi[kSelOb];       // their indices
+  uint32_t n_ob;              // history tokens held out of band
+};
+
+// Lean rows (see the section comment).  Returns false when the chunk needs
+// the exact path; all threads call it and get the same answer.
+template <int DT, int NL, bool MASK>
+__device__ __forceinline__ bool select_lean(SelLds& L, const SampleArgs& a, const RowCfg& cfg, const SelNeeds& nd,
+                                            const RowBuf& rb, const float (&x)[NL * (DT == HI_ROCM_DTYPE_BF16 ? 8 : 4)],
+                                            const SelIn<NL>& in, const SelHist& hv, int c0, int len, int64_t slot) {
+  constexpr int EPL = DT == HI_ROCM_DTYPE_BF16 ? 8 : 4;
+  constexpr int E = NL * EPL;
+  constexpr int GS = E / 4;
+  constexpr int NBW = (E + 31) / 32;  // bitmask words per lane
+  static_assert(NBW <= 2, "survivor bitmask words");
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const int wid = tid >> 6;
+
+  // phase A: group maxima (history tokens keep their raw logit here)
+  float G[4];
+  #pragma unroll
+  for (int g = 0; g < 4; ++g) G[g] = -__builtin_inff();
+  #pragma unroll
+  for (int i = 0; i < E; ++i) G[i / GS] = fmaxf(G[i / GS], x[i]);
+
+  // bound
+  const uint32_t k1 = nd.sel ? (uint32_t)cfg.k_sel : 1u;
+  const uint32_t need = (k1 + (NT / 64) - 1) / (NT / 64) + (hv.on ? L.hw[wid] : 0u);
+  uint32_t gk[4];
+  bool inf = false;
+  #pragma unroll
+  for (int g = 0; g < 4; ++g) { gk[g] = okey(G[g]); inf |= G[g] == __builtin_inff(); }
+  uint32_t prefix = 0u;
+  #pragma unroll 1
+  for (int bit = 31; bit >= 12; --bit) {
+    const uint32_t probe = prefix | (1u << bit);
+    uint32_t c = 0u;
+    #pragma unroll
+    for (int g = 0; g < 4; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
+    if (c >= need) prefix = probe;
+  }
+  const bool bad = __ballot(inf) != 0ull || need > 4u * 64u || prefix <= kKeyNegInf;
+  if (lane == 0u) { L.wkey[wid] = prefix; L.wflag[wid] = bad ? 1u : 0u; }
+  __syncthreads();
+  uint32_t tk = L.wkey[0];
+  uint32_t rare = L.wflag[0];
+  #pragma unroll
+  for (int w = 1; w < NT / 64; ++w) { tk = min(tk, L.wkey[w]); rare |= L.wflag[w]; }
+  if (rare) return false;
+  const float t = okey_inv(tk);
+  const float a2 = 1.4426950408889634f / cfg.t_eff;
+
+  // phase B: survivor bitmasks (element i of word w at bit nb - 1 - (i - 32 w))
+  uint32_t bm[NBW];
+  #pragma unroll
+  for (int w = 0; w < NBW; ++w) bm[w] = 0u;
+  #pragma unroll
+  for (int i = 0; i < E; ++i) bm[i >> 5] = (bm[i >> 5] << 1) + (x[i] >= t ? 1u : 0u);
+  float rest = 0.f;
+  if (nd.lse) {
+    // the normaliser rest relative to t (history tokens count out of band)
+    #pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int li0 = (j * NT + tid) * EPL;
+      const uint32_t hb = (hv.on && li0 < len) ? hv.bitmap[li0 >> 5] >> (li0 & 31) : 0u;
+      #pragma unroll
+      for (int q = 0; q < EPL; ++q) {
+        const float v = x[j * EPL + q];
+        rest += (v < t && !((hb >> q) & 1u)) ? __builtin_amdgcn_exp2f((v - t) * a2) : 0.f;
+      }
+    }
+  }
+  // survivors of this lane: streamed ones (re-read, history tokens
+  // skipped) and out-of-band history tokens
+  uint32_t nbits = 0u;
+  #pragma unroll
+  for (int w = 0; w < NBW; ++w) nbits += (uint32_t)__popc(bm[w]);
+  uint32_t nob = 0u;
+  #pragma unroll
+  for (int i = 0; i < kSelOb; ++i) {
+    const float o = in.ob[i];
+    nob += o >= t ? 1u : 0u;
+    if (nd.lse) rest += o < t ? __builtin_amdgcn_exp2f((o - t) * a2) : 0.f;
+  }
+  // the wave's list: out-of-band survivors, then the streamed ones in rounds
+  // of up to kLaneSurv per lane (a list past kSurvCap takes the exact path)
+  uint64_t* surv = L.surv[wid];
+  uint32_t mkey = 0u;
+  uint32_t wtot;
+  {
+    uint32_t incl = nob;
+    #pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t tv = (uint32_t)__shfl_up((int)incl, o, 64);
+      if (lane >= (uint32_t)o) incl += tv;
+    }
+    uint32_t pos = incl - nob;
+    wtot = (uint32_t)__shfl((int)incl, 63, 64);
+    #pragma unroll
+    for (int i = 0; i < kSelOb; ++i) {
+      if (in.ob[i] >= t) {
+        const uint32_t kv = okey(in.ob[i]);
+        surv[pos++] = cand_key(kv, in.obi[i]);
+        mkey = max(mkey, kv);
+      }
+    }
+  }
+  (void)nbits;
+  #pragma unroll 1
+  while (__ballot(bm[0] != 0u || bm[NBW - 1] != 0u) != 0ull && wtot <= (uint32_t)kSurvCap) {
+    float sv[kLaneSurv];
+    uint32_t si[kLaneSurv];
+    uint32_t sok = 0u;  // bit s: slot s holds a survivor
+    #pragma unroll
+    for (int s = 0; s < kLaneSurv; ++s) {
+      int w = 0;
+      #pragma unroll
+      for (int ww = NBW - 1; ww >= 0; --ww) if (bm[ww] != 0u) w = ww;
+      const uint32_t word = w == 0 ? bm[0] : bm[NBW - 1];
+      const int nb = (w + 1) * 32 <= E ? 32 : E - w * 32;
+      const bool has = word != 0u;
+      const int b = has ? 31 - __clz(word) : 0;
+      const int i = w * 32 + (nb - 1 - b);
+      if (has) {
+        if (w == 0) bm[0] &= ~(1u << b);
+        else bm[NBW - 1] &= ~(1u << b);
+      }
+      const int j = i / EPL, q = i % EPL;
+      const uint32_t li = (uint32_t)((j * NT + tid) * EPL + q);
+      const bool take = has && !hist_marked(hv, li);
+      si[s] = li;
+      sv[s] = take ? load_one<DT>(rb, li) : 0.f;
+      sok |= take ? (1u << s) : 0u;
+    }
+    const uint32_t mine = (uint32_t)__popc(sok);
+    uint32_t incl = mine;
+    #pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t tv = (uint32_t)__shfl_up((int)incl, o, 64);
+      if (lane >= (uint32_t)o) incl += tv;
+    }
+    const uint32_t rtot = (uint32_t)__shfl((int)incl, 63, 64);
+    if (wtot + rtot <= (uint32_t)kSurvCap) {
+      uint32_t pos = wtot + incl - mine;
+      #pragma unroll
+      for (int s = 0; s < kLaneSurv; ++s) {
+        if ((sok >> s) & 1u) {
+          const uint32_t kv = okey(sv[s]);
+          surv[pos++] = cand_key(kv, (uint32_t)c0 + si[s]);
+          mkey = max(mkey, kv);
+        }
+      }
+    }
+    wtot += rtot;
+  }
+  // the wave's smallest and largest entries, and the finite-lane argmax key
+  // (index mod 256, index) among its largest values
+  (void)mkey;
+  wave_lds_sync();
+  const uint32_t wn = min(wtot, (uint32_t)kSurvCap);
+  uint64_t wmin = ~0ull, wmax = 0ull;
+  for (uint32_t i = lane; i < wn; i += 64u) {
+    const uint64_t e = surv[i];
+    wmin = e < wmin ? e : wmin;
+    wmax = e > wmax ? e : wmax;
+  }
+  wmin = wave_min_u64(wmin);
+  wmax = wave_max_u64(wmax);
+  uint64_t wfin = ~0ull;
+  if (nd.fin) {
+    for (uint32_t i = lane; i < wn; i += 64u) {
+      const uint64_t e = surv[i];
+      if (cand_skey(e) == cand_skey(wmax)) {
+        const uint32_t idx = cand_idx(e);
+        const uint64_t fk = ((uint64_t)(idx & 255u) << 32) | idx;
+        wfin = fk < wfin ? fk : wfin;
+      }
+    }
+    wfin = wave_min_u64(wfin);
+  }
+  if (nd.lse) rest = wave_sum_f32(rest);
+  if (lane == 0u) {
+    L.wcnt[wid] = wtot;
+    L.red64[wid] = wmin;
+    L.red64b[wid] = wmax;
+    L.red64c[wid] = wfin;
+    L.redf[wid] = rest;
+  }
+  __syncthreads();
+  uint32_t n = 0u, off = 0u;
+  uint64_t best = 0ull;
+  #pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    if (L.wcnt[w] > (uint32_t)kSurvCap) return false;
+    if (w < wid) off += L.wcnt[w];
+    n += L.wcnt[w];
+    best = L.red64b[w] > best ? L.red64b[w] : best;
+  }
+  if (nd.sel && n > (uint32_t)kFast) return false;
+  const uint32_t mk = cand_skey(best);
+  const float m = okey_inv(mk);
+  if ((nd.ieee || nd.fin) && m == 0.f) return false;  // -0 / +0 ties: IEEE compare rules
+
+  // every survivor is a candidate: each wave writes its list at its offset
+  if (nd.sel) {
+    uint64_t* cand = a.cand + slot * kFast + off;
+    for (uint32_t i = lane; i < wtot; i += 64u) cand[i] = surv[i];
+  }
+  if (wid != 0) return true;
+  if (lane == 0u) {
+    ChunkStat bs;
+    stat_init(bs);
+    bs.max_l = m;
+    bs.any_finite = 1u;
+    uint64_t mn = ~0ull, fb = ~0ull;
+    float rs = 0.f;
+    #pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+      mn = L.red64[w] < mn ? L.red64[w] : mn;
+      if (cand_skey(L.red64b[w]) == mk) fb = L.red64c[w] < fb ? L.red64c[w] : fb;
+      rs += L.redf[w];
+    }
+    if (nd.sel) {
+      bs.n_cand = n;
+      bs.trunc = n < (uint32_t)len ? 1u : 0u;
+      bs.min_kept = mn;
+      // the logits that are not candidates have keys below tk
+      bs.unkept_key = n < (uint32_t)len ? tk - 1u : 0u;
+      bs.lse_m = m / cfg.t_eff;
+      bs.lse_sum = nd.lse ? rs * __builtin_amdgcn_exp2f((t - m) * a2) : 0.f;
+    }
+    if (nd.ieee) { bs.am_ieee_v = m; bs.am_ieee_i = cand_idx(best); }
+    if (nd.fin) { bs.am_fin_v = m; bs.am_fin_i = (uint32_t)fb; }
+    a.stats[slot] = bs;
+  }
+  return true;
+}
+
+// Rows that keep their scaled logits (see the section comment).  Returns
+// false when the chunk needs the exact path; all threads call it.
+template <int DT, int NL, bool MASK>
+__device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, const RowCfg& cfg, const SelNeeds& nd,
+                                            float (&x)[NL * (DT == HI_ROCM_DTYPE_BF16 ? 8 : 4)], const SelIn<NL>& in,
+                                            const SelHist& hv, int row, int c0, int len, int64_t slot) {
+  constexpr int EPL = DT == HI_ROCM_DTYPE_BF16 ? 8 : 4;
+  constexpr int E = NL * EPL;
+  constexpr int GS = E / 4;
+  constexpr uint32_t EMASK = (1u << EPL) - 1u;
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const int wid = tid >> 6;
+
+  // phase A: history tokens absent (NaN), maxima
+  float G[4];
+  #pragma unroll
+  for (int g = 0; g < 4; ++g) G[g] = -__builtin_inff();
+  #pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int li0 = (j * NT + tid) * EPL;
+    if (hv.on) {
+      const uint32_t hb = li0 < len ? (hv.bitmap[li0 >> 5] >> (li0 & 31)) & EMASK : 0u;
+      #pragma unroll
+      for (int q = 0; q < EPL; ++q) x[j * EPL + q] = ((hb >> q) & 1u) ? __builtin_nanf("") : x[j * EPL + q];
+    }
+    #pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const int i = j * EPL + q;
+      G[i / GS] = fmaxf(G[i / GS], x[i]);
+    }
+  }
+  float lm = fmaxf(fmaxf(G[0], G[1]), fmaxf(G[2], G[3]));
+  #pragma unroll
+  for (int i = 0; i < kSelOb; ++i) lm = fmaxf(lm, in.ob[i]);
+
+  // wave bound (candidates for logprobs) and workgroup statistics
+  const float wm = wave_max_f32(lm);
+  uint32_t flag = (hv.ovf || wm == __builtin_inff()) ? 1u : 0u;
+  uint32_t tkey = 0xffffffffu;
+  if (nd.sel) {
+    const uint32_t k1w = ((uint32_t)cfg.k_sel + (NT / 64) - 1) / (NT / 64);
+    const int J = k1w <= 16u ? 1 : (k1w <= 32u ? 2 : 4);
+    uint32_t gk[4];
+    if (J == 1) {
+      gk[0] = okey(fmaxf(fmaxf(G[0], G[1]), fmaxf(G[2], G[3])));
+      gk[1] = gk[2] = gk[3] = 0u;
+    } else if (J == 2) {
+      gk[0] = okey(fmaxf(G[0], G[1]));
+      gk[1] = okey(fmaxf(G[2], G[3]));
+      gk[2] = gk[3] = 0u;
+    } else {
+      #pragma unroll
+      for (int g = 0; g < 4; ++g) gk[g] = okey(G[g]);
+    }
+    uint32_t prefix = 0u;
+    #pragma unroll 1
+    for (int bit = 31; bit >= 12; --bit) {
+      const uint32_t probe = prefix | (1u << bit);
+      uint32_t c = 0u;
+      #pragma unroll
+      for (int g = 0; g < 4; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
+      if (c >= k1w) prefix = probe;
+    }
+    tkey = prefix;
+    if (prefix <= kKeyNegInf) flag = 1u;
+  }
+  if (lane == 0u) { L.wmax[wid] = wm; L.wkey[wid] = tkey; L.wflag[wid] = flag; }
+  __syncthreads();
+  float m = L.wmax[0];
+  uint32_t tk = L.wkey[0];
+  uint32_t rare = L.wflag[0];
+  #pragma unroll
+  for (int w = 1; w < NT / 64; ++w) { m = fmaxf(m, L.wmax[w]); tk = min(tk, L.wkey[w]); rare |= L.wflag[w]; }
+  if (!finitef_(m) || ((nd.ieee || nd.fin) && m == 0.f)) rare = 1u;
+  if (rare) return false;
+  // candidates need t = the bound; an argmax alone needs the ties of m
+  const float t = nd.sel ? okey_inv(tk) : m;
+  const float a2 = 1.4426950408889634f / cfg.t_eff;
+
+  // phase B
+  uint32_t cnt = 0u;
+  float rest = 0.f;
+  uint64_t* surv = L.surv[wid];
+  #pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int li0 = (j * NT + tid) * EPL;
+    #pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const float v = x[j * EPL + q];
+      if (nd.surv) {
+        const bool s = v >= t;
+        const uint64_t bmk = __ballot(s);
+        if (bmk != 0ull) {
+          const uint32_t p = cnt + lanes_below(bmk);
+          if (s && p < (uint32_t)kSurvCap) surv[p] = cand_key(okey(v), (uint32_t)(c0 + li0 + q));
+          cnt += (uint32_t)__popcll(bmk);
+        }
+      }
+      if (nd.lse) rest += v < t ? __builtin_amdgcn_exp2f((v - m) * a2) : 0.f;
+    }
+    if (cfg.store_s) {
+      float svl[EPL];
+      #pragma unroll
+      for (int q = 0; q < EPL; ++q) {
+        const float v = x[j * EPL + q];
+        svl[q] = finitef_(v) ? v / cfg.t_eff : -__builtin_inff();
+      }
+      float* dst = a.ws_s + (int64_t)row * a.V + c0 + li0;
+      const uint32_t hb = (hv.on && li0 < len) ? (hv.bitmap[li0 >> 5] >> (li0 & 31)) & EMASK : 0u;
+      if (li0 + EPL <= len && hb == 0u && ((a.V & 3) == 0)) {
+        #pragma unroll
+        for (int q = 0; q < EPL; q += 4) *(float4*)(dst + q) = make_float4(svl[q], svl[q + 1], svl[q + 2], svl[q + 3]);
+      } else {
+        #pragma unroll
+        for (int q = 0; q < EPL; ++q) if (li0 + q < len && !((hb >> q) & 1u)) dst[q] = svl[q];
+      }
+    }
+  }
+  #pragma unroll
+  for (int i = 0; i < kSelOb; ++i) {
+    const float v = in.ob[i];
+    if (nd.surv) {
+      const bool s = v >= t;
+      const uint64_t bmk = __ballot(s);
+      if (bmk != 0ull) {
+        const uint32_t p = cnt + lanes_below(bmk);
+        if (s && p < (uint32_t)kSurvCap) surv[p] = cand_key(okey(v), in.obi[i]);
+        cnt += (uint32_t)__popcll(bmk);
+      }
+    }
+    if (nd.lse) rest += v < t ? __builtin_amdgcn_exp2f((v - m) * a2) : 0.f;
+    if (cfg.store_s && (uint32_t)(i * NT + tid) < in.n_ob)
+      a.ws_s[(int64_t)row * a.V + in.obi[i]] = finitef_(v) ? v / cfg.t_eff : -__builtin_inff();
+  }
+  if (nd.lse) rest = wave_sum_f32(rest);
+  if (lane == 0u) { L.wcnt[wid] = cnt; L.redf[wid] = rest; }
+  __syncthreads();
+  uint32_t n = 0u;
+  #pragma unroll
+  for (int w = 0; w < NT / 64; ++w) { n += L.wcnt[w]; rare |= L.wcnt[w] > (uint32_t)kSurvCap ? 1u : 0u; }
+  if (rare) return false;
+  if (wid != 0) return true;
+
+  // wave 0: the chunk's top k_sel of the survivors, argmaxes, record
+  Segs<NT / 64> sg;
+  float rs = 0.f;
+  #pragma unroll
+  for (int w = 0; w < NT / 64; ++w) { sg.p[w] = L.surv[w]; sg.n[w] = L.wcnt[w]; rs += L.redf[w]; }
+  sg.ns = NT / 64;
+  const uint32_t k = (uint32_t)cfg.k_sel;
+  uint64_t thr = 0ull;
+  if (nd.sel && n > k) thr = wave_select_skip(sg, k, L.hist);
+  const uint32_t mkey = okey(m);
+  uint64_t* cand = a.cand + slot * kFast;
+  uint32_t wpos = 0u, unkept = 0u;
+  uint64_t minkept = ~0ull, best = 0ull, finb = ~0ull;
+  float urest = 0.f;
+  #pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    const uint32_t nw = sg.n[w];
+    for (uint32_t b0 = 0; b0 < nw; b0 += 64u) {
+      const uint32_t i = b0 + lane;
+      const bool valid = i < nw;
+      const uint64_t e = valid ? sg.p[w][i] : 0ull;
+      const bool keep = valid && nd.sel && e >= thr;
+      const uint64_t km = __ballot(keep);
+      if (keep) {
+        cand[wpos + lanes_below(km)] = e;
+        minkept = e < minkept ? e : minkept;
+      }
+      wpos += (uint32_t)__popcll(km);
+      if (valid) {
+        best = e > best ? e : best;
+        if (cand_skey(e) == mkey) {
+          const uint32_t idx = cand_idx(e);
+          const uint64_t fk = ((uint64_t)(idx & 255u) << 32) | idx;
+          finb = fk < finb ? fk : finb;
+        }
+        if (nd.sel && !keep) {
+          unkept = max(unkept, cand_skey(e));
+          if (nd.lse) urest += __builtin_amdgcn_exp2f((okey_inv(cand_skey(e)) - m) * a2);
+        }
+      }
+    }
+  }
+  minkept = wave_min_u64(minkept);
+  best = wave_max_u64(best);
+  finb = wave_min_u64(finb);
+  unkept = wave_max_u32(unkept);
+  if (nd.lse) urest = wave_sum_f32(urest);
+  if (lane == 0u) {
+    ChunkStat bs;
+    stat_init(bs);
+    bs.max_l = m;
+    bs.any_finite = 1u;
+    if (nd.sel) {
+      bs.n_cand = wpos;
+      bs.trunc = (uint32_t)len > k ? 1u : 0u;
+      bs.min_kept = minkept;
+      bs.unkept_key = max(unkept, n < (uint32_t)len ? tk - 1u : 0u);
+      bs.lse_m = m / cfg.t_eff;
+      bs.lse_sum = nd.lse ? rs + urest : 0.f;
+    }
+    if (nd.ieee) { bs.am_ieee_v = m; bs.am_ieee_i = cand_idx(best); }
+    if (nd.fin) { bs.am_fin_v = m; bs.am_fin_i = (uint32_t)finb; }
+    a.stats[slot] = bs;
+  }
+  return true;
+}
+
+// The streaming select pass.  DT: logit dtype; NL: 16-byte loads per
+// thread; MASK: an allowed-token bitmask is given.
+template <int DT, int NL, bool MASK>
+__global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  SelLds& L = *reinterpret_cast<SelLds*>(lds_raw);
+  constexpr int EPL = DT == HI_ROCM_DTYPE_BF16 ? 8 : 4;  // logits per 16-byte load
+  constexpr int ESZ = DT == HI_ROCM_DTYPE_BF16 ? 2 : 4;
+  constexpr int E = NL * EPL;                             // logits per thread
+  constexpr int CH = NT * E;
+  static_assert(E % 4 == 0 && CH % 32 == 0, "chunk shape");
+  const int tid = threadIdx.x;
+  const int row = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int c0 = chunk * CH;
+  const int len = min(CH, a.V - c0);
+  const int64_t slot = (int64_t)row * a.n_chunks + chunk;
+
+  // 1. the row's history list, then the chunk's logits and mask words
+  uint32_t h0 = 0u, h1 = 0u;
+  uint32_t hid[kSelHistPer], hcs[kSelHistPer];
+  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; }
+  #pragma unroll
+  for (int r = 0; r < kSelHistPer; ++r) {
+    const uint32_t h = h0 + (uint32_t)(r * NT + tid);
+    hid[r] = h < h1 ? a.hids[h] : 0xffffffffu;
+    hcs[r] = h < h1 ? a.hcnt[h] : 0u;
+  }
+  const RowBuf rb = row_buf<DT, MASK>(a, row, c0, c0 + len);
+  SelIn<NL> in;
+  #pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int li0 = (j * NT + tid) * EPL;
+    in.raw[j] = __builtin_amdgcn_raw_buffer_load_b128(rb.logits, li0 * ESZ, 0, 0);
+    if (MASK) in.mw[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb.mask, (li0 >> 5) * 4, 0, 0);
+  }
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  const SelNeeds nd = sel_needs(a, cfg);
+
+  // 2. history table, then the out-of-band history logits
+  const SelHist hv = stage_history_sel(a, c0, len, EPL, reinterpret_cast<uint32_t*>(lds_raw + kSelHead), L.hw, hid,
+                                       hcs, h0, h1);
+  in.n_ob = hv.on ? min(hv.distinct, kSelHistCap) : 0u;
+  uint32_t obm[kSelOb];
+  #pragma unroll
+  for (int i = 0; i < kSelOb; ++i) {
+    const uint32_t r = (uint32_t)(i * NT + tid);
+    in.obi[i] = r < in.n_ob ? hv.ids[r] : (uint32_t)c0;
+    const uint32_t li = in.obi[i] - (uint32_t)c0;
+    in.ob[i] = load_one<DT>(rb, li);
+    obm[i] = MASK ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rb.mask, (li >> 5) * 4, 0, 0) >> (li & 31u) : 1u;
+  }
+  #pragma unroll
+  for (int i = 0; i < kSelOb; ++i) {
+    const uint32_t r = (uint32_t)(i * NT + tid);
+    if (r < in.n_ob) {
+      const float l = (obm[i] & 1u) ? in.ob[i] : -__builtin_inff();
+      in.ob[i] = apply_penalties(l, hv.cnts[r], cfg);
+    } else {
+      in.ob[i] = __builtin_nanf("");
+    }
+  }
+
+  // 3. the chunk's logits as floats: mask as -inf, past the range absent
+  float x[E];
+  #pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int li0 = (j * NT + tid) * EPL;
+    float v[EPL];
+    unpack16<DT, EPL>(in.raw[j], v);
+    if (MASK) {
+      const uint32_t bits = in.mw[j] >> (li0 & 31);
+      #pragma unroll
+      for (int q = 0; q < EPL; ++q) v[q] = ((bits >> q) & 1u) ? v[q] : -__builtin_inff();
+    }
+    if (len != CH) {
+      #pragma unroll
+      for (int q = 0; q < EPL; ++q) v[q] = li0 + q < len ? v[q] : __builtin_nanf("");
+    }
+    #pragma unroll
+    for (int q = 0; q < EPL; ++q) x[j * EPL + q] = v[q];
+  }
+
+  // 4. the row's path
+  bool done;
+  if (cfg.store_s) {
+    done = select_wide<DT, NL, MASK>(L, a, cfg, nd, x, in, hv, row, c0, len, slot);
+  } else if (hv.ovf) {
+    done = false;
+  } else {
+    done = select_lean<DT, NL, MASK>(L, a, cfg, nd, rb, x, in, hv, c0, len, slot);
+  }
+  if (done) return;
+  __syncthreads();
+  select_exact(L, a, cfg, hv, nd, row, c0, len, slot);
+}
+
+// LDS of the general scan kernel.
 size_t generic_chunk_lds_bytes(int chunk, bool hist) {
   return ((sizeof(ScanLds) + 15) & ~(size_t)15) +
          (hist ? (size_t)chunk / 8 + 2 * kHashCap * sizeof(uint32_t) : 0);
 }
-constexpr size_t kRowUnionBytes =
-    ((sizeof(FinLds) > sizeof(LeanLds<kRowThreads / 64>) ? sizeof(FinLds) : sizeof(LeanLds<kRowThreads / 64>)) + 15) &
-    ~(size_t)15;
-size_t row_lds_bytes(int V, bool hist) {
-  return kRowUnionBytes + (hist ? hist_lds_bytes(V, kRowHistCap) : 0);
-}
-constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
-template <int NTH, int VEC, int D, int DT, bool MASK>
-__device__ __forceinline__ void scan_lean_dispatch(const SampleArgs& a, const RowCfg& cfg, LeanLds<NTH / 64>& L,
-                                                   const RowBuf& rb, float (&tl)[D][VEC * 4],
-                                                   uint32_t (&tmw)[D][VEC], const HistView& hv, int row,
-                                                   int64_t slot, int c0, int c1) {
-  if (hv.on && hv.ovf) scan_lean<NTH, VEC, D, DT, MASK, true>(a, cfg, L, rb, tl, tmw, hv, row, slot, c0, c1);
-  else scan_lean<NTH, VEC, D, DT, MASK, false>(a, cfg, L, rb, tl, tmw, hv, row, slot, c0, c1);
-}
-
-// One workgroup per (chunk, row): the lean pass over a chunk, finished by
-// finish_kernel.  Used when a row's history table does not fit the row
-// kernel's LDS.
-template <int VEC, int TILES, int DT, bool MASK>
-__global__ void __launch_bounds__(NT) scan_kernel(SampleArgs a) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  constexpr int CH = NT * VEC * 4 * TILES;
-  static_assert(CH <= 65536, "chunk");
-  const int row = blockIdx.y;
-  const int chunk = blockIdx.x;
-  const int c0 = chunk * CH;
-  const int c1 = min(c0 + CH, a.V);
-  // every load of the chunk is issued first, so that the parameter and
-  // history reads below overlap them
-  const RowBuf rb = row_buf<DT, MASK>(a, row, c0, c1);
-  float tl[TILES][VEC * 4];
-  uint32_t tmw[TILES][VEC];
-  #pragma unroll
-  for (int t = 0; t < TILES; ++t) buf_load<NT, VEC, DT, MASK>(rb, t * NT * VEC * 4, tl[t], tmw[t]);
-  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
-  HistView hv;
-  hv.on = false;
-  hv.ovf = false;
-  if (a.hoff)
-    hv = stage_history_rank<NT>(a, row, c0, c1 - c0, kChunkHistCap,
-                                reinterpret_cast<uint32_t*>(lds_raw + ((sizeof(LeanLds<NT / 64>) + 15) & ~(size_t)15)));
-  scan_lean_dispatch<NT, VEC, TILES, DT, MASK>(a, cfg, *reinterpret_cast<LeanLds<NT / 64>*>(lds_raw), rb, tl, tmw,
-                                               hv, row, (int64_t)row * a.n_chunks + chunk, c0, c1);
-}
-
-// One workgroup per row: kRowThreads threads stream the whole row with D
-// tiles of loads in flight per thread; then the waves past the first four
-// end (a barrier waits only for the waves still running) and the first four
-// finish the row in place (the row is one chunk for the finish code).
-template <int VEC, int D, int DT, bool MASK>
-__global__ void __launch_bounds__(kRowThreads) row_kernel(SampleArgs a) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  constexpr int NTH = kRowThreads;
-  constexpr int TILE = NTH * VEC * 4;
-  const int row = blockIdx.x;
-  const int V = a.V;
-  const RowBuf rb = row_buf<DT, MASK>(a, row, 0, V);
-  float tl[D][VEC * 4];
-  uint32_t tmw[D][VEC];
-  #pragma unroll
-  for (int t = 0; t < D; ++t) buf_load<NTH, VEC, DT, MASK>(rb, t * TILE, tl[t], tmw[t]);
-  const RowCfg cfg = load_cfg(a.pv, row, V, a.n_lp, a.need_lse);
-  HistView hv;
-  hv.on = false;
-  hv.ovf = false;
-  if (a.hoff)
-    hv = stage_history_rank<NTH>(a, row, 0, V, kRowHistCap, reinterpret_cast<uint32_t*>(lds_raw + kRowUnionBytes));
-  scan_lean_dispatch<NTH, VEC, D, DT, MASK>(a, cfg, *reinterpret_cast<LeanLds<NTH / 64>*>(lds_raw), rb, tl, tmw,
-                                            hv, row, row, 0, V);
-  if (threadIdx.x >= NT) return;
-  __syncthreads();  // the row's record and candidates are visible to the workgroup
-  finish_row(*reinterpret_cast<FinLds*>(lds_raw), a, row, cfg);
-}
-
-// The general pass with a block-level running selection of up to kFast
-// candidates per chunk: used when more than kLeanK logprobs are requested.
 template <int VEC, int TILES>
 __global__ void __launch_bounds__(NT) scan_generic_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -2452,6 +2940,8 @@ __global__ void __launch_bounds__(NT) finish_kernel(SampleArgs a) {
   __shared__ FinLds fs;
   const int row = blockIdx.x;
   const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  if (finish_lean(fs, a, row, cfg)) return;
+  __syncthreads();
   finish_row(fs, a, row, cfg);
 }
 
@@ -2580,80 +3070,64 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
 // --------------------------------------------------------------------------
 // launch wrappers (called from the host API)
 
-bool row_mode(int V, int n_lp, int vec_ok, bool hist) {
-  return n_lp <= kLeanK && vec_ok && row_lds_bytes(V, hist) <= kMaxLds;
-}
+// Chunks of the streaming select pass: 64 logits per thread when the batch
+// alone gives at least 4 workgroups per CU, 16 otherwise.
+constexpr int kSelChunkLarge = NT * 64;
+constexpr int kSelChunkSmall = NT * 16;
+
+bool select_mode(int n_lp, int vec_ok) { return n_lp <= kLeanK && vec_ok; }
 
 int choose_chunk(int B, int V, int n_lp, int vec_ok, bool hist) {
-  // one workgroup per row when the row fits the row kernel's LDS;
-  // otherwise chunks: fewer, larger ones when the batch alone fills the GPU
-  if (row_mode(V, n_lp, vec_ok, hist)) return V;
+  (void)hist;
+  if (select_mode(n_lp, vec_ok)) {
+    const long wg_large = (long)B * ((V + kSelChunkLarge - 1) / kSelChunkLarge);
+    return wg_large >= 1024 ? kSelChunkLarge : kSelChunkSmall;
+  }
   const long wg_large = (long)B * ((V + kChunk - 1) / kChunk);
   return wg_large >= 512 ? kChunk : kChunkSmall;
 }
 
-// Dynamic LDS above 64 KiB needs the kernel's attribute raised once.
-template <typename K>
-hipError_t allow_lds(K kernel, size_t bytes) {
-  if (bytes <= 65536) return hipSuccess;
-  return hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-}
-
 hipError_t launch_chunked(const SampleArgs& a, hipStream_t stream) {
   const bool hist = a.hoff != nullptr;
-  const bool large = a.chunk == kChunk;
   dim3 grid(a.n_chunks, a.B);
-  if (a.n_lp > kLeanK || !a.vec_ok) {
-    if (large)
-      hipLaunchKernelGGL((scan_generic_kernel<kVecLarge, kTilesLarge>), grid, dim3(NT),
-                         generic_chunk_lds_bytes(kChunk, hist), stream, a);
-    else
-      hipLaunchKernelGGL((scan_generic_kernel<kVecSmall, 1>), grid, dim3(NT),
-                         generic_chunk_lds_bytes(kChunkSmall, hist), stream, a);
-  } else {
-    constexpr int TL = kChunk / (NT * kLeanVec * 4);
-    constexpr int TS = kChunkSmall / (NT * kLeanVec * 4);
-    static_assert(TL * NT * kLeanVec * 4 == kChunk && TS * NT * kLeanVec * 4 == kChunkSmall, "chunk sizes");
-    const size_t lds = lean_chunk_lds_bytes(large ? kChunk : kChunkSmall, hist);
-#define HI_ROCM_LAUNCH_LEAN(DT, M)                                                                   \
-  do {                                                                                              \
-    if (large) hipLaunchKernelGGL((scan_kernel<kLeanVec, TL, DT, M>), grid, dim3(NT), lds, stream, a); \
-    else hipLaunchKernelGGL((scan_kernel<kLeanVec, TS, DT, M>), grid, dim3(NT), lds, stream, a);       \
-  } while (0)
-    if (a.dtype == HI_ROCM_DTYPE_BF16) {
-      if (a.mask) HI_ROCM_LAUNCH_LEAN(HI_ROCM_DTYPE_BF16, true);
-      else HI_ROCM_LAUNCH_LEAN(HI_ROCM_DTYPE_BF16, false);
-    } else {
-      if (a.mask) HI_ROCM_LAUNCH_LEAN(HI_ROCM_DTYPE_F32, true);
-      else HI_ROCM_LAUNCH_LEAN(HI_ROCM_DTYPE_F32, false);
-    }
-#undef HI_ROCM_LAUNCH_LEAN
-  }
+  if (a.chunk == kChunk)
+    hipLaunchKernelGGL((scan_generic_kernel<kVecLarge, kTilesLarge>), grid, dim3(NT),
+                       generic_chunk_lds_bytes(kChunk, hist), stream, a);
+  else
+    hipLaunchKernelGGL((scan_generic_kernel<kVecSmall, 1>), grid, dim3(NT),
+                       generic_chunk_lds_bytes(kChunkSmall, hist), stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(finish_kernel, dim3(a.B), dim3(NT), 0, stream, a);
   return hipGetLastError();
 }
 
-constexpr int kRowDepth = 4;  // tiles of loads in flight per thread
-
-template <int DT, bool MASK>
-hipError_t launch_row_t(const SampleArgs& a, hipStream_t stream) {
-  const size_t lds = row_lds_bytes(a.V, a.hoff != nullptr);
-  auto kern = row_kernel<kLeanVec, kRowDepth, DT, MASK>;
-  hipError_t e = allow_lds(kern, lds);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(a.B), dim3(kRowThreads), lds, stream, a);
+template <int DT, int NL, bool MASK>
+hipError_t launch_select_t(const SampleArgs& a, hipStream_t stream) {
+  constexpr int E = NL * (DT == HI_ROCM_DTYPE_BF16 ? 8 : 4);
+  const size_t lds = kSelHead + (a.hoff ? sel_hist_bytes(NT * E) : 0);
+  hipLaunchKernelGGL((select_kernel<DT, NL, MASK>), dim3(a.n_chunks, a.B), dim3(NT), lds, stream, a);
   return hipGetLastError();
 }
 
+template <int DT, bool MASK>
+hipError_t launch_select_d(const SampleArgs& a, hipStream_t stream) {
+  constexpr int EPL = DT == HI_ROCM_DTYPE_BF16 ? 8 : 4;
+  if (a.chunk == kSelChunkLarge) return launch_select_t<DT, kSelChunkLarge / NT / EPL, MASK>(a, stream);
+  return launch_select_t<DT, kSelChunkSmall / NT / EPL, MASK>(a, stream);
+}
+
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
-  if (a.n_chunks == 1 && a.chunk == a.V && row_mode(a.V, a.n_lp, a.vec_ok, a.hoff != nullptr)) {
-    if (a.dtype == HI_ROCM_DTYPE_BF16)
-      return a.mask ? launch_row_t<HI_ROCM_DTYPE_BF16, true>(a, stream) : launch_row_t<HI_ROCM_DTYPE_BF16, false>(a, stream);
-    return a.mask ? launch_row_t<HI_ROCM_DTYPE_F32, true>(a, stream) : launch_row_t<HI_ROCM_DTYPE_F32, false>(a, stream);
-  }
-  return launch_chunked(a, stream);
+  if (!select_mode(a.n_lp, a.vec_ok) || (a.chunk != kSelChunkLarge && a.chunk != kSelChunkSmall))
+    return launch_chunked(a, stream);
+  hipError_t e;
+  if (a.dtype == HI_ROCM_DTYPE_BF16)
+    e = a.mask ? launch_select_d<HI_ROCM_DTYPE_BF16, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_BF16, false>(a, stream);
+  else
+    e = a.mask ? launch_select_d<HI_ROCM_DTYPE_F32, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_F32, false>(a, stream);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(finish_kernel, dim3(a.B), dim3(NT), 0, stream, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_argmax(const float* logits, uint32_t* out, int B, int64_t row_stride,

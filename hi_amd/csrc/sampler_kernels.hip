@@ -115,16 +115,20 @@ __device__ __forceinline__ int next_pow2(int x) {
 
 __device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V, int n_lp, int need_lse) {
   RowCfg c;
+  // The batch-wide values first; the per-row modes replace them.  (Every
+  // field is defined before the mode branches: a three-way if/else-if here
+  // has been compiled for gfx950 with top_k undefined on the uniform path.)
+  c.T = pv.T; c.top_p = pv.top_p; c.top_k = pv.top_k;
   c.min_p = 0.f; c.rep = 1.f; c.freq = 0.f; c.pres = 0.f; c.eos = 0u; c.flags = 0u;
-  if (pv.mode == kParamsRows) {
+  const int mode = pv.mode;
+  if (mode == kParamsSoA) {
+    c.T = pv.temps[row]; c.top_p = pv.top_ps[row]; c.top_k = pv.top_ks[row];
+  }
+  if (mode == kParamsRows) {
     const hi_rocm_row_params p = pv.rows[row];
     c.T = p.temperature; c.top_p = p.top_p; c.min_p = p.min_p;
     c.rep = p.repetition_penalty; c.freq = p.frequency_penalty; c.pres = p.presence_penalty;
     c.top_k = p.top_k; c.eos = p.eos_id; c.flags = p.flags;
-  } else if (pv.mode == kParamsSoA) {
-    c.T = pv.temps[row]; c.top_p = pv.top_ps[row]; c.top_k = pv.top_ks[row];
-  } else {
-    c.T = pv.T; c.top_p = pv.top_p; c.top_k = pv.top_k;
   }
   const bool greedy = !(finitef_(c.T) && c.T > 0.f);
   const bool minp_on = finitef_(c.min_p) && c.min_p > 0.f;
@@ -167,11 +171,110 @@ __device__ __forceinline__ float apply_penalties(float l, uint32_t cnt, const Ro
   return l;
 }
 
-// ---- block-level reductions (wave64 shuffles, then LDS) -------------------
+// ---- wave-wide reductions and scans on DPP lane moves ---------------------
+//
+// A reduction combines each lane with its quad neighbours (quad_perm), then
+// the mirrored lanes of its half row and row (row_half_mirror, row_mirror),
+// so that every lane of a 16-lane row holds the row's result; row_bcast:15
+// and row_bcast:31 then fold the rows into lane 63, which readlane hands to
+// every lane.  The scan is the Hillis-Steele sequence row_shr:1,2,4,8
+// followed by the same two row broadcasts.  Each step is one VALU
+// instruction with no LDS round trip.
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+constexpr int kDppShr1 = 0x111;        // row_shr:1 (+1, +3, +7 for :2, :4, :8)
+constexpr int kDppBcast15 = 0x142;     // row_bcast:15
+constexpr int kDppBcast31 = 0x143;     // row_bcast:31
+
+// v moved by CTRL; lanes of rows outside ROW_MASK (or with no source lane
+// when BC) get `old`.
+template <int CTRL, int ROW_MASK = 0xf, bool BC = false>
+__device__ __forceinline__ uint32_t dpp32(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xf, BC);
+}
+
+// Reduction of a 32-bit value under a commutative, associative op with
+// identity `id`.
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce32(uint32_t v, uint32_t id, Op op) {
+  v = op(v, dpp32<kDppXor1>(id, v));
+  v = op(v, dpp32<kDppXor2>(id, v));
+  v = op(v, dpp32<kDppHalfMirror>(id, v));
+  v = op(v, dpp32<kDppMirror>(id, v));
+  v = op(v, dpp32<kDppBcast15, 0xa>(id, v));
+  v = op(v, dpp32<kDppBcast31, 0xc>(id, v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// The same for 64-bit values (both halves move together).
+template <typename Op>
+__device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, uint64_t id, Op op) {
+  const uint32_t il = (uint32_t)id, ih = (uint32_t)(id >> 32);
+  auto step = [&](auto mov) {
+    const uint64_t t = ((uint64_t)mov(ih, (uint32_t)(v >> 32)) << 32) | mov(il, (uint32_t)v);
+    v = op(v, t);
+  };
+  step([](uint32_t o, uint32_t x) { return dpp32<kDppXor1>(o, x); });
+  step([](uint32_t o, uint32_t x) { return dpp32<kDppXor2>(o, x); });
+  step([](uint32_t o, uint32_t x) { return dpp32<kDppHalfMirror>(o, x); });
+  step([](uint32_t o, uint32_t x) { return dpp32<kDppMirror>(o, x); });
+  step([](uint32_t o, uint32_t x) { return dpp32<kDppBcast15, 0xa>(o, x); });
+  step([](uint32_t o, uint32_t x) { return dpp32<kDppBcast31, 0xc>(o, x); });
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  return __uint_as_float(wave_reduce32(__float_as_uint(v), 0xff800000u, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
+}
+// Sum in a fixed tree order (deterministic).
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  return __uint_as_float(wave_reduce32(__float_as_uint(v), 0u, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return wave_reduce32(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  return wave_reduce32(v, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  return wave_reduce64(v, 0ull, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  return wave_reduce64(v, ~0ull, [](uint64_t a, uint64_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  return __longlong_as_double((long long)wave_reduce64((uint64_t)__double_as_longlong(v), 0ull, [](uint64_t a, uint64_t b) {
+    return (uint64_t)__double_as_longlong(__longlong_as_double((long long)a) + __longlong_as_double((long long)b));
+  }));
+}
+
+// Inclusive prefix sum over the wave in lane order.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  v += dpp32<kDppShr1, 0xf, true>(0u, v);
+  v += dpp32<kDppShr1 + 1, 0xf, true>(0u, v);
+  v += dpp32<kDppShr1 + 3, 0xf, true>(0u, v);
+  v += dpp32<kDppShr1 + 7, 0xf, true>(0u, v);
+  v += dpp32<kDppBcast15, 0xa>(0u, v);
+  v += dpp32<kDppBcast31, 0xc>(0u, v);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_last_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// ---- block-level reductions (DPP within each wave, then LDS) --------------
 
 template <int N>
 __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = wave_sum_u32(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wid] = v;
@@ -183,7 +286,7 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
 
 template <int N>
 __device__ __forceinline__ float block_sum_f32(float v, float* red) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = wave_sum_f32(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wid] = v;
@@ -195,7 +298,7 @@ __device__ __forceinline__ float block_sum_f32(float v, float* red) {
 
 template <int N>
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = wave_sum_f64(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wid] = v;
@@ -207,7 +310,7 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
 
 template <int N>
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
-  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor(v, o, 64));
+  v = wave_max_u32(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wid] = v;
@@ -223,39 +326,9 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Wave-wide reductions (every lane gets the result).
-__device__ __forceinline__ float wave_max_f32(float v) {
-  #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum_f32(float v) {
-  #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) { const uint64_t t = shfl_xor_u64(v, o); v = t > v ? t : v; }
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-  #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) { const uint64_t t = shfl_xor_u64(v, o); v = t < v ? t : v; }
-  return v;
-}
-
 template <int N>
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t t = shfl_xor_u64(v, o);
-    if (t > v) v = t;
-  }
+  v = wave_max_u64(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wid] = v;
@@ -274,11 +347,7 @@ __device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* red) {
 template <int N>
 __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* red, uint32_t* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  uint32_t inc = v;
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t t = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += t;
-  }
+  const uint32_t inc = wave_incl_scan_u32(v);
   __syncthreads();
   if (lane == 63) red[wid] = inc;
   __syncthreads();
@@ -403,11 +472,7 @@ __device__ __forceinline__ uint64_t radix_select_top(uint32_t* hist, uint32_t* s
       uint32_t loc[4], lsum = 0;
       #pragma unroll
       for (int q = 0; q < 4; ++q) { loc[q] = hist[255 - 4 * tid - q]; lsum += loc[q]; }
-      uint32_t inc = lsum;
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(inc, o, 64);
-        if (tid >= o) inc += t;
-      }
+      const uint32_t inc = wave_incl_scan_u32(lsum);
       const uint32_t above = inc - lsum;
       if (above < remaining && remaining <= above + lsum) {
         uint32_t acc = above;
@@ -1164,11 +1229,7 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
       uint32_t loc[4], lsum = 0;
       #pragma unroll
       for (int q = 0; q < 4; ++q) { loc[q] = hist[255 - 4 * tid - q]; lsum += loc[q]; }
-      uint32_t inc = lsum;
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(inc, o, 64);
-        if (tid >= o) inc += t;
-      }
+      const uint32_t inc = wave_incl_scan_u32(lsum);
       const uint32_t above = inc - lsum;
       if (above < remaining && remaining <= above + lsum) {
         uint32_t acc = above;
@@ -1193,6 +1254,173 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
 
 constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
 
+// Sequential f32 sums over the wave's lanes: lane l returns
+// ((start + v_0) + v_1) + ... + v_l, the reference's left-to-right fold
+// (gpu.rs:834-836, 851, 878, 889-896).  64 dependent steps: each moves the
+// running sums one lane up (wave_shr:1; lane 0 takes `start`) and adds.
+__device__ __forceinline__ float wave_fold_f32(float v, float start) {
+  float p = start + v;
+  #pragma unroll
+  for (int s = 1; s < 64; ++s)
+    p = __uint_as_float(dpp32<0x138>(__float_as_uint(start), __float_as_uint(p))) + v;
+  return p;
+}
+
+// Steps 4-9 of the lean finish over the candidates fs.cbig[0, n) of `row`
+// (candidate keys, any order; n >= 1).  M is the row max of s; ub_key bounds
+// the processed-logit keys of the row's logits that are not candidates (0:
+// none); part is this thread's share of the logprob normaliser over those
+// logits (double, relative to M).  Returns false when the row needs the
+// general finish; all threads return the same.
+__device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, int n,
+                                            float M, uint32_t ub_key, double part) {
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const bool want_lp = a.n_lp > 0 || a.out_token_lp != nullptr;
+  if (want_lp) {
+    // the candidates' share, in double (fixed order)
+    for (int j = tid; j < n; j += NT) {
+      const uint32_t kv = cand_skey(fs.cbig[j]);
+      if (kv > kKeyNegInf) part += exp((double)key_to_s(kv, cfg.t_eff) - (double)M);
+    }
+  }
+
+  // 4. the top kk by (processed logit desc, index asc)
+  const int kk = min(cfg.k_sel, n);
+  uint64_t thr = 0ull;
+  if (n > kk) thr = block_select_skip(fs.cbig, n, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b);
+  if (tid == 0) fs.counter = 0u;
+  __syncthreads();
+  uint64_t below = 0ull;  // largest candidate left out
+  for (int j = tid; j < n; j += NT) {
+    const uint64_t x = fs.cbig[j];
+    if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
+    else below = x > below ? x : below;
+  }
+  below = block_max_u64<NT>(below, fs.red64);  // has barriers: fs.buf is complete
+
+  // 5. weights and rank keys; the smallest selected weight w_b
+  uint64_t rk = 0ull;
+  uint32_t pk = 0u;
+  uint32_t wbits = 0xffffffffu;
+  if (tid < kk) {
+    const uint64_t x = fs.buf[tid];
+    const float sx = key_to_s(cand_skey(x), cfg.t_eff);
+    const float w = exact_expf(sx - M);
+    rk = rank_key(w, cand_idx(x));
+    pk = okey(sx);
+    wbits = __float_as_uint(w);
+  }
+  const float w_b = __uint_as_float(~block_max_u32<NT>(~wbits, fs.redu));
+  // 6. could a logit outside the selection tie with w_b?  Weights are
+  //    monotone in the key, so the largest excluded key decides (finish_row
+  //    resolves those rows exactly).
+  const uint32_t xk = max(ub_key, below != 0ull ? cand_skey(below) : 0u);
+  if (w_b > 0.f && xk > kKeyNegInf && exact_expf(key_to_s(xk, cfg.t_eff) - M) == w_b) return false;
+
+  // 7. rank order by counting (kk <= NT: one entry per thread)
+  if (tid < kk) fs.buf[tid] = rk;
+  __syncthreads();
+  if (tid < kk) {
+    uint32_t r = 0u;
+    for (int j = 0; j < kk; ++j) r += fs.buf[j] > rk;
+    fs.cbig[r] = rk;
+    fs.aux[r] = pk;
+  }
+  __syncthreads();
+
+  // 8. the draw, by every wave from registers (gpu.rs:831-899)
+  const int k = min(cfg.k_eff, kk);
+  constexpr int DM = kLeanK / 64;
+  float fa[DM], pa[DM], fb[DM], qa[DM];
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const float w = i < k ? rank_w(fs.cbig[i]) : 0.f;
+    fa[m] = w < cfg.min_p ? 0.f : w;  // min-p: excluded like w <= 0 (gpu.rs:847-849)
+  }
+  // P_i: the sequential sum of fa[0..i]: the total of gpu.rs:834-836 (the
+  // kept weights in rank order) and, at positive entries, the candidate
+  // total and CDF of gpu.rs:874-896 (min-p zeros sit at the end)
+  float P = -0.0f;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    if (m * 64 < k) {
+      pa[m] = wave_fold_f32(fa[m], P);
+      P = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), min(63, k - 1 - m * 64)));
+    } else {
+      pa[m] = P;
+    }
+  }
+  const float total = P;
+  if (!(total > 0.f) || !finitef_(total)) return false;  // argmax_host fallback
+  // the nucleus: cum_p over w / total of the positive entries (gpu.rs:843-856)
+  float Q = 0.f;
+  int m_end = 0;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    fb[m] = fa[m] > 0.f ? fa[m] / total : 0.f;
+    qa[m] = Q;
+    if (m * 64 < k) {
+      qa[m] = wave_fold_f32(fb[m], Q);
+      Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(qa[m]), min(63, k - 1 - m * 64)));
+    }
+    (void)i;
+  }
+  int last_pos = -1;   // last positive entry
+  int cut = -1;        // first positive entry where cum_p reaches the cutoff
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const bool pos = i < k && fa[m] > 0.f;
+    const uint64_t pm = __ballot(pos);
+    if (pm != 0ull) last_pos = m * 64 + 63 - __clzll((unsigned long long)pm);
+    const uint64_t cm = __ballot(pos && cfg.cutoff < 1.f && qa[m] >= cfg.cutoff);
+    if (cut < 0 && cm != 0ull) cut = m * 64 + __ffsll((unsigned long long)cm) - 1;
+  }
+  if (last_pos < 0) return false;  // no candidate: argmax_host fallback
+  m_end = cut >= 0 ? cut + 1 : last_pos + 1;
+  const int me = m_end - 1;
+  float ct = 0.f;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m)
+    if ((me >> 6) == m) ct = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), me & 63));
+  if (!(ct > 0.f) || !finitef_(ct)) return false;
+  // inverse CDF: the first candidate whose cumulative weight passes target
+  const float target = clamp_uniform(row_uniform(a.pv, row)) * ct;
+  int pick = -1;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const uint64_t hit = __ballot(i < m_end && fa[m] > 0.f && target < pa[m]);
+    if (pick < 0 && hit != 0ull) pick = m * 64 + __ffsll((unsigned long long)hit) - 1;
+  }
+  if (pick < 0) pick = me;
+  const uint32_t token = cand_idx(fs.cbig[pick]);
+  if (tid == 0) a.out_tokens[row] = token;
+  if (!want_lp) return true;
+
+  // 9. logprobs of the processed distribution (extension)
+  const double log_sum = log(block_sum_f64<NT>(part, fs.redd));
+  const int N = a.n_lp;
+  for (int j = tid; j < N; j += NT) {
+    float lp = -__builtin_inff();
+    uint32_t id = 0xffffffffu;
+    if (j < kk) {
+      id = cand_idx(fs.cbig[j]);
+      lp = (float)(((double)okey_inv(fs.aux[j]) - (double)M) - log_sum);
+    }
+    a.out_lp_ids[(int64_t)row * N + j] = id;
+    a.out_lp[(int64_t)row * N + j] = lp;
+  }
+  if (a.out_token_lp && tid == 0)
+    a.out_token_lp[row] = (float)(((double)okey_inv(fs.aux[pick]) - (double)M) - log_sum);
+  return true;
+}
+
+// Lean finish of the chunk pass: merges the chunk records and gathers their
+// candidates, then finish_core.
 __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg) {
   const int tid = threadIdx.x;
   const uint32_t lane = (uint32_t)tid & 63u;
@@ -1205,16 +1433,16 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   const int nch = a.n_chunks;
   if (nch > kLeanChunks) return false;
   const ChunkStat* stats = a.stats + (int64_t)row * nch;
-  const int k_sel = cfg.k_sel;
 
   // 1. the chunk records, merged by every wave on its own; candidate counts
-  //    and their chunk-major offsets
+  //    and their chunk-major offsets; the largest key left out of them
   constexpr int CQ = kLeanChunks / 64;
   float mx = -__builtin_inff();
-  uint32_t anyf = 0u;
+  uint32_t anyf = 0u, ub = 0u;
   float iv = -__builtin_inff(), fv = -__builtin_inff();
   uint32_t ii = 0xffffffffu, fi = 0xffffffffu;
   uint32_t cnt[CQ];
+  double part = 0.0;  // the other logits' share of the logprob normaliser
   #pragma unroll
   for (int q = 0; q < CQ; ++q) {
     const int c = q * 64 + (int)lane;
@@ -1224,6 +1452,7 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
     cnt[q] = cs.n_cand;
     mx = fmaxf(mx, cs.max_l);
     anyf |= cs.any_finite;
+    if (cs.trunc) ub = max(ub, cs.unkept_key);
     if (cs.am_ieee_i != 0xffffffffu &&
         (ii == 0xffffffffu || cs.am_ieee_v > iv || (cs.am_ieee_v == iv && cs.am_ieee_i < ii))) {
       iv = cs.am_ieee_v; ii = cs.am_ieee_i;
@@ -1237,22 +1466,29 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
       if (take) { fv = cs.am_fin_v; fi = cs.am_fin_i; }
     }
   }
-  #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    anyf |= (uint32_t)__shfl_xor((int)anyf, o, 64);
-    const float ov = __shfl_xor(iv, o, 64);
-    const uint32_t oi = (uint32_t)__shfl_xor((int)ii, o, 64);
-    if (oi != 0xffffffffu && (ii == 0xffffffffu || ov > iv || (ov == iv && oi < ii))) { iv = ov; ii = oi; }
-    const float pv = __shfl_xor(fv, o, 64);
-    const uint32_t pi = (uint32_t)__shfl_xor((int)fi, o, 64);
-    if (pi != 0xffffffffu) {
-      bool take = fi == 0xffffffffu || pv > fv;
-      if (!take && pv == fv) {
-        const uint32_t ra = fi & 255u, rb = pi & 255u;
-        take = rb < ra || (rb == ra && pi < fi);
-      }
-      if (take) { fv = pv; fi = pi; }
+  mx = wave_max_f32(mx);
+  anyf = wave_reduce32(anyf, 0u, [](uint32_t x, uint32_t y) { return x | y; });
+  ub = wave_max_u32(ub);
+  // argmax merges as 64-bit keys: IEEE (value desc, index asc) and the
+  // finite-lane rule (value desc, index mod 256 asc, index asc)
+  {
+    // -0 and +0 compare equal under IEEE '>': both map to the +0 key
+    const float iz = iv == 0.f ? 0.f : iv;
+    const uint64_t ik = ii == 0xffffffffu ? 0ull
+                        : ((uint64_t)okey(iz) << 32) | (uint64_t)(0xffffffffu - ii);
+    const uint64_t best = wave_max_u64(ik);
+    ii = best == 0ull ? 0xffffffffu : 0xffffffffu - (uint32_t)best;
+  }
+  {
+    const float fz = fv == 0.f ? 0.f : fv;
+    const uint64_t fk = fi == 0xffffffffu ? 0ull
+                        : ((uint64_t)okey(fz) << 32) | (uint64_t)(0xffffffffu - (((fi & 255u) << 23) | (fi >> 8)));
+    const uint64_t best = wave_max_u64(fk);
+    if (best == 0ull) {
+      fi = 0xffffffffu;
+    } else {
+      const uint32_t c = 0xffffffffu - (uint32_t)best;
+      fi = ((c & 0x7fffffu) << 8) | (c >> 23);
     }
   }
   const bool eos = a.mask && !anyf;
@@ -1265,18 +1501,22 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   }
   const float M = finitef_(mx) ? mx / cfg.t_eff : -__builtin_inff();
   if (eos || !finitef_(M)) return false;
+  if (want_lp && tid < 64) {
+    #pragma unroll
+    for (int q = 0; q < CQ; ++q) {
+      const int c = q * 64 + (int)lane;
+      if (c >= nch) continue;
+      const ChunkStat& cs = stats[c];
+      if (cs.lse_sum > 0.f) part += (double)cs.lse_sum * exp((double)cs.lse_m - (double)M);
+    }
+  }
   uint32_t offq[CQ];  // exclusive offset of chunk q * 64 + lane
   uint32_t n_total = 0u;
   #pragma unroll
   for (int q = 0; q < CQ; ++q) {
-    uint32_t incl = cnt[q];
-    #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t t = (uint32_t)__shfl_up((int)incl, o, 64);
-      if (lane >= (uint32_t)o) incl += t;
-    }
+    const uint32_t incl = wave_incl_scan_u32(cnt[q]);
     offq[q] = n_total + incl - cnt[q];
-    n_total += (uint32_t)__shfl((int)incl, 63, 64);
+    n_total += wave_last_u32(incl);
   }
   if (n_total > (uint32_t)kGather || n_total == 0u) return false;
   if (tid < 64) {
@@ -1307,149 +1547,7 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
     }
   }
   __syncthreads();
-  double part = 0.0;  // the candidates' share of the logprob normaliser
-  if (want_lp) {
-    #pragma unroll
-    for (int r = 0; r < kFinPer; ++r) {
-      const uint32_t j = (uint32_t)(tid + r * NT);
-      if (j < n_total && cand_skey(cr[r]) > kKeyNegInf)
-        part += exp((double)key_to_s(cand_skey(cr[r]), cfg.t_eff) - (double)M);
-    }
-  }
-
-  // 4. the top kk by (processed logit desc, index asc)
-  const int kk = min(k_sel, (int)n_total);
-  uint64_t thr = 0ull;
-  if ((int)n_total > kk) thr = block_select_skip(fs.cbig, (int)n_total, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b);
-  if (tid == 0) fs.counter = 0u;
-  __syncthreads();
-  uint64_t below = 0ull;  // largest candidate left out
-  for (int j = tid; j < (int)n_total; j += NT) {
-    const uint64_t x = fs.cbig[j];
-    if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
-    else below = x > below ? x : below;
-  }
-  below = block_max_u64<NT>(below, fs.red64);  // has barriers: fs.buf is complete
-
-  // 5. weights in rank order keys; the smallest selected weight w_b
-  uint64_t rk = 0ull;
-  uint32_t pk = 0u;
-  uint32_t wbits = 0xffffffffu;
-  if (tid < kk) {
-    const uint64_t x = fs.buf[tid];
-    const float sx = key_to_s(cand_skey(x), cfg.t_eff);
-    const float w = exact_expf(sx - M);
-    rk = rank_key(w, cand_idx(x));
-    pk = okey(sx);
-    wbits = __float_as_uint(w);
-  }
-  const float w_b = __uint_as_float(~block_max_u32<NT>(~wbits, fs.redu));
-  // 6. could a logit outside the candidates tie with w_b?  (finish_row
-  //    resolves those rows exactly)
-  uint32_t tie = 0u;
-  if (w_b > 0.f) {
-    if (tid == 0 && below != 0ull && exact_expf(key_to_s(cand_skey(below), cfg.t_eff) - M) == w_b) tie = 1u;
-    for (int c = tid; c < nch; c += NT) {
-      const ChunkStat& cs = stats[c];
-      if (cs.trunc && exact_expf(key_to_s(cs.unkept_key, cfg.t_eff) - M) == w_b) tie = 1u;
-    }
-  }
-  if (tid < kk) fs.buf[tid] = rk;
-  if (block_max_u32<NT>(tie, fs.redu)) return false;  // has barriers: rank keys are visible
-
-  // 7. rank order by counting (kk <= NT: one entry per thread)
-  if (tid < kk) {
-    uint32_t r = 0u;
-    for (int j = 0; j < kk; ++j) r += fs.buf[j] > rk;
-    fs.cbig[r] = rk;
-    fs.aux[r] = pk;
-  }
-  __syncthreads();
-
-  // 8. the draw, by every wave from registers (gpu.rs:831-899)
-  const int k = min(cfg.k_eff, kk);
-  constexpr int DM = kLeanK / 64;
-  float fa[DM], pa[DM];
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int i = m * 64 + (int)lane;
-    const float w = i < k ? rank_w(fs.cbig[i]) : 0.f;
-    fa[m] = w < cfg.min_p ? 0.f : w;
-    pa[m] = 0.f;
-  }
-  // P_i: the sequential f32 sum of fa[0..i] (gpu.rs:834-836 total, and the
-  // candidate total and CDF walk of gpu.rs:874-896 at positive entries; the
-  // zero entries of min-p sit at the end of the rank order)
-  float P = -0.0f;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int cnt = min(64, k - m * 64);
-    for (int l = 0; l < cnt; ++l) {
-      P = P + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa[m]), l));
-      pa[m] = lane == (uint32_t)l ? P : pa[m];
-    }
-  }
-  const float total = P;
-  if (!(total > 0.f) || !finitef_(total)) return false;  // argmax_host fallback
-  // the nucleus: cum_p over w / total in rank order (gpu.rs:843-856)
-  float fb[DM];
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) fb[m] = fa[m] / total;
-  float Q = 0.f;
-  int m_end = 0;
-  bool stop = false;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int cnt = stop ? 0 : min(64, k - m * 64);
-    for (int l = 0; l < cnt; ++l) {
-      if (!(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa[m]), l)) > 0.f)) continue;
-      m_end = m * 64 + l + 1;
-      Q += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb[m]), l));
-      if (cfg.cutoff < 1.f && Q >= cfg.cutoff) { stop = true; break; }
-    }
-  }
-  if (m_end == 0) return false;  // no candidate: argmax_host fallback
-  const int me = m_end - 1;
-  float ct = 0.f;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m)
-    if ((me >> 6) == m) ct = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pa[m]), me & 63));
-  if (!(ct > 0.f) || !finitef_(ct)) return false;
-  // inverse CDF: the first candidate whose cumulative weight passes target
-  const float target = clamp_uniform(row_uniform(a.pv, row)) * ct;
-  int pick = -1;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int i = m * 64 + (int)lane;
-    const uint64_t hit = __ballot(i < m_end && target < pa[m]);
-    if (pick < 0 && hit != 0ull) pick = m * 64 + __ffsll((unsigned long long)hit) - 1;
-  }
-  if (pick < 0) pick = me;
-  const uint32_t token = cand_idx(fs.cbig[pick]);
-  if (tid == 0) a.out_tokens[row] = token;
-  if (!want_lp) return true;
-
-  // 9. logprobs of the processed distribution (extension): the normaliser
-  //    from the candidates (above) and each chunk's other logits
-  for (int c = tid; c < nch; c += NT) {
-    const ChunkStat& cs = stats[c];
-    if (cs.lse_sum > 0.f) part += (double)cs.lse_sum * exp((double)cs.lse_m - (double)M);
-  }
-  const double log_sum = log(block_sum_f64<NT>(part, fs.redd));
-  const int N = a.n_lp;
-  for (int j = tid; j < N; j += NT) {
-    float lp = -__builtin_inff();
-    uint32_t id = 0xffffffffu;
-    if (j < kk) {
-      id = cand_idx(fs.cbig[j]);
-      lp = (float)(((double)okey_inv(fs.aux[j]) - (double)M) - log_sum);
-    }
-    a.out_lp_ids[(int64_t)row * N + j] = id;
-    a.out_lp[(int64_t)row * N + j] = lp;
-  }
-  if (a.out_token_lp && tid == 0)
-    a.out_token_lp[row] = (float)(((double)okey_inv(fs.aux[pick]) - (double)M) - log_sum);
-  return true;
+  return finish_core(fs, a, row, cfg, (int)n_total, M, ub, part);
 }
 
 // ==========================================================================
@@ -1710,12 +1808,7 @@ __device__ __forceinline__ uint64_t wave_select(const Segs<NS>& sg, uint32_t nee
     const uint4 h = *reinterpret_cast<const uint4*>(hist + 252 - 4 * lane);
     const uint32_t cs[4] = {h.w, h.z, h.y, h.x};
     const uint32_t lsum = cs[0] + cs[1] + cs[2] + cs[3];
-    uint32_t inc = lsum;
-    #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t t = (uint32_t)__shfl_up((int)inc, o, 64);
-      if (lane >= (uint32_t)o) inc += t;
-    }
+    const uint32_t inc = wave_incl_scan_u32(lsum);
     uint32_t acc = inc - lsum, d = 0, da = 0, dc = 0;
     #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -2204,12 +2297,7 @@ __device__ __forceinline__ uint64_t wave_select_skip(const Segs<NS>& sg, uint32_
     const uint4 h = *reinterpret_cast<const uint4*>(hist + 252 - 4 * lane);
     const uint32_t cs[4] = {h.w, h.z, h.y, h.x};
     const uint32_t lsum = cs[0] + cs[1] + cs[2] + cs[3];
-    uint32_t inc = lsum;
-    #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t t = (uint32_t)__shfl_up((int)inc, o, 64);
-      if (lane >= (uint32_t)o) inc += t;
-    }
+    const uint32_t inc = wave_incl_scan_u32(lsum);
     uint32_t acc = inc - lsum, d = 0, da = 0, dc = 0;
     #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -2448,14 +2536,9 @@ __device__ __forceinline__ bool select_lean(SelLds& L, const SampleArgs& a, cons
   uint32_t mkey = 0u;
   uint32_t wtot;
   {
-    uint32_t incl = nob;
-    #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t tv = (uint32_t)__shfl_up((int)incl, o, 64);
-      if (lane >= (uint32_t)o) incl += tv;
-    }
+    const uint32_t incl = wave_incl_scan_u32(nob);
     uint32_t pos = incl - nob;
-    wtot = (uint32_t)__shfl((int)incl, 63, 64);
+    wtot = wave_last_u32(incl);
     #pragma unroll
     for (int i = 0; i < kSelOb; ++i) {
       if (in.ob[i] >= t) {
@@ -2493,13 +2576,8 @@ __device__ __forceinline__ bool select_lean(SelLds& L, const SampleArgs& a, cons
       sok |= take ? (1u << s) : 0u;
     }
     const uint32_t mine = (uint32_t)__popc(sok);
-    uint32_t incl = mine;
-    #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t tv = (uint32_t)__shfl_up((int)incl, o, 64);
-      if (lane >= (uint32_t)o) incl += tv;
-    }
-    const uint32_t rtot = (uint32_t)__shfl((int)incl, 63, 64);
+    const uint32_t incl = wave_incl_scan_u32(mine);
+    const uint32_t rtot = wave_last_u32(incl);
     if (wtot + rtot <= (uint32_t)kSurvCap) {
       uint32_t pos = wtot + incl - mine;
       #pragma unroll
@@ -2807,11 +2885,11 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
   return true;
 }
 
-// The streaming select pass.  DT: logit dtype; NL: 16-byte loads per
-// thread; MASK: an allowed-token bitmask is given.
+// One (chunk, row) of the streaming select pass, by one workgroup.  DT:
+// logit dtype; NL: 16-byte loads per thread; MASK: an allowed-token bitmask
+// is given.  lds_raw holds SelLds and the history table.
 template <int DT, int NL, bool MASK>
-__global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
-  extern __shared__ __align__(16) unsigned char lds_raw[];
+__device__ __forceinline__ void select_chunk(const SampleArgs& a, int row, int chunk, unsigned char* lds_raw) {
   SelLds& L = *reinterpret_cast<SelLds*>(lds_raw);
   constexpr int EPL = DT == HI_ROCM_DTYPE_BF16 ? 8 : 4;  // logits per 16-byte load
   constexpr int ESZ = DT == HI_ROCM_DTYPE_BF16 ? 2 : 4;
@@ -2819,8 +2897,6 @@ __global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
   constexpr int CH = NT * E;
   static_assert(E % 4 == 0 && CH % 32 == 0, "chunk shape");
   const int tid = threadIdx.x;
-  const int row = blockIdx.y;
-  const int chunk = blockIdx.x;
   const int c0 = chunk * CH;
   const int len = min(CH, a.V - c0);
   const int64_t slot = (int64_t)row * a.n_chunks + chunk;
@@ -2902,6 +2978,13 @@ __global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
   if (done) return;
   __syncthreads();
   select_exact(L, a, cfg, hv, nd, row, c0, len, slot);
+}
+
+// The streaming select pass: workgroup (chunk, row).
+template <int DT, int NL, bool MASK>
+__global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  select_chunk<DT, NL, MASK>(a, blockIdx.y, blockIdx.x, lds_raw);
 }
 
 // LDS of the general scan kernel.

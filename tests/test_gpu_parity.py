@@ -151,6 +151,49 @@ def test_reference_device_grid_via_abi(hip, oracle):
     assert cases >= 200
 
 
+@pytest.mark.parametrize("B,V", [(128, 129280), (3, 151936)])
+def test_uniform_launchers_every_chunk_shape(hip, oracle, B, V):
+    """Batch-wide parameters (kernels.cu:14737-14880 launchers) on the
+    streaming pass's large chunks (B=128: 1024 workgroups) and small ones,
+    against the host ranked sampler row by row; then the per-row SoA
+    launcher on the same rows."""
+    torch = _torch()
+    lib = hip.load()
+    stream = torch.cuda.Stream()
+    rng = np.random.default_rng(B * 7 + V)
+    x = (rng.standard_normal((B, V)) * 3.0).astype(F32)
+    u = rng.random(B).astype(F32)
+    logits, samples = dev(x), dev(u)
+    out = torch.zeros(B, dtype=torch.int32, device="cuda")
+    for t, tp, tk in ((0.7, float("inf"), 1), (1.0, 0.9, 40), (0.8, 0.95, 0), (1.2, float("inf"), 200),
+                       (1.0, 0.5, 2000)):
+        with torch.cuda.stream(stream):
+            hip.check(lib.hi_rocm_launch_sample_batched_last_token(
+                logits.data_ptr(), out.data_ptr(), samples.data_ptr(), B, 1, V, t, tp, tk, 1,
+                stream.cuda_stream))
+        stream.synchronize()
+        got = out.cpu().numpy().view(np.uint32).tolist()
+        want = [oracle.ranked_sample(x[b], t, tp, tk or None, float(u[b])) for b in range(B)]
+        say(f"uniform B={B} V={V} t={t} tp={tp} tk={tk}")
+        assert got == want, [(b, g, w_) for b, (g, w_) in enumerate(zip(got, want)) if g != w_][:8]
+        temps = dev(np.full(B, t, F32))
+        tps = dev(np.full(B, tp, F32))
+        tks = dev(np.full(B, tk, np.int32))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            hip.check(lib.hi_rocm_launch_select_batched_last_token_per_row(
+                logits.data_ptr(), out.data_ptr(), samples.data_ptr(), temps.data_ptr(),
+                tps.data_ptr(), tks.data_ptr(), B, 1, V, 1, stream.cuda_stream))
+        stream.synchronize()
+        assert out.cpu().numpy().view(np.uint32).tolist() == want
+    # the single-row launcher: the last row of a [rows, V] matrix
+    with torch.cuda.stream(stream):
+        hip.check(lib.hi_rocm_launch_sample_last_row(
+            logits.data_ptr(), out.data_ptr(), B, V, 0.9, 0.8, 50, float(u[0]), stream.cuda_stream))
+    stream.synchronize()
+    assert int(out[0].item()) & 0xffffffff == oracle.ranked_sample(x[B - 1], 0.9, 0.8, 50, float(u[0]))
+
+
 def test_reference_host_grid_per_row(hip, oracle):
     """gpu.rs:29582-29633 grid as one heterogeneous batch per vocabulary,
     through the C++ mirror of select_batched_last_token_per_row."""

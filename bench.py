@@ -80,6 +80,63 @@ def time_large_batch(torch, w, steps, warmup):
     return total_ms / steps, per, wall, out
 
 
+def time_parts(torch, w, steps):
+    """Per-part device time of a step: the library records hipEvents on the
+    launch stream before the pass over the logits, between it and the
+    finish, and after the finish (hi_rocm_profile_begin / _end)."""
+    import ctypes
+    from hi_amd import _lib
+    lib = _lib.load()
+    smp, a = _prepare(torch, w)
+    stream = torch.cuda.Stream()
+    out = None
+    with torch.cuda.stream(stream):
+        for _ in range(5):
+            out = _step(smp, a, w, out, stream)
+    torch.cuda.synchronize()
+    _lib.check(lib.hi_rocm_profile_begin(steps))
+    with torch.cuda.stream(stream):
+        for _ in range(steps):
+            out = _step(smp, a, w, out, stream)
+    p, f, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
+    _lib.check(lib.hi_rocm_profile_end(ctypes.byref(p), ctypes.byref(f), ctypes.byref(n)))
+    assert n.value == steps, (n.value, steps)
+    return p.value * 1000.0 / steps, f.value * 1000.0 / steps
+
+
+def pmc_probe(torch, w, steps, copy_mib=512):
+    """Workload for the rocprofv3 --pmc passes: C3 steps, then one plain
+    device copy of copy_mib MiB whose FETCH_SIZE / WRITE_SIZE calibrate the
+    counters (a copy reads and writes exactly its size)."""
+    smp, a = _prepare(torch, w)
+    stream = torch.cuda.Stream()
+    out = None
+    with torch.cuda.stream(stream):
+        for _ in range(steps):
+            out = _step(smp, a, w, out, stream)
+    torch.cuda.synchronize()
+    n = copy_mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_probe": w.name, "steps": steps, "copy_bytes": n * 4}))
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the pass over the logits, measured by the
+    committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by a
+    copy of known size), or None when no summary is present."""
+    path = os.path.join(ROOT, "profiles", "select_kernel_c3_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].strip())
+    return None
+
+
 def time_graph_b1(torch, w, steps, warmup):
     """B=1: one hipGraph replay per step (the step has no host sync)."""
     smp, a = _prepare(torch, w)
@@ -114,7 +171,7 @@ def time_graph_b1(torch, w, steps, warmup):
     return graph_us, eager_us
 
 
-def cpu_baseline(w, budget_s=12.0):
+def cpu_baseline(w, budget_s=15.0):
     """The oracle (a C restatement of the reference CPU sampler plus the
     extension stages), single thread, rows processed serially like the
     reference's host loop.  Bounded sample: rows of the same workload until
@@ -125,7 +182,7 @@ def cpu_baseline(w, budget_s=12.0):
     rows_done = 0
     t0 = time.perf_counter()
     b = 0
-    while time.perf_counter() - t0 < budget_s and rows_done < 4 * B:
+    while time.perf_counter() - t0 < budget_s:
         sel = slice(b, b + 1)
         h = None
         if w.hist_offsets is not None:
@@ -148,7 +205,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run C3 steps then a plain copy of known size, for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}): the sampler's rows are "
@@ -161,12 +220,20 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     w3 = config3()
+    if args.pmc_probe:
+        pmc_probe(torch, w3, args.steps)
+        return
     ms, per, wall, _ = time_large_batch(torch, w3, args.steps, args.warmup)
     rows_per_s = w3.batch / (ms / 1000.0)
     alg_bytes = w3.algorithmic_bytes()
     achieved = alg_bytes / (ms / 1000.0) / 1e9
+    pass_us, finish_us = time_parts(torch, w3, args.steps)
     w1 = config1()
     b1_graph_us, b1_eager_us = time_graph_b1(torch, w1, max(args.steps, 100), 20)
+    b1_pass_us, b1_finish_us = time_parts(torch, w1, max(args.steps, 100))
+    # the dominant kernel of the C3 step: the pass over the logits (it reads
+    # every algorithmic byte of the step)
+    kernel_gbs = alg_bytes / (pass_us * 1e-6) / 1e9
 
     res = {
         "metric": METRIC,
@@ -190,11 +257,14 @@ def main():
         "b1_us_per_step_graph": b1_graph_us,
         "b1_us_per_step_eager": b1_eager_us,
         "b1_workload": w1.name,
-        "hbm_fraction": achieved / HBM_PEAK_GBS,
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "sampler step (scan_chunks + finish_rows)",
-                     "algorithmic_bytes_per_step": alg_bytes},
+        "b1_kernel_us": {"select_pass": b1_pass_us, "finish": b1_finish_us},
+        "step_hbm_fraction": achieved / HBM_PEAK_GBS,
+        "step_kernel_us": {"select_pass": pass_us, "finish": finish_us},
+        "roofline": {"bound": "hbm", "achieved": kernel_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": kernel_gbs / HBM_PEAK_GBS, "traffic": traffic_from_profile(),
+                     "kernel": "hi_rocm::select_kernel<0, 16, false> (C3 pass over the logits)",
+                     "kernel_avg_us": pass_us,
+                     "algorithmic_bytes_per_launch": alg_bytes},
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w3, args.cpu_budget)

@@ -46,6 +46,9 @@ SIGNATURES = {
     "hi_rocm_launch_select_batched_last_token_per_row": (
         _i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "hi_rocm_sampler_reserve": (_i, [_i, _i, _i]),
+    "hi_rocm_profile_begin": (_i, [_i]),
+    "hi_rocm_profile_end": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(_i)]),
     "hi_rocm_sampler_workspace_bytes": (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
     "hi_rocm_sample": (_i, [_vp, _i, _i, _i, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                             _vp, _i, _vp, _sz, _vp]),

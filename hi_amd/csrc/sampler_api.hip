@@ -12,6 +12,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "hi_rocm.h"
 #include "sampler_internal.h"
@@ -94,13 +95,35 @@ hi_rocm::SampleArgs base_args(const void* logits, int dtype, int B, int V, int64
 }
 
 // Run the two sampling kernels with the library workspace.
+// Measurement hook state of the calling thread: one set of events per
+// sampler call while a profile is open (hi_rocm_profile_begin / _end).
+struct ProfileState {
+  std::vector<hi_rocm::LaunchEvents> events;
+  size_t used = 0;
+  bool open = false;
+};
+thread_local ProfileState g_prof;
+
+const hi_rocm::LaunchEvents* next_events() {
+  if (!g_prof.open || g_prof.used >= g_prof.events.size()) return nullptr;
+  return &g_prof.events[g_prof.used++];
+}
+
+void destroy_events() {
+  for (auto& le : g_prof.events)
+    for (hipEvent_t ev : le.ev) (void)hipEventDestroy(ev);
+  g_prof.events.clear();
+  g_prof.used = 0;
+  g_prof.open = false;
+}
+
 int run_with_internal_ws(hi_rocm::SampleArgs& a, hipStream_t stream) {
   const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(a.B, a.V);
   void* ws = nullptr;
   int rc = internal_workspace(L.total, &ws);
   if (rc != HI_ROCM_OK) return rc;
   carve(a, ws, L);
-  hipError_t e = hi_rocm::launch_sample(a, stream);
+  hipError_t e = hi_rocm::launch_sample(a, stream, next_events());
   if (e != hipSuccess) return hip_fail(e, "sampler launch");
   return HI_ROCM_OK;
 }
@@ -281,8 +304,51 @@ int hi_rocm_sample(const void* logits, int dtype, int batch, int vocab, int64_t 
   a.out_lp_ids = out_logprob_ids;
   a.out_token_lp = out_token_logprobs;
   carve(a, workspace, L);
-  hipError_t e = hi_rocm::launch_sample(a, (hipStream_t)stream);
+  hipError_t e = hi_rocm::launch_sample(a, (hipStream_t)stream, next_events());
   if (e != hipSuccess) return hip_fail(e, "sampler launch");
+  return HI_ROCM_OK;
+}
+
+int hi_rocm_profile_begin(int max_calls) {
+  if (max_calls <= 0) return fail(HI_ROCM_ERR_ARGS, "hi_rocm_profile_begin: max_calls <= 0");
+  destroy_events();
+  g_prof.events.resize((size_t)max_calls);
+  for (auto& le : g_prof.events) {
+    for (hipEvent_t& ev : le.ev) {
+      hipError_t e = hipEventCreate(&ev);
+      if (e != hipSuccess) {
+        ev = nullptr;
+        destroy_events();
+        return hip_fail(e, "hipEventCreate");
+      }
+    }
+  }
+  g_prof.open = true;
+  return HI_ROCM_OK;
+}
+
+int hi_rocm_profile_end(double* pass_ms, double* finish_ms, int* calls) {
+  if (pass_ms == nullptr || finish_ms == nullptr || calls == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_profile_end: null output");
+  if (!g_prof.open) return fail(HI_ROCM_ERR_ARGS, "hi_rocm_profile_end: no open profile");
+  double p = 0.0, f = 0.0;
+  for (size_t i = 0; i < g_prof.used; ++i) {
+    const hi_rocm::LaunchEvents& le = g_prof.events[i];
+    hipError_t e = hipEventSynchronize(le.ev[2]);
+    float a = 0.f, b = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&a, le.ev[0], le.ev[1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&b, le.ev[1], le.ev[2]);
+    if (e != hipSuccess) {
+      destroy_events();
+      return hip_fail(e, "profile events");
+    }
+    p += a;
+    f += b;
+  }
+  *pass_ms = p;
+  *finish_ms = f;
+  *calls = (int)g_prof.used;
+  destroy_events();
   return HI_ROCM_OK;
 }
 

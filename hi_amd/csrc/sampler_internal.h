@@ -143,7 +143,14 @@ inline WorkspaceLayout workspace_layout(int max_batch, int V) {
   return L;
 }
 
-hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
+// Measurement hook: when given, the launcher records ev[0] before its first
+// kernel, ev[1] after the pass over the logits and ev[2] after the finish,
+// all on the launch stream (ev[1] == ev[2] for a one-kernel step).
+struct LaunchEvents {
+  hipEvent_t ev[3];
+};
+
+hipError_t launch_sample(const SampleArgs& a, hipStream_t stream, const LaunchEvents* le = nullptr);
 hipError_t launch_argmax(const float* logits, uint32_t* out, int B, int64_t row_stride,
                          int64_t row_offset, int cols, hipStream_t stream);
 hipError_t launch_debug_expf(const float* x, float* y, int64_t n, hipStream_t stream);

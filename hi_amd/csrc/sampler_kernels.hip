@@ -3170,19 +3170,27 @@ int choose_chunk(int B, int V, int n_lp, int vec_ok, bool hist) {
   return wg_large >= 512 ? kChunk : kChunkSmall;
 }
 
-hipError_t launch_chunked(const SampleArgs& a, hipStream_t stream) {
+hipError_t record(const LaunchEvents* le, int i, hipStream_t stream) {
+  return le ? hipEventRecord(le->ev[i], stream) : hipSuccess;
+}
+
+hipError_t launch_chunked(const SampleArgs& a, hipStream_t stream, const LaunchEvents* le) {
   const bool hist = a.hoff != nullptr;
   dim3 grid(a.n_chunks, a.B);
+  hipError_t e = record(le, 0, stream);
+  if (e != hipSuccess) return e;
   if (a.chunk == kChunk)
     hipLaunchKernelGGL((scan_generic_kernel<kVecLarge, kTilesLarge>), grid, dim3(NT),
                        generic_chunk_lds_bytes(kChunk, hist), stream, a);
   else
     hipLaunchKernelGGL((scan_generic_kernel<kVecSmall, 1>), grid, dim3(NT),
                        generic_chunk_lds_bytes(kChunkSmall, hist), stream, a);
-  hipError_t e = hipGetLastError();
+  e = hipGetLastError();
+  if (e == hipSuccess) e = record(le, 1, stream);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(finish_kernel, dim3(a.B), dim3(NT), 0, stream, a);
-  return hipGetLastError();
+  e = hipGetLastError();
+  return e == hipSuccess ? record(le, 2, stream) : e;
 }
 
 template <int DT, int NL, bool MASK>
@@ -3200,17 +3208,20 @@ hipError_t launch_select_d(const SampleArgs& a, hipStream_t stream) {
   return launch_select_t<DT, kSelChunkSmall / NT / EPL, MASK>(a, stream);
 }
 
-hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
+hipError_t launch_sample(const SampleArgs& a, hipStream_t stream, const LaunchEvents* le) {
   if (!select_mode(a.n_lp, a.vec_ok) || (a.chunk != kSelChunkLarge && a.chunk != kSelChunkSmall))
-    return launch_chunked(a, stream);
-  hipError_t e;
+    return launch_chunked(a, stream, le);
+  hipError_t e = record(le, 0, stream);
+  if (e != hipSuccess) return e;
   if (a.dtype == HI_ROCM_DTYPE_BF16)
     e = a.mask ? launch_select_d<HI_ROCM_DTYPE_BF16, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_BF16, false>(a, stream);
   else
     e = a.mask ? launch_select_d<HI_ROCM_DTYPE_F32, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_F32, false>(a, stream);
+  if (e == hipSuccess) e = record(le, 1, stream);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(finish_kernel, dim3(a.B), dim3(NT), 0, stream, a);
-  return hipGetLastError();
+  e = hipGetLastError();
+  return e == hipSuccess ? record(le, 2, stream) : e;
 }
 
 hipError_t launch_argmax(const float* logits, uint32_t* out, int B, int64_t row_stride,

@@ -175,6 +175,16 @@ int hi_rocm_debug_distribution(const void* logits, int dtype, int batch, int voc
  * dsv4_gpu.rs:7332 for its own device expf. */
 int hi_rocm_debug_expf(const float* x, float* y, int64_t n, void* stream);
 
+/* Measurement hooks (no counterpart in the reference; for benchmarks).
+ * hi_rocm_profile_begin opens a profile on the calling thread: each of its
+ * next max_calls sampler calls records three hipEvents on its own stream,
+ * before its first kernel, between the pass over the logits and the finish,
+ * and after the finish.  hi_rocm_profile_end waits for them, returns the
+ * summed durations of the two parts (ms) and the number of calls recorded,
+ * and closes the profile.  Not for use under stream capture. */
+int hi_rocm_profile_begin(int max_calls);
+int hi_rocm_profile_end(double* pass_ms, double* finish_ms, int* calls);
+
 /* Thread-local message for the last non-zero status. */
 const char* hi_rocm_last_error(void);
 

@@ -1270,10 +1270,11 @@ __device__ __forceinline__ float wave_fold_f32(float v, float start) {
 // (candidate keys, any order; n >= 1).  M is the row max of s; ub_key bounds
 // the processed-logit keys of the row's logits that are not candidates (0:
 // none); part is this thread's share of the logprob normaliser over those
-// logits (double, relative to M).  Returns false when the row needs the
+// logits (double, relative to M); when n exceeds the selection size, its
+// last key must be above `above`.  Returns false when the row needs the
 // general finish; all threads return the same.
 __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, int n,
-                                            float M, uint32_t ub_key, double part) {
+                                            float M, uint32_t ub_key, double part, uint32_t above = 0u) {
   const int tid = threadIdx.x;
   const uint32_t lane = (uint32_t)tid & 63u;
   const bool want_lp = a.n_lp > 0 || a.out_token_lp != nullptr;
@@ -1289,6 +1290,9 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   const int kk = min(cfg.k_sel, n);
   uint64_t thr = 0ull;
   if (n > kk) thr = block_select_skip(fs.cbig, n, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b);
+  // the caller's candidates hold the row's top kk only if the kk-th key is
+  // above `above` (the largest key the caller may have left out)
+  if (n > kk && cand_skey(thr) <= above) return false;
   if (tid == 0) fs.counter = 0u;
   __syncthreads();
   uint64_t below = 0ull;  // largest candidate left out
@@ -3158,6 +3162,441 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
 constexpr int kSelChunkLarge = NT * 64;
 constexpr int kSelChunkSmall = NT * 16;
 
+// ==========================================================================
+// Row kernel: one workgroup streams a whole row and finishes it in place
+// ==========================================================================
+//
+// For large batches (kRowMinBatch rows or more, f32 logits, no logprobs) one
+// workgroup of kRowThreads per row replaces the select pass and the finish
+// kernel.  Sixteen waves share a CU (four per SIMD), so one wave's LDS
+// round trips and branches overlap the others' work and loads.
+//  - The row's history is staged once in LDS: per 32 logits a word of
+//    marks and the number of marked logits before it, and the summed count
+//    and id of every distinct history token by rank.
+//  - The row streams through a register pipeline kRowDepth tiles deep per
+//    wave (tile = kRowTile logits, 16-byte loads); per logit the common case
+//    is one max.
+//  - Each wave keeps the top kw of its own logits (by candidate key) in an
+//    LDS list, kw = ceil(k/16) + ceil(sqrt(k)) + 4: a logit whose key passes
+//    the wave's threshold is appended, and when the list passes kRowHW
+//    entries the wave keeps its kw largest and raises the threshold to the
+//    last one's key.  A later logit with that key has a larger index and
+//    ranks below all kept ones, so the test is strict.  The first tile
+//    starts from a bound of the wave's group maxima instead of -inf.
+//  - History tokens are captured from the stream by rank (their logits are
+//    processed after it) and kept out of the test.
+//  - Every logit left out has a key at or below the largest wave threshold
+//    Tm, so the union of the lists and the processed history logits above
+//    Tm holds the row's top k whenever its k-th key is above Tm (a wave
+//    holding more than kw of the row's top k breaks that and sends the row
+//    to the general path; with kw at mean + 4 sd of that count it does not
+//    happen for rows whose top tokens are spread over the vocabulary).
+// The first four waves then run finish_core; the others end there.  Rows the
+// fast path does not cover (other row classes, more than kRowHistCap
+// distinct history tokens, a list overflow, no finite logit, a tie
+// finish_core will not resolve) run the chunk select and the finish of the
+// two-kernel path inside the same workgroup, on its first four waves.
+
+constexpr int kRowThreads = 1024;
+constexpr int kRowWaves = kRowThreads / 64;
+constexpr int kRowTV = 2;                             // 16-byte loads per thread per tile
+constexpr int kRowEl = kRowTV * 4;                    // logits per thread per tile
+constexpr int kRowTile = kRowThreads * kRowEl;        // 8192 logits
+constexpr int kRowDepth = 4;                          // tiles in flight per wave
+constexpr int kRowHW = 128;                           // list length that triggers a selection
+constexpr int kRowCap = 256;                          // list capacity (past it: general path)
+constexpr int kRowHistCap = 2048;                     // distinct history tokens per row
+constexpr int kRowHistPer = kRowHistCap / kRowThreads;  // history entries per thread in registers
+constexpr int kRowMaxV = 1 << 18;
+constexpr int kRowMinBatch = 192;
+constexpr int kRowKwMax = kLeanK / 16 + 16 + 4;       // kw at k = kLeanK (sqrt(256) = 16)
+static_assert(kRowKwMax < kRowHW, "a full list holds more than kw entries");
+
+struct RowLds {
+  uint64_t wbuf[kRowWaves][kRowCap];   // per-wave candidate lists
+  uint32_t ob_raw[kRowHistCap];        // logit (mask applied) of the history token of rank r
+  uint32_t ob_cnt[kRowHistCap];        // its summed count
+  uint32_t ob_id[kRowHistCap];         // its id
+  float xscr[kRowWaves][64 * kRowEl];  // a wave's tile, when a branch needs single logits
+  // the fields below stay valid while the finish reuses the space above
+  uint32_t whist[kRowWaves][256];
+  uint32_t wthr[kRowWaves];
+  uint32_t wbad[kRowWaves];
+  uint32_t redu[kRowWaves];
+  uint64_t red64[kRowWaves];
+};
+constexpr size_t kRowHead = (sizeof(RowLds) + 15) & ~(size_t)15;
+static_assert(sizeof(FinLds) <= offsetof(RowLds, whist), "finish LDS must fit the stream's lists");
+
+// Keeps the `need` largest entries of the wave's list (unique keys,
+// need <= n) at its front; returns the key of the last one kept.
+__device__ __forceinline__ uint32_t row_wave_keep(uint64_t* wl, uint32_t& n, uint32_t need, uint32_t* hist) {
+  const uint32_t lane = threadIdx.x & 63u;
+  wave_lds_sync();
+  Segs<1> sg;
+  sg.p[0] = wl;
+  sg.n[0] = n;
+  sg.ns = 1;
+  const uint64_t thr = wave_select_skip<1>(sg, need, hist);
+  uint32_t nn = 0u;
+  for (uint32_t b = 0; b < n; b += 64u) {
+    const uint32_t i = b + lane;
+    const uint64_t x = i < n ? wl[i] : 0ull;
+    const bool keep = i < n && x >= thr;
+    const uint64_t m = __ballot(keep);
+    wave_lds_sync();  // the block is read before any lane writes
+    if (keep) wl[nn + lanes_below(m)] = x;
+    nn += (uint32_t)__popcll(m);
+  }
+  wave_lds_sync();
+  n = nn;
+  return cand_skey(thr);
+}
+
+// A wave's tile in LDS (float4 j of lane l at j * 256 + 4 l): branches that
+// need single logits read them back by element (per-lane indices into a
+// register array would move the tile to scratch memory).
+__device__ __forceinline__ void row_spill(float* xs, const float (&x)[kRowEl]) {
+  const uint32_t lane = threadIdx.x & 63u;
+  #pragma unroll
+  for (int j = 0; j < kRowTV; ++j)
+    *reinterpret_cast<float4*>(xs + j * 256 + 4 * lane) = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+  wave_lds_sync();
+}
+__device__ __forceinline__ float row_elem(const float* xs, uint32_t e) {
+  return xs[(e >> 2) * 256u + 4u * (threadIdx.x & 63u) + (e & 3u)];
+}
+
+constexpr uint32_t kKeyNegZero = 0x7fffffffu;  // okey(-0.0f)
+constexpr uint32_t kKeyPosInf = 0xff800000u;   // okey(+inf)
+
+// The fast path of one row; false sends the row to the general path (all
+// threads return the same).  h0, h1: the row's history range.
+template <bool MASK>
+__device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t h0,
+                                           uint32_t h1, unsigned char* lds_raw) {
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const int wid = tid >> 6;
+  const int V = a.V;
+  const int Wm = (V + 31) >> 5;
+  const int ntiles = (V + kRowTile - 1) / kRowTile;
+  // word w of the row's history: {bits of logits 32w..32w+31, marked logits before 32w}
+  uint2* hw = reinterpret_cast<uint2*>(lds_raw + kRowHead);
+
+  // 1. the row's history entries, then the first kRowDepth tiles in flight
+  //    (loads past the row read zero); the history is waited for first
+  const bool hist = h1 > h0;
+  uint32_t hid[kRowHistPer], hcs[kRowHistPer];
+  #pragma unroll
+  for (int r = 0; r < kRowHistPer; ++r) {
+    const uint32_t h = h0 + (uint32_t)(r * kRowThreads + tid);
+    hid[r] = h < h1 ? a.hids[h] : 0xffffffffu;
+    hcs[r] = h < h1 ? a.hcnt[h] : 0u;
+  }
+  const char* rbase = (const char*)a.logits + (int64_t)row * a.row_stride * 4;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)rbase, (short)0, V * 4, kBufferConfig);
+  __amdgpu_buffer_rsrc_t ms;
+  if (MASK)
+    ms = __builtin_amdgcn_make_buffer_rsrc((void*)(a.mask + (int64_t)row * a.mask_words), (short)0, Wm * 4,
+                                           kBufferConfig);
+  i32x4_t buf[kRowDepth][kRowTV];
+  uint32_t mw[kRowDepth][kRowTV];
+  #pragma unroll
+  for (int d = 0; d < kRowDepth; ++d) {
+    #pragma unroll
+    for (int j = 0; j < kRowTV; ++j) {
+      const int e0 = d * kRowTile + (j * kRowThreads + tid) * 4;
+      buf[d][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * 4, 0, 0);
+      if (MASK) mw[d][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (e0 >> 5) * 4, 0, 0);
+    }
+  }
+
+  // 2. the history: marks and rank prefix, summed counts and ids by rank
+  uint32_t distinct = 0u;
+  if (hist) {
+    constexpr uint32_t kFirst = (uint32_t)(kRowHistPer * kRowThreads);
+    for (int i = tid; i < Wm; i += kRowThreads) hw[i] = make_uint2(0u, 0u);
+    __syncthreads();
+    auto mark = [&](uint32_t id) {
+      if (id < (uint32_t)V) atomicOr(&hw[id >> 5].x, 1u << (id & 31u));
+    };
+    #pragma unroll
+    for (int r = 0; r < kRowHistPer; ++r) mark(hid[r]);
+    for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) mark(a.hids[h]);
+    __syncthreads();
+    const int PW = (Wm + kRowThreads - 1) / kRowThreads;
+    uint32_t loc = 0u;
+    for (int i = 0; i < PW; ++i) {
+      const int w = tid * PW + i;
+      if (w < Wm) loc += (uint32_t)__popc(hw[w].x);
+    }
+    uint32_t run = block_excl_scan_u32<kRowThreads>(loc, L.redu, &distinct);
+    if (distinct > (uint32_t)kRowHistCap) return false;
+    for (int i = 0; i < PW; ++i) {
+      const int w = tid * PW + i;
+      if (w < Wm) { hw[w].y = run; run += (uint32_t)__popc(hw[w].x); }
+    }
+    for (uint32_t r = tid; r < distinct; r += kRowThreads) L.ob_cnt[r] = 0u;
+    __syncthreads();
+    auto add = [&](uint32_t id, uint32_t c) {
+      if (id < (uint32_t)V) {
+        const uint2 hv = hw[id >> 5];
+        const uint32_t rank = hv.y + (uint32_t)__popc(hv.x & ((1u << (id & 31u)) - 1u));
+        atomicAdd(&L.ob_cnt[rank], c);
+        L.ob_id[rank] = id;  // every occurrence writes the same id
+      }
+    };
+    #pragma unroll
+    for (int r = 0; r < kRowHistPer; ++r) add(hid[r], hcs[r]);
+    for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) add(a.hids[h], a.hcnt[h]);
+    __syncthreads();
+  }
+
+  // 3. the stream
+  const uint32_t kk = (uint32_t)cfg.k_sel;  // 1..kLeanK
+  const uint32_t kw = min(kk, (kk + 15u) / 16u + (uint32_t)ceilf(sqrtf((float)kk)) + 4u);
+  uint64_t* wl = L.wbuf[wid];
+  uint32_t* wh = L.whist[wid];
+  float* xs = L.xscr[wid];
+  uint32_t wn = 0u;              // entries in this wave's list
+  uint32_t T = kKeyNegInf;       // the wave's threshold key (strict)
+  float tf = -__builtin_inff();  // the float of T
+  bool bad = false;              // the list overflowed
+  // Every slot is processed and refilled on every pass, also past the row's
+  // last tile (those logits read as -inf and their loads move no memory):
+  // with no conditional load in the loop the compiler keeps the other
+  // slot's loads in flight while it waits for one slot.
+  const int npass = (ntiles + kRowDepth - 1) / kRowDepth;
+  for (int p = 0; p < npass; ++p) {
+    #pragma unroll
+    for (int d = 0; d < kRowDepth; ++d) {
+      const int t = p * kRowDepth + d;
+      const int base = t * kRowTile;
+      float x[kRowEl];
+      #pragma unroll
+      for (int j = 0; j < kRowTV; ++j) {
+        const int e0 = base + (j * kRowThreads + tid) * 4;
+        const uint32_t mbits = MASK ? mw[d][j] >> (e0 & 31) : 0xfu;
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float v = __int_as_float(buf[d][j][q]);
+          if (MASK && !((mbits >> q) & 1u)) v = -__builtin_inff();
+          x[j * 4 + q] = v;
+        }
+      }
+      if (base + kRowTile > V) {
+        #pragma unroll
+        for (int j = 0; j < kRowTV; ++j) {
+          const int e0 = base + (j * kRowThreads + tid) * 4;
+          #pragma unroll
+          for (int q = 0; q < 4; ++q) if (e0 + q >= V) x[j * 4 + q] = -__builtin_inff();
+        }
+      }
+      // history tokens of this lane: captured by rank (one per lane per
+      // round), then left out of the test
+      bool spilled = false;
+      uint32_t mk = 0u;
+      if (hist) {
+        #pragma unroll
+        for (int j = 0; j < kRowTV; ++j) {
+          const int e0 = base + (j * kRowThreads + tid) * 4;
+          const uint32_t bits = e0 < V ? hw[e0 >> 5].x : 0u;
+          mk |= ((bits >> (e0 & 31)) & 0xfu) << (4 * j);
+        }
+        if (__ballot(mk != 0u) != 0ull) {
+          row_spill(xs, x);
+          spilled = true;
+          uint32_t cm = mk;
+          while (__ballot(cm != 0u) != 0ull) {
+            if (cm != 0u) {
+              const uint32_t e = (uint32_t)__builtin_ctz(cm);
+              cm &= cm - 1u;
+              const uint32_t li = (uint32_t)(base + ((int)(e >> 2) * kRowThreads + tid) * 4) + (e & 3u);
+              const uint2 h = hw[li >> 5];
+              const uint32_t rank = h.y + (uint32_t)__popc(h.x & ((1u << (li & 31u)) - 1u));
+              L.ob_raw[rank] = __float_as_uint(row_elem(xs, e));
+            }
+          }
+        }
+      }
+      if (d == 0 && p == 0) {
+        // first tile: a bound with at least kw of the wave's logits at or
+        // above it, from its group maxima (4 logits of a lane each,
+        // history tokens left out): the largest prefix of 20 key bits that
+        // kw group maxima reach
+        constexpr int NG = kRowEl / 4;
+        uint32_t gk[NG];
+        #pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          float gm = -__builtin_inff();
+          #pragma unroll
+          for (int q = 0; q < 4; ++q) gm = ((mk >> (4 * g + q)) & 1u) ? gm : fmaxf(gm, x[4 * g + q]);
+          gk[g] = lkey(gm);
+        }
+        uint32_t prefix = 0u;
+        #pragma unroll 1
+        for (int bit = 31; bit >= 12; --bit) {
+          const uint32_t probe = prefix | (1u << bit);
+          uint32_t c = 0u;
+          #pragma unroll
+          for (int g = 0; g < NG; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
+          if (c >= kw) prefix = probe;
+        }
+        if (prefix > kKeyNegInf + 1u) {
+          T = prefix - 1u;
+          tf = okey_inv(T);
+        }
+      }
+      float mx = x[0];
+      #pragma unroll
+      for (int e = 1; e < kRowEl; ++e) mx = fmaxf(mx, x[e]);
+      if (__ballot(mx >= tf) != 0ull) {
+        // survivors: key above T, i.e. x > tf (NaN never passes; +inf passes
+        // and sends the row to the general path at the end); the
+        // signed-zero threshold compares keys
+        uint32_t sb = 0u;
+        if (T == kKeyNegZero) {
+          #pragma unroll
+          for (int e = 0; e < kRowEl; ++e) sb |= lkey(x[e]) > T ? (1u << e) : 0u;
+        } else {
+          #pragma unroll
+          for (int e = 0; e < kRowEl; ++e) sb |= x[e] > tf ? (1u << e) : 0u;
+        }
+        sb &= ~mk;
+        if (__ballot(sb != 0u) != 0ull) {
+          if (!spilled) row_spill(xs, x);
+          // appended one per lane per round (the list stops at its capacity)
+          for (;;) {
+            const uint64_t m = __ballot(sb != 0u);
+            if (m == 0ull) break;
+            const uint32_t add = (uint32_t)__popcll(m);
+            if (wn + add > (uint32_t)kRowCap) {
+              bad = true;
+              break;
+            }
+            if (sb != 0u) {
+              const uint32_t e = (uint32_t)__builtin_ctz(sb);
+              sb &= sb - 1u;
+              const uint32_t idx = (uint32_t)(base + ((int)(e >> 2) * kRowThreads + tid) * 4) + (e & 3u);
+              wl[wn + lanes_below(m)] = cand_key(okey(row_elem(xs, e)), idx);
+            }
+            wn += add;
+          }
+          if (wn > (uint32_t)kRowHW) {
+            T = row_wave_keep(wl, wn, kw, wh);
+            tf = okey_inv(T);
+          }
+        }
+      }
+      wave_lds_sync();  // the tile's reads of xs are done before the next spill
+      // refill this slot with tile t + kRowDepth
+      #pragma unroll
+      for (int j = 0; j < kRowTV; ++j) {
+        const int e0 = (t + kRowDepth) * kRowTile + (j * kRowThreads + tid) * 4;
+        buf[d][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * 4, 0, 0);
+        if (MASK) mw[d][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (e0 >> 5) * 4, 0, 0);
+      }
+    }
+  }
+  if (wn > kw) T = row_wave_keep(wl, wn, kw, wh);
+  if (lane == 0u) {
+    L.wthr[wid] = T;
+    L.wbad[wid] = bad ? 1u : 0u;
+  }
+  __syncthreads();  // lists, thresholds and captured history logits complete
+  uint32_t Tm = L.wthr[0];
+  uint32_t anybad = L.wbad[0];
+  #pragma unroll
+  for (int w = 1; w < kRowWaves; ++w) { Tm = max(Tm, L.wthr[w]); anybad |= L.wbad[w]; }
+  if (anybad) return false;
+
+  // 4. the candidates: list entries and processed history logits >= Tm
+  constexpr int kLq = (kRowKwMax + 63) / 64;
+  uint64_t sc[kLq];
+  uint64_t hc[kRowHistPer];
+  uint32_t mine = 0u;
+  uint64_t top = 0ull;
+  #pragma unroll
+  for (int q = 0; q < kLq; ++q) {
+    const uint32_t i = lane + 64u * q;
+    const uint64_t c = i < wn ? wl[i] : 0ull;
+    const bool keep = i < wn && cand_skey(c) >= Tm;
+    sc[q] = keep ? c : 0ull;
+    mine += keep ? 1u : 0u;
+    top = sc[q] > top ? sc[q] : top;
+  }
+  #pragma unroll
+  for (int q = 0; q < kRowHistPer; ++q) {
+    const uint32_t r = (uint32_t)(tid + kRowThreads * q);
+    hc[q] = 0ull;
+    if (r < distinct) {
+      const float pl = apply_penalties(__uint_as_float(L.ob_raw[r]), L.ob_cnt[r], cfg);
+      const uint32_t k = lkey(pl);
+      if (k > kKeyNegInf && k >= Tm) hc[q] = cand_key(k, L.ob_id[r]);
+    }
+    mine += hc[q] != 0ull ? 1u : 0u;
+    top = hc[q] > top ? hc[q] : top;
+  }
+  uint32_t n = 0u;
+  uint32_t pos = block_excl_scan_u32<kRowThreads>(mine, L.redu, &n);  // barriers: LDS inputs read
+  top = block_max_u64<kRowThreads>(top, L.red64);
+  // +inf logits rank as -inf (gpu.rs:767-777): the general path resolves
+  // them; fewer candidates than kk hold the row's top kk only if nothing
+  // finite was left out
+  if (n == 0u || n > (uint32_t)kGather || cand_skey(top) >= kKeyPosInf) return false;
+  if (n < kk && Tm > kKeyNegInf) return false;
+  FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
+  #pragma unroll
+  for (int q = 0; q < kLq; ++q) if (sc[q] != 0ull) fs.cbig[pos++] = sc[q];
+  #pragma unroll
+  for (int q = 0; q < kRowHistPer; ++q) if (hc[q] != 0ull) fs.cbig[pos++] = hc[q];
+  __syncthreads();
+  if (wid >= NT / 64) return true;  // the finish runs on the first NT threads
+  const float M = key_to_s(cand_skey(top), cfg.t_eff);
+  return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm);
+}
+
+// One workgroup per row (see the section comment).
+template <bool MASK>
+__global__ void __launch_bounds__(kRowThreads) row_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  RowLds& L = *reinterpret_cast<RowLds*>(lds_raw);
+  const int row = blockIdx.x;
+  uint32_t h0 = 0u, h1 = 0u;
+  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; }
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  if (cfg.cls == kTopK && !cfg.wide) {
+    if (row_stream<MASK>(L, a, row, cfg, h0, h1, lds_raw)) return;
+    __syncthreads();
+  }
+  // the general path, on the first NT threads: the chunk select and the
+  // finish of the two-kernel path (ended waves no longer count at barriers)
+  if (threadIdx.x >= NT) return;
+  for (int c = 0; c < a.n_chunks; ++c) {
+    select_chunk<HI_ROCM_DTYPE_F32, kSelChunkLarge / NT / 4, MASK>(a, row, c, lds_raw);
+    __syncthreads();
+  }
+  FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
+  if (finish_lean(fs, a, row, cfg)) return;
+  __syncthreads();
+  finish_row(fs, a, row, cfg);
+}
+
+size_t row_lds_bytes(int V) {
+  const size_t fast = kRowHead + sizeof(uint2) * ((V + 31) / 32);
+  const size_t general = kSelHead + sel_hist_bytes(kSelChunkLarge);
+  size_t b = fast > general ? fast : general;
+  return b > sizeof(FinLds) ? b : sizeof(FinLds);
+}
+
+constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950
+
+bool row_kernel_fits(const SampleArgs& a) {
+  return a.dtype == HI_ROCM_DTYPE_F32 && a.B >= kRowMinBatch && a.n_lp == 0 && a.out_token_lp == nullptr &&
+         a.vec_ok && a.chunk == kSelChunkLarge && a.V <= kRowMaxV && row_lds_bytes(a.V) <= kLdsPerCu;
+}
+
 bool select_mode(int n_lp, int vec_ok) { return n_lp <= kLeanK && vec_ok; }
 
 int choose_chunk(int B, int V, int n_lp, int vec_ok, bool hist) {
@@ -3208,11 +3647,30 @@ hipError_t launch_select_d(const SampleArgs& a, hipStream_t stream) {
   return launch_select_t<DT, kSelChunkSmall / NT / EPL, MASK>(a, stream);
 }
 
+template <bool MASK>
+hipError_t launch_rows(const SampleArgs& a, hipStream_t stream) {
+  const size_t lds = row_lds_bytes(a.V);
+  static size_t attr = 0;  // largest dynamic LDS size set so far
+  if (lds > attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)row_kernel<MASK>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+    attr = lds;
+  }
+  hipLaunchKernelGGL(row_kernel<MASK>, dim3(a.B), dim3(kRowThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream, const LaunchEvents* le) {
   if (!select_mode(a.n_lp, a.vec_ok) || (a.chunk != kSelChunkLarge && a.chunk != kSelChunkSmall))
     return launch_chunked(a, stream, le);
   hipError_t e = record(le, 0, stream);
   if (e != hipSuccess) return e;
+  if (row_kernel_fits(a)) {
+    e = a.mask ? launch_rows<true>(a, stream) : launch_rows<false>(a, stream);
+    if (e == hipSuccess) e = record(le, 1, stream);
+    return e == hipSuccess ? record(le, 2, stream) : e;
+  }
   if (a.dtype == HI_ROCM_DTYPE_BF16)
     e = a.mask ? launch_select_d<HI_ROCM_DTYPE_BF16, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_BF16, false>(a, stream);
   else

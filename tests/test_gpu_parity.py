@@ -151,12 +151,12 @@ def test_reference_device_grid_via_abi(hip, oracle):
     assert cases >= 200
 
 
-@pytest.mark.parametrize("B,V", [(128, 129280), (3, 151936)])
+@pytest.mark.parametrize("B,V", [(128, 129280), (3, 151936), (256, 70001)])
 def test_uniform_launchers_every_chunk_shape(hip, oracle, B, V):
     """Batch-wide parameters (kernels.cu:14737-14880 launchers) on the
-    streaming pass's large chunks (B=128: 1024 workgroups) and small ones,
-    against the host ranked sampler row by row; then the per-row SoA
-    launcher on the same rows."""
+    streaming pass's large chunks (B=128: 1024 workgroups), small ones, and
+    the one-workgroup-per-row kernel (B=256), against the host ranked
+    sampler row by row; then the per-row SoA launcher on the same rows."""
     torch = _torch()
     lib = hip.load()
     stream = torch.cuda.Stream()
@@ -327,6 +327,75 @@ def _mixed_edge_workload(rng, B, V, with_hist=True, with_mask=False):
         mask = rng.integers(0, 2 ** 32, (B, W), dtype=np.uint64).astype(np.uint32)
         mask[0] = 0
     return Workload("edge", x, p, u, offs, ids, cnts, mask, 8)
+
+
+def _large_batch_workload(rng, V, with_mask):
+    """B=256 without logprobs: the one-workgroup-per-row kernel.  Most rows
+    are top-k rows like config 3 (its fast path); rows 0-12 are the cases
+    it hands to the general path or must get right on the way."""
+    from hi_amd.sampler import row_params
+    B = 256
+    x = rng.normal(0, 2.5, (B, V)).astype(F32)
+    x[np.arange(B)[:, None], rng.integers(0, V, (B, 16))] += F32(8.0)
+    p = row_params(B, temperature=0.8, top_p=1.0)
+    p["temperature"] = rng.uniform(0.3, 1.2, B)
+    p["top_k"] = rng.choice([1, 20, 50, 100, 256], B)
+    p["top_p"] = rng.uniform(0.8, 1.0, B)
+    p["min_p"] = rng.choice([0.0, 0.05], B)
+    p["repetition_penalty"] = rng.choice([1.0, 1.3], B)
+    p["frequency_penalty"] = rng.choice([0.0, 0.2], B)
+    p["presence_penalty"] = rng.choice([0.0, 0.3], B)
+    p["temperature"][0] = 0.0                        # greedy
+    p["top_k"][1], p["top_p"][1] = 0, 0.9           # top-p only
+    p["top_k"][2] = 1000                            # top-k above the lean limit
+    p["top_k"][3], p["top_p"][3], p["min_p"][3] = 0, 1.0, 0.0  # temperature only
+    x[4, :] = -np.inf
+    x[4, 7] = 1.0                                   # one finite logit, k > 1
+    x[5, :] = -np.inf                               # nothing finite
+    x[6] = np.tile(np.array([1.5, 0.25, -2.0], F32), V // 3 + 1)[:V]  # tie surface
+    x[7, 100:110] = np.inf
+    x[7, 200] = np.nan                              # non-finite logits rank as -inf
+    x[8, ::7] = 3.0                                 # many equal logits at the top
+    x[12, :] = 0.0
+    x[12, 1::2] = -0.0                              # signed zeros only
+    u = rng.random(B).astype(F32)
+    u[13] = 0.99999994
+    # histories: Zipf ids with counts; row 9 has more distinct ids than the
+    # row kernel's table, row 10 repeats ids, row 11 has none
+    ids_l, cnt_l, offs = [], [], np.zeros(B + 1, np.uint32)
+    for b in range(B):
+        if b == 9:
+            r = rng.permutation(V)[:3000]
+        elif b == 11:
+            r = np.zeros(0, np.int64)
+        else:
+            r = np.minimum(rng.zipf(1.2, 600) - 1, V + 5)
+            if b == 10:
+                r = np.concatenate([r, r[:50]])
+        ids_l.append(r.astype(np.uint32))
+        cnt_l.append(rng.integers(1, 5, len(r)).astype(np.uint32))
+        offs[b + 1] = offs[b] + len(r)
+    ids, cnts = np.concatenate(ids_l), np.concatenate(cnt_l)
+    mask = None
+    if with_mask:
+        W = (V + 31) // 32
+        mask = rng.integers(0, 2 ** 32, (B, W), dtype=np.uint64).astype(np.uint32)
+        mask[11] = 0                                # fully masked: EOS
+        p["eos_id"][11] = 17
+    return Workload("large-batch", x, p, u, offs, ids, cnts, mask, 0)
+
+
+@pytest.mark.parametrize("V,with_mask", [(70001, False), (129280, False), (65600, True)])
+def test_large_batch_row_kernel(hip, oracle, V, with_mask):
+    """One workgroup per row (B >= 192, no logprobs) against the oracle,
+    twice (the second call reuses the workspace)."""
+    rng = np.random.default_rng(V + with_mask)
+    w = _large_batch_workload(rng, V, with_mask)
+    say(f"large batch V={V} mask={with_mask}")
+    got = run_gpu(w, token_logprobs=False, repeat=2)
+    assert np.array_equal(got[0]["tokens"], got[1]["tokens"]), "not deterministic"
+    want = run_oracle(oracle, w)
+    compare(w, got[0], want, f"large batch V={V}")
 
 
 @pytest.mark.parametrize("V", [37, 1000, 8192, 8193, 20011, 70000])

@@ -125,10 +125,10 @@ def pmc_probe(torch, w, steps, copy_mib=512):
 
 
 def traffic_from_profile():
-    """HBM bytes per launch of the pass over the logits, measured by the
+    """HBM bytes per launch of the C3 step's kernel, measured by the
     committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by a
     copy of known size), or None when no summary is present."""
-    path = os.path.join(ROOT, "profiles", "select_kernel_c3_hbm_traffic.md")
+    path = os.path.join(ROOT, "profiles", "row_kernel_c3_hbm_traffic.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -231,8 +231,9 @@ def main():
     w1 = config1()
     b1_graph_us, b1_eager_us = time_graph_b1(torch, w1, max(args.steps, 100), 20)
     b1_pass_us, b1_finish_us = time_parts(torch, w1, max(args.steps, 100))
-    # the dominant kernel of the C3 step: the pass over the logits (it reads
-    # every algorithmic byte of the step)
+    # the dominant kernel of the C3 step: at B >= 192 (no logprobs) the step
+    # is one row_kernel launch, which reads every algorithmic byte and also
+    # finishes the rows; the library's events bracket that one kernel
     kernel_gbs = alg_bytes / (pass_us * 1e-6) / 1e9
 
     res = {
@@ -262,7 +263,7 @@ def main():
         "step_kernel_us": {"select_pass": pass_us, "finish": finish_us},
         "roofline": {"bound": "hbm", "achieved": kernel_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": kernel_gbs / HBM_PEAK_GBS, "traffic": traffic_from_profile(),
-                     "kernel": "hi_rocm::select_kernel<0, 16, false> (C3 pass over the logits)",
+                     "kernel": "hi_rocm::row_kernel<false> (C3: one workgroup per row, whole step)",
                      "kernel_avg_us": pass_us,
                      "algorithmic_bytes_per_launch": alg_bytes},
     }

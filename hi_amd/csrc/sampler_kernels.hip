@@ -31,6 +31,8 @@
 #include <float.h>
 #include <stddef.h>
 
+#include <type_traits>
+
 #include "hi_rocm.h"
 #include "exact_expf.h"
 #include "sampler_internal.h"
@@ -149,6 +151,12 @@ __device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V,
   if (need_lse) c.k_sel = max(c.k_sel, kLseTop);
   if (c.k_sel > V) c.k_sel = V;
   c.store_s = c.cls == kTopP || c.cls == kTempOnly || c.wide;
+  // Every caller's row is uniform over the workgroup: the float fields are
+  // kept in scalar registers (as vector values they would hold vector
+  // registers for the whole kernel, or be spilled to scratch memory)
+  auto su = [](float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); };
+  c.T = su(c.T); c.top_p = su(c.top_p); c.min_p = su(c.min_p); c.rep = su(c.rep);
+  c.freq = su(c.freq); c.pres = su(c.pres); c.t_eff = su(c.t_eff); c.cutoff = su(c.cutoff);
   return c;
 }
 
@@ -1254,15 +1262,22 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
 
 constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
 
-// Sequential f32 sums over the wave's lanes: lane l returns
+// Sequential f32 sums over the wave's lanes: lane l < n returns
 // ((start + v_0) + v_1) + ... + v_l, the reference's left-to-right fold
-// (gpu.rs:834-836, 851, 878, 889-896).  64 dependent steps: each moves the
-// running sums one lane up (wave_shr:1; lane 0 takes `start`) and adds.
-__device__ __forceinline__ float wave_fold_f32(float v, float start) {
+// (gpu.rs:834-836, 851, 878, 889-896); lanes from n on hold partial sums.
+// n - 1 dependent steps: each moves the running sums one lane up
+// (wave_shr:1; lane 0 takes `start`) and adds.
+__device__ __forceinline__ float wave_fold_f32(float v, float start, int n) {
+  // after step s lanes [0, s] hold their sums: lanes [0, n) need n - 1 steps
   float p = start + v;
-  #pragma unroll
-  for (int s = 1; s < 64; ++s)
-    p = __uint_as_float(dpp32<0x138>(__float_as_uint(start), __float_as_uint(p))) + v;
+  int s = 1;
+  #pragma unroll 1
+  for (; s + 8 <= n; s += 8) {
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) p = __uint_as_float(dpp32<0x138>(__float_as_uint(start), __float_as_uint(p))) + v;
+  }
+  #pragma unroll 1
+  for (; s < n; ++s) p = __uint_as_float(dpp32<0x138>(__float_as_uint(start), __float_as_uint(p))) + v;
   return p;
 }
 
@@ -1350,7 +1365,7 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   #pragma unroll
   for (int m = 0; m < DM; ++m) {
     if (m * 64 < k) {
-      pa[m] = wave_fold_f32(fa[m], P);
+      pa[m] = wave_fold_f32(fa[m], P, min(64, k - m * 64));
       P = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), min(63, k - 1 - m * 64)));
     } else {
       pa[m] = P;
@@ -1367,7 +1382,7 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
     fb[m] = fa[m] > 0.f ? fa[m] / total : 0.f;
     qa[m] = Q;
     if (m * 64 < k) {
-      qa[m] = wave_fold_f32(fb[m], Q);
+      qa[m] = wave_fold_f32(fb[m], Q, min(64, k - m * 64));
       Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(qa[m]), min(63, k - 1 - m * 64)));
     }
     (void)i;
@@ -3170,12 +3185,9 @@ constexpr int kSelChunkSmall = NT * 16;
 // workgroup of kRowThreads per row replaces the select pass and the finish
 // kernel.  Sixteen waves share a CU (four per SIMD), so one wave's LDS
 // round trips and branches overlap the others' work and loads.
-//  - The row's history is staged once in LDS: per 32 logits a word of
-//    marks and the number of marked logits before it, and the summed count
-//    and id of every distinct history token by rank.
 //  - The row streams through a register pipeline kRowDepth tiles deep per
-//    wave (tile = kRowTile logits, 16-byte loads); per logit the common case
-//    is one max.
+//    wave (tile = kRowTile logits, 16-byte loads).  Per logit the common
+//    case is one max over its raw bits.
 //  - Each wave keeps the top kw of its own logits (by candidate key) in an
 //    LDS list, kw = ceil(k/16) + ceil(sqrt(k)) + 4: a logit whose key passes
 //    the wave's threshold is appended, and when the list passes kRowHW
@@ -3183,28 +3195,32 @@ constexpr int kSelChunkSmall = NT * 16;
 //    last one's key.  A later logit with that key has a larger index and
 //    ranks below all kept ones, so the test is strict.  The first tile
 //    starts from a bound of the wave's group maxima instead of -inf.
-//  - History tokens are captured from the stream by rank (their logits are
-//    processed after it) and kept out of the test.
+//  - History tokens stream like the others (their raw logits).  The history
+//    is ranked in LDS once the first tile has arrived (a word of marks per
+//    32 logits and the number of marked logits before it), and its logits
+//    are loaded while the stream runs; after it their penalties are
+//    applied, and list entries that are history tokens are dropped.
 //  - Every logit left out has a key at or below the largest wave threshold
 //    Tm, so the union of the lists and the processed history logits above
-//    Tm holds the row's top k whenever its k-th key is above Tm (a wave
-//    holding more than kw of the row's top k breaks that and sends the row
-//    to the general path; with kw at mean + 4 sd of that count it does not
-//    happen for rows whose top tokens are spread over the vocabulary).
+//    Tm holds the row's top k whenever its k-th key is above Tm (finish_core
+//    checks that).  A wave holding more than kw of the row's top k breaks it
+//    and sends the row to the general path; with kw at mean + 4 sd of that
+//    count it does not happen for rows whose top tokens are spread over the
+//    vocabulary.
 // The first four waves then run finish_core; the others end there.  Rows the
 // fast path does not cover (other row classes, more than kRowHistCap
-// distinct history tokens, a list overflow, no finite logit, a tie
-// finish_core will not resolve) run the chunk select and the finish of the
-// two-kernel path inside the same workgroup, on its first four waves.
+// distinct history tokens, a list overflow, no finite logit, +inf logits, a
+// tie finish_core will not resolve) run the chunk select and the finish of
+// the two-kernel path inside the same workgroup, on its first four waves.
 
 constexpr int kRowThreads = 1024;
 constexpr int kRowWaves = kRowThreads / 64;
-constexpr int kRowTV = 2;                             // 16-byte loads per thread per tile
+constexpr int kRowTV = 4;                             // 16-byte loads per thread per tile
 constexpr int kRowEl = kRowTV * 4;                    // logits per thread per tile
-constexpr int kRowTile = kRowThreads * kRowEl;        // 8192 logits
-constexpr int kRowDepth = 4;                          // tiles in flight per wave
-constexpr int kRowHW = 128;                           // list length that triggers a selection
-constexpr int kRowCap = 256;                          // list capacity (past it: general path)
+constexpr int kRowTile = kRowThreads * kRowEl;        // 16384 logits
+constexpr int kRowDepth = 2;                          // tiles in flight per wave
+constexpr int kRowHW = 64;                            // list length that triggers a selection
+constexpr int kRowCap = 128;                          // list capacity (past it: general path)
 constexpr int kRowHistCap = 2048;                     // distinct history tokens per row
 constexpr int kRowHistPer = kRowHistCap / kRowThreads;  // history entries per thread in registers
 constexpr int kRowMaxV = 1 << 18;
@@ -3217,16 +3233,16 @@ struct RowLds {
   uint32_t ob_raw[kRowHistCap];        // logit (mask applied) of the history token of rank r
   uint32_t ob_cnt[kRowHistCap];        // its summed count
   uint32_t ob_id[kRowHistCap];         // its id
-  float xscr[kRowWaves][64 * kRowEl];  // a wave's tile, when a branch needs single logits
+  float xscr[kRowWaves][64 * kRowEl];  // a wave's tile when a branch needs single logits; also
+                                       // the wave's selection histogram
   // the fields below stay valid while the finish reuses the space above
-  uint32_t whist[kRowWaves][256];
   uint32_t wthr[kRowWaves];
   uint32_t wbad[kRowWaves];
   uint32_t redu[kRowWaves];
   uint64_t red64[kRowWaves];
 };
 constexpr size_t kRowHead = (sizeof(RowLds) + 15) & ~(size_t)15;
-static_assert(sizeof(FinLds) <= offsetof(RowLds, whist), "finish LDS must fit the stream's lists");
+static_assert(sizeof(FinLds) <= offsetof(RowLds, wthr), "finish LDS must fit the stream's lists");
 
 // Keeps the `need` largest entries of the wave's list (unique keys,
 // need <= n) at its front; returns the key of the last one kept.
@@ -3267,14 +3283,19 @@ __device__ __forceinline__ float row_elem(const float* xs, uint32_t e) {
   return xs[(e >> 2) * 256u + 4u * (threadIdx.x & 63u) + (e & 3u)];
 }
 
+// Cache policy of the stream's loads: non-temporal (the nt bit of gfx950's
+// buffer loads), so that the logits, each read once, do not push the code
+// and the small per-row data out of the L2 cache.
+constexpr int kStreamLoad = 2;
+
 constexpr uint32_t kKeyNegZero = 0x7fffffffu;  // okey(-0.0f)
 constexpr uint32_t kKeyPosInf = 0xff800000u;   // okey(+inf)
 
 // The fast path of one row; false sends the row to the general path (all
-// threads return the same).  h0, h1: the row's history range.
+// threads return the same).
 template <bool MASK>
-__device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t h0,
-                                           uint32_t h1, unsigned char* lds_raw) {
+__device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int row, const RowCfg& cfg,
+                                           unsigned char* lds_raw) {
   const int tid = threadIdx.x;
   const uint32_t lane = (uint32_t)tid & 63u;
   const int wid = tid >> 6;
@@ -3283,23 +3304,37 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   const int ntiles = (V + kRowTile - 1) / kRowTile;
   // word w of the row's history: {bits of logits 32w..32w+31, marked logits before 32w}
   uint2* hw = reinterpret_cast<uint2*>(lds_raw + kRowHead);
+  const float* lrow = reinterpret_cast<const float*>((const char*)a.logits + (int64_t)row * a.row_stride * 4);
+  const uint32_t* mrow = MASK ? a.mask + (int64_t)row * a.mask_words : nullptr;
 
   // 1. the row's history entries, then the first kRowDepth tiles in flight
-  //    (loads past the row read zero); the history is waited for first
+  //    (loads past the row read zero)
+  const uint32_t h0 = a.hoff ? a.hoff[row] : 0u;
+  const uint32_t h1 = a.hoff ? a.hoff[row + 1] : 0u;
   const bool hist = h1 > h0;
+  // unconditional range-checked loads (entries past the row read zero): a
+  // load under a condition would leave the compiler unsure how many loads
+  // are in flight in the stream loop, and it would then wait for all
   uint32_t hid[kRowHistPer], hcs[kRowHistPer];
-  #pragma unroll
-  for (int r = 0; r < kRowHistPer; ++r) {
-    const uint32_t h = h0 + (uint32_t)(r * kRowThreads + tid);
-    hid[r] = h < h1 ? a.hids[h] : 0xffffffffu;
-    hcs[r] = h < h1 ? a.hcnt[h] : 0u;
+  {
+    // (a scalar: a range in a vector register would make each load a loop)
+    const int nh = __builtin_amdgcn_readfirstlane(hist ? (int)(h1 - h0) : 0);
+    const __amdgpu_buffer_rsrc_t ri =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.hids + h0), (short)0, nh * 4, kBufferConfig);
+    const __amdgpu_buffer_rsrc_t rc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.hcnt + h0), (short)0, nh * 4, kBufferConfig);
+    #pragma unroll
+    for (int r = 0; r < kRowHistPer; ++r) {
+      const int h = r * kRowThreads + tid;
+      hid[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ri, h * 4, 0, 0);
+      hcs[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, h * 4, 0, 0);
+      if (h >= nh) hid[r] = 0xffffffffu;
+    }
   }
-  const char* rbase = (const char*)a.logits + (int64_t)row * a.row_stride * 4;
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)rbase, (short)0, V * 4, kBufferConfig);
+  asm volatile("" ::: "memory");  // the history loads go out before the tiles
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)lrow, (short)0, V * 4, kBufferConfig);
   __amdgpu_buffer_rsrc_t ms;
-  if (MASK)
-    ms = __builtin_amdgcn_make_buffer_rsrc((void*)(a.mask + (int64_t)row * a.mask_words), (short)0, Wm * 4,
-                                           kBufferConfig);
+  if (MASK) ms = __builtin_amdgcn_make_buffer_rsrc((void*)mrow, (short)0, Wm * 4, kBufferConfig);
   i32x4_t buf[kRowDepth][kRowTV];
   uint32_t mw[kRowDepth][kRowTV];
   #pragma unroll
@@ -3307,16 +3342,145 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     #pragma unroll
     for (int j = 0; j < kRowTV; ++j) {
       const int e0 = d * kRowTile + (j * kRowThreads + tid) * 4;
-      buf[d][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * 4, 0, 0);
+      buf[d][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * 4, 0, kStreamLoad);
       if (MASK) mw[d][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (e0 >> 5) * 4, 0, 0);
     }
   }
 
-  // 2. the history: marks and rank prefix, summed counts and ids by rank
+  // 2. the stream state
+  const uint32_t kk = (uint32_t)cfg.k_sel;  // 1..kLeanK
+  const uint32_t kw = min(kk, (kk + 15u) / 16u + (uint32_t)ceilf(sqrtf((float)kk)) + 4u);
+  uint64_t* wl = L.wbuf[wid];
+  float* xs = L.xscr[wid];
+  uint32_t* wh = reinterpret_cast<uint32_t*>(xs);  // the selection histogram (xs is idle then)
+  uint32_t wn = 0u;              // entries in this wave's list
+  uint32_t T = kKeyNegInf;       // the wave's threshold key (strict)
+  float tf = -__builtin_inff();  // the float of T
+  int32_t ti = INT32_MIN;        // the bits of tf when T is a positive key, else INT32_MIN
+  auto set_t = [&](uint32_t key) {
+    T = key;
+    tf = okey_inv(key);
+    ti = key > 0x80000000u ? (int32_t)__float_as_uint(tf) : INT32_MIN;
+  };
+  bool bad = false;              // the list overflowed
+
+  // One tile: tile t from slot D, which is then refilled with tile
+  // t + kRowDepth.  Every slot is processed and refilled on every pass, also
+  // past the row's last tile (those logits read as -inf and their loads move
+  // no memory): with no conditional load in the loop the compiler keeps the
+  // other slot's loads in flight while it waits for one slot.
+  auto step = [&](auto slot, int t, bool first) {
+    constexpr int D = decltype(slot)::value;
+    const int base = t * kRowTile;
+    float x[kRowEl];
+    #pragma unroll
+    for (int j = 0; j < kRowTV; ++j) {
+      const int e0 = base + (j * kRowThreads + tid) * 4;
+      const uint32_t mbits = MASK ? mw[D][j] >> (e0 & 31) : 0xfu;
+      #pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v = __int_as_float(buf[D][j][q]);
+        if (MASK && !((mbits >> q) & 1u)) v = -__builtin_inff();
+        x[j * 4 + q] = v;
+      }
+    }
+    if (base + kRowTile > V) {
+      #pragma unroll
+      for (int j = 0; j < kRowTV; ++j) {
+        const int e0 = base + (j * kRowThreads + tid) * 4;
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) if (e0 + q >= V) x[j * 4 + q] = -__builtin_inff();
+      }
+    }
+    if (first) {
+      // first tile: a bound with at least kw of the wave's logits at or
+      // above it, from its group maxima (4 logits of a lane each): the
+      // largest prefix of 20 key bits that kw group maxima reach
+      constexpr int NG = kRowEl / 4;
+      uint32_t gk[NG];
+      #pragma unroll
+      for (int g = 0; g < NG; ++g)
+        gk[g] = lkey(fmaxf(fmaxf(x[4 * g], x[4 * g + 1]), fmaxf(x[4 * g + 2], x[4 * g + 3])));
+      uint32_t prefix = 0u;
+      #pragma unroll 1
+      for (int bit = 31; bit >= 12; --bit) {
+        const uint32_t probe = prefix | (1u << bit);
+        uint32_t c = 0u;
+        #pragma unroll
+        for (int g = 0; g < NG; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
+        if (c >= kw) prefix = probe;
+      }
+      if (prefix > kKeyNegInf + 1u) set_t(prefix - 1u);
+    }
+    // any logit above the threshold?  Against a positive threshold the raw
+    // bits compare as signed integers (negative logits fall below; a NaN
+    // passes here and fails the exact test); against any other ti is
+    // INT_MIN and every tile takes the exact test
+    int32_t mi = (int32_t)__float_as_uint(x[0]);
+    #pragma unroll
+    for (int e = 1; e < kRowEl; ++e) mi = max(mi, (int32_t)__float_as_uint(x[e]));
+    if (__ballot(mi > ti) != 0ull) {
+      // survivors: key above T, i.e. x > tf (NaN never passes; +inf passes
+      // and sends the row to the general path at the end); the signed-zero
+      // threshold compares keys
+      uint32_t sb = 0u;
+      if (T == kKeyNegZero) {
+        #pragma unroll
+        for (int e = 0; e < kRowEl; ++e) sb |= lkey(x[e]) > T ? (1u << e) : 0u;
+      } else {
+        #pragma unroll
+        for (int e = 0; e < kRowEl; ++e) sb |= x[e] > tf ? (1u << e) : 0u;
+      }
+      if (__ballot(sb != 0u) != 0ull) {
+        row_spill(xs, x);
+        // appended one per lane per round (the list stops at its capacity)
+        for (;;) {
+          const uint64_t m = __ballot(sb != 0u);
+          if (m == 0ull) break;
+          const uint32_t add = (uint32_t)__popcll(m);
+          if (wn + add > (uint32_t)kRowCap) {
+            bad = true;
+            break;
+          }
+          if (sb != 0u) {
+            const uint32_t e = (uint32_t)__builtin_ctz(sb);
+            sb &= sb - 1u;
+            const uint32_t idx = (uint32_t)(base + ((int)(e >> 2) * kRowThreads + tid) * 4) + (e & 3u);
+            wl[wn + lanes_below(m)] = cand_key(okey(row_elem(xs, e)), idx);
+          }
+          wn += add;
+        }
+        if (wn > (uint32_t)kRowHW) set_t(row_wave_keep(wl, wn, kw, wh));
+        wave_lds_sync();  // xs is read before the next spill
+      }
+    }
+    #pragma unroll
+    for (int j = 0; j < kRowTV; ++j) {
+      const int e0 = (t + kRowDepth) * kRowTile + (j * kRowThreads + tid) * 4;
+      buf[D][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * 4, 0, kStreamLoad);
+      if (MASK) mw[D][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (e0 >> 5) * 4, 0, 0);
+    }
+  };
+  using Slot0 = std::integral_constant<int, 0>;
+  using Slot1 = std::integral_constant<int, 1>;
+  static_assert(kRowDepth == 2, "the stream alternates two slots");
+
+  // 3. the history ranked once the first tile has arrived: waiting for it
+  //    waits for the history entries too (loads complete in order and they
+  //    were issued first), so the ranking never waits for memory, it runs
+  //    while tile 1 is in flight, and the loop sees only tile loads in
+  //    flight.  Marks and rank prefix, then the summed count and id of each
+  //    distinct token by rank, whose logit is loaded during the stream.
+  #pragma unroll
+  for (int j = 0; j < kRowTV; ++j) {
+    asm volatile("" ::"v"(buf[0][j]));
+    if (MASK) asm volatile("" ::"v"(mw[0][j]));
+  }
+  constexpr uint32_t kFirst = (uint32_t)(kRowHistPer * kRowThreads);
   uint32_t distinct = 0u;
   if (hist) {
-    constexpr uint32_t kFirst = (uint32_t)(kRowHistPer * kRowThreads);
     for (int i = tid; i < Wm; i += kRowThreads) hw[i] = make_uint2(0u, 0u);
+    for (int r = tid; r < kRowHistCap; r += kRowThreads) L.ob_cnt[r] = 0u;
     __syncthreads();
     auto mark = [&](uint32_t id) {
       if (id < (uint32_t)V) atomicOr(&hw[id >> 5].x, 1u << (id & 31u));
@@ -3325,24 +3489,38 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     for (int r = 0; r < kRowHistPer; ++r) mark(hid[r]);
     for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) mark(a.hids[h]);
     __syncthreads();
-    const int PW = (Wm + kRowThreads - 1) / kRowThreads;
-    uint32_t loc = 0u;
-    for (int i = 0; i < PW; ++i) {
-      const int w = tid * PW + i;
-      if (w < Wm) loc += (uint32_t)__popc(hw[w].x);
+    // prefix: wave v owns the contiguous words [v * PB, (v + 1) * PB), read
+    // 64 consecutive words at a time (no LDS bank conflicts)
+    const int PB = (((Wm + kRowWaves - 1) / kRowWaves) + 63) & ~63;
+    const int w0 = wid * PB;
+    uint32_t wsum = 0u;
+    for (int b = 0; b < PB; b += 64) {
+      const int w = w0 + b + (int)lane;
+      wsum += w < Wm ? (uint32_t)__popc(hw[w].x) : 0u;
     }
-    uint32_t run = block_excl_scan_u32<kRowThreads>(loc, L.redu, &distinct);
+    wsum = wave_sum_u32(wsum);
+    if (lane == 0u) L.redu[wid] = wsum;
+    __syncthreads();
+    uint32_t run = 0u;
+    #pragma unroll
+    for (int v = 0; v < kRowWaves; ++v) {
+      const uint32_t c = L.redu[v];
+      run += v < wid ? c : 0u;
+      distinct += c;
+    }
     if (distinct > (uint32_t)kRowHistCap) return false;
-    for (int i = 0; i < PW; ++i) {
-      const int w = tid * PW + i;
-      if (w < Wm) { hw[w].y = run; run += (uint32_t)__popc(hw[w].x); }
+    for (int b = 0; b < PB; b += 64) {
+      const int w = w0 + b + (int)lane;
+      const uint32_t c = w < Wm ? (uint32_t)__popc(hw[w].x) : 0u;
+      const uint32_t incl = wave_incl_scan_u32(c);
+      if (w < Wm) hw[w].y = run + incl - c;
+      run += wave_last_u32(incl);
     }
-    for (uint32_t r = tid; r < distinct; r += kRowThreads) L.ob_cnt[r] = 0u;
     __syncthreads();
     auto add = [&](uint32_t id, uint32_t c) {
       if (id < (uint32_t)V) {
-        const uint2 hv = hw[id >> 5];
-        const uint32_t rank = hv.y + (uint32_t)__popc(hv.x & ((1u << (id & 31u)) - 1u));
+        const uint2 h = hw[id >> 5];
+        const uint32_t rank = h.y + (uint32_t)__popc(h.x & ((1u << (id & 31u)) - 1u));
         atomicAdd(&L.ob_cnt[rank], c);
         L.ob_id[rank] = id;  // every occurrence writes the same id
       }
@@ -3350,168 +3528,57 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     #pragma unroll
     for (int r = 0; r < kRowHistPer; ++r) add(hid[r], hcs[r]);
     for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) add(a.hids[h], a.hcnt[h]);
-    __syncthreads();
+  }
+  // the history tokens' logits, in flight during the stream: unconditional
+  // range-checked loads (an id past the row reads zero and is not stored)
+  uint32_t hraw[kRowHistPer], hmw[kRowHistPer];
+  #pragma unroll
+  for (int r = 0; r < kRowHistPer; ++r) {
+    hraw[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(hid[r] * 4u), 0, 0);
+    if (MASK) hmw[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (int)((hid[r] >> 5) * 4u), 0, 0);
   }
 
-  // 3. the stream
-  const uint32_t kk = (uint32_t)cfg.k_sel;  // 1..kLeanK
-  const uint32_t kw = min(kk, (kk + 15u) / 16u + (uint32_t)ceilf(sqrtf((float)kk)) + 4u);
-  uint64_t* wl = L.wbuf[wid];
-  uint32_t* wh = L.whist[wid];
-  float* xs = L.xscr[wid];
-  uint32_t wn = 0u;              // entries in this wave's list
-  uint32_t T = kKeyNegInf;       // the wave's threshold key (strict)
-  float tf = -__builtin_inff();  // the float of T
-  bool bad = false;              // the list overflowed
-  // Every slot is processed and refilled on every pass, also past the row's
-  // last tile (those logits read as -inf and their loads move no memory):
-  // with no conditional load in the loop the compiler keeps the other
-  // slot's loads in flight while it waits for one slot.
-  const int npass = (ntiles + kRowDepth - 1) / kRowDepth;
+  // 4. the first tile
+  step(Slot0{}, 0, true);
+
+  // 5. the rest of the row, tiles 1, 2, ... (the last pass may run past it)
+  const int npass = ntiles / 2;
   for (int p = 0; p < npass; ++p) {
-    #pragma unroll
-    for (int d = 0; d < kRowDepth; ++d) {
-      const int t = p * kRowDepth + d;
-      const int base = t * kRowTile;
-      float x[kRowEl];
-      #pragma unroll
-      for (int j = 0; j < kRowTV; ++j) {
-        const int e0 = base + (j * kRowThreads + tid) * 4;
-        const uint32_t mbits = MASK ? mw[d][j] >> (e0 & 31) : 0xfu;
-        #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float v = __int_as_float(buf[d][j][q]);
-          if (MASK && !((mbits >> q) & 1u)) v = -__builtin_inff();
-          x[j * 4 + q] = v;
-        }
-      }
-      if (base + kRowTile > V) {
-        #pragma unroll
-        for (int j = 0; j < kRowTV; ++j) {
-          const int e0 = base + (j * kRowThreads + tid) * 4;
-          #pragma unroll
-          for (int q = 0; q < 4; ++q) if (e0 + q >= V) x[j * 4 + q] = -__builtin_inff();
-        }
-      }
-      // history tokens of this lane: captured by rank (one per lane per
-      // round), then left out of the test
-      bool spilled = false;
-      uint32_t mk = 0u;
-      if (hist) {
-        #pragma unroll
-        for (int j = 0; j < kRowTV; ++j) {
-          const int e0 = base + (j * kRowThreads + tid) * 4;
-          const uint32_t bits = e0 < V ? hw[e0 >> 5].x : 0u;
-          mk |= ((bits >> (e0 & 31)) & 0xfu) << (4 * j);
-        }
-        if (__ballot(mk != 0u) != 0ull) {
-          row_spill(xs, x);
-          spilled = true;
-          uint32_t cm = mk;
-          while (__ballot(cm != 0u) != 0ull) {
-            if (cm != 0u) {
-              const uint32_t e = (uint32_t)__builtin_ctz(cm);
-              cm &= cm - 1u;
-              const uint32_t li = (uint32_t)(base + ((int)(e >> 2) * kRowThreads + tid) * 4) + (e & 3u);
-              const uint2 h = hw[li >> 5];
-              const uint32_t rank = h.y + (uint32_t)__popc(h.x & ((1u << (li & 31u)) - 1u));
-              L.ob_raw[rank] = __float_as_uint(row_elem(xs, e));
-            }
-          }
-        }
-      }
-      if (d == 0 && p == 0) {
-        // first tile: a bound with at least kw of the wave's logits at or
-        // above it, from its group maxima (4 logits of a lane each,
-        // history tokens left out): the largest prefix of 20 key bits that
-        // kw group maxima reach
-        constexpr int NG = kRowEl / 4;
-        uint32_t gk[NG];
-        #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          float gm = -__builtin_inff();
-          #pragma unroll
-          for (int q = 0; q < 4; ++q) gm = ((mk >> (4 * g + q)) & 1u) ? gm : fmaxf(gm, x[4 * g + q]);
-          gk[g] = lkey(gm);
-        }
-        uint32_t prefix = 0u;
-        #pragma unroll 1
-        for (int bit = 31; bit >= 12; --bit) {
-          const uint32_t probe = prefix | (1u << bit);
-          uint32_t c = 0u;
-          #pragma unroll
-          for (int g = 0; g < NG; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
-          if (c >= kw) prefix = probe;
-        }
-        if (prefix > kKeyNegInf + 1u) {
-          T = prefix - 1u;
-          tf = okey_inv(T);
-        }
-      }
-      float mx = x[0];
-      #pragma unroll
-      for (int e = 1; e < kRowEl; ++e) mx = fmaxf(mx, x[e]);
-      if (__ballot(mx >= tf) != 0ull) {
-        // survivors: key above T, i.e. x > tf (NaN never passes; +inf passes
-        // and sends the row to the general path at the end); the
-        // signed-zero threshold compares keys
-        uint32_t sb = 0u;
-        if (T == kKeyNegZero) {
-          #pragma unroll
-          for (int e = 0; e < kRowEl; ++e) sb |= lkey(x[e]) > T ? (1u << e) : 0u;
-        } else {
-          #pragma unroll
-          for (int e = 0; e < kRowEl; ++e) sb |= x[e] > tf ? (1u << e) : 0u;
-        }
-        sb &= ~mk;
-        if (__ballot(sb != 0u) != 0ull) {
-          if (!spilled) row_spill(xs, x);
-          // appended one per lane per round (the list stops at its capacity)
-          for (;;) {
-            const uint64_t m = __ballot(sb != 0u);
-            if (m == 0ull) break;
-            const uint32_t add = (uint32_t)__popcll(m);
-            if (wn + add > (uint32_t)kRowCap) {
-              bad = true;
-              break;
-            }
-            if (sb != 0u) {
-              const uint32_t e = (uint32_t)__builtin_ctz(sb);
-              sb &= sb - 1u;
-              const uint32_t idx = (uint32_t)(base + ((int)(e >> 2) * kRowThreads + tid) * 4) + (e & 3u);
-              wl[wn + lanes_below(m)] = cand_key(okey(row_elem(xs, e)), idx);
-            }
-            wn += add;
-          }
-          if (wn > (uint32_t)kRowHW) {
-            T = row_wave_keep(wl, wn, kw, wh);
-            tf = okey_inv(T);
-          }
-        }
-      }
-      wave_lds_sync();  // the tile's reads of xs are done before the next spill
-      // refill this slot with tile t + kRowDepth
-      #pragma unroll
-      for (int j = 0; j < kRowTV; ++j) {
-        const int e0 = (t + kRowDepth) * kRowTile + (j * kRowThreads + tid) * 4;
-        buf[d][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * 4, 0, 0);
-        if (MASK) mw[d][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (e0 >> 5) * 4, 0, 0);
-      }
-    }
+    step(Slot1{}, 2 * p + 1, false);
+    step(Slot0{}, 2 * p + 2, false);
   }
   if (wn > kw) T = row_wave_keep(wl, wn, kw, wh);
   if (lane == 0u) {
     L.wthr[wid] = T;
     L.wbad[wid] = bad ? 1u : 0u;
   }
-  __syncthreads();  // lists, thresholds and captured history logits complete
+  if (hist) {
+    auto put = [&](uint32_t id, uint32_t raw) {
+      const uint2 h = hw[id >> 5];
+      L.ob_raw[h.y + (uint32_t)__popc(h.x & ((1u << (id & 31u)) - 1u))] = raw;
+    };
+    constexpr uint32_t kNegInfBits = 0xff800000u;
+    #pragma unroll
+    for (int r = 0; r < kRowHistPer; ++r) {
+      if (hid[r] < (uint32_t)V) put(hid[r], MASK && !((hmw[r] >> (hid[r] & 31u)) & 1u) ? kNegInfBits : hraw[r]);
+    }
+    for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) {
+      const uint32_t id = a.hids[h];
+      if (id < (uint32_t)V) {
+        const bool off = MASK && !((mrow[id >> 5] >> (id & 31u)) & 1u);
+        put(id, off ? kNegInfBits : __float_as_uint(lrow[id]));
+      }
+    }
+  }
+  __syncthreads();  // lists, thresholds and the history complete
   uint32_t Tm = L.wthr[0];
   uint32_t anybad = L.wbad[0];
   #pragma unroll
   for (int w = 1; w < kRowWaves; ++w) { Tm = max(Tm, L.wthr[w]); anybad |= L.wbad[w]; }
   if (anybad) return false;
 
-  // 4. the candidates: list entries and processed history logits >= Tm
+  // 6. the candidates: list entries that are not history tokens and
+  //    processed history logits, at or above Tm
   constexpr int kLq = (kRowKwMax + 63) / 64;
   uint64_t sc[kLq];
   uint64_t hc[kRowHistPer];
@@ -3521,7 +3588,11 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   for (int q = 0; q < kLq; ++q) {
     const uint32_t i = lane + 64u * q;
     const uint64_t c = i < wn ? wl[i] : 0ull;
-    const bool keep = i < wn && cand_skey(c) >= Tm;
+    bool keep = i < wn && cand_skey(c) >= Tm;
+    if (keep && hist) {
+      const uint32_t id = cand_idx(c);
+      keep = !((hw[id >> 5].x >> (id & 31u)) & 1u);
+    }
     sc[q] = keep ? c : 0ull;
     mine += keep ? 1u : 0u;
     top = sc[q] > top ? sc[q] : top;
@@ -3538,9 +3609,24 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     mine += hc[q] != 0ull ? 1u : 0u;
     top = hc[q] > top ? hc[q] : top;
   }
-  uint32_t n = 0u;
-  uint32_t pos = block_excl_scan_u32<kRowThreads>(mine, L.redu, &n);  // barriers: LDS inputs read
-  top = block_max_u64<kRowThreads>(top, L.red64);
+  // one barrier for the candidates' positions and the row's top key
+  uint32_t pos, n = 0u;
+  {
+    const uint32_t incl = wave_incl_scan_u32(mine);
+    const uint64_t wtop = wave_max_u64(top);
+    if (lane == 63u) { L.redu[wid] = incl; L.red64[wid] = wtop; }
+    __syncthreads();  // also: every LDS input above has been read
+    uint32_t before = 0u;
+    top = 0ull;
+    #pragma unroll
+    for (int v = 0; v < kRowWaves; ++v) {
+      const uint32_t c = L.redu[v];
+      before += v < wid ? c : 0u;
+      n += c;
+      top = L.red64[v] > top ? L.red64[v] : top;
+    }
+    pos = before + incl - mine;
+  }
   // +inf logits rank as -inf (gpu.rs:767-777): the general path resolves
   // them; fewer candidates than kk hold the row's top kk only if nothing
   // finite was left out
@@ -3563,11 +3649,9 @@ __global__ void __launch_bounds__(kRowThreads) row_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   RowLds& L = *reinterpret_cast<RowLds*>(lds_raw);
   const int row = blockIdx.x;
-  uint32_t h0 = 0u, h1 = 0u;
-  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; }
   const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
   if (cfg.cls == kTopK && !cfg.wide) {
-    if (row_stream<MASK>(L, a, row, cfg, h0, h1, lds_raw)) return;
+    if (row_stream<MASK>(L, a, row, cfg, lds_raw)) return;
     __syncthreads();
   }
   // the general path, on the first NT threads: the chunk select and the

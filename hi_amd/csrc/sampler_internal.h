@@ -54,6 +54,7 @@ struct RowCfg {
   bool wide;      // top-k row with k_eff > kLeanK
   int k_sel;      // candidates each chunk keeps
   bool store_s;   // scaled logits go to the workspace
+  float u;        // the row's uniform for the draw
 };
 
 // Per (row, chunk) statistics written by the scan, merged by the finish.

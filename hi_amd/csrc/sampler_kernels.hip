@@ -115,6 +115,10 @@ __device__ __forceinline__ int next_pow2(int x) {
 
 // ---- parameters ----------------------------------------------------------
 
+__device__ __forceinline__ float row_uniform(const ParamsView& pv, int row) {
+  return pv.uniforms ? pv.uniforms[row] : pv.uniform_value;
+}
+
 __device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V, int n_lp, int need_lse) {
   RowCfg c;
   // The batch-wide values first; the per-row modes replace them.  (Every
@@ -157,12 +161,10 @@ __device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V,
   auto su = [](float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); };
   c.T = su(c.T); c.top_p = su(c.top_p); c.min_p = su(c.min_p); c.rep = su(c.rep);
   c.freq = su(c.freq); c.pres = su(c.pres); c.t_eff = su(c.t_eff); c.cutoff = su(c.cutoff);
+  c.u = su(row_uniform(pv, row));  // loaded with the parameters, long before the draw
   return c;
 }
 
-__device__ __forceinline__ float row_uniform(const ParamsView& pv, int row) {
-  return pv.uniforms ? pv.uniforms[row] : pv.uniform_value;
-}
 
 // Stages 2 and 3 of the processed logit (the mask is applied by the caller):
 // repetition penalty per occurrence (crates/hi-mlx/src/generate.rs:60-70),
@@ -177,6 +179,12 @@ __device__ __forceinline__ float apply_penalties(float l, uint32_t cnt, const Ro
   l = l - fc;
   l = l - c.pres;
   return l;
+}
+
+// apply_penalties for rows without a repetition penalty, with no branch.
+__device__ __forceinline__ float apply_penalties_norep(float l, uint32_t cnt, const RowCfg& c) {
+  const float p = (l - c.freq * (float)cnt) - c.pres;
+  return cnt == 0u ? l : p;
 }
 
 // ---- wave-wide reductions and scans on DPP lane moves ---------------------
@@ -1104,7 +1112,7 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
   const float M = finitef_(rs.max_l) ? rs.max_l / cfg.t_eff : -__builtin_inff();
   const uint32_t am_ieee = rs.am_ieee_i == 0xffffffffu ? 0u : rs.am_ieee_i;
   const uint32_t am_fin = rs.am_fin_i == 0xffffffffu ? 0u : rs.am_fin_i;
-  const float u = row_uniform(a.pv, row);
+  const float u = cfg.u;
 
   const bool eos = a.mask && !rs.any_finite;
   uint32_t token;
@@ -1265,19 +1273,47 @@ constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
 // Sequential f32 sums over the wave's lanes: lane l < n returns
 // ((start + v_0) + v_1) + ... + v_l, the reference's left-to-right fold
 // (gpu.rs:834-836, 851, 878, 889-896); lanes from n on hold partial sums.
-// n - 1 dependent steps: each moves the running sums one lane up
-// (wave_shr:1; lane 0 takes `start`) and adds.
+// Lane 0 holds start + v_0 from the outset; each step adds v to the running
+// sums moved one lane up (wave_shr:1 filling lane 0 with zero, which the
+// compiler fuses into the add).  After step s lanes [0, s] hold their
+// final sums and later steps leave them unchanged, so steps run in groups
+// of 8 (n - 1 steps are needed).  No lane's sum is -0 (the terms and
+// `start` are not negative), so 0 + x == x at lane 0.
+__device__ __forceinline__ float wave_fold_u(float u) {
+  return __uint_as_float(dpp32<0x138, 0xf, true>(0u, __float_as_uint(u)));
+}
 __device__ __forceinline__ float wave_fold_f32(float v, float start, int n) {
-  // after step s lanes [0, s] hold their sums: lanes [0, n) need n - 1 steps
-  float p = start + v;
-  int s = 1;
+  const float u = (threadIdx.x & 63u) == 0u ? start + v : v;
+  float p = u;
   #pragma unroll 1
-  for (; s + 8 <= n; s += 8) {
+  for (int s = 1; s < n; s += 8) {
     #pragma unroll
-    for (int i = 0; i < 8; ++i) p = __uint_as_float(dpp32<0x138>(__float_as_uint(start), __float_as_uint(p))) + v;
+    for (int i = 0; i < 8; ++i) p = wave_fold_u(p) + u;
   }
+  return p;
+}
+
+// wave_fold_f32 that stops once a lane at or below the last final one has
+// hit set and p >= cutoff; returns the first such lane (-1: none, all n
+// lanes final).  Lanes past the returned one may hold partial sums.
+__device__ __forceinline__ float wave_fold_f32_until(float v, float start, int n, bool hit, float cutoff,
+                                                     int& first) {
+  const int lane = (int)(threadIdx.x & 63u);
+  const float u = lane == 0 ? start + v : v;
+  float p = u;
+  first = -1;
   #pragma unroll 1
-  for (; s < n; ++s) p = __uint_as_float(dpp32<0x138>(__float_as_uint(start), __float_as_uint(p))) + v;
+  for (int s = 0;; s += 8) {
+    // lanes [0, s] are final
+    const uint64_t m = __ballot(hit && lane <= s && p >= cutoff);
+    if (m != 0ull) {
+      first = __ffsll((unsigned long long)m) - 1;
+      break;
+    }
+    if (s >= n - 1) break;
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) p = wave_fold_u(p) + u;
+  }
   return p;
 }
 
@@ -1373,33 +1409,33 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   }
   const float total = P;
   if (!(total > 0.f) || !finitef_(total)) return false;  // argmax_host fallback
-  // the nucleus: cum_p over w / total of the positive entries (gpu.rs:843-856)
-  float Q = 0.f;
-  int m_end = 0;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int i = m * 64 + (int)lane;
-    fb[m] = fa[m] > 0.f ? fa[m] / total : 0.f;
-    qa[m] = Q;
-    if (m * 64 < k) {
-      qa[m] = wave_fold_f32(fb[m], Q, min(64, k - m * 64));
-      Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(qa[m]), min(63, k - 1 - m * 64)));
-    }
-    (void)i;
-  }
+  // the nucleus: cum_p over w / total of the positive entries (gpu.rs:843-856),
+  // folded only as far as the first one that reaches the cutoff
   int last_pos = -1;   // last positive entry
   int cut = -1;        // first positive entry where cum_p reaches the cutoff
   #pragma unroll
   for (int m = 0; m < DM; ++m) {
     const int i = m * 64 + (int)lane;
-    const bool pos = i < k && fa[m] > 0.f;
-    const uint64_t pm = __ballot(pos);
+    const uint64_t pm = __ballot(i < k && fa[m] > 0.f);
     if (pm != 0ull) last_pos = m * 64 + 63 - __clzll((unsigned long long)pm);
-    const uint64_t cm = __ballot(pos && cfg.cutoff < 1.f && qa[m] >= cfg.cutoff);
-    if (cut < 0 && cm != 0ull) cut = m * 64 + __ffsll((unsigned long long)cm) - 1;
+  }
+  if (cfg.cutoff < 1.f) {
+    float Q = 0.f;
+    #pragma unroll
+    for (int m = 0; m < DM; ++m) {
+      if (cut < 0 && m * 64 < k) {
+        const int i = m * 64 + (int)lane;
+        const bool pos = i < k && fa[m] > 0.f;
+        fb[m] = pos ? fa[m] / total : 0.f;
+        int first;
+        qa[m] = wave_fold_f32_until(fb[m], Q, min(64, k - m * 64), pos, cfg.cutoff, first);
+        if (first >= 0) cut = m * 64 + first;
+        else Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(qa[m]), min(63, k - 1 - m * 64)));
+      }
+    }
   }
   if (last_pos < 0) return false;  // no candidate: argmax_host fallback
-  m_end = cut >= 0 ? cut + 1 : last_pos + 1;
+  const int m_end = cut >= 0 ? cut + 1 : last_pos + 1;
   const int me = m_end - 1;
   float ct = 0.f;
   #pragma unroll
@@ -1407,7 +1443,7 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
     if ((me >> 6) == m) ct = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), me & 63));
   if (!(ct > 0.f) || !finitef_(ct)) return false;
   // inverse CDF: the first candidate whose cumulative weight passes target
-  const float target = clamp_uniform(row_uniform(a.pv, row)) * ct;
+  const float target = clamp_uniform(cfg.u) * ct;
   int pick = -1;
   #pragma unroll
   for (int m = 0; m < DM; ++m) {
@@ -3207,7 +3243,8 @@ constexpr int kSelChunkSmall = NT * 16;
 //    and sends the row to the general path; with kw at mean + 4 sd of that
 //    count it does not happen for rows whose top tokens are spread over the
 //    vocabulary.
-// The first four waves then run finish_core; the others end there.  Rows the
+// Once every wave has written its list, the others end and the first four
+// waves (one per SIMD) gather the candidates and run finish_core.  Rows the
 // fast path does not cover (other row classes, more than kRowHistCap
 // distinct history tokens, a list overflow, no finite logit, +inf logits, a
 // tie finish_core will not resolve) run the chunk select and the finish of
@@ -3238,11 +3275,15 @@ struct RowLds {
   // the fields below stay valid while the finish reuses the space above
   uint32_t wthr[kRowWaves];
   uint32_t wbad[kRowWaves];
+  uint32_t wcnt[kRowWaves];
   uint32_t redu[kRowWaves];
   uint64_t red64[kRowWaves];
 };
 constexpr size_t kRowHead = (sizeof(RowLds) + 15) & ~(size_t)15;
 static_assert(sizeof(FinLds) <= offsetof(RowLds, wthr), "finish LDS must fit the stream's lists");
+static_assert(offsetof(RowLds, ob_raw) % 16 == 0 && offsetof(RowLds, ob_cnt) % 16 == 0 &&
+                  offsetof(RowLds, ob_id) % 16 == 0,
+              "the history arrays are read 16 bytes at a time");
 
 // Keeps the `need` largest entries of the wave's list (unique keys,
 // need <= n) at its front; returns the key of the last one kept.
@@ -3551,6 +3592,7 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   if (lane == 0u) {
     L.wthr[wid] = T;
     L.wbad[wid] = bad ? 1u : 0u;
+    L.wcnt[wid] = wn;
   }
   if (hist) {
     auto put = [&](uint32_t id, uint32_t raw) {
@@ -3571,43 +3613,79 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     }
   }
   __syncthreads();  // lists, thresholds and the history complete
+
+  // 6. the rest runs on the first NT threads, one wave per SIMD; the other
+  //    waves end here (ended waves no longer count at barriers)
+  if (wid >= NT / 64) return true;
   uint32_t Tm = L.wthr[0];
   uint32_t anybad = L.wbad[0];
   #pragma unroll
   for (int w = 1; w < kRowWaves; ++w) { Tm = max(Tm, L.wthr[w]); anybad |= L.wbad[w]; }
   if (anybad) return false;
 
-  // 6. the candidates: list entries that are not history tokens and
-  //    processed history logits, at or above Tm
-  constexpr int kLq = (kRowKwMax + 63) / 64;
-  uint64_t sc[kLq];
-  uint64_t hc[kRowHistPer];
+  // the candidates: list entries that are not history tokens and processed
+  // history logits, at or above Tm.  Wave f reads the lists f, f + 4, ...
+  // (lane l their entry l: a list holds at most kRowKwMax < 64 entries)
+  constexpr int kFinWaves = NT / 64;
+  constexpr int kLists = kRowWaves / kFinWaves;
+  constexpr int kHq = kRowHistCap / NT;
+  uint64_t sc[kLists];
+  uint64_t hc[kHq];
   uint32_t mine = 0u;
   uint64_t top = 0ull;
-  #pragma unroll
-  for (int q = 0; q < kLq; ++q) {
-    const uint32_t i = lane + 64u * q;
-    const uint64_t c = i < wn ? wl[i] : 0ull;
-    bool keep = i < wn && cand_skey(c) >= Tm;
-    if (keep && hist) {
-      const uint32_t id = cand_idx(c);
-      keep = !((hw[id >> 5].x >> (id & 31u)) & 1u);
+  {
+    // every LDS read is issued before any result is used
+    uint32_t nv[kLists], mk[kLists];
+    #pragma unroll
+    for (int m = 0; m < kLists; ++m) {
+      const int v = wid + kFinWaves * m;
+      nv[m] = L.wcnt[v];
+      sc[m] = L.wbuf[v][lane];
     }
-    sc[q] = keep ? c : 0ull;
-    mine += keep ? 1u : 0u;
-    top = sc[q] > top ? sc[q] : top;
+    if (hist) {
+      #pragma unroll
+      for (int m = 0; m < kLists; ++m) mk[m] = hw[min(cand_idx(sc[m]), (uint32_t)V - 1u) >> 5].x;
+    }
+    #pragma unroll
+    for (int m = 0; m < kLists; ++m) {
+      bool keep = lane < nv[m] && cand_skey(sc[m]) >= Tm;
+      if (hist) keep = keep && !((mk[m] >> (cand_idx(sc[m]) & 31u)) & 1u);
+      sc[m] = keep ? sc[m] : 0ull;
+      mine += keep ? 1u : 0u;
+      top = sc[m] > top ? sc[m] : top;
+    }
   }
   #pragma unroll
-  for (int q = 0; q < kRowHistPer; ++q) {
-    const uint32_t r = (uint32_t)(tid + kRowThreads * q);
-    hc[q] = 0ull;
-    if (r < distinct) {
-      const float pl = apply_penalties(__uint_as_float(L.ob_raw[r]), L.ob_cnt[r], cfg);
-      const uint32_t k = lkey(pl);
-      if (k > kKeyNegInf && k >= Tm) hc[q] = cand_key(k, L.ob_id[r]);
+  for (int q = 0; q < kHq; ++q) hc[q] = 0ull;
+  const uint32_t r0 = (uint32_t)tid * (uint32_t)kHq;  // this thread's ranks: r0 .. r0 + kHq - 1
+  if (r0 < distinct) {
+    static_assert(kHq % 4 == 0, "ranks are read four at a time");
+    uint32_t raw[kHq], cnt[kHq], ids[kHq];
+    #pragma unroll
+    for (int q = 0; q < kHq; q += 4) {
+      const uint4 x = *reinterpret_cast<const uint4*>(&L.ob_raw[r0 + q]);
+      const uint4 c = *reinterpret_cast<const uint4*>(&L.ob_cnt[r0 + q]);
+      const uint4 i = *reinterpret_cast<const uint4*>(&L.ob_id[r0 + q]);
+      raw[q] = x.x; raw[q + 1] = x.y; raw[q + 2] = x.z; raw[q + 3] = x.w;
+      cnt[q] = c.x; cnt[q + 1] = c.y; cnt[q + 2] = c.z; cnt[q + 3] = c.w;
+      ids[q] = i.x; ids[q + 1] = i.y; ids[q + 2] = i.z; ids[q + 3] = i.w;
     }
-    mine += hc[q] != 0ull ? 1u : 0u;
-    top = hc[q] > top ? hc[q] : top;
+    float pl[kHq];
+    if (cfg.rep_on) {
+      #pragma unroll
+      for (int q = 0; q < kHq; ++q) pl[q] = apply_penalties(__uint_as_float(raw[q]), cnt[q], cfg);
+    } else {
+      #pragma unroll
+      for (int q = 0; q < kHq; ++q) pl[q] = apply_penalties_norep(__uint_as_float(raw[q]), cnt[q], cfg);
+    }
+    #pragma unroll
+    for (int q = 0; q < kHq; ++q) {
+      const uint32_t k = lkey(pl[q]);
+      const bool keep = r0 + q < distinct && k > kKeyNegInf && k >= Tm;
+      hc[q] = keep ? cand_key(k, ids[q]) : 0ull;
+      mine += keep ? 1u : 0u;
+      top = hc[q] > top ? hc[q] : top;
+    }
   }
   // one barrier for the candidates' positions and the row's top key
   uint32_t pos, n = 0u;
@@ -3619,7 +3697,7 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     uint32_t before = 0u;
     top = 0ull;
     #pragma unroll
-    for (int v = 0; v < kRowWaves; ++v) {
+    for (int v = 0; v < kFinWaves; ++v) {
       const uint32_t c = L.redu[v];
       before += v < wid ? c : 0u;
       n += c;
@@ -3634,11 +3712,10 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   if (n < kk && Tm > kKeyNegInf) return false;
   FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
   #pragma unroll
-  for (int q = 0; q < kLq; ++q) if (sc[q] != 0ull) fs.cbig[pos++] = sc[q];
+  for (int m = 0; m < kLists; ++m) if (sc[m] != 0ull) fs.cbig[pos++] = sc[m];
   #pragma unroll
-  for (int q = 0; q < kRowHistPer; ++q) if (hc[q] != 0ull) fs.cbig[pos++] = hc[q];
+  for (int q = 0; q < kHq; ++q) if (hc[q] != 0ull) fs.cbig[pos++] = hc[q];
   __syncthreads();
-  if (wid >= NT / 64) return true;  // the finish runs on the first NT threads
   const float M = key_to_s(cand_skey(top), cfg.t_eff);
   return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm);
 }

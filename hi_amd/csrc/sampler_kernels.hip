@@ -547,6 +547,8 @@ struct FinLds {
   uint32_t sel[4];
   uint32_t counter, n_ext, token, flag;
   float fval0, fval1;
+  uint64_t below;   // largest candidate left out of the selection
+  uint32_t wmin;    // bits of the smallest selected weight
 };
 constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
 
@@ -1205,46 +1207,59 @@ constexpr int kFinPer = kGather / NT;  // candidates each thread gathers
 
 // Threshold T such that exactly k of items[0, n) (unique keys, LDS) are
 // >= T, 1 <= k <= n: an 8-bit MSD radix select over the workgroup that
-// starts below the items' common high bits.  All threads call it.
+// starts below the common high bits of the keys' bounds lo <= key <= hi
+// (lo > hi: the bounds are the keys' own minimum and maximum, found here).
+// Two 256-bin histograms (hist[0, 512)) alternate, so a pass takes two
+// barriers: counts, then the chosen bin.  All threads call it.
 __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int n, uint32_t k, uint32_t* hist,
-                                                      uint32_t* sel, uint64_t* reda, uint64_t* redb) {
+                                                      uint32_t* sel, uint64_t* reda, uint64_t* redb,
+                                                      uint64_t lo = ~0ull, uint64_t hi_b = 0ull) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
-  uint64_t mn = ~0ull, mx = 0ull;
-  for (int i = tid; i < n; i += NT) {
-    const uint64_t x = items[i];
-    mn = x < mn ? x : mn;
-    mx = x > mx ? x : mx;
+  uint64_t mn = lo, mx = hi_b;
+  for (int b = tid; b < 256; b += NT) hist[b] = 0u;
+  if (lo > hi_b) {
+    mn = ~0ull;
+    mx = 0ull;
+    for (int i = tid; i < n; i += NT) {
+      const uint64_t x = items[i];
+      mn = x < mn ? x : mn;
+      mx = x > mx ? x : mx;
+    }
+    mn = wave_min_u64(mn);
+    mx = wave_max_u64(mx);
+    if (lane == 0) { reda[wid] = mn; redb[wid] = mx; }
   }
-  mn = wave_min_u64(mn);
-  mx = wave_max_u64(mx);
-  if (lane == 0) { reda[wid] = mn; redb[wid] = mx; }
-  __syncthreads();
-  mn = reda[0];
-  mx = redb[0];
-  #pragma unroll
-  for (int w = 1; w < NT / 64; ++w) { mn = reda[w] < mn ? reda[w] : mn; mx = redb[w] > mx ? redb[w] : mx; }
+  __syncthreads();  // also: hist[0, 256) is zero
+  if (lo > hi_b) {
+    mn = reda[0];
+    mx = redb[0];
+    #pragma unroll
+    for (int w = 1; w < NT / 64; ++w) { mn = reda[w] < mn ? reda[w] : mn; mx = redb[w] > mx ? redb[w] : mx; }
+  }
   if (mn == mx) return mx;
   int hi = 64 - __clzll(mn ^ mx);
   uint64_t prefix = hi >= 64 ? 0ull : (mx >> hi) << hi;
   uint32_t remaining = k;
+  int cur = 0;
   #pragma unroll 1
   while (hi > 0) {
     const int db = hi >= 8 ? 8 : hi;
-    const int lo = hi - db;
+    const int lo_bit = hi - db;
     const uint64_t hp = hi >= 64 ? 0ull : (prefix >> hi);
-    for (int b = tid; b < 256; b += NT) hist[b] = 0u;
-    __syncthreads();
+    uint32_t* h = hist + cur * 256;
+    uint32_t* o = hist + (cur ^ 1) * 256;  // the next pass's bins: last read before the previous barrier
+    for (int b = tid; b < 256; b += NT) o[b] = 0u;
     for (int i = tid; i < n; i += NT) {
       const uint64_t x = items[i];
-      if (hi >= 64 || (x >> hi) == hp) atomicAdd(&hist[(uint32_t)(x >> lo) & ((1u << db) - 1u)], 1u);
+      if (hi >= 64 || (x >> hi) == hp) atomicAdd(&h[(uint32_t)(x >> lo_bit) & ((1u << db) - 1u)], 1u);
     }
     __syncthreads();
     if (tid < 64) {
       // lane l owns bins 255-4l .. 252-4l (descending)
       uint32_t loc[4], lsum = 0;
       #pragma unroll
-      for (int q = 0; q < 4; ++q) { loc[q] = hist[255 - 4 * tid - q]; lsum += loc[q]; }
+      for (int q = 0; q < 4; ++q) { loc[q] = h[255 - 4 * tid - q]; lsum += loc[q]; }
       const uint32_t inc = wave_incl_scan_u32(lsum);
       const uint32_t above = inc - lsum;
       if (above < remaining && remaining <= above + lsum) {
@@ -1259,10 +1274,11 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
       }
     }
     __syncthreads();
-    prefix |= (uint64_t)sel[0] << lo;
+    prefix |= (uint64_t)sel[0] << lo_bit;
     remaining -= sel[1];
     const bool done = sel[2] == remaining;
-    hi = lo;
+    hi = lo_bit;
+    cur ^= 1;
     if (done) break;
   }
   return prefix;
@@ -1322,10 +1338,12 @@ __device__ __forceinline__ float wave_fold_f32_until(float v, float start, int n
 // the processed-logit keys of the row's logits that are not candidates (0:
 // none); part is this thread's share of the logprob normaliser over those
 // logits (double, relative to M); when n exceeds the selection size, its
-// last key must be above `above`.  Returns false when the row needs the
+// last key must be above `above`; lo <= hi bound the candidates' keys when
+// the caller knows them (lo > hi: unknown).  Returns false when the row needs the
 // general finish; all threads return the same.
 __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, int n,
-                                            float M, uint32_t ub_key, double part, uint32_t above = 0u) {
+                                            float M, uint32_t ub_key, double part, uint32_t above = 0u,
+                                            uint64_t lo = ~0ull, uint64_t hi = 0ull) {
   const int tid = threadIdx.x;
   const uint32_t lane = (uint32_t)tid & 63u;
   const bool want_lp = a.n_lp > 0 || a.out_token_lp != nullptr;
@@ -1340,45 +1358,73 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   // 4. the top kk by (processed logit desc, index asc)
   const int kk = min(cfg.k_sel, n);
   uint64_t thr = 0ull;
-  if (n > kk) thr = block_select_skip(fs.cbig, n, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b);
+  if (tid == 0) { fs.counter = 0u; fs.below = 0ull; fs.wmin = 0xffffffffu; }
+  if (n > kk) thr = block_select_skip(fs.cbig, n, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b, lo, hi);
+  else __syncthreads();  // the counters above are set
   // the caller's candidates hold the row's top kk only if the kk-th key is
   // above `above` (the largest key the caller may have left out)
   if (n > kk && cand_skey(thr) <= above) return false;
-  if (tid == 0) fs.counter = 0u;
-  __syncthreads();
-  uint64_t below = 0ull;  // largest candidate left out
-  for (int j = tid; j < n; j += NT) {
-    const uint64_t x = fs.cbig[j];
-    if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
-    else below = x > below ? x : below;
+  // the selection into fs.buf and the largest candidate left out, both
+  // complete at one barrier (one LDS atomic per wave: same-address atomics
+  // of every lane would be serialised)
+  {
+    uint32_t c = 0u;
+    uint64_t below = 0ull;
+    for (int j = tid; j < n; j += NT) {
+      const uint64_t x = fs.cbig[j];
+      c += x >= thr ? 1u : 0u;
+      if (x < thr) below = x > below ? x : below;
+    }
+    const uint32_t incl = wave_incl_scan_u32(c);
+    uint32_t base = 0u;
+    if (lane == 63u) base = atomicAdd(&fs.counter, incl);
+    uint32_t at = (uint32_t)__builtin_amdgcn_readlane((int)base, 63) + incl - c;
+    for (int j = tid; j < n; j += NT) {
+      const uint64_t x = fs.cbig[j];
+      if (x >= thr) fs.buf[at++] = x;
+    }
+    below = wave_max_u64(below);
+    if (lane == 0u && below != 0ull) atomicMax((unsigned long long*)&fs.below, (unsigned long long)below);
   }
-  below = block_max_u64<NT>(below, fs.red64);  // has barriers: fs.buf is complete
+  __syncthreads();
+  const uint64_t below = fs.below;  // largest candidate left out (0: none)
 
   // 5. weights and rank keys; the smallest selected weight w_b
   uint64_t rk = 0ull;
   uint32_t pk = 0u;
-  uint32_t wbits = 0xffffffffu;
+  uint32_t wnot = 0u;  // ~(bits of w): w >= 0, so its bits order as the value
   if (tid < kk) {
     const uint64_t x = fs.buf[tid];
     const float sx = key_to_s(cand_skey(x), cfg.t_eff);
     const float w = exact_expf(sx - M);
     rk = rank_key(w, cand_idx(x));
     pk = okey(sx);
-    wbits = __float_as_uint(w);
+    wnot = ~__float_as_uint(w);
+    fs.buf[tid] = rk;
   }
-  const float w_b = __uint_as_float(~block_max_u32<NT>(~wbits, fs.redu));
+  if (tid < ((kk + 63) & ~63)) {
+    wnot = wave_max_u32(wnot);
+    if (lane == 0u) atomicMin(&fs.wmin, ~wnot);
+  }
+  __syncthreads();
+  const float w_b = __uint_as_float(fs.wmin);
   // 6. could a logit outside the selection tie with w_b?  Weights are
   //    monotone in the key, so the largest excluded key decides (finish_row
   //    resolves those rows exactly).
   const uint32_t xk = max(ub_key, below != 0ull ? cand_skey(below) : 0u);
   if (w_b > 0.f && xk > kKeyNegInf && exact_expf(key_to_s(xk, cfg.t_eff) - M) == w_b) return false;
 
-  // 7. rank order by counting (kk <= NT: one entry per thread)
-  if (tid < kk) fs.buf[tid] = rk;
-  __syncthreads();
+  // 7. rank order by counting (kk <= NT: one entry per thread); two keys
+  //    per LDS read
   if (tid < kk) {
     uint32_t r = 0u;
-    for (int j = 0; j < kk; ++j) r += fs.buf[j] > rk;
+    const int kk2 = kk & ~1;
+    #pragma unroll 4
+    for (int j = 0; j < kk2; j += 2) {
+      const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&fs.buf[j]);
+      r += (y.x > rk ? 1u : 0u) + (y.y > rk ? 1u : 0u);
+    }
+    if (kk & 1) r += fs.buf[kk - 1] > rk ? 1u : 0u;
     fs.cbig[r] = rk;
     fs.aux[r] = pk;
   }
@@ -3717,7 +3763,8 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   for (int q = 0; q < kHq; ++q) if (hc[q] != 0ull) fs.cbig[pos++] = hc[q];
   __syncthreads();
   const float M = key_to_s(cand_skey(top), cfg.t_eff);
-  return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm);
+  // key bounds for the selection: every candidate's key is at least Tm
+  return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm, (uint64_t)Tm << 32, top);
 }
 
 // One workgroup per row (see the section comment).

@@ -57,6 +57,9 @@ int internal_workspace(size_t bytes, void** out) {
     }
     e = hipMalloc(&ws.ptr, bytes);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(sampler workspace)");
+    // the per-row chunk counters start at zero; the kernels leave them so
+    e = hipMemset(ws.ptr, 0, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMemset(sampler workspace)");
     ws.bytes = bytes;
   }
   *out = ws.ptr;
@@ -71,6 +74,7 @@ void carve(hi_rocm::SampleArgs& a, void* ws, const hi_rocm::WorkspaceLayout& L) 
   a.ws_w = (float*)(base + L.ws_w);
   a.ws_list = (uint64_t*)(base + L.ws_list);
   a.list_stride = L.list_stride;
+  a.done = (uint32_t*)(base + L.done);
   a.chunk = hi_rocm::choose_chunk(a.B, a.V, a.n_lp, a.vec_ok, a.hoff != nullptr);
   a.n_chunks = (a.V + a.chunk - 1) / a.chunk;
 }

@@ -104,10 +104,16 @@ struct SampleArgs {
   float* ws_w;         // [B][V]
   uint64_t* ws_list;   // [B][list_stride]
   int64_t list_stride;
+  uint32_t* done;      // [kFusedMaxRows] chunks of the row finished (zero between launches)
 };
 
+// Batches whose (chunk, row) grid has at most this many workgroups run the
+// select and the finish as one kernel; that bounds their rows too.
+constexpr int kFusedMaxWorkgroups = 512;
+constexpr int kFusedMaxRows = kFusedMaxWorkgroups;
+
 struct WorkspaceLayout {
-  size_t stats, cand, ws_s, ws_w, ws_list, total;
+  size_t stats, cand, ws_s, ws_w, ws_list, done, total;
   int64_t slots;       // (row, chunk) records reserved
   int64_t list_stride;
 };
@@ -135,6 +141,9 @@ inline WorkspaceLayout workspace_layout(int max_batch, int V) {
   }
   L.list_stride = next_pow2_i64(V);
   size_t off = 0;
+  // the fused path's per-row counters first, at the same place in every
+  // layout (calls of any shape may share a workspace)
+  L.done = off; off = align(off + (size_t)kFusedMaxRows * sizeof(uint32_t));
   L.stats = off; off = align(off + (size_t)L.slots * sizeof(ChunkStat));
   L.cand = off; off = align(off + (size_t)L.slots * kFast * sizeof(uint64_t));
   L.ws_s = off; off = align(off + (size_t)max_batch * V * sizeof(float));

@@ -146,7 +146,9 @@ int hi_rocm_sampler_workspace_bytes(int max_batch, int vocab, int n_logprobs,
  *                index asc) with log-softmax of the processed distribution
  *   out_token_logprobs f32[batch] log-prob of the sampled token, or NULL
  *   workspace    >= hi_rocm_sampler_workspace_bytes(batch, vocab, n_logprobs);
- *                one stream at a time per workspace
+ *                zero-filled before its first use (it holds per-row counters
+ *                that every call leaves at zero); one stream at a time per
+ *                workspace
  * No allocation and no host synchronisation: safe to capture in a hipGraph.
  */
 int hi_rocm_sample(const void* logits, int dtype, int batch, int vocab, int64_t row_stride,

@@ -3661,7 +3661,6 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     step(Slot1{}, 2 * p + 1, false);
     step(Slot0{}, 2 * p + 2, false);
   }
-  if (wn > kw) T = row_wave_keep(wl, wn, kw, wh);
   if (lane == 0u) {
     L.wthr[wid] = T;
     L.wbad[wid] = bad ? 1u : 0u;
@@ -3698,10 +3697,11 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
 
   // the candidates: list entries that are not history tokens and processed
   // history logits, at or above Tm.  Wave f reads the lists f, f + 4, ...
-  // (lane l their entry l: a list holds at most kRowKwMax < 64 entries)
+  // (lane l their entries l and l + 64: a list holds at most kRowCap)
   constexpr int kFinWaves = NT / 64;
-  constexpr int kLists = kRowWaves / kFinWaves;
+  constexpr int kLists = kRowWaves / kFinWaves * (kRowCap / 64);
   constexpr int kHq = kRowHistCap / NT;
+  static_assert(kRowCap == 128, "two list entries per lane");
   uint64_t sc[kLists];
   uint64_t hc[kHq];
   uint32_t mine = 0u;
@@ -3711,9 +3711,10 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     uint32_t nv[kLists], mk[kLists];
     #pragma unroll
     for (int m = 0; m < kLists; ++m) {
-      const int v = wid + kFinWaves * m;
-      nv[m] = L.wcnt[v];
-      sc[m] = L.wbuf[v][lane];
+      const int v = wid + kFinWaves * (m >> 1);
+      const uint32_t i = lane + 64u * (m & 1);
+      nv[m] = L.wcnt[v] > i ? 1u : 0u;
+      sc[m] = L.wbuf[v][i];
     }
     if (hist) {
       #pragma unroll
@@ -3721,7 +3722,7 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     }
     #pragma unroll
     for (int m = 0; m < kLists; ++m) {
-      bool keep = lane < nv[m] && cand_skey(sc[m]) >= Tm;
+      bool keep = nv[m] != 0u && cand_skey(sc[m]) >= Tm;
       if (hist) keep = keep && !((mk[m] >> (cand_idx(sc[m]) & 31u)) & 1u);
       sc[m] = keep ? sc[m] : 0ull;
       mine += keep ? 1u : 0u;

@@ -3304,11 +3304,12 @@ constexpr int kSelChunkSmall = NT * 16;
 //    last one's key.  A later logit with that key has a larger index and
 //    ranks below all kept ones, so the test is strict.  The first tile
 //    starts from a bound of the wave's group maxima instead of -inf.
+//  - The first tiles are issued before the row's parameters are read.
 //  - History tokens stream like the others (their raw logits).  The history
-//    is ranked in LDS once the first tile has arrived (a word of marks per
-//    32 logits and the number of marked logits before it), and its logits
-//    are loaded while the stream runs; after it their penalties are
-//    applied, and list entries that are history tokens are dropped.
+//    is ranked in LDS after the first tile (a word of marks per 32 logits
+//    and the number of marked logits before it), and its logits are loaded
+//    while the stream runs; after it their penalties are applied, and list
+//    entries that are history tokens are dropped.
 //  - Every logit left out has a key at or below the largest wave threshold
 //    Tm, so the union of the lists and the processed history logits above
 //    Tm holds the row's top k whenever its k-th key is above Tm (finish_core
@@ -3405,11 +3406,44 @@ constexpr int kStreamLoad = 2;
 constexpr uint32_t kKeyNegZero = 0x7fffffffu;  // okey(-0.0f)
 constexpr uint32_t kKeyPosInf = 0xff800000u;   // okey(+inf)
 
-// The fast path of one row; false sends the row to the general path (all
-// threads return the same).
+// The row's tiles in flight: kRowDepth slots of kRowTV 16-byte loads per
+// thread (and their mask words), with the buffer resources they use.
+template <bool MASK>
+struct RowPipe {
+  __amdgpu_buffer_rsrc_t rs, ms;
+  i32x4_t buf[kRowDepth][kRowTV];
+  uint32_t mw[kRowDepth][kRowTV];
+};
+
+// Issues the row's first kRowDepth tiles (range-checked: loads past the row
+// read zero).  They need only the kernel arguments, so they go out before
+// the row's parameters arrive.
+template <bool MASK>
+__device__ __forceinline__ void row_issue(const SampleArgs& a, int row, RowPipe<MASK>& pp) {
+  const int tid = threadIdx.x;
+  const int V = a.V;
+  const float* lrow = reinterpret_cast<const float*>((const char*)a.logits + (int64_t)row * a.row_stride * 4);
+  pp.rs = __builtin_amdgcn_make_buffer_rsrc((void*)lrow, (short)0, V * 4, kBufferConfig);
+  if (MASK) {
+    const uint32_t* mrow = a.mask + (int64_t)row * a.mask_words;
+    pp.ms = __builtin_amdgcn_make_buffer_rsrc((void*)mrow, (short)0, ((V + 31) >> 5) * 4, kBufferConfig);
+  }
+  #pragma unroll
+  for (int d = 0; d < kRowDepth; ++d) {
+    #pragma unroll
+    for (int j = 0; j < kRowTV; ++j) {
+      const int e0 = d * kRowTile + (j * kRowThreads + tid) * 4;
+      pp.buf[d][j] = __builtin_amdgcn_raw_buffer_load_b128(pp.rs, e0 * 4, 0, kStreamLoad);
+      if (MASK) pp.mw[d][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(pp.ms, (e0 >> 5) * 4, 0, 0);
+    }
+  }
+}
+
+// The fast path of one row, with its first tiles in flight (row_issue);
+// false sends the row to the general path (all threads return the same).
 template <bool MASK>
 __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int row, const RowCfg& cfg,
-                                           unsigned char* lds_raw) {
+                                           unsigned char* lds_raw, RowPipe<MASK>& pp) {
   const int tid = threadIdx.x;
   const uint32_t lane = (uint32_t)tid & 63u;
   const int wid = tid >> 6;
@@ -3421,8 +3455,7 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   const float* lrow = reinterpret_cast<const float*>((const char*)a.logits + (int64_t)row * a.row_stride * 4);
   const uint32_t* mrow = MASK ? a.mask + (int64_t)row * a.mask_words : nullptr;
 
-  // 1. the row's history entries, then the first kRowDepth tiles in flight
-  //    (loads past the row read zero)
+  // 1. the row's history entries (after the first tiles)
   const uint32_t h0 = a.hoff ? a.hoff[row] : 0u;
   const uint32_t h1 = a.hoff ? a.hoff[row + 1] : 0u;
   const bool hist = h1 > h0;
@@ -3445,21 +3478,10 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
       if (h >= nh) hid[r] = 0xffffffffu;
     }
   }
-  asm volatile("" ::: "memory");  // the history loads go out before the tiles
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)lrow, (short)0, V * 4, kBufferConfig);
-  __amdgpu_buffer_rsrc_t ms;
-  if (MASK) ms = __builtin_amdgcn_make_buffer_rsrc((void*)mrow, (short)0, Wm * 4, kBufferConfig);
-  i32x4_t buf[kRowDepth][kRowTV];
-  uint32_t mw[kRowDepth][kRowTV];
-  #pragma unroll
-  for (int d = 0; d < kRowDepth; ++d) {
-    #pragma unroll
-    for (int j = 0; j < kRowTV; ++j) {
-      const int e0 = d * kRowTile + (j * kRowThreads + tid) * 4;
-      buf[d][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * 4, 0, kStreamLoad);
-      if (MASK) mw[d][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (e0 >> 5) * 4, 0, 0);
-    }
-  }
+  const __amdgpu_buffer_rsrc_t rs = pp.rs;
+  const __amdgpu_buffer_rsrc_t ms = pp.ms;
+  auto& buf = pp.buf;
+  auto& mw = pp.mw;
 
   // 2. the stream state
   const uint32_t kk = (uint32_t)cfg.k_sel;  // 1..kLeanK
@@ -3579,17 +3601,13 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   using Slot1 = std::integral_constant<int, 1>;
   static_assert(kRowDepth == 2, "the stream alternates two slots");
 
-  // 3. the history ranked once the first tile has arrived: waiting for it
-  //    waits for the history entries too (loads complete in order and they
-  //    were issued first), so the ranking never waits for memory, it runs
-  //    while tile 1 is in flight, and the loop sees only tile loads in
-  //    flight.  Marks and rank prefix, then the summed count and id of each
-  //    distinct token by rank, whose logit is loaded during the stream.
-  #pragma unroll
-  for (int j = 0; j < kRowTV; ++j) {
-    asm volatile("" ::"v"(buf[0][j]));
-    if (MASK) asm volatile("" ::"v"(mw[0][j]));
-  }
+  // 3. the first tile
+  step(Slot0{}, 0, true);
+
+  // 4. the history ranked, while tile 2 is in flight (its entries were
+  //    issued before it, so they have arrived): marks and rank prefix, then
+  //    the summed count and id of each distinct token by rank, whose logit
+  //    is loaded during the stream
   constexpr uint32_t kFirst = (uint32_t)(kRowHistPer * kRowThreads);
   uint32_t distinct = 0u;
   if (hist) {
@@ -3651,9 +3669,6 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     hraw[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(hid[r] * 4u), 0, 0);
     if (MASK) hmw[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (int)((hid[r] >> 5) * 4u), 0, 0);
   }
-
-  // 4. the first tile
-  step(Slot0{}, 0, true);
 
   // 5. the rest of the row, tiles 1, 2, ... (the last pass may run past it)
   const int npass = ntiles / 2;
@@ -3801,9 +3816,11 @@ __global__ void __launch_bounds__(kRowThreads) row_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   RowLds& L = *reinterpret_cast<RowLds*>(lds_raw);
   const int row = blockIdx.x;
+  RowPipe<MASK> pp;
+  row_issue<MASK>(a, row, pp);  // unused by rows that take the general path
   const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
   if (cfg.cls == kTopK && !cfg.wide) {
-    if (row_stream<MASK>(L, a, row, cfg, lds_raw)) return;
+    if (row_stream<MASK>(L, a, row, cfg, lds_raw, pp)) return;
     __syncthreads();
   }
   // the general path, on the first NT threads: the chunk select and the

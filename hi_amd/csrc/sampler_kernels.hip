@@ -3406,18 +3406,21 @@ constexpr int kStreamLoad = 2;
 constexpr uint32_t kKeyNegZero = 0x7fffffffu;  // okey(-0.0f)
 constexpr uint32_t kKeyPosInf = 0xff800000u;   // okey(+inf)
 
-// The row's tiles in flight: kRowDepth slots of kRowTV 16-byte loads per
-// thread (and their mask words), with the buffer resources they use.
+// The row's loads in flight: kRowDepth slots of kRowTV 16-byte loads per
+// thread (and their mask words) with the buffer resources they use, and the
+// row's history entries.
 template <bool MASK>
 struct RowPipe {
   __amdgpu_buffer_rsrc_t rs, ms;
   i32x4_t buf[kRowDepth][kRowTV];
   uint32_t mw[kRowDepth][kRowTV];
+  uint32_t h0, h1;                   // the row's history entries [h0, h1)
+  uint32_t hid[kRowHistPer], hcs[kRowHistPer];
 };
 
 // Issues the row's first kRowDepth tiles (range-checked: loads past the row
-// read zero).  They need only the kernel arguments, so they go out before
-// the row's parameters arrive.
+// read zero), then its history entries.  They need only the kernel
+// arguments, so they go out before the row's parameters arrive.
 template <bool MASK>
 __device__ __forceinline__ void row_issue(const SampleArgs& a, int row, RowPipe<MASK>& pp) {
   const int tid = threadIdx.x;
@@ -3437,6 +3440,24 @@ __device__ __forceinline__ void row_issue(const SampleArgs& a, int row, RowPipe<
       if (MASK) pp.mw[d][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(pp.ms, (e0 >> 5) * 4, 0, 0);
     }
   }
+  // unconditional range-checked loads (entries past the row read zero): a
+  // load under a condition would leave the compiler unsure how many loads
+  // are in flight in the stream loop, and it would then wait for all
+  pp.h0 = a.hoff ? a.hoff[row] : 0u;
+  pp.h1 = a.hoff ? a.hoff[row + 1] : 0u;
+  // (a scalar: a range in a vector register would make each load a loop)
+  const int nh = __builtin_amdgcn_readfirstlane(pp.h1 > pp.h0 ? (int)(pp.h1 - pp.h0) : 0);
+  const __amdgpu_buffer_rsrc_t ri =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.hids + pp.h0), (short)0, nh * 4, kBufferConfig);
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.hcnt + pp.h0), (short)0, nh * 4, kBufferConfig);
+  #pragma unroll
+  for (int r = 0; r < kRowHistPer; ++r) {
+    const int h = r * kRowThreads + tid;
+    pp.hid[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ri, h * 4, 0, 0);
+    pp.hcs[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, h * 4, 0, 0);
+    if (h >= nh) pp.hid[r] = 0xffffffffu;
+  }
 }
 
 // The fast path of one row, with its first tiles in flight (row_issue);
@@ -3455,29 +3476,11 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   const float* lrow = reinterpret_cast<const float*>((const char*)a.logits + (int64_t)row * a.row_stride * 4);
   const uint32_t* mrow = MASK ? a.mask + (int64_t)row * a.mask_words : nullptr;
 
-  // 1. the row's history entries (after the first tiles)
-  const uint32_t h0 = a.hoff ? a.hoff[row] : 0u;
-  const uint32_t h1 = a.hoff ? a.hoff[row + 1] : 0u;
+  // 1. the loads in flight
+  const uint32_t h0 = pp.h0, h1 = pp.h1;
   const bool hist = h1 > h0;
-  // unconditional range-checked loads (entries past the row read zero): a
-  // load under a condition would leave the compiler unsure how many loads
-  // are in flight in the stream loop, and it would then wait for all
-  uint32_t hid[kRowHistPer], hcs[kRowHistPer];
-  {
-    // (a scalar: a range in a vector register would make each load a loop)
-    const int nh = __builtin_amdgcn_readfirstlane(hist ? (int)(h1 - h0) : 0);
-    const __amdgpu_buffer_rsrc_t ri =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(a.hids + h0), (short)0, nh * 4, kBufferConfig);
-    const __amdgpu_buffer_rsrc_t rc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(a.hcnt + h0), (short)0, nh * 4, kBufferConfig);
-    #pragma unroll
-    for (int r = 0; r < kRowHistPer; ++r) {
-      const int h = r * kRowThreads + tid;
-      hid[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ri, h * 4, 0, 0);
-      hcs[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, h * 4, 0, 0);
-      if (h >= nh) hid[r] = 0xffffffffu;
-    }
-  }
+  auto& hid = pp.hid;
+  auto& hcs = pp.hcs;
   const __amdgpu_buffer_rsrc_t rs = pp.rs;
   const __amdgpu_buffer_rsrc_t ms = pp.ms;
   auto& buf = pp.buf;
@@ -3601,13 +3604,14 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   using Slot1 = std::integral_constant<int, 1>;
   static_assert(kRowDepth == 2, "the stream alternates two slots");
 
-  // 3. the first tile
+  // 3. the first two tiles
   step(Slot0{}, 0, true);
+  step(Slot1{}, 1, false);
 
-  // 4. the history ranked, while tile 2 is in flight (its entries were
-  //    issued before it, so they have arrived): marks and rank prefix, then
-  //    the summed count and id of each distinct token by rank, whose logit
-  //    is loaded during the stream
+  // 4. the history ranked, while tiles 2 and 3 are in flight (its entries
+  //    were issued before them, so they have arrived): marks and rank
+  //    prefix, then the summed count and id of each distinct token by rank,
+  //    whose logit is loaded during the stream
   constexpr uint32_t kFirst = (uint32_t)(kRowHistPer * kRowThreads);
   uint32_t distinct = 0u;
   if (hist) {
@@ -3670,11 +3674,11 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     if (MASK) hmw[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (int)((hid[r] >> 5) * 4u), 0, 0);
   }
 
-  // 5. the rest of the row, tiles 1, 2, ... (the last pass may run past it)
-  const int npass = ntiles / 2;
-  for (int p = 0; p < npass; ++p) {
+  // 5. the rest of the row, tiles 2, 3, ... (the last pass may run past it)
+  const int npass = (ntiles + 1) / 2;
+  for (int p = 1; p < npass; ++p) {
+    step(Slot0{}, 2 * p, false);
     step(Slot1{}, 2 * p + 1, false);
-    step(Slot0{}, 2 * p + 2, false);
   }
   if (lane == 0u) {
     L.wthr[wid] = T;

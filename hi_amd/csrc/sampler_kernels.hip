@@ -1620,6 +1620,9 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
     n_total += wave_last_u32(incl);
   }
   if (n_total > (uint32_t)kGather || n_total == 0u) return false;
+  // chunks keep fewer than k_sel candidates when the row has many: with a
+  // chunk truncated, fewer than k_sel candidates cannot hold the top k_sel
+  if (ub != 0u && n_total < (uint32_t)cfg.k_sel) return false;
   if (tid < 64) {
     #pragma unroll
     for (int q = 0; q < CQ; ++q) if (q * 64 + (int)lane < nch) fs.aux[q * 64 + lane] = offq[q];
@@ -1648,7 +1651,8 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
     }
   }
   __syncthreads();
-  return finish_core(fs, a, row, cfg, (int)n_total, M, ub, part);
+  // the k_sel-th candidate must be above every key a chunk left out
+  return finish_core(fs, a, row, cfg, (int)n_total, M, ub, part, ub);
 }
 
 // ==========================================================================
@@ -2194,11 +2198,12 @@ __device__ __forceinline__ void stage_history_hash(const SampleArgs& a, uint32_t
 //   phase A   per-lane maxima of 4 groups of E/4 logits (allowed-token mask
 //             as -inf; history tokens keep their raw logit here);
 //   bound     each wave binary-searches, with ballots and popcounts, the
-//             largest key t_w such that at least ceil(k/4) + h_w of its
+//             largest key t_w such that at least ceil(m/4) + h_w of its
 //             group maxima are >= t_w, h_w being the history tokens among
-//             the wave's logits: at least ceil(k/4) of those maxima are then
+//             the wave's logits: at least ceil(m/4) of those maxima are then
 //             distinct non-history logits, so the workgroup bound
-//             t = min t_w has at least k logits >= t;
+//             t = min t_w has at least m logits >= t (m = chunk_keep: k
+//             when the row has few chunks);
 //   phase B   one compare per logit builds a per-lane survivor bitmask; a
 //             short per-lane loop re-reads the few survivors (L2 hits),
 //             skipping history tokens, whose penalised values were computed
@@ -2216,6 +2221,21 @@ __device__ __forceinline__ void stage_history_hash(const SampleArgs& a, uint32_t
 // failed bound or too many survivors take select_exact(), which reads the
 // chunk again and recomputes everything element by element with integer
 // keys.  Every path writes the same record and candidates.
+
+// Candidates a lean chunk guarantees: at least its top k_sel, or fewer when
+// the row is split into many chunks.  A chunk holds on average
+// mu = k_sel / n_chunks of the row's top k_sel; it keeps at least
+// ceil(mu + 4 sqrt(mu) + 4) (at least kLseTop on logprob rows, whose
+// normaliser sums the largest terms from the candidates).  A chunk holding
+// more of the row's top k_sel than it kept is caught by the finish (the
+// k_sel-th key is not above the largest key left out), and the row takes
+// the exact finish.
+__device__ __forceinline__ uint32_t chunk_keep(uint32_t k_sel, int n_chunks, bool lse) {
+  const float mu = (float)k_sel / (float)n_chunks;
+  uint32_t m = (uint32_t)ceilf(mu + 4.f * sqrtf(mu) + 4.f);
+  if (lse) m = max(m, (uint32_t)kLseTop);
+  return min(m, k_sel);
+}
 
 constexpr int kSurvCap = 640;              // survivors per wave
 constexpr uint32_t kSelHistCap = 1024;     // distinct history tokens per chunk held in LDS
@@ -2573,7 +2593,8 @@ __device__ __forceinline__ bool select_lean(SelLds& L, const SampleArgs& a, cons
   for (int i = 0; i < E; ++i) G[i / GS] = fmaxf(G[i / GS], x[i]);
 
   // bound
-  const uint32_t k1 = nd.sel ? (uint32_t)cfg.k_sel : 1u;
+  const uint32_t keep = chunk_keep((uint32_t)cfg.k_sel, a.n_chunks, nd.lse);
+  const uint32_t k1 = nd.sel ? keep : 1u;
   const uint32_t need = (k1 + (NT / 64) - 1) / (NT / 64) + (hv.on ? L.hw[wid] : 0u);
   uint32_t gk[4];
   bool inf = false;

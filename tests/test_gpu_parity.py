@@ -398,6 +398,36 @@ def test_large_batch_row_kernel(hip, oracle, V, with_mask):
     compare(w, got[0], want, f"large batch V={V}")
 
 
+@pytest.mark.parametrize("n_lp", [0, 40])
+def test_top_k_clustered_in_one_chunk(hip, oracle, n_lp):
+    """Small batches split each row into many chunks, and a chunk keeps only
+    as many candidates as a spread-out row needs.  Rows whose whole top k
+    sits in one chunk (or two) must still come out exact: the finish sees
+    the k-th candidate at or below a key that chunk left out and takes the
+    exact path."""
+    from hi_amd.sampler import row_params
+    rng = np.random.default_rng(4242 + n_lp)
+    B, V = 4, 151936
+    x = rng.normal(0, 3.0, (B, V)).astype(F32)
+    x[0, 4096:4136] += F32(20.0)                    # the top 40 in chunk 1
+    x[1, 8192:8212] += F32(20.0)                    # 20 in chunk 2 ...
+    x[1, 151000:151020] += F32(20.0)                # ... and 20 in the last chunk
+    x[2, 100:110] += F32(20.0)                      # ten, plus a spread tail
+    p = row_params(B, temperature=0.7, top_p=0.9, top_k=40)
+    p["repetition_penalty"] = F32(1.1)
+    p["top_k"][3] = 256                             # the lean path's largest k
+    u = rng.random(B).astype(F32)
+    ids = rng.integers(0, V, 64 * B).astype(np.uint32)
+    ids[:8] = np.arange(4096, 4104, dtype=np.uint32)  # history inside the cluster
+    cnts = rng.integers(1, 4, 64 * B).astype(np.uint32)
+    offs = (np.arange(B + 1) * 64).astype(np.uint32)
+    w = Workload("clustered", x, p, u, offs, ids, cnts, None, n_lp)
+    say(f"clustered top-k n_lp={n_lp}")
+    got = run_gpu(w)
+    want = run_oracle(oracle, w)
+    compare(w, got, want, f"clustered n_lp={n_lp}")
+
+
 @pytest.mark.parametrize("V", [37, 1000, 8192, 8193, 20011, 70000])
 def test_edge_mixed_batches(hip, oracle, V):
     rng = np.random.default_rng(V)

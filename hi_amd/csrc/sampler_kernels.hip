@@ -1285,6 +1285,7 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
 }
 
 constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
+constexpr int kSpecChunks = 40;   // rows of up to this many chunks load their candidates early
 
 // Sequential f32 sums over the wave's lanes: lane l < n returns
 // ((start + v_0) + v_1) + ... + v_l, the reference's left-to-right fold
@@ -1534,6 +1535,22 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   const int nch = a.n_chunks;
   if (nch > kLeanChunks) return false;
   const ChunkStat* stats = a.stats + (int64_t)row * nch;
+  const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
+
+  // 0. rows of few chunks: the first 64 candidate slots of every chunk are
+  //    loaded before the records arrive (one round trip for both; wave w
+  //    takes chunks w, w + 4, ...); the counts in the records then say which
+  //    slots are candidates
+  constexpr int kSpecPer = kSpecChunks / (NT / 64);
+  const bool spec = nch <= kSpecChunks;
+  uint64_t sp[kSpecPer];
+  if (spec) {
+    #pragma unroll
+    for (int i = 0; i < kSpecPer; ++i) {
+      const int c = (tid >> 6) + (NT / 64) * i;
+      sp[i] = c < nch ? cand[(int64_t)c * kFast + lane] : 0ull;
+    }
+  }
 
   // 1. the chunk records, merged by every wave on its own; candidate counts
   //    and their chunk-major offsets; the largest key left out of them
@@ -1631,9 +1648,21 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   __syncthreads();
 
   // 2. the candidates into LDS (chunk-major): all loads first
+  if (spec) {
+    #pragma unroll
+    for (int i = 0; i < kSpecPer; ++i) {
+      const int c = (tid >> 6) + (NT / 64) * i;
+      if (c < nch) {
+        const uint32_t o = fs.aux[c], nc = fs.aux[c + 1] - o;
+        if (lane < nc) fs.cbig[o + lane] = sp[i];
+        for (uint32_t j = 64u + lane; j < nc; j += 64u) fs.cbig[o + j] = cand[(int64_t)c * kFast + j];
+      }
+    }
+    __syncthreads();
+    return finish_core(fs, a, row, cfg, (int)n_total, M, ub, part, ub);
+  }
   uint64_t cr[kFinPer];
   {
-    const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
     int c = 0;
     #pragma unroll
     for (int r = 0; r < kFinPer; ++r) {

@@ -2621,10 +2621,14 @@ __device__ __forceinline__ bool select_lean(SelLds& L, const SampleArgs& a, cons
   #pragma unroll
   for (int i = 0; i < E; ++i) G[i / GS] = fmaxf(G[i / GS], x[i]);
 
-  // bound
+  // bound.  In a chunk shorter than one load per thread (the row's last)
+  // only the first `act` waves hold logits: they share the count, and the
+  // others set no bound.
   const uint32_t keep = chunk_keep((uint32_t)cfg.k_sel, a.n_chunks, nd.lse);
   const uint32_t k1 = nd.sel ? keep : 1u;
-  const uint32_t need = (k1 + (NT / 64) - 1) / (NT / 64) + (hv.on ? L.hw[wid] : 0u);
+  const uint32_t act = (uint32_t)min(NT / 64, (len + 64 * EPL - 1) / (64 * EPL));
+  const bool idle = (uint32_t)wid >= act;
+  const uint32_t need = (k1 + act - 1) / act + (hv.on ? L.hw[wid] : 0u);
   uint32_t gk[4];
   bool inf = false;
   #pragma unroll
@@ -2638,8 +2642,8 @@ __device__ __forceinline__ bool select_lean(SelLds& L, const SampleArgs& a, cons
     for (int g = 0; g < 4; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
     if (c >= need) prefix = probe;
   }
-  const bool bad = __ballot(inf) != 0ull || need > 4u * 64u || prefix <= kKeyNegInf;
-  if (lane == 0u) { L.wkey[wid] = prefix; L.wflag[wid] = bad ? 1u : 0u; }
+  const bool bad = !idle && (__ballot(inf) != 0ull || need > 4u * 64u || prefix <= kKeyNegInf);
+  if (lane == 0u) { L.wkey[wid] = idle ? 0xffffffffu : prefix; L.wflag[wid] = bad ? 1u : 0u; }
   __syncthreads();
   uint32_t tk = L.wkey[0];
   uint32_t rare = L.wflag[0];

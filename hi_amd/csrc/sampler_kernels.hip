@@ -3146,22 +3146,31 @@ __global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
 // batches: the last workgroup of a row to finish its chunk (a device-scope
 // counter per row) runs the row's finish.  The other workgroups' records
 // and candidates are released by their fence before the counter update and
-// acquired by the last one's fence after it; the last one also sets the
-// counter back to zero for the next launch.  No workgroup waits for another.
+// acquired by the last one's fence after it (one thread fences for the
+// workgroup, between barriers); the last one also sets the counter back to
+// zero for the next launch.  No workgroup waits for another.
 template <int DT, int NL, bool MASK>
 __global__ void __launch_bounds__(NT) select_finish_kernel(SampleArgs a, uint32_t flag_off) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const int row = blockIdx.y;
   select_chunk<DT, NL, MASK>(a, row, blockIdx.x, lds_raw);
   uint32_t* last = reinterpret_cast<uint32_t*>(lds_raw + flag_off);  // past both LDS layouts
-  __threadfence();
+  // every wave waits for its stores to reach L2 (a workgroup barrier alone
+  // does not), then one device-scope fence writes them back before the
+  // counter update
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   uint32_t* counter = a.done + row;
-  if (threadIdx.x == 0) *last = atomicAdd(counter, 1u) == (uint32_t)(a.n_chunks - 1) ? 1u : 0u;
+  if (threadIdx.x == 0) {
+    __threadfence();
+    *last = atomicAdd(counter, 1u) == (uint32_t)(a.n_chunks - 1) ? 1u : 0u;
+    if (*last) {
+      __threadfence();  // acquire: the caches hold no stale record or candidate
+      *counter = 0u;
+    }
+  }
   __syncthreads();
   if (*last == 0u) return;
-  __threadfence();
-  if (threadIdx.x == 0) *counter = 0u;
   FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
   const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
   if (finish_lean(fs, a, row, cfg)) return;

@@ -1402,6 +1402,7 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
     pk = okey(sx);
     wnot = ~__float_as_uint(w);
     fs.buf[tid] = rk;
+    fs.hist[tid] = 0u;  // its rank, summed in step 7
   }
   if (tid < ((kk + 63) & ~63)) {
     wnot = wave_max_u32(wnot);
@@ -1415,19 +1416,41 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   const uint32_t xk = max(ub_key, below != 0ull ? cand_skey(below) : 0u);
   if (w_b > 0.f && xk > kKeyNegInf && exact_expf(key_to_s(xk, cfg.t_eff) - M) == w_b) return false;
 
-  // 7. rank order by counting (kk <= NT: one entry per thread); two keys
-  //    per LDS read
-  if (tid < kk) {
-    uint32_t r = 0u;
-    const int kk2 = kk & ~1;
-    #pragma unroll 4
-    for (int j = 0; j < kk2; j += 2) {
-      const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&fs.buf[j]);
-      r += (y.x > rk ? 1u : 0u) + (y.y > rk ? 1u : 0u);
+  // 7. rank order by counting: an entry's rank is the number of rank keys
+  //    above its own.  `parts` threads share each entry's count (every
+  //    thread works when kk <= NT / 2), reading two keys per LDS read; the
+  //    parts add up in LDS.
+  {
+    const int parts = kk <= NT / 4 ? 4 : (kk <= NT / 2 ? 2 : 1);
+    const int G = NT / parts;
+    const int e = tid % G, part = tid / G;
+    if (e < kk) {
+      const uint64_t me = fs.buf[e];
+      const int span = ((kk + parts - 1) / parts + 1) & ~1;  // even: 16-byte reads
+      const int j0 = part * span, j1 = min(kk, j0 + span);
+      uint32_t r = 0u;
+      int j = j0;
+      #pragma unroll 4
+      for (; j + 2 <= j1; j += 2) {
+        const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(&fs.buf[j]);
+        r += (y.x > me ? 1u : 0u) + (y.y > me ? 1u : 0u);
+      }
+      if (j < j1) r += fs.buf[j] > me ? 1u : 0u;
+      if (parts == 1) {
+        fs.cbig[r] = rk;
+        fs.aux[r] = pk;
+      } else if (r != 0u) {
+        atomicAdd(&fs.hist[e], r);
+      }
     }
-    if (kk & 1) r += fs.buf[kk - 1] > rk ? 1u : 0u;
-    fs.cbig[r] = rk;
-    fs.aux[r] = pk;
+    if (parts > 1) {
+      __syncthreads();
+      if (tid < kk) {
+        const uint32_t r = fs.hist[tid];
+        fs.cbig[r] = rk;
+        fs.aux[r] = pk;
+      }
+    }
   }
   __syncthreads();
 
@@ -1441,15 +1464,26 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
     const float w = i < k ? rank_w(fs.cbig[i]) : 0.f;
     fa[m] = w < cfg.min_p ? 0.f : w;  // min-p: excluded like w <= 0 (gpu.rs:847-849)
   }
+  // the weights are in rank order, so the positive ones are a prefix
+  // [0, last_pos] (min-p and underflow zeros sit at the end)
+  int last_pos = -1;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const uint64_t pm = __ballot(i < k && fa[m] > 0.f);
+    if (pm != 0ull) last_pos = m * 64 + 63 - __clzll((unsigned long long)pm);
+  }
+  if (last_pos < 0) return false;  // no candidate: argmax_host fallback
   // P_i: the sequential sum of fa[0..i]: the total of gpu.rs:834-836 (the
-  // kept weights in rank order) and, at positive entries, the candidate
-  // total and CDF of gpu.rs:874-896 (min-p zeros sit at the end)
+  // kept weights in rank order; the zeros after last_pos add nothing) and,
+  // at positive entries, the candidate total and CDF of gpu.rs:874-896
+  const int kp = last_pos + 1;
   float P = -0.0f;
   #pragma unroll
   for (int m = 0; m < DM; ++m) {
-    if (m * 64 < k) {
-      pa[m] = wave_fold_f32(fa[m], P, min(64, k - m * 64));
-      P = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), min(63, k - 1 - m * 64)));
+    if (m * 64 < kp) {
+      pa[m] = wave_fold_f32(fa[m], P, min(64, kp - m * 64));
+      P = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), min(63, kp - 1 - m * 64)));
     } else {
       pa[m] = P;
     }
@@ -1458,30 +1492,22 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   if (!(total > 0.f) || !finitef_(total)) return false;  // argmax_host fallback
   // the nucleus: cum_p over w / total of the positive entries (gpu.rs:843-856),
   // folded only as far as the first one that reaches the cutoff
-  int last_pos = -1;   // last positive entry
   int cut = -1;        // first positive entry where cum_p reaches the cutoff
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int i = m * 64 + (int)lane;
-    const uint64_t pm = __ballot(i < k && fa[m] > 0.f);
-    if (pm != 0ull) last_pos = m * 64 + 63 - __clzll((unsigned long long)pm);
-  }
   if (cfg.cutoff < 1.f) {
     float Q = 0.f;
     #pragma unroll
     for (int m = 0; m < DM; ++m) {
-      if (cut < 0 && m * 64 < k) {
+      if (cut < 0 && m * 64 < kp) {
         const int i = m * 64 + (int)lane;
-        const bool pos = i < k && fa[m] > 0.f;
+        const bool pos = i < kp;
         fb[m] = pos ? fa[m] / total : 0.f;
         int first;
-        qa[m] = wave_fold_f32_until(fb[m], Q, min(64, k - m * 64), pos, cfg.cutoff, first);
+        qa[m] = wave_fold_f32_until(fb[m], Q, min(64, kp - m * 64), pos, cfg.cutoff, first);
         if (first >= 0) cut = m * 64 + first;
-        else Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(qa[m]), min(63, k - 1 - m * 64)));
+        else Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(qa[m]), min(63, kp - 1 - m * 64)));
       }
     }
   }
-  if (last_pos < 0) return false;  // no candidate: argmax_host fallback
   const int m_end = cut >= 0 ? cut + 1 : last_pos + 1;
   const int me = m_end - 1;
   float ct = 0.f;

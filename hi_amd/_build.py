@@ -21,6 +21,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar kernel arguments arrive in SGPRs at wave launch
+    "-mllvm", "-amdgpu-kernarg-preload-count=8",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -3903,12 +3903,20 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm, (uint64_t)Tm << 32, top);
 }
 
-// One workgroup per row (see the section comment).
+// One workgroup per row (see the section comment).  The first tiles' loads
+// need only the logits, the row stride and V: they lead the kernel's
+// arguments, which gfx950 preloads into scalar registers at wave launch
+// (the library is built with -amdgpu-kernarg-preload-count), so the loads
+// do not wait for an argument fetch.
 template <bool MASK>
-__global__ void __launch_bounds__(kRowThreads) row_kernel(SampleArgs a) {
+__global__ void __launch_bounds__(kRowThreads) row_kernel(const void* logits, int64_t row_stride, int V,
+                                                          SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   RowLds& L = *reinterpret_cast<RowLds*>(lds_raw);
   const int row = blockIdx.x;
+  a.logits = logits;  // the same values, from the preloaded arguments
+  a.row_stride = row_stride;
+  a.V = V;
   RowPipe<MASK> pp;
   row_issue<MASK>(a, row, pp);  // unused by rows that take the general path
   const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
@@ -4033,7 +4041,7 @@ hipError_t launch_rows(const SampleArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     attr = lds;
   }
-  hipLaunchKernelGGL(row_kernel<MASK>, dim3(a.B), dim3(kRowThreads), lds, stream, a);
+  hipLaunchKernelGGL(row_kernel<MASK>, dim3(a.B), dim3(kRowThreads), lds, stream, a.logits, a.row_stride, a.V, a);
   return hipGetLastError();
 }
 

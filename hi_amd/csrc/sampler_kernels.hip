@@ -115,8 +115,16 @@ __device__ __forceinline__ int next_pow2(int x) {
 
 // ---- parameters ----------------------------------------------------------
 
+// A value no kernel writes, read through the constant address space: at a
+// workgroup-uniform address the compiler reads it with a scalar load, which
+// does not wait behind the vector loads in flight.
+template <typename T>
+__device__ __forceinline__ T const_load(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
 __device__ __forceinline__ float row_uniform(const ParamsView& pv, int row) {
-  return pv.uniforms ? pv.uniforms[row] : pv.uniform_value;
+  return pv.uniforms ? const_load(pv.uniforms + row) : pv.uniform_value;
 }
 
 __device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V, int n_lp, int need_lse) {
@@ -128,13 +136,14 @@ __device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V,
   c.min_p = 0.f; c.rep = 1.f; c.freq = 0.f; c.pres = 0.f; c.eos = 0u; c.flags = 0u;
   const int mode = pv.mode;
   if (mode == kParamsSoA) {
-    c.T = pv.temps[row]; c.top_p = pv.top_ps[row]; c.top_k = pv.top_ks[row];
+    c.T = const_load(pv.temps + row); c.top_p = const_load(pv.top_ps + row); c.top_k = const_load(pv.top_ks + row);
   }
   if (mode == kParamsRows) {
-    const hi_rocm_row_params p = pv.rows[row];
-    c.T = p.temperature; c.top_p = p.top_p; c.min_p = p.min_p;
-    c.rep = p.repetition_penalty; c.freq = p.frequency_penalty; c.pres = p.presence_penalty;
-    c.top_k = p.top_k; c.eos = p.eos_id; c.flags = p.flags;
+    const hi_rocm_row_params* p = pv.rows + row;
+    c.T = const_load(&p->temperature); c.top_p = const_load(&p->top_p); c.min_p = const_load(&p->min_p);
+    c.rep = const_load(&p->repetition_penalty); c.freq = const_load(&p->frequency_penalty);
+    c.pres = const_load(&p->presence_penalty); c.top_k = const_load(&p->top_k); c.eos = const_load(&p->eos_id);
+    c.flags = const_load(&p->flags);
   }
   const bool greedy = !(finitef_(c.T) && c.T > 0.f);
   const bool minp_on = finitef_(c.min_p) && c.min_p > 0.f;
@@ -3532,8 +3541,8 @@ __device__ __forceinline__ void row_issue(const SampleArgs& a, int row, RowPipe<
   // unconditional range-checked loads (entries past the row read zero): a
   // load under a condition would leave the compiler unsure how many loads
   // are in flight in the stream loop, and it would then wait for all
-  pp.h0 = a.hoff ? a.hoff[row] : 0u;
-  pp.h1 = a.hoff ? a.hoff[row + 1] : 0u;
+  pp.h0 = a.hoff ? const_load(a.hoff + row) : 0u;
+  pp.h1 = a.hoff ? const_load(a.hoff + row + 1) : 0u;
   // (a scalar: a range in a vector register would make each load a loop)
   const int nh = __builtin_amdgcn_readfirstlane(pp.h1 > pp.h0 ? (int)(pp.h1 - pp.h0) : 0);
   const __amdgpu_buffer_rsrc_t ri =
@@ -3903,6 +3912,46 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm, (uint64_t)Tm << 32, top);
 }
 
+// The general path of a row (see the section comment), on the first NT
+// threads: the chunk select and the finish of the two-kernel path.  It is
+// not inlined, so that its register demand (it spills) stays out of the
+// fast path's code.  `ap` points at the row kernel's own SampleArgs
+// argument in the kernel argument segment: a pointer to a local copy would
+// make every workgroup store that copy to scratch memory on entry.
+typedef const __attribute__((address_space(4))) SampleArgs KernargSampleArgs;
+
+template <bool MASK>
+__device__ __noinline__ void row_general(KernargSampleArgs* ap, int row) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  SampleArgs a;
+  {
+    static_assert(sizeof(SampleArgs) % 8 == 0, "copied 8 bytes at a time");
+    typedef const __attribute__((address_space(4))) uint64_t KernargWord;
+    KernargWord* w = (KernargWord*)ap;
+    uint64_t* d = reinterpret_cast<uint64_t*>(&a);
+    #pragma unroll
+    for (int i = 0; i < (int)(sizeof(SampleArgs) / 8); ++i) d[i] = w[i];
+  }
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  for (int c = 0; c < a.n_chunks; ++c) {
+    select_chunk<HI_ROCM_DTYPE_F32, kSelChunkLarge / NT / 4, MASK>(a, row, c, lds_raw);
+    __syncthreads();
+  }
+  FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
+  if (finish_lean(fs, a, row, cfg)) return;
+  __syncthreads();
+  finish_row(fs, a, row, cfg);
+}
+
+// The row kernel's arguments as its argument segment lays them out: each at
+// the next offset aligned for its type, as in this struct.
+struct RowKernelArgs {
+  const void* logits;
+  int64_t row_stride;
+  int V;
+  SampleArgs a;
+};
+
 // One workgroup per row (see the section comment).  The first tiles' loads
 // need only the logits, the row stride and V: they lead the kernel's
 // arguments, which gfx950 preloads into scalar registers at wave launch
@@ -3924,17 +3973,10 @@ __global__ void __launch_bounds__(kRowThreads) row_kernel(const void* logits, in
     if (row_stream<MASK>(L, a, row, cfg, lds_raw, pp)) return;
     __syncthreads();
   }
-  // the general path, on the first NT threads: the chunk select and the
-  // finish of the two-kernel path (ended waves no longer count at barriers)
   if (threadIdx.x >= NT) return;
-  for (int c = 0; c < a.n_chunks; ++c) {
-    select_chunk<HI_ROCM_DTYPE_F32, kSelChunkLarge / NT / 4, MASK>(a, row, c, lds_raw);
-    __syncthreads();
-  }
-  FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
-  if (finish_lean(fs, a, row, cfg)) return;
-  __syncthreads();
-  finish_row(fs, a, row, cfg);
+  typedef const __attribute__((address_space(4))) char KernargByte;
+  row_general<MASK>(
+      (KernargSampleArgs*)((KernargByte*)__builtin_amdgcn_kernarg_segment_ptr() + offsetof(RowKernelArgs, a)), row);
 }
 
 size_t row_lds_bytes(int V) {

@@ -8,8 +8,9 @@ logits already resident in HBM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Prints one JSON line.  The CPU baseline (the oracle, single thread, on a
-bounded sample of the same rows) is timed on this host in the same run.
+Prints one JSON line.  The CPU baselines (the oracle on a bounded sample
+of the same rows: single thread, rows serial; and rows split over every
+usable core) are timed on this host in the same run.
 """
 import argparse
 import json
@@ -223,6 +224,35 @@ def cpu_baseline(w, budget_s=15.0):
             "sample": f"{rows_done} rows of {w.name} (oracle, 1 thread, serial rows), {el:.1f} s"}
 
 
+def host_cores():
+    """Cores this process may use: its CPU affinity, capped by
+    OMP_NUM_THREADS where the environment sets it."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        n = min(n, int(os.environ.get("OMP_NUM_THREADS", n)))
+    except ValueError:
+        pass
+    return max(1, n)
+
+
+def cpu_baseline_all_cores(w, budget_s=8.0):
+    """The same oracle with the batch's rows split over every usable core
+    (the second CPU figure of the measurement plan): whole batches until the
+    time budget is used."""
+    from oracle import oracle
+    oracle.build()
+    cores = host_cores()
+    rows_done = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        oracle.sample_rows(w.logits, w.params, w.uniforms, w.hist_offsets, w.hist_ids, w.hist_counts,
+                           w.mask_words, w.n_logprobs, threads=cores)
+        rows_done += w.batch
+    el = time.perf_counter() - t0
+    return {"value": rows_done / el, "unit": "rows/s", "cores": cores, "kind": "port",
+            "sample": f"{rows_done} rows of {w.name} (oracle, rows split over {cores} threads), {el:.1f} s"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -302,6 +332,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w3, args.cpu_budget)
+        res["cpu_baseline_all_cores"] = cpu_baseline_all_cores(w3)
     print(json.dumps(res))
 
 

@@ -523,6 +523,53 @@ def test_graph_replays_match_eager(hip, oracle):
         del junk
 
 
+@pytest.mark.parametrize("cfg", [1, 3])
+def test_graph_fed_parameters(hip, oracle, cfg):
+    """One capture, then every input rewritten in place between replays, as
+    a decode loop does (new logits from the forward pass, new row
+    parameters, uniforms and histories): each replay must equal the oracle
+    on that replay's inputs.  Config 1 runs the fused small-batch kernel,
+    config 3 the one-workgroup-per-row kernel."""
+    torch = _torch()
+    from hi_amd import sampler as S
+    ws = [CONFIGS[cfg](seed=s) for s in (cfg, 100 + cfg, 200 + cfg)]
+    w0 = ws[0]
+    cap = max(len(w.hist_ids) for w in ws)
+    logits = dev(w0.logits)
+    params = S.params_to_device(w0.params)
+    unif = dev(w0.uniforms)
+    offs = dev(w0.hist_offsets)
+    ids = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    cnts = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    smp = S.Sampler(w0.batch, w0.vocab, w0.n_logprobs)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        out = smp.sample(logits, params, unif, offs, ids, cnts, n_logprobs=w0.n_logprobs, stream=stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        smp.sample(logits, params, unif, offs, ids, cnts, n_logprobs=w0.n_logprobs, out=out, stream=stream)
+    torch.cuda.synchronize()
+    for rep, w in enumerate(ws + ws[:1]):
+        say(f"graph-fed config {cfg} replay {rep}")
+        logits.copy_(dev(w.logits))
+        params.copy_(S.params_to_device(w.params))
+        unif.copy_(dev(w.uniforms))
+        offs.copy_(dev(w.hist_offsets))
+        n = len(w.hist_ids)
+        ids[:n].copy_(dev(w.hist_ids))
+        cnts[:n].copy_(dev(w.hist_counts))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = {k: v.cpu().numpy() for k, v in out.items()}
+        got["tokens"] = got["tokens"].view(np.uint32)
+        if "logprob_ids" in got:
+            got["logprob_ids"] = got["logprob_ids"].view(np.uint32)
+        got.pop("token_logprobs", None)
+        compare(w, got, run_oracle(oracle, w), f"graph-fed config {cfg} replay {rep}")
+
+
 def test_workspace_reuse_across_batch_sizes(hip, oracle):
     """One workspace, successive calls with different batch sizes (the chunk
     size and the per-row tickets change between calls)."""

@@ -196,6 +196,42 @@ def time_graph_b1(torch, w, steps, warmup):
     return graph_us, in_graph_us, eager_us
 
 
+def time_indexer_select(torch, shapes=((1162, 512), (65536, 2048)), launches=200):
+    """DSV4 indexer block selection (hi_rocm_launch_dsv4_indexer_select):
+    us per launch over back-to-back launches on one stream, bracketed by HIP
+    events on that stream.  Algorithmic bytes per launch: n scores f32 read,
+    n marks u8 and min(k, n) int32 indices written.  One workgroup per
+    launch, so the bound is latency, not HBM."""
+    import ctypes
+    from hi_amd import _lib
+    from hi_amd.workloads import indexer_test_scores
+    lib = _lib.load()
+    out = []
+    stream = torch.cuda.Stream()
+    for n, k in shapes:
+        x = torch.from_numpy(indexer_test_scores(n) if n <= 4096 else
+                             np.random.default_rng(1).standard_normal(n).astype(np.float32)).cuda()
+        marks = torch.empty(n, dtype=torch.uint8, device="cuda")
+        sel = torch.empty(min(n, k), dtype=torch.int32, device="cuda")
+        s = ctypes.c_void_p(stream.cuda_stream)
+        args = (x.data_ptr(), n, k, marks.data_ptr(), sel.data_ptr(), s)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for _ in range(20):
+                _lib.check(lib.hi_rocm_launch_dsv4_indexer_select(*args))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(launches):
+                _lib.check(lib.hi_rocm_launch_dsv4_indexer_select(*args))
+            e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / launches
+        alg = n * 4 + n + min(n, k) * 4
+        out.append({"n_blocks": n, "top_k": k, "us_per_launch": us, "algorithmic_bytes": alg,
+                    "gbs": alg / us / 1e3})
+    return out
+
+
 def cpu_baseline(w, budget_s=15.0):
     """The oracle (a C restatement of the reference CPU sampler plus the
     extension stages), single thread, rows processed serially like the
@@ -330,6 +366,7 @@ def main():
                      "kernel_avg_us_library_events": pass_us,
                      "algorithmic_bytes_per_launch": alg_bytes},
     }
+    res["dsv4_indexer_select"] = time_indexer_select(torch)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w3, args.cpu_budget)
         res["cpu_baseline_all_cores"] = cpu_baseline_all_cores(w3)

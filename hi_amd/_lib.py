@@ -39,6 +39,7 @@ _vp, _i, _f, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c
 SIGNATURES = {
     # include/hi_rocm.h
     "hi_rocm_launch_argmax": (_i, [_vp, _vp, _i, _vp]),
+    "hi_rocm_launch_dsv4_indexer_select": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "hi_rocm_launch_argmax_last_row": (_i, [_vp, _vp, _i, _i, _vp]),
     "hi_rocm_launch_argmax_batched_last_token": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "hi_rocm_launch_sample_last_row": (_i, [_vp, _vp, _i, _i, _f, _f, _i, _f, _vp]),

@@ -388,4 +388,15 @@ int hi_rocm_debug_expf(const float* x, float* y, int64_t n, void* stream) {
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug expf launch");
 }
 
+int hi_rocm_launch_dsv4_indexer_select(const void* scores, int n_blocks, int top_k, void* marks,
+                                       void* sel_out, void* stream) {
+  if (scores == nullptr || marks == nullptr || sel_out == nullptr || n_blocks <= 0 || top_k <= 0 ||
+      stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_launch_dsv4_indexer_select: invalid arguments");
+  hipError_t e = hi_rocm::launch_index_select((const float*)scores, n_blocks, top_k,
+                                              (uint8_t*)marks, (int32_t*)sel_out,
+                                              (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "indexer select launch");
+}
+
 }  // extern "C"

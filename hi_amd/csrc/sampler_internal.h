@@ -167,4 +167,8 @@ hipError_t launch_debug_expf(const float* x, float* y, int64_t n, hipStream_t st
 hipError_t launch_debug_distribution(const SampleArgs& a, float* out_proc, float* out_probs,
                                      hipStream_t stream);
 
+// Exact top-k block selection of the DSV4 indexer (index_select.hip).
+hipError_t launch_index_select(const float* scores, int n, int top_k, uint8_t* marks, int32_t* sel,
+                               hipStream_t stream);
+
 }  // namespace hi_rocm

@@ -214,3 +214,17 @@ def lcg_logits(seed: int, n: int, spread: float) -> np.ndarray:
         u = np.float32(s >> 40) / np.float32(1 << 24)
         out[i] = (u - np.float32(0.5)) * np.float32(spread)
     return out
+
+
+def indexer_test_scores(n: int) -> np.ndarray:
+    """The scores of the reference's indexer-select test
+    (crates/hi-cuda/src/dsv4_gpu.rs:7282-7289): a hash of the index folded to
+    64 levels in [0, 1), so most scores tie.  u32 wrapping arithmetic."""
+    idx = np.arange(n, dtype=np.uint64)
+    mixed = (idx * np.uint64(0x9E3779B9) + np.uint64(0x85EBCA6B)) & np.uint64(0xFFFFFFFF)
+    return (((mixed >> np.uint64(8)) % np.uint64(64)).astype(np.float32) / np.float32(64.0))
+
+
+# The (n_blocks, top_k) shapes of that test; 1162 is its 4.6k-token
+# production shape.
+INDEXER_TEST_SHAPES = [(3, 1), (513, 512), (700, 512), (1162, 512), (4096, 512)]

@@ -171,6 +171,17 @@ int hi_rocm_debug_distribution(const void* logits, int dtype, int batch, int voc
                                const uint32_t* hist_counts, const uint32_t* mask_words,
                                float* out_processed, float* out_probs, void* stream);
 
+/* kernels.cu:2696 hi_cuda_launch_dsv4_indexer_select (Rust wrapper
+ * kernels.rs:3455 launch_dsv4_indexer_select): the exact top-k block
+ * selection of the DSV4 sparse-attention indexer.  scores: f32[n_blocks];
+ * keeps take = min(top_k, n_blocks) blocks ranked by total_cmp descending,
+ * the lower index first on equal scores (dsv4_cpu.rs:3258-3270);
+ * sel_out: int32[take], the kept indices in ascending order; marks:
+ * uint8[n_blocks], 1 for a kept block and 0 otherwise.  Status 1 for null
+ * pointers, n_blocks <= 0, top_k <= 0 or a null stream, as the reference. */
+int hi_rocm_launch_dsv4_indexer_select(const void* scores, int n_blocks, int top_k, void* marks,
+                                       void* sel_out, void* stream);
+
 /* Debug export: y[i] = the device weight function exp(x[i]) for n floats
  * (device arrays).  Bit-identical to host glibc expf.  No reference
  * counterpart; the reference's closest check is crates/hi-cuda/src/

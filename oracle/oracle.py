@@ -115,6 +115,9 @@ def lib() -> ctypes.CDLL:
         L.hro_sample_rows.argtypes = [ctypes.POINTER(_Batch), ctypes.c_int]
         L.hro_expf_array.restype = None
         L.hro_expf_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.hro_indexer_select.restype = ctypes.c_int64
+        L.hro_indexer_select.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_void_p, ctypes.c_void_p]
         L.hro_fold_f32.restype = ctypes.c_float
         L.hro_fold_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64]
         _lib = L
@@ -254,3 +257,16 @@ def sample_rows(logits, params, uniforms, hist_offsets=None, hist_ids=None, hist
     if rc != 0:
         raise ValueError(f"oracle rejected the batch (status {rc})")
     return out
+
+
+def indexer_select(scores, top_k):
+    """DSV4 indexer block selection (dsv4_cpu.rs:3258-3270): the kept block
+    indices, ascending, and the uint8 marks."""
+    x = _f32(scores)
+    n = x.size
+    marks = np.zeros(n, dtype=np.uint8)
+    sel = np.zeros(max(1, min(int(top_k), n)), dtype=np.int32)
+    took = lib().hro_indexer_select(_ptr(x), n, int(top_k), _ptr(marks), _ptr(sel))
+    if took < 0:
+        raise ValueError("indexer_select: n and top_k must be positive")
+    return sel[:took], marks

@@ -607,3 +607,52 @@ int64_t hro_expf_count_mismatch(uint32_t lo_bits, const uint32_t* dev_bits, int6
 
 /* Sequential f32 fold exactly as Rust's Sum (used by tests of the device fold). */
 float hro_fold_f32(const float* x, int64_t n) { return fold_sum(x, n, 1); }
+
+/* ---- DSV4 indexer block selection -------------------------------------
+ * Follows the host's indexer_select_math, crates/hi-cuda/src/dsv4_cpu.rs:
+ * 3258-3270 (and the test's host_select, dsv4_gpu.rs:7260-7275): sort
+ * (index, score) by score with f32::total_cmp descending, then index
+ * ascending; take min(top_k, n); sort the taken indices ascending.
+ * total_cmp order is the unsigned order of the key below. */
+static uint32_t hro_total_key(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+typedef struct { uint32_t key; int32_t idx; } hro_scored;
+
+static int hro_rank_cmp(const void* a, const void* b) {
+  const hro_scored* x = (const hro_scored*)a;
+  const hro_scored* y = (const hro_scored*)b;
+  if (x->key != y->key) return x->key > y->key ? -1 : 1;
+  return x->idx < y->idx ? -1 : (x->idx > y->idx);
+}
+
+static int hro_int_cmp(const void* a, const void* b) {
+  const int32_t x = *(const int32_t*)a, y = *(const int32_t*)b;
+  return x < y ? -1 : (x > y);
+}
+
+/* Returns take (the entries written to sel), or -1 for bad arguments or no
+ * memory.  marks[b] = 1 for a kept block, else 0. */
+int64_t hro_indexer_select(const float* scores, int64_t n, int64_t top_k, uint8_t* marks,
+                           int32_t* sel) {
+  if (n <= 0 || top_k <= 0) return -1;
+  const int64_t take = top_k < n ? top_k : n;
+  hro_scored* r = (hro_scored*)malloc((size_t)n * sizeof(hro_scored));
+  if (r == NULL) return -1;
+  for (int64_t i = 0; i < n; ++i) {
+    r[i].key = hro_total_key(scores[i]);
+    r[i].idx = (int32_t)i;
+  }
+  qsort(r, (size_t)n, sizeof(hro_scored), hro_rank_cmp);
+  memset(marks, 0, (size_t)n);
+  for (int64_t i = 0; i < take; ++i) {
+    sel[i] = r[i].idx;
+    marks[r[i].idx] = 1;
+  }
+  free(r);
+  qsort(sel, (size_t)take, sizeof(int32_t), hro_int_cmp);
+  return take;
+}

@@ -64,6 +64,13 @@ def test_launchers_reject_bad_arguments_without_a_gpu():
     assert lib.hi_rocm_launch_sample_batched_last_token(p, p, None, 1, 1, 8, 1.0, 0.9, 4, 0, s) == 1
     assert lib.hi_rocm_launch_select_batched_last_token_per_row(p, p, p, p, p, None, 1, 1, 8, 0, s) == 1
     assert b"invalid" in lib.hi_rocm_last_error()
+    # kernels.cu:2698-2701: null pointers, n_blocks <= 0, top_k <= 0, null stream
+    assert lib.hi_rocm_launch_dsv4_indexer_select(None, 8, 2, p, p, s) == 1
+    assert lib.hi_rocm_launch_dsv4_indexer_select(p, 8, 2, None, p, s) == 1
+    assert lib.hi_rocm_launch_dsv4_indexer_select(p, 8, 2, p, None, s) == 1
+    assert lib.hi_rocm_launch_dsv4_indexer_select(p, 0, 2, p, p, s) == 1
+    assert lib.hi_rocm_launch_dsv4_indexer_select(p, 8, 0, p, p, s) == 1
+    assert lib.hi_rocm_launch_dsv4_indexer_select(p, 8, 2, p, p, None) == 1
     # hi_rocm_sample: bad dtype, stride below vocab, history without counts
     params = np.zeros(40, np.uint8)
     assert lib.hi_rocm_sample(p, 7, 1, 8, 8, params.ctypes.data, p, None, None, None, None, p,

@@ -31,6 +31,8 @@ def _dev(torch, x):
     x = np.ascontiguousarray(x)
     if x.dtype == np.uint32:
         x = x.view(np.int32)
+    if x.dtype == np.uint16:  # bf16 bit patterns
+        return torch.from_numpy(x.view(np.int16)).to("cuda").view(torch.bfloat16)
     return torch.from_numpy(x).to("cuda")
 
 
@@ -84,6 +86,33 @@ def time_large_batch(torch, w, steps, warmup):
     torch.cuda.synchronize()
     per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)])
     return total_ms / steps, per, wall
+
+
+def time_config(torch, w, steps, warmup):
+    """One of the other configurations (C2, C4, C5): K eager steps of the
+    whole pipeline on one stream between two HIP events on that stream.
+    Algorithmic bytes per step are the workload's input and output bytes,
+    each counted once; the fraction is of the 8 TB/s HBM peak."""
+    smp, a = _prepare(torch, w)
+    stream = torch.cuda.Stream()
+    out = None
+    with torch.cuda.stream(stream):
+        for _ in range(max(warmup, 1)):
+            out = _step(smp, a, w, out, stream)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for _ in range(steps):
+            out = _step(smp, a, w, out, stream)
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1000.0 / steps
+    alg = w.algorithmic_bytes()
+    gbs = alg / (us * 1e-6) / 1e9
+    return {"workload": w.name, "us_per_step": us, "rows_per_s": w.batch / (us * 1e-6),
+            "algorithmic_bytes": alg, "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+            "floor_us": alg / (HBM_PEAK_GBS * 1e9) * 1e6}
 
 
 def time_parts(torch, w, steps):
@@ -366,6 +395,9 @@ def main():
                      "kernel_avg_us_library_events": pass_us,
                      "algorithmic_bytes_per_launch": alg_bytes},
     }
+    from hi_amd.workloads import config2, config4, config5
+    res["other_configs"] = {f"c{i}": time_config(torch, mk(), args.steps, args.warmup)
+                            for i, mk in ((2, config2), (4, config4), (5, config5))}
     res["dsv4_indexer_select"] = time_indexer_select(torch)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w3, args.cpu_budget)

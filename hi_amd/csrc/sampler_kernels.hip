@@ -74,6 +74,20 @@ __device__ __forceinline__ float key_to_s(uint32_t key, float t_eff) {
   return okey_inv(key) / t_eff;
 }
 
+// Tie order of the finite-lane argmax (kernels.cu:7775-7801).  Thread t of
+// 256 keeps the first maximum among indices t, t+256, ...; the tree then
+// halves the stride from 128 to 1 and keeps the lower slot unless the upper
+// one is strictly larger.  The slot compared last (bit 0 of t) weighs most,
+// so among tied maxima the smallest 8-bit bit reversal of (idx mod 256)
+// wins, then the smallest idx.  fin_order packs that order into one integer
+// (smaller wins); fin_index inverts it.
+__device__ __forceinline__ uint32_t fin_order(uint32_t idx) {
+  return (__builtin_bitreverse32(idx) & 0xff000000u) | (idx >> 8);
+}
+__device__ __forceinline__ uint32_t fin_index(uint32_t ord) {
+  return ((ord & 0x00ffffffu) << 8) | (__builtin_bitreverse32(ord) & 0xffu);
+}
+
 // Rust's f32::total_cmp as a signed key (gpu.rs:744).
 __device__ __forceinline__ int32_t total_key(float f) {
   const int32_t i = (int32_t)__float_as_uint(f);
@@ -397,10 +411,7 @@ __device__ __forceinline__ void stat_merge(ChunkStat& a, const ChunkStat& b) {
   }
   if (b.am_fin_i != 0xffffffffu) {
     bool take = a.am_fin_i == 0xffffffffu || b.am_fin_v > a.am_fin_v;
-    if (!take && b.am_fin_v == a.am_fin_v) {
-      const uint32_t ra = a.am_fin_i & 255u, rb = b.am_fin_i & 255u;
-      take = rb < ra || (rb == ra && b.am_fin_i < a.am_fin_i);
-    }
+    if (!take && b.am_fin_v == a.am_fin_v) take = fin_order(b.am_fin_i) < fin_order(a.am_fin_i);
     if (take) { a.am_fin_v = b.am_fin_v; a.am_fin_i = b.am_fin_i; }
   }
   a.any_finite |= b.any_finite;
@@ -1612,10 +1623,7 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
     }
     if (cs.am_fin_i != 0xffffffffu) {
       bool take = fi == 0xffffffffu || cs.am_fin_v > fv;
-      if (!take && cs.am_fin_v == fv) {
-        const uint32_t ra = fi & 255u, rb = cs.am_fin_i & 255u;
-        take = rb < ra || (rb == ra && cs.am_fin_i < fi);
-      }
+      if (!take && cs.am_fin_v == fv) take = fin_order(cs.am_fin_i) < fin_order(fi);
       if (take) { fv = cs.am_fin_v; fi = cs.am_fin_i; }
     }
   }
@@ -1623,7 +1631,7 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   anyf = wave_reduce32(anyf, 0u, [](uint32_t x, uint32_t y) { return x | y; });
   ub = wave_max_u32(ub);
   // argmax merges as 64-bit keys: IEEE (value desc, index asc) and the
-  // finite-lane rule (value desc, index mod 256 asc, index asc)
+  // finite-lane rule (value desc, then fin_order asc)
   {
     // -0 and +0 compare equal under IEEE '>': both map to the +0 key
     const float iz = iv == 0.f ? 0.f : iv;
@@ -1635,14 +1643,9 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   {
     const float fz = fv == 0.f ? 0.f : fv;
     const uint64_t fk = fi == 0xffffffffu ? 0ull
-                        : ((uint64_t)okey(fz) << 32) | (uint64_t)(0xffffffffu - (((fi & 255u) << 23) | (fi >> 8)));
+                        : ((uint64_t)okey(fz) << 32) | (uint64_t)(0xffffffffu - fin_order(fi));
     const uint64_t best = wave_max_u64(fk);
-    if (best == 0ull) {
-      fi = 0xffffffffu;
-    } else {
-      const uint32_t c = 0xffffffffu - (uint32_t)best;
-      fi = ((c & 0x7fffffu) << 8) | (c >> 23);
-    }
+    fi = best == 0ull ? 0xffffffffu : fin_index(0xffffffffu - (uint32_t)best);
   }
   const bool eos = a.mask && !anyf;
   if (cfg.cls == kGreedy) {
@@ -1877,7 +1880,7 @@ __device__ __forceinline__ void stat_add(ChunkStat& st, const StatNeeds& nd, uin
   if (nd.ieee && l > st.am_ieee_v) { st.am_ieee_v = l; st.am_ieee_i = e; }
   if (nd.fin && finitef_(l) &&
       (st.am_fin_i == 0xffffffffu || l > st.am_fin_v ||
-       (l == st.am_fin_v && (e & 255u) < (st.am_fin_i & 255u)))) {
+       (l == st.am_fin_v && fin_order(e) < fin_order(st.am_fin_i)))) {
     st.am_fin_v = l; st.am_fin_i = e;
   }
 }
@@ -2545,7 +2548,7 @@ __device__ __forceinline__ void select_exact(SelLds& L, const SampleArgs& a, con
     if (nd.ieee && l > st.am_ieee_v) { st.am_ieee_v = l; st.am_ieee_i = e; }
     if (nd.fin && finitef_(l) &&
         (st.am_fin_i == 0xffffffffu || l > st.am_fin_v ||
-         (l == st.am_fin_v && (e & 255u) < (st.am_fin_i & 255u)))) {
+         (l == st.am_fin_v && fin_order(e) < fin_order(st.am_fin_i)))) {
       st.am_fin_v = l; st.am_fin_i = e;
     }
   }
@@ -2800,7 +2803,7 @@ __device__ __forceinline__ bool select_lean(SelLds& L, const SampleArgs& a, cons
       const uint64_t e = surv[i];
       if (cand_skey(e) == cand_skey(wmax)) {
         const uint32_t idx = cand_idx(e);
-        const uint64_t fk = ((uint64_t)(idx & 255u) << 32) | idx;
+        const uint64_t fk = ((uint64_t)fin_order(idx) << 32) | idx;
         wfin = fk < wfin ? fk : wfin;
       }
     }
@@ -3040,7 +3043,7 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
         best = e > best ? e : best;
         if (cand_skey(e) == mkey) {
           const uint32_t idx = cand_idx(e);
-          const uint64_t fk = ((uint64_t)(idx & 255u) << 32) | idx;
+          const uint64_t fk = ((uint64_t)fin_order(idx) << 32) | idx;
           finb = fk < finb ? fk : finb;
         }
         if (nd.sel && !keep) {

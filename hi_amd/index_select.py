@@ -13,7 +13,8 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .sampler import _host_stream
+
+_side_streams = {}
 
 
 def launch_dsv4_indexer_select(scores: torch.Tensor, n_blocks: int, top_k: int,
@@ -34,9 +35,30 @@ def launch_dsv4_indexer_select(scores: torch.Tensor, n_blocks: int, top_k: int,
     if sel_out.dtype != torch.int32 or not sel_out.is_cuda or sel_out.numel() < min(top_k, n_blocks):
         raise ValueError("dsv4 indexer select output too small")
     lib = _lib.load()
+    side = None
+    if stream is None or stream.cuda_stream == 0:
+        cur = torch.cuda.current_stream()
+        if cur.cuda_stream == 0:
+            # the C ABI (like kernels.cu:2696) rejects the null stream: run on
+            # a side stream ordered after the current one, then order the
+            # current stream after the launch so its later reads see the
+            # results, and keep the caching allocator from reusing the
+            # tensors while the side stream still uses them
+            dev = scores.device.index if scores.device.index is not None else torch.cuda.current_device()
+            side = _side_streams.get(dev)
+            if side is None:
+                side = _side_streams[dev] = torch.cuda.Stream(device=dev)
+            side.wait_stream(cur)
+            stream = side
+        else:
+            stream = cur
     _lib.check(lib.hi_rocm_launch_dsv4_indexer_select(
         scores.data_ptr(), int(n_blocks), int(top_k), marks.data_ptr(), sel_out.data_ptr(),
-        _host_stream(stream)))
+        int(stream.cuda_stream)))
+    if side is not None:
+        torch.cuda.current_stream().wait_stream(side)
+        for t in (scores, marks, sel_out):
+            t.record_stream(side)
 
 
 def dsv4_indexer_select(scores: torch.Tensor, top_k: int,

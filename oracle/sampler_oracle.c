@@ -92,23 +92,31 @@ int64_t hro_argmax_ieee(const float* x, int64_t n) {
   return bi;
 }
 
-/* kernels.cu:7775-7801: thread t (of 256) keeps the first finite maximum among
- * indices t, t+256, ...; the tree keeps the lower thread on ties.  So among
- * tied finite maxima the smallest (idx mod 256) wins, then the smallest idx.
- * With no finite value the result is 0 and *max_out is -inf. */
+/* kernels.cu:7775-7801, restated literally: 256 lanes, lane t scans indices
+ * t, t+256, ... and keeps the first finite value that is strictly larger than
+ * its running maximum (start -inf, argmax 0); then a tree over the lanes with
+ * strides 128, 64, ..., 1, where slot t takes slot t+s only when that value is
+ * strictly larger.  On tied maxima this prefers the smallest 8-bit bit
+ * reversal of (idx mod 256), then the smallest idx.  With no finite value the
+ * result is 0 and *max_out is -inf. */
 int64_t hro_argmax_finite_lane(const float* x, int64_t n, float* max_out) {
-  float best = -INFINITY;
-  int64_t bi = 0;
-  int have = 0;
-  for (int64_t i = 0; i < n; ++i) {
-    float v = x[i];
-    if (!is_finite_f(v)) continue;
-    if (!have || v > best || (v == best && (i % 256) < (bi % 256))) {
-      best = v; bi = i; have = 1;
+  float lmax[256];
+  int64_t larg[256];
+  for (int t = 0; t < 256; ++t) {
+    lmax[t] = -INFINITY;
+    larg[t] = 0;
+    for (int64_t i = t; i < n; i += 256) {
+      const float v = x[i];
+      if (is_finite_f(v) && v > lmax[t]) { lmax[t] = v; larg[t] = i; }
     }
   }
-  if (max_out) *max_out = best;
-  return have ? bi : 0;
+  for (int s = 128; s > 0; s >>= 1) {
+    for (int t = 0; t < s; ++t) {
+      if (lmax[t + s] > lmax[t]) { lmax[t] = lmax[t + s]; larg[t] = larg[t + s]; }
+    }
+  }
+  if (max_out) *max_out = lmax[0];
+  return larg[0];
 }
 
 /* ------------------------------------------------------------------------- */

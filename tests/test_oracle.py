@@ -189,6 +189,33 @@ def test_closed_forms(oracle):
         assert oracle.ranked_sample(x, 0.8, 0.95, 30, float("nan")) == first
 
 
+def test_top_p_normaliser_closed_forms(oracle):
+    """gpu.rs:834-838: with top_k set, the top-p normaliser is the kept mass;
+    without it, the whole vocabulary's mass.  Equal logits give equal
+    weights 1, so the nucleus is fixed by counting: n equal weights, top_p
+    0.5 and a normaliser of m keep the first ceil(m / 2) ranks (cum_p of
+    rank r is (r + 1) / m, exact for these m)."""
+    x = np.zeros(4, F32)
+    # no top_k: total 4, cum_p 0.25, 0.5 -> ranks {0, 1}
+    assert oracle.ranked_sample(x, 1.0, 0.5, None, 0.4) == 0
+    assert oracle.ranked_sample(x, 1.0, 0.5, None, 0.75) == 1
+    # top_k 2: total 2 (the kept mass), cum_p 0.5 at rank 0 -> {0}
+    for u in (0.0, 0.4, 0.75, 0.99999994):
+        assert oracle.ranked_sample(x, 1.0, 0.5, 2, u) == 0
+    # top_k 3: total 3, cum_p 1/3, 2/3 -> {0, 1}
+    assert oracle.ranked_sample(x, 1.0, 0.5, 3, 0.75) == 1
+    # top_k 4 = V: total 4 again -> {0, 1}
+    assert oracle.ranked_sample(x, 1.0, 0.5, 4, 0.75) == 1
+    # eight equal weights, top_p 0.25: without top_k {0, 1}; top_k 4 keeps
+    # mass 4, so cum_p 0.25 at rank 0 -> {0}
+    y = np.zeros(8, F32)
+    assert oracle.ranked_sample(y, 1.0, 0.25, None, 0.9) == 1
+    assert oracle.ranked_sample(y, 1.0, 0.25, 4, 0.9) == 0
+    # the full sort gives the same answers
+    assert oracle.ranked_sample_brute(y, 1.0, 0.25, 4, 0.9) == 0
+    assert oracle.ranked_sample_brute(x, 1.0, 0.5, 2, 0.75) == 0
+
+
 def test_inverse_cdf_invariants(oracle):
     """lib.rs:25972-26054: each pick lies in its CDF bin, picks monotone in u."""
     rng = np.random.default_rng(5)
@@ -278,15 +305,49 @@ def test_temp_only_independent(oracle):
             assert oracle.temp_only_sample(x, 0.9, u) == _py_temp_only(oracle.expf, x, 0.9, u)
 
 
+def _bitrev8(r):
+    return int(f"{r & 255:08b}"[::-1], 2)
+
+
 def test_finite_lane_argmax_rule(oracle):
-    # equal maxima at 300 and 5: 300 % 256 = 44 > 5, so index 5 wins; at 260
-    # (residue 4) and 5: 260 wins although its index is larger.
+    # kernels.cu:7780-7801: lane t of 256 keeps its first maximum; the tree
+    # (strides 128 .. 1, strict >) decides bit 0 of the lane last, so tied
+    # maxima go to the smallest bit reversal of (idx mod 256), then the
+    # smallest idx.  Maxima at 300 (residue 44, reversed 52) and 5 (residue
+    # 5, reversed 160): 300 wins.  Adding 260 (residue 4, reversed 32): 260.
     x = np.zeros(600, F32)
     x[300] = x[5] = 3.0
-    assert oracle.argmax_finite_lane(x)[0] == 5
+    assert oracle.argmax_finite_lane(x)[0] == 300
     x[260] = 3.0
     assert oracle.argmax_finite_lane(x)[0] == 260
     assert oracle.argmax_ieee(x) == 5
+    # residues 1 (reversed 128) and 2 (reversed 64): 2 wins; 0 beats both
+    z = np.zeros(8, F32)
+    z[1] = z[2] = 1.0
+    assert oracle.argmax_finite_lane(z)[0] == 2
+    z[0] = 1.0
+    assert oracle.argmax_finite_lane(z)[0] == 0
+    # same residue: the lower index (lane t keeps its first maximum)
+    y2 = np.zeros(1000, F32)
+    y2[7 + 512] = y2[7 + 256] = 2.0
+    assert oracle.argmax_finite_lane(y2)[0] == 7 + 256
+    # every tie pattern on random inputs equals the closed form
+    rng = np.random.default_rng(11)
+    for trial in range(300):
+        n = int(rng.integers(1, 2000))
+        v = rng.integers(0, 4, n).astype(F32)
+        if trial % 5 == 0:
+            v[rng.integers(0, n, max(1, n // 7))] = np.nan
+        if trial % 7 == 0:
+            v[rng.integers(0, n, max(1, n // 9))] = np.inf
+        fin = np.isfinite(v)
+        if not fin.any():
+            assert oracle.argmax_finite_lane(v)[0] == 0
+            continue
+        m = v[fin].max()
+        ties = np.flatnonzero(fin & (v == m))
+        want = min(ties, key=lambda i: (_bitrev8(int(i)), int(i)))
+        assert oracle.argmax_finite_lane(v)[0] == want, trial
     # non-finite values never win the finite argmax; IEEE argmax keeps +inf
     y = np.array([1.0, np.inf, 2.0, np.nan], F32)
     assert oracle.argmax_finite_lane(y)[0] == 2

@@ -381,6 +381,15 @@ int hi_rocm_debug_distribution(const void* logits, int dtype, int batch, int voc
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug distribution launch");
 }
 
+int hi_rocm_debug_fold(const float* terms, const uint32_t* counts, int runs, float start,
+                      float* out_start, float* out_final, void* stream) {
+  if (terms == nullptr || counts == nullptr || out_start == nullptr || out_final == nullptr || runs <= 0 ||
+      runs > hi_rocm::kDebugFoldMaxRuns || stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_fold: invalid arguments");
+  hipError_t e = hi_rocm::launch_debug_fold(terms, counts, runs, start, out_start, out_final, (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug fold launch");
+}
+
 int hi_rocm_debug_expf(const float* x, float* y, int64_t n, void* stream) {
   if (x == nullptr || y == nullptr || n <= 0)
     return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_expf: invalid arguments");

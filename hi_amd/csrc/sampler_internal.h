@@ -164,6 +164,10 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t stream, const LaunchEv
 hipError_t launch_argmax(const float* logits, uint32_t* out, int B, int64_t row_stride,
                          int64_t row_offset, int cols, hipStream_t stream);
 hipError_t launch_debug_expf(const float* x, float* y, int64_t n, hipStream_t stream);
+constexpr int kDebugFoldMaxRuns = 65536;
+size_t debug_fold_lds(int R);
+hipError_t launch_debug_fold(const float* x, const uint32_t* m, int R, float a0, float* out_start,
+                             float* out_final, hipStream_t stream);
 hipError_t launch_debug_distribution(const SampleArgs& a, float* out_proc, float* out_probs,
                                      hipStream_t stream);
 

@@ -35,6 +35,7 @@
 
 #include "hi_rocm.h"
 #include "exact_expf.h"
+#include "fold_wg.h"
 #include "sampler_internal.h"
 
 namespace hi_rocm {
@@ -3306,6 +3307,20 @@ __global__ void __launch_bounds__(1024) argmax_rows_kernel(const float* logits, 
 // Debug kernels
 // ==========================================================================
 
+// The workgroup fold of runs (fold_wg.h) on its own: out_start[r] gets the
+// sequential f32 fold value before run r, *out_final the value after the
+// last run.  Terms and counts are read from global memory.
+__global__ void __launch_bounds__(NT) debug_fold_kernel(const float* x, const uint32_t* m, int R, float a0,
+                                                        float* out_start, float* out_final) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  auto& L = *reinterpret_cast<fold::WgLds<NT>*>(lds_raw);
+  uint8_t* pe = lds_raw + sizeof(fold::WgLds<NT>);
+  const float fin = fold::fold_runs<NT>(
+      L, pe, R, a0, [&](int r) { return x[r]; }, [&](int r) { return m[r]; },
+      [&](int r, float v) { out_start[r] = v; });
+  if (threadIdx.x == 0) *out_final = fin;
+}
+
 __global__ void debug_expf_kernel(const float* x, float* y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = exact_expf(x[i]);
@@ -4124,6 +4139,18 @@ hipError_t launch_argmax(const float* logits, uint32_t* out, int B, int64_t row_
   const int vec_ok = (((uintptr_t)(logits + row_offset) & 15u) == 0) && (row_stride % 4 == 0);
   hipLaunchKernelGGL(argmax_rows_kernel, dim3(B), dim3(1024), 0, stream, logits, out, B, row_stride,
                      row_offset, cols, vec_ok);
+  return hipGetLastError();
+}
+
+size_t debug_fold_lds(int R) { return sizeof(fold::WgLds<NT>) + (size_t)R + 1; }
+
+hipError_t launch_debug_fold(const float* x, const uint32_t* m, int R, float a0, float* out_start,
+                             float* out_final, hipStream_t stream) {
+  const size_t lds = debug_fold_lds(R);
+  hipError_t e = hipFuncSetAttribute((const void*)debug_fold_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(debug_fold_kernel, dim3(1), dim3(NT), lds, stream, x, m, R, a0, out_start, out_final);
   return hipGetLastError();
 }
 

@@ -182,6 +182,15 @@ int hi_rocm_debug_distribution(const void* logits, int dtype, int batch, int voc
 int hi_rocm_launch_dsv4_indexer_select(const void* scores, int n_blocks, int top_k, void* marks,
                                        void* sel_out, void* stream);
 
+/* Debug export: the workgroup form of the sequential f32 fold that every
+ * sum of the sampler's draw uses (the reference's folds at gpu.rs:834-838,
+ * :851, :878, :889-896), on its own.  runs (1 .. 65536) runs of equal terms:
+ * terms[r] (f32 >= 0) repeated counts[r] >= 1 times, folded left to right
+ * from start; out_start[r] = the value before run r, *out_final = the value
+ * after the last run (device arrays).  No reference counterpart. */
+int hi_rocm_debug_fold(const float* terms, const uint32_t* counts, int runs, float start,
+                       float* out_start, float* out_final, void* stream);
+
 /* Debug export: y[i] = the device weight function exp(x[i]) for n floats
  * (device arrays).  Bit-identical to host glibc expf.  No reference
  * counterpart; the reference's closest check is crates/hi-cuda/src/

@@ -38,6 +38,8 @@ struct WgLds {
   Map tcarry[NTH];          // map of the thread's segment before its first run
   uint32_t tk[NTH];         // segment ordinal at the thread's first run
   Map seg_map[kWgSeg];      // map of segment k (its runs before boundary run k)
+  Map seg_alt[kWgSeg];      // the same terms in the binade below (fold_plan<.., true>)
+  Map walt[NTH / 64];
   uint32_t seg_A[kWgSeg];   // A at segment k's start (chain)
   uint32_t seg_e[kWgSeg];   // binade of segment k
   uint32_t bnd_run[kWgSeg]; // run index of boundary run k
@@ -56,6 +58,16 @@ __device__ __forceinline__ void seg_combine(uint32_t f1, Map m1, uint32_t& f2, M
   f2 |= f1;
 }
 
+// What m copies of x add to an f32 sum in binade e, as a double: the
+// rounded increments (exact halves counted as half an ulp), or the exact
+// amount when the run leaves the binade.
+__device__ __forceinline__ double rounded_inc(float x, uint32_t m, int e) {
+  const Map mp = run_map(classify(x, e), m);
+  if (mp.t0 >= kTop) return (double)m * (double)x;
+  const double ulp = __builtin_ldexp(1.0, e - 150);
+  return 0.5 * ((double)mp.t0 + (double)mp.t1) * ulp;
+}
+
 template <int NTH>
 __device__ __forceinline__ void block_of(int pos, int R, int& r0, int& r1) {
   const int n = R - pos;
@@ -65,9 +77,18 @@ __device__ __forceinline__ void block_of(int pos, int R, int& r0, int& r1) {
   r1 = r0 + J < R ? r0 + J : R;
 }
 
+// The map of a run in binade e, and (ALT) in the binade below.
+template <bool ALT>
+__device__ __forceinline__ void run_maps(float x, uint32_t m, int e, Map& mp, Map& ma) {
+  mp = run_map(classify(x, e), m);
+  if (ALT) ma = e > 1 ? run_map(classify(x, e - 1), m) : mp;
+}
+
 // Plan of runs [pos, R) from the predicted start value `base`.  pe has
-// room for R + 1 entries.  Ends with a barrier.
-template <int NTH, typename TermF, typename MultF>
+// room for R + 1 entries.  With ALT, every segment also gets its map in the
+// binade below its predicted one (seg_alt), for a start value that lags
+// the prediction.  Ends with a barrier.
+template <int NTH, typename TermF, typename MultF, bool ALT = false>
 __device__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, int R, double base, TermF term, MultF mult) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   int r0, r1;
@@ -96,32 +117,77 @@ __device__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, int R, double bas
   }
   if (tid == NTH - 1) pe[R] = (uint8_t)binade((float)(base + all));
   __syncthreads();
+  // 1b. refine with the increments the fold makes in those binades: terms
+  //     below half an ulp add nothing to an f32 sum, so exact sums run ahead
+  //     of it (a value just below a power of two can stay there while the
+  //     exact sum passes it, which would mispredict every later boundary)
+  my = 0.0;
+  for (int r = r0; r < r1; ++r) my += rounded_inc(term(r), mult(r), pe[r]);
+  inc = my;
+  #pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const double o = shfl_up_f64(inc, d);
+    if (lane >= d) inc += o;
+  }
+  __syncthreads();
+  if (lane == 63) L.dsum[wid] = inc;
+  __syncthreads();
+  before = 0.0;
+  all = 0.0;
+  #pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) {
+    if (w < wid) before += L.dsum[w];
+    all += L.dsum[w];
+  }
+  P = base + (before + (inc - my));
+  uint8_t eprev = 0;
+  for (int r = r0; r < r1; ++r) {
+    const double d = rounded_inc(term(r), mult(r), pe[r]);
+    eprev = (uint8_t)binade((float)P);
+    P += d;
+    pe[r] = eprev;  // pe[r] is read above before it is rewritten
+  }
+  __syncthreads();
+  if (tid == NTH - 1) pe[R] = (uint8_t)binade((float)(base + all));
+  __syncthreads();
   // 2. per-thread summary: boundary runs, the map before the first one
   //    (head) and after the last one (tail)
   uint32_t nbt = 0u;
   Map head = map_identity(), tail = map_identity();
+  Map head_a = map_identity(), tail_a = map_identity();
   for (int r = r0; r < r1; ++r) {
     const int e = pe[r];
     if (e != pe[r + 1]) {
       ++nbt;
       tail = map_identity();
+      tail_a = map_identity();
     } else {
-      const Map mp = run_map(classify(term(r), e), mult(r));
-      if (nbt) tail = compose(tail, mp);
-      else head = compose(head, mp);
+      Map mp, ma;
+      run_maps<ALT>(term(r), mult(r), e, mp, ma);
+      if (nbt) {
+        tail = compose(tail, mp);
+        if (ALT) tail_a = compose(tail_a, ma);
+      } else {
+        head = compose(head, mp);
+        if (ALT) head_a = compose(head_a, ma);
+      }
     }
   }
   // 3. segmented exclusive scan over threads: the map of the segment the
   //    thread starts in, up to its first run; and the boundary ordinal
   uint32_t f = nbt ? 1u : 0u;
   Map m = nbt ? tail : head;
+  Map ma = nbt ? tail_a : head_a;
   uint32_t cnt = nbt;
   #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const uint32_t of = (uint32_t)__shfl_up((int)f, (unsigned)d, 64);
     const Map om = Map{(uint32_t)__shfl_up((int)m.t0, (unsigned)d, 64), (uint32_t)__shfl_up((int)m.t1, (unsigned)d, 64)};
+    Map oa = map_identity();
+    if (ALT) oa = Map{(uint32_t)__shfl_up((int)ma.t0, (unsigned)d, 64), (uint32_t)__shfl_up((int)ma.t1, (unsigned)d, 64)};
     const uint32_t oc = (uint32_t)__shfl_up((int)cnt, (unsigned)d, 64);
     if (lane >= d) {
+      if (ALT && !f) ma = compose(oa, ma);
       seg_combine(of, om, f, m);
       cnt += oc;
     }
@@ -129,25 +195,30 @@ __device__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, int R, double bas
   if (lane == 63) {
     L.wflag[wid] = f;
     L.wmap[wid] = m;
+    if (ALT) L.walt[wid] = ma;
     L.wcnt[wid] = cnt;
   }
   // exclusive: the inclusive value of the lane below
   uint32_t ef = (uint32_t)__shfl_up((int)f, 1u, 64);
   Map em = Map{(uint32_t)__shfl_up((int)m.t0, 1u, 64), (uint32_t)__shfl_up((int)m.t1, 1u, 64)};
+  Map ea = map_identity();
+  if (ALT) ea = Map{(uint32_t)__shfl_up((int)ma.t0, 1u, 64), (uint32_t)__shfl_up((int)ma.t1, 1u, 64)};
   uint32_t ec = (uint32_t)__shfl_up((int)cnt, 1u, 64);
   if (lane == 0) {
     ef = 0u;
     em = map_identity();
+    ea = map_identity();
     ec = 0u;
   }
   __syncthreads();
   uint32_t cf = 0u, cc = 0u, tot = 0u;
-  Map cm = map_identity();
+  Map cm = map_identity(), ca = map_identity();
   #pragma unroll
   for (int w = 0; w < NTH / 64; ++w) {
     if (w < wid) {
       uint32_t ff = L.wflag[w];
       Map mm = L.wmap[w];
+      if (ALT) ca = ff ? L.walt[w] : compose(ca, L.walt[w]);
       seg_combine(cf, cm, ff, mm);
       cf = ff;
       cm = mm;
@@ -155,6 +226,7 @@ __device__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, int R, double bas
     }
     tot += L.wcnt[w];
   }
+  if (ALT && !ef) ea = compose(ca, ea);
   seg_combine(cf, cm, ef, em);  // previous waves, then the lanes below
   L.tcarry[tid] = em;
   L.tk[tid] = cc + ec;
@@ -163,21 +235,27 @@ __device__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, int R, double bas
   //    (and the thread holding the last run, for the last segment)
   {
     uint32_t k = cc + ec;
-    Map cur = em;
+    Map cur = em, cura = ea;
     for (int r = r0; r < r1; ++r) {
       const int e = pe[r];
       if (e != pe[r + 1]) {
         L.seg_map[k] = cur;
+        if (ALT) L.seg_alt[k] = cura;
         L.seg_e[k] = (uint32_t)e;
         L.bnd_run[k] = (uint32_t)r;
         ++k;
         cur = map_identity();
+        cura = map_identity();
       } else {
-        cur = compose(cur, run_map(classify(term(r), e), mult(r)));
+        Map mp, mq;
+        run_maps<ALT>(term(r), mult(r), e, mp, mq);
+        cur = compose(cur, mp);
+        if (ALT) cura = compose(cura, mq);
       }
     }
     if (r0 < r1 && r1 == R) {
       L.seg_map[k] = cur;
+      if (ALT) L.seg_alt[k] = cura;
       L.seg_e[k] = pe[R];
     }
   }

@@ -75,6 +75,10 @@ void carve(hi_rocm::SampleArgs& a, void* ws, const hi_rocm::WorkspaceLayout& L) 
   a.ws_list = (uint64_t*)(base + L.ws_list);
   a.list_stride = L.list_stride;
   a.done = (uint32_t*)(base + L.done);
+  a.wstat = (hi_rocm::WideStat*)(base + L.wstat);
+  a.wfold = (hi_rocm::ChunkFold*)(base + L.wfold);
+  a.wrow = (hi_rocm::WideRow*)(base + L.wrow);
+  a.diag = (uint32_t*)(base + L.diag);
   a.chunk = hi_rocm::choose_chunk(a.B, a.V, a.n_lp, a.vec_ok, a.hoff != nullptr);
   a.n_chunks = (a.V + a.chunk - 1) / a.chunk;
 }
@@ -122,6 +126,7 @@ void destroy_events() {
 }
 
 int run_with_internal_ws(hi_rocm::SampleArgs& a, hipStream_t stream) {
+  if (a.B > hi_rocm::kDoneRows) return fail(HI_ROCM_ERR_UNSUPPORTED, "batch above 65536 rows");
   const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(a.B, a.V);
   void* ws = nullptr;
   int rc = internal_workspace(L.total, &ws);
@@ -264,6 +269,7 @@ static int check_sample_args(const void* logits, int dtype, int batch, int vocab
   if (logits == nullptr || params == nullptr || out_tokens == nullptr || batch <= 0 ||
       vocab <= 0 || row_stride < vocab)
     return fail(HI_ROCM_ERR_ARGS, "hi_rocm: invalid logits/params/outputs/sizes");
+  if (batch > hi_rocm::kDoneRows) return fail(HI_ROCM_ERR_UNSUPPORTED, "batch above 65536 rows");
   if (dtype != HI_ROCM_DTYPE_F32 && dtype != HI_ROCM_DTYPE_BF16)
     return fail(HI_ROCM_ERR_ARGS, "hi_rocm: unknown dtype");
   if ((hist_offsets == nullptr) != (hist_ids == nullptr) ||
@@ -388,6 +394,19 @@ int hi_rocm_debug_fold(const float* terms, const uint32_t* counts, int runs, flo
     return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_fold: invalid arguments");
   hipError_t e = hi_rocm::launch_debug_fold(terms, counts, runs, start, out_start, out_final, (hipStream_t)stream);
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug fold launch");
+}
+
+int hi_rocm_debug_wide_paths(const void* workspace, size_t workspace_bytes, int batch, int vocab,
+                             uint32_t* out_paths, void* stream) {
+  if (workspace == nullptr || out_paths == nullptr || batch <= 0 || vocab <= 0 || batch > hi_rocm::kDoneRows ||
+      !vocab_ok(vocab))
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_wide_paths: invalid arguments");
+  const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(batch, vocab);
+  if (workspace_bytes < L.total) return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_wide_paths: workspace too small");
+  hipError_t e = hipMemcpyAsync(out_paths, (const char*)workspace + L.diag, (size_t)batch * 4,
+                                hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug wide paths copy");
 }
 
 int hi_rocm_debug_expf(const float* x, float* y, int64_t n, void* stream) {

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "hi_rocm.h"
+#include "exact_fold.h"
 
 namespace hi_rocm {
 
@@ -77,6 +78,46 @@ struct ChunkStat {
 };
 static_assert(sizeof(ChunkStat) == 64, "ChunkStat layout");
 
+// Per (row, chunk) mass histogram of a top-p row, written by the select
+// pass: bin j holds the sum of w' = exp(s - ms) (approximate exp) over the
+// chunk's logits with w' in (2^-(j+1), 2^-j], the last bin also everything
+// below.  It only sizes the nucleus superset; no result depends on it.
+constexpr int kWideBins = 32;
+struct WideStat {
+  float ms;                  // the chunk's max scaled logit (the bins' reference)
+  uint32_t valid;            // 1: written by this call's select pass
+  float hist[kWideBins];
+  double pred;               // predicted fold value before the chunk (written by the row's last chunk)
+};
+
+// Per-row result of the select pass's last workgroup for a top-p row.
+struct WideRow {
+  float M;                   // the row max of s
+  float w_lo;                // the nucleus superset: weights >= w_lo
+  uint32_t valid;            // 0: the row takes the general finish
+  uint32_t pad;
+};
+static_assert(sizeof(WideStat) == 144, "WideStat layout");
+
+// Per (row, chunk) result of the wide pass for a top-p row: the plan of the
+// chunk's part of the vocabulary-order weight fold (segments of one binade
+// and the boundary terms between them) and the number of distinct-weight
+// runs of the nucleus superset it wrote.
+constexpr int kFoldSegs = 12;
+struct ChunkFold {
+  uint32_t nseg;             // segments; 0: the plan did not fit (the finish refolds the chunk)
+  uint32_t nonempty;         // bit k: segment k has terms
+  uint32_t nruns;            // superset runs written; kFoldNone: the chunk's table overflowed
+  uint32_t has_end;          // chunk 0: `end` is the exact fold of its weights from -0.0
+  float end;
+  uint32_t pad[3];
+  uint32_t seg_e[kFoldSegs];
+  fold::Map seg_map[kFoldSegs];
+  fold::Map seg_alt[kFoldSegs];  // the same terms in the binade below seg_e
+  float bnd_x[kFoldSegs];
+};
+constexpr uint32_t kFoldNone = 0xffffffffu;
+
 struct SampleArgs {
   const void* logits;  // row 0 of the batch
   int dtype;
@@ -102,18 +143,37 @@ struct SampleArgs {
   uint64_t* cand;      // [B][n_chunks][kFast]
   float* ws_s;         // [B][V]
   float* ws_w;         // [B][V]
-  uint64_t* ws_list;   // [B][list_stride]
+  uint64_t* ws_list;   // [B][list_stride]; the wide pass's superset runs
   int64_t list_stride;
-  uint32_t* done;      // [kFusedMaxRows] chunks of the row finished (zero between launches)
+  uint32_t* done;      // [kDoneRows] chunks of the row finished (zero between launches)
+  WideStat* wstat;     // [B][n_chunks]
+  ChunkFold* wfold;    // [B][n_chunks]
+  WideRow* wrow;       // [B]
+  uint32_t* diag;      // [B] how the wide pass finished each top-p row (WidePath)
+};
+
+// diag values for top-p rows of the chunked path (0: not a top-p row of
+// that path, or an older call).
+enum WidePath : uint32_t {
+  kWideDone = 1,          // finished by the wide pass
+  kWideNoStats = 2,       // a chunk took the select pass's exact path, or no finite logit
+  kWideChunkFull = 3,     // a chunk's table of distinct weights overflowed
+  kWideTotal = 4,         // the normaliser is not positive and finite (argmax fallback)
+  kWideMergeFull = 5,     // the row's table of distinct weights overflowed
+  kWideNoCutoff = 6,      // the cutoff lies outside the superset
+  kWideDrawFail = 7,      // the candidate total or the drawn index could not be resolved
 };
 
 // Batches whose (chunk, row) grid has at most this many workgroups run the
 // select and the finish as one kernel; that bounds their rows too.
 constexpr int kFusedMaxWorkgroups = 512;
 constexpr int kFusedMaxRows = kFusedMaxWorkgroups;
+// Per-row counters of the kernels whose last workgroup of a row finishes it
+// (both leave them at zero); this also bounds the rows of one call.
+constexpr int kDoneRows = 65536;
 
 struct WorkspaceLayout {
-  size_t stats, cand, ws_s, ws_w, ws_list, done, total;
+  size_t stats, cand, ws_s, ws_w, ws_list, done, wstat, wfold, wrow, diag, total;
   int64_t slots;       // (row, chunk) records reserved
   int64_t list_stride;
 };
@@ -143,8 +203,12 @@ inline WorkspaceLayout workspace_layout(int max_batch, int V) {
   size_t off = 0;
   // the fused path's per-row counters first, at the same place in every
   // layout (calls of any shape may share a workspace)
-  L.done = off; off = align(off + (size_t)kFusedMaxRows * sizeof(uint32_t));
+  L.done = off; off = align(off + (size_t)kDoneRows * sizeof(uint32_t));
   L.stats = off; off = align(off + (size_t)L.slots * sizeof(ChunkStat));
+  L.wstat = off; off = align(off + (size_t)L.slots * sizeof(WideStat));
+  L.wfold = off; off = align(off + (size_t)L.slots * sizeof(ChunkFold));
+  L.wrow = off; off = align(off + (size_t)max_batch * sizeof(WideRow));
+  L.diag = off; off = align(off + (size_t)max_batch * sizeof(uint32_t));
   L.cand = off; off = align(off + (size_t)L.slots * kFast * sizeof(uint64_t));
   L.ws_s = off; off = align(off + (size_t)max_batch * V * sizeof(float));
   L.ws_w = off; off = align(off + (size_t)max_batch * V * sizeof(float));

@@ -31,7 +31,10 @@
 #include <float.h>
 #include <stddef.h>
 
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "hi_rocm.h"
 #include "exact_expf.h"
@@ -1124,9 +1127,11 @@ __device__ __forceinline__ uint32_t row_argmax_total(FinLds& fs, const SampleArg
   return 0xffffffffu - (uint32_t)best;
 }
 
+__device__ void finish_logprobs(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t token,
+                                float M, bool eos, int ranked_k);
+
 __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg) {
   const int tid = threadIdx.x;
-  const int V = a.V;
   ChunkStat st;
   stat_init(st);
   for (int c = tid; c < a.n_chunks; c += NT) stat_merge(st, a.stats[(int64_t)row * a.n_chunks + c]);
@@ -1158,9 +1163,19 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
   }
   if (tid == 0) a.out_tokens[row] = token;
   if (a.n_lp <= 0 && !a.out_token_lp) return;
-
-  // Logprobs of the processed distribution (extension).
   __syncthreads();
+  finish_logprobs(fs, a, row, cfg, token, M, eos, ranked_k);
+}
+
+// Logprobs of the processed distribution (extension) once the row's token
+// is known: the top n_lp in rank order and the token's own.  M is the row
+// max of s; fs.buf / fs.pay hold the first ranked_k entries of the rank
+// order (0: none yet).  The normaliser sums the candidates of every chunk
+// in double and the other logits from each chunk's mass.
+__device__ void finish_logprobs(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t token,
+                                float M, bool eos, int ranked_k) {
+  const int tid = threadIdx.x;
+  const int V = a.V;
   const int N = a.n_lp;
   if (eos || !finitef_(M)) {
     for (int j = tid; j < N; j += NT) {
@@ -2314,6 +2329,7 @@ constexpr int kLaneSurv = 6;               // streamed survivors a lane takes pe
 struct SelLds {
   uint64_t surv[NT / 64][kSurvCap];
   uint32_t hist[256];
+  float whist[kWideBins];     // top-p rows: the chunk's mass histogram (WideStat)
   uint32_t sel[4];
   uint32_t hw[NT / 64];       // history tokens among each wave's logits
   uint32_t wcnt[NT / 64];
@@ -2512,6 +2528,7 @@ struct SelNeeds {
   bool sel;         // candidates (k_sel > 0)
   bool surv;        // a survivor list at all (sel or an argmax)
   bool lse;         // normaliser rest for logprobs
+  bool whist;       // top-p rows: the chunk's mass histogram for the wide pass
 };
 
 __device__ __forceinline__ SelNeeds sel_needs(const SampleArgs& a, const RowCfg& cfg) {
@@ -2521,7 +2538,17 @@ __device__ __forceinline__ SelNeeds sel_needs(const SampleArgs& a, const RowCfg&
   n.sel = cfg.k_sel > 0;
   n.surv = n.sel || n.ieee || n.fin;
   n.lse = a.need_lse != 0;
+  n.whist = cfg.cls == kTopP;
   return n;
+}
+
+// Adds one processed logit v (NaN: absent) to a top-p row's chunk mass
+// histogram: w' = exp((v - m) / T) = 2^r, bin floor(-r), clamped.
+__device__ __forceinline__ void wide_hist_add(float* whist, float v, float m, float a2) {
+  if (!finitef_(v)) return;
+  const float r = (v - m) * a2;
+  const int j = -r < (float)(kWideBins - 1) ? (int)(-r) : kWideBins - 1;
+  atomicAdd(&whist[j], __builtin_amdgcn_exp2f(r));
 }
 
 // Exact pass over the chunk from global memory, element by element.  Used
@@ -2597,11 +2624,26 @@ __device__ __forceinline__ void select_exact(SelLds& L, const SampleArgs& a, con
     bs.lse_m = lm;
     bs.lse_sum = nd.lse ? rest : 0.f;
   }
+  if (nd.whist && tid < kWideBins) L.whist[tid] = 0.f;
+  __syncthreads();
   if (cfg.store_s) {
     float* srow = a.ws_s + (int64_t)row * a.V + c0;
-    for (int li = tid; li < len; li += NT) srow[li] = key_to_s(lkey(proc(li)), cfg.t_eff);
+    for (int li = tid; li < len; li += NT) {
+      const float l = proc(li);
+      srow[li] = key_to_s(lkey(l), cfg.t_eff);
+      if (nd.whist) wide_hist_add(L.whist, l, lmax, a2);
+    }
   }
   if (tid == 0) a.stats[slot] = bs;
+  if (nd.whist) {
+    __syncthreads();
+    WideStat* ws = a.wstat + slot;
+    if (tid < kWideBins) ws->hist[tid] = L.whist[tid];
+    if (tid == 0) {
+      ws->ms = finitef_(lmax) ? lmax / cfg.t_eff : lmax;
+      ws->valid = 1u;
+    }
+  }
 }
 
 // Raw logits of load j as floats.
@@ -2936,13 +2978,17 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
     if (prefix <= kKeyNegInf) flag = 1u;
   }
   if (lane == 0u) { L.wmax[wid] = wm; L.wkey[wid] = tkey; L.wflag[wid] = flag; }
+  if (nd.whist && tid < kWideBins) L.whist[tid] = 0.f;
   __syncthreads();
   float m = L.wmax[0];
   uint32_t tk = L.wkey[0];
   uint32_t rare = L.wflag[0];
   #pragma unroll
   for (int w = 1; w < NT / 64; ++w) { m = fmaxf(m, L.wmax[w]); tk = min(tk, L.wkey[w]); rare |= L.wflag[w]; }
-  if (!finitef_(m) || ((nd.ieee || nd.fin) && m == 0.f)) rare = 1u;
+  // a chunk with no finite logit is fine for a row that only needs its
+  // scaled logits and mass (a top-p row's masked-out or short chunk)
+  const bool empty_ok = m == -__builtin_inff() && !nd.sel && !nd.ieee && !nd.fin && !nd.lse;
+  if ((!finitef_(m) && !empty_ok) || ((nd.ieee || nd.fin) && m == 0.f)) rare = 1u;
   if (rare) return false;
   // candidates need t = the bound; an argmax alone needs the ties of m
   const float t = nd.sel ? okey_inv(tk) : m;
@@ -2968,6 +3014,7 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
         }
       }
       if (nd.lse) rest += v < t ? __builtin_amdgcn_exp2f((v - m) * a2) : 0.f;
+      if (nd.whist) wide_hist_add(L.whist, v, m, a2);
     }
     if (cfg.store_s) {
       float svl[EPL];
@@ -3000,6 +3047,7 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
       }
     }
     if (nd.lse) rest += v < t ? __builtin_amdgcn_exp2f((v - m) * a2) : 0.f;
+    if (nd.whist) wide_hist_add(L.whist, v, m, a2);
     if (cfg.store_s && (uint32_t)(i * NT + tid) < in.n_ob)
       a.ws_s[(int64_t)row * a.V + in.obi[i]] = finitef_(v) ? v / cfg.t_eff : -__builtin_inff();
   }
@@ -3063,7 +3111,7 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
     ChunkStat bs;
     stat_init(bs);
     bs.max_l = m;
-    bs.any_finite = 1u;
+    bs.any_finite = finitef_(m) ? 1u : 0u;
     if (nd.sel) {
       bs.n_cand = wpos;
       bs.trunc = (uint32_t)len > k ? 1u : 0u;
@@ -3075,6 +3123,14 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
     if (nd.ieee) { bs.am_ieee_v = m; bs.am_ieee_i = cand_idx(best); }
     if (nd.fin) { bs.am_fin_v = m; bs.am_fin_i = (uint32_t)finb; }
     a.stats[slot] = bs;
+  }
+  if (nd.whist) {
+    WideStat* ws = a.wstat + slot;
+    if (lane < (uint32_t)kWideBins) ws->hist[lane] = L.whist[lane];
+    if (lane == 0u) {
+      ws->ms = m / cfg.t_eff;
+      ws->valid = 1u;
+    }
   }
   return true;
 }
@@ -3175,10 +3231,32 @@ __device__ __forceinline__ void select_chunk(const SampleArgs& a, int row, int c
 }
 
 // The streaming select pass: workgroup (chunk, row).
+__device__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg);
+
 template <int DT, int NL, bool MASK>
 __global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  select_chunk<DT, NL, MASK>(a, blockIdx.y, blockIdx.x, lds_raw);
+  const int row = blockIdx.y;
+  select_chunk<DT, NL, MASK>(a, row, blockIdx.x, lds_raw);
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  if (cfg.cls != kTopP) return;
+  // top-p rows: the last workgroup of the row merges the chunks' maxima and
+  // mass histograms for the wide pass (as select_finish_kernel's counter)
+  SelLds& L = *reinterpret_cast<SelLds*>(lds_raw);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  uint32_t* counter = a.done + row;
+  if (threadIdx.x == 0) {
+    __threadfence();
+    L.wflag[0] = atomicAdd(counter, 1u) == (uint32_t)(a.n_chunks - 1) ? 1u : 0u;
+    if (L.wflag[0]) {
+      __threadfence();
+      *counter = 0u;
+    }
+  }
+  __syncthreads();
+  if (L.wflag[0] == 0u) return;
+  wide_row_prepare(L, a, row, cfg);
 }
 
 // The streaming select pass and the finish in one launch, for small
@@ -3256,6 +3334,627 @@ __global__ void __launch_bounds__(NT) finish_kernel(SampleArgs a) {
   if (finish_lean(fs, a, row, cfg)) return;
   __syncthreads();
   finish_row(fs, a, row, cfg);
+}
+
+// ==========================================================================
+// Wide pass: top-p rows without a top-k bound (gpu.rs:820-899 with
+// top_k unset), chunk-parallel
+// ==========================================================================
+//
+// The reference walks such a row's whole rank order with three sequential
+// f32 folds: the normaliser over every weight in vocabulary order
+// (gpu.rs:837), then cum_p += w / total in rank order up to the cutoff
+// (:843-856), then the candidate total and the inverse CDF (:874-899).  Here
+// the select pass leaves the scaled logits s in ws_s and a mass histogram
+// per chunk (WideStat); then one workgroup per (chunk, row):
+//   1. merges the row's chunk maxima (M) and histograms: a conservative
+//      weight bound w_lo such that the weights >= w_lo hold at least
+//      cutoff + kWideMargin of the mass (every weight of the nucleus is
+//      >= w_lo unless the f32 folds differ from exact sums by more than the
+//      margin, which the finish detects), and the predicted sum before the
+//      chunk;
+//   2. computes its weights w = expf(s - M) exactly (min-p zeros them),
+//      plans its part of the vocabulary-order fold (fold_plan: segments of
+//      one predicted binade and boundary terms) and writes the plan;
+//   3. counts its weights >= w_lo by distinct value in an LDS hash: the
+//      rank order only needs each distinct weight's multiplicity (equal
+//      weights rank by index, and the folds do not see indices);
+//   4. bumps the row's counter; the last workgroup finishes the row:
+//      chains the chunk plans into the exact normaliser (refolding a chunk
+//      whose prediction missed), merges the chunks' runs, sorts them
+//      (weight descending), folds cum_p, the candidate total and the CDF
+//      over the runs with the closed forms for equal terms, and finds the
+//      drawn index among the equal weights of the drawn run.
+// Rows whose chunks took the select pass's exact path, whose tables
+// overflow, or whose nucleus is not inside the superset take finish_row.
+
+constexpr float kWideMargin = 0.005f;  // extra probability mass of the superset
+constexpr int kWideChunkHash = 2048;   // distinct superset weights per chunk
+constexpr int kWideFinHash = 2048;     // distinct superset weights per row
+constexpr int kWideRunCap = kWideFinHash;
+constexpr int kWideBatch = 64;         // chunk plans the chain holds in LDS at a time
+constexpr int kWideGBins = 64;         // threshold bins (binades of w below M)
+
+// LDS of a (chunk, row) workgroup; the chunk's weights and fold binades
+// follow at wide_w_off / wide_pe_off.
+struct WideChunkLds {
+  fold::WgLds<NT> fl;
+  uint32_t hkey[kWideChunkHash];
+  uint32_t hcnt[kWideChunkHash];
+  uint32_t hmin[kWideChunkHash];
+  uint32_t nrun, ovf, last;
+};
+constexpr size_t kWideChunkHead = (sizeof(WideChunkLds) + 15) & ~(size_t)15;
+// Weights sit in LDS with one pad word per 16, so that threads reading
+// their own 16 consecutive terms hit distinct banks.
+__host__ __device__ inline int wide_pad(int i) { return i + (i >> 4); }
+__host__ __device__ inline size_t wide_w_bytes(int chunk) { return (size_t)wide_pad(chunk) * 4 + 16; }
+__host__ __device__ inline size_t wide_w_off(int) { return kWideChunkHead; }
+__host__ __device__ inline size_t wide_pe_off(int chunk) { return kWideChunkHead + wide_w_bytes(chunk); }
+__host__ __device__ inline size_t wide_chunk_lds(int chunk) { return wide_pe_off(chunk) + (size_t)chunk + 16; }
+
+// LDS of the row finish.  Its phases reuse one union: the chain (chunk
+// plans, and the refold arrays past them), the merge (hash table and sort
+// keys), the draw (runs in rank order and the fold values before them).
+struct WideFinLds {
+  fold::WgLds<NT> fl;
+  union {
+    struct {
+      ChunkFold batch[kWideBatch];
+    } ch;
+    struct {
+      uint32_t hkey[kWideFinHash];
+      uint32_t hcnt[kWideFinHash];
+      uint32_t hmin[kWideFinHash];
+      uint64_t sortk[kWideRunCap];
+    } mg;
+    struct {
+      float rx[kWideRunCap];   // weight of run r (rank order)
+      uint32_t rm[kWideRunCap];  // its multiplicity
+      uint32_t ri[kWideRunCap];  // its smallest index
+      float st[kWideRunCap];   // cum_p before run r
+      float st2[kWideRunCap];  // candidate weight sum before run r
+    } fo;
+    uint32_t cntc[kWideRunCap];  // the drawn weight's multiplicity per chunk
+  } u;
+  uint8_t pe[kWideRunCap + 4];
+  uint32_t noff[NT + 1];
+  uint32_t cnt, fail_c, rsel, csel, tok;
+  float acc;
+};
+// The refold arrays (weights, then fold binades) start after the chain's
+// plans, inside or past the union.
+__host__ __device__ inline size_t wide_fin_w_off() {
+  return (offsetof(WideFinLds, u) + sizeof(ChunkFold) * kWideBatch + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t wide_fin_lds(int chunk) {
+  const size_t r = wide_fin_w_off() + wide_w_bytes(chunk) + (size_t)chunk + 16;
+  return r > sizeof(WideFinLds) ? r : sizeof(WideFinLds);
+}
+
+__device__ __forceinline__ uint32_t wide_hash(uint32_t key, int log2n) {
+  return (key * 0x9E3779B1u) >> (32 - log2n);
+}
+
+// Inserts `count` copies of weight bits `key` with smallest index `idx`
+// into an LDS table of 2^log2n slots (key 0 = empty; weights here are > 0).
+// Returns false when the table is full.
+__device__ __forceinline__ bool wide_insert(uint32_t* hkey, uint32_t* hcnt, uint32_t* hmin, int log2n,
+                                            uint32_t key, uint32_t count, uint32_t idx) {
+  const uint32_t mask = (1u << log2n) - 1u;
+  uint32_t h = wide_hash(key, log2n);
+  for (uint32_t probe = 0; probe <= mask; ++probe, h = (h + 1u) & mask) {
+    const uint32_t old = atomicCAS(&hkey[h], 0u, key);
+    if (old == 0u || old == key) {
+      atomicAdd(&hcnt[h], count);
+      atomicMin(&hmin[h], idx);
+      return true;
+    }
+  }
+  return false;
+}
+
+// Step 1, once per top-p row, by the select pass's last workgroup of the
+// row: M, the superset bound w_lo and the predicted fold value before each
+// chunk (WideRow, WideStat::pred).  The masses use approximate exp; they
+// only size the superset and predict binades.
+__device__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg) {
+  const int tid = threadIdx.x;
+  const int nch = a.n_chunks;
+  const ChunkStat* stats = a.stats + (int64_t)row * nch;
+  WideStat* wst = a.wstat + (int64_t)row * nch;
+  uint32_t mk = 0u, bad = 0u;
+  for (int c = tid; c < nch; c += NT) {
+    mk = max(mk, okey(stats[c].max_l));
+    bad |= wst[c].valid ^ 1u;
+  }
+  unsigned long long* gmass = reinterpret_cast<unsigned long long*>(L.surv[0]);  // kWideGBins entries
+  if (tid < kWideGBins) gmass[tid] = 0ull;
+  mk = block_max_u32<NT>(mk, L.redu);
+  bad = block_max_u32<NT>(bad, L.redu);
+  const float ml = okey_inv(mk);
+  const float M = finitef_(ml) ? ml / cfg.t_eff : -__builtin_inff();
+  WideRow* wr = a.wrow + row;
+  if (!finitef_(M) || bad) {
+    if (tid == 0) { wr->valid = 0u; wr->M = M; wr->w_lo = 0.f; }
+    return;
+  }
+  // chunk masses relative to M: in fixed point per binade of their lower
+  // end (for w_lo), and in double per chunk (for the predictions)
+  double* cmass = reinterpret_cast<double*>(L.surv[1]);  // up to kSurvCap chunks at a time
+  double S = 0.0;  // thread 0: the running prediction
+  for (int cb = 0; cb < nch; cb += kSurvCap) {
+    const int nb = min(kSurvCap, nch - cb);
+    for (int i = tid; i < nb; i += NT) {
+      const WideStat& ws = wst[cb + i];
+      const float lb = (M - ws.ms) * 1.4426950408889634f;  // log2 of M's weight over the chunk max's
+      const float r = __builtin_amdgcn_exp2f(-lb);
+      double cm = 0.0;
+      for (int j = 0; j < kWideBins; ++j) {
+        const float m = ws.hist[j] * r;
+        if (!(m > 0.f)) continue;
+        cm += (double)m;
+        int g = j == kWideBins - 1 ? kWideGBins - 1 : (int)floorf((float)(j + 1) + lb);
+        g = g < kWideGBins ? g : kWideGBins - 1;
+        atomicAdd(&gmass[g], (unsigned long long)((double)m * 4294967296.0));
+      }
+      cmass[i] = cm;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int i = 0; i < nb; ++i) {
+        wst[cb + i].pred = S;
+        S += cmass[i];
+      }
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    unsigned long long tot = 0ull;
+    for (int g = 0; g < kWideGBins; ++g) tot += gmass[g];
+    const double frac = (double)cfg.cutoff + (double)kWideMargin;
+    float w_lo = 0.f;
+    if (cfg.cutoff < 1.f && frac < 1.0) {
+      const unsigned long long target = (unsigned long long)(frac * (double)tot);
+      unsigned long long cum = 0ull;
+      for (int g = 0; g < kWideGBins - 1; ++g) {
+        cum += gmass[g];
+        if (cum >= target) { w_lo = __builtin_ldexpf(1.f, -(g + 1)); break; }
+      }
+    }
+    wr->w_lo = fmaxf(w_lo, cfg.min_p);
+    wr->M = M;
+    wr->valid = 1u;
+  }
+}
+
+// Steps 2-3 for one (chunk, row), with the row's M, w_lo and the chunk's
+// predicted start S.
+__device__ void wide_chunk_work(WideChunkLds& L, unsigned char* lds_raw, const SampleArgs& a, int row, int chunk,
+                                const RowCfg& cfg, float M, float w_lo, double S) {
+  const int tid = threadIdx.x;
+  const int c0 = chunk * a.chunk;
+  const int len = min(a.chunk, a.V - c0);
+  float* w = reinterpret_cast<float*>(lds_raw + wide_w_off(a.chunk));
+  uint8_t* pe = lds_raw + wide_pe_off(a.chunk);
+  const float* srow = a.ws_s + (int64_t)row * a.V + c0;
+  for (int i = tid; i < len; i += NT) {
+    const float x = exact_expf(srow[i] - M);
+    w[wide_pad(i)] = x < cfg.min_p ? 0.f : x;  // min-p: excluded like a zero weight
+  }
+  for (int h = tid; h < kWideChunkHash; h += NT) { L.hkey[h] = 0u; L.hcnt[h] = 0u; L.hmin[h] = 0xffffffffu; }
+  if (tid == 0) { L.nrun = 0u; L.ovf = 0u; }
+  __syncthreads();
+  // the chunk's part of the vocabulary-order fold: chunk 0 starts from
+  // the known -0.0 and folds exactly; the others plan from a predicted start
+  ChunkFold* cf = a.wfold + (int64_t)row * a.n_chunks + chunk;
+  auto tf = [&](int r) { return w[wide_pad(r)]; };
+  auto mf = [](int) { return 1u; };
+  if (chunk == 0) {
+    const float end = fold::fold_runs<NT>(L.fl, pe, len, -0.0f, tf, mf, [](int, float) {});
+    if (tid == 0) { cf->has_end = 1u; cf->end = end; cf->nseg = 1u; }
+  } else {
+    if (tid == 0) cf->has_end = 0u;
+    fold::fold_plan<NT, decltype(tf), decltype(mf), true>(L.fl, pe, 0, len, S, tf, mf);
+  }
+  const uint32_t nb = L.fl.nb;
+  const uint32_t nseg = nb + 1u;
+  if (chunk != 0 && tid < 64) {
+    const uint32_t k = (uint32_t)tid;
+    bool ne = false;
+    if (k < nseg && nseg <= (uint32_t)kFoldSegs) {
+      const int first = k == 0 ? 0 : (int)L.fl.bnd_run[k - 1] + 1;
+      const int last = k < nb ? (int)L.fl.bnd_run[k] - 1 : len - 1;
+      ne = first <= last;
+      cf->seg_e[k] = L.fl.seg_e[k];
+      cf->seg_map[k] = L.fl.seg_map[k];
+      cf->seg_alt[k] = L.fl.seg_alt[k];
+      if (k < nb) cf->bnd_x[k] = w[wide_pad((int)L.fl.bnd_run[k])];
+    }
+    const uint64_t nem = __ballot(ne);
+    if (tid == 0) {
+      cf->nseg = nseg <= (uint32_t)kFoldSegs ? nseg : 0u;
+      cf->nonempty = (uint32_t)nem;
+    }
+  }
+  // the superset's distinct weights
+  constexpr int kLog2 = 11;
+  static_assert((1 << kLog2) == kWideChunkHash, "hash size");
+  bool full = false;
+  for (int i = tid; i < len; i += NT) {
+    const float x = w[wide_pad(i)];
+    if (x > 0.f && x >= w_lo)
+      full |= !wide_insert(L.hkey, L.hcnt, L.hmin, kLog2, __float_as_uint(x), 1u, (uint32_t)i);
+  }
+  if (full) L.ovf = 1u;
+  __syncthreads();
+  uint64_t* out = a.ws_list + (int64_t)row * a.list_stride + (int64_t)chunk * a.chunk;
+  for (int h = tid; h < kWideChunkHash; h += NT) {
+    const uint32_t k = L.hkey[h];
+    if (k != 0u) {
+      const uint32_t p = atomicAdd(&L.nrun, 1u);
+      out[p] = ((uint64_t)k << 32) | ((uint64_t)L.hcnt[h] << 16) | (uint64_t)L.hmin[h];
+    }
+  }
+  __syncthreads();
+  if (tid == 0) cf->nruns = L.ovf ? kFoldNone : L.nrun;
+}
+
+// The exact fold value after chunk c's weights, from `acc` before them:
+// reads the chunk's scaled logits again (the chain's fallback when the
+// chunk's predicted binades missed).  All threads call it.
+__device__ float wide_refold(WideFinLds& F, unsigned char* lds_raw, const SampleArgs& a, int row, int c, float M,
+                             const RowCfg& cfg, float acc) {
+  const int c0 = c * a.chunk;
+  const int len = min(a.chunk, a.V - c0);
+  float* w = reinterpret_cast<float*>(lds_raw + wide_fin_w_off());
+  uint8_t* pe = lds_raw + wide_fin_w_off() + wide_w_bytes(a.chunk);
+  const float* srow = a.ws_s + (int64_t)row * a.V + c0;
+  for (int i = threadIdx.x; i < len; i += NT) {
+    const float x = exact_expf(srow[i] - M);
+    w[wide_pad(i)] = x < cfg.min_p ? 0.f : x;
+  }
+  __syncthreads();
+  return fold::fold_runs<NT>(F.fl, pe, len, acc, [&](int r) { return w[wide_pad(r)]; }, [](int) { return 1u; },
+                             [](int, float) {});
+}
+
+// Calls f(c, e) for every superset run entry e of chunk c of `row`, in
+// parallel: chunks in blocks of NT, their run counts scanned into offsets.
+template <typename F>
+__device__ __forceinline__ void wide_for_each_run(WideFinLds& W, const SampleArgs& a, int row, F f) {
+  const int tid = threadIdx.x;
+  const int nch = a.n_chunks;
+  const ChunkFold* folds = a.wfold + (int64_t)row * nch;
+  for (int cb = 0; cb < nch; cb += NT) {
+    const int c = cb + tid;
+    const uint32_t n = c < nch ? folds[c].nruns : 0u;
+    uint32_t tot;
+    const uint32_t off = block_excl_scan_u32<NT>(n, W.fl.wcnt, &tot);
+    W.noff[tid] = off;
+    if (tid == 0) W.noff[NT] = tot;
+    __syncthreads();
+    for (uint32_t p = (uint32_t)tid; p < tot; p += NT) {
+      int lo = 0, hi = NT - 1;  // the last block whose offset is <= p
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (W.noff[mid] <= p) lo = mid; else hi = mid - 1;
+      }
+      const uint64_t* src = a.ws_list + (int64_t)row * a.list_stride + (int64_t)(cb + lo) * a.chunk;
+      f(cb + lo, src[p - W.noff[lo]]);
+    }
+    __syncthreads();
+  }
+}
+
+// Step 4: the row finish by the last workgroup.  Returns the token, or
+// 0xffffffff when the row must take finish_row (nothing written); `path`
+// gets the WidePath code.
+__device__ uint32_t wide_finish(unsigned char* lds_raw, const SampleArgs& a, int row, const RowCfg& cfg, float M,
+                                float w_lo, uint32_t& path) {
+  WideFinLds& F = *reinterpret_cast<WideFinLds*>(lds_raw);
+  const int tid = threadIdx.x;
+  const int nch = a.n_chunks;
+  const ChunkFold* folds = a.wfold + (int64_t)row * nch;
+
+  // a. the normaliser: the chunk plans chained in vocabulary order
+  //    (Rust's Sum folds from -0.0)
+  float acc = -0.0f;
+  bool ovf = false;
+  for (int cb = 0; cb < nch; cb += kWideBatch) {
+    const int nb = min(kWideBatch, nch - cb);
+    {
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(folds + cb);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(F.u.ch.batch);
+      const int words = nb * (int)(sizeof(ChunkFold) / 4);
+      for (int i = tid; i < words; i += NT) dst[i] = src[i];
+    }
+    __syncthreads();
+    for (int i = tid; i < nb; i += NT)
+      if (F.u.ch.batch[i].nruns == kFoldNone) ovf = true;
+    int c = cb;
+    while (c < cb + nb) {
+      if (tid == 0) {
+        float x = acc;
+        uint32_t fail = 0xffffffffu;
+        for (int cc = c; cc < cb + nb; ++cc) {
+          const ChunkFold& cf = F.u.ch.batch[cc - cb];
+          if (cf.has_end) { x = cf.end; continue; }  // chunk 0, from -0.0
+          if (cf.nseg == 0u) { fail = (uint32_t)cc; break; }
+          float y = x;
+          bool ok = true;
+          for (uint32_t k = 0; k < cf.nseg; ++k) {
+            if ((cf.nonempty >> k) & 1u) {
+              const int e = (int)cf.seg_e[k];
+              const int ey = fold::binade(y);
+              const uint32_t A = fold::to_A(y);
+              // in the predicted binade, or (a start that lags the
+              // prediction) in the one below
+              const fold::Map mp = ey == e ? cf.seg_map[k] : cf.seg_alt[k];
+              const uint32_t t = fold::apply(mp, A & 1u);
+              if ((ey != e && (ey != e - 1 || e <= 1)) || (uint64_t)A + t >= fold::kTop) { ok = false; break; }
+              y = fold::from_A(A + t, ey);
+            }
+            if (k + 1u < cf.nseg) y = fold::fadd(y, cf.bnd_x[k]);
+          }
+          if (!ok) { fail = (uint32_t)cc; break; }
+          x = y;
+        }
+        F.acc = x;
+        F.fail_c = fail;
+      }
+      __syncthreads();
+      acc = F.acc;
+      const uint32_t fail = F.fail_c;
+      __syncthreads();
+      if (fail == 0xffffffffu) break;
+      acc = wide_refold(F, lds_raw, a, row, (int)fail, M, cfg, acc);
+      c = (int)fail + 1;
+    }
+    __syncthreads();
+  }
+  ovf = __syncthreads_or(ovf);
+  const float total = acc;
+  path = kWideTotal;
+  if (!(total > 0.f) || !finitef_(total)) return 0xffffffffu;  // argmax_host fallback (finish_row)
+  path = kWideChunkFull;
+  if (ovf) return 0xffffffffu;
+  path = kWideMergeFull;
+
+  // c. merge the chunks' runs by weight
+  constexpr int kLog2 = 11;
+  static_assert((1 << kLog2) == kWideFinHash, "hash size");
+  for (int h = tid; h < kWideFinHash; h += NT) {
+    F.u.mg.hkey[h] = 0u;
+    F.u.mg.hcnt[h] = 0u;
+    F.u.mg.hmin[h] = 0xffffffffu;
+  }
+  if (tid == 0) F.cnt = 0u;
+  __syncthreads();
+  bool full = false;
+  wide_for_each_run(F, a, row, [&](int c, uint64_t e) {
+    full |= !wide_insert(F.u.mg.hkey, F.u.mg.hcnt, F.u.mg.hmin, kLog2, (uint32_t)(e >> 32),
+                         (uint32_t)(e >> 16) & 0xffffu, (uint32_t)(c * a.chunk) + ((uint32_t)e & 0xffffu));
+  });
+  if (__syncthreads_or(full)) return 0xffffffffu;
+  path = kWideDrawFail;
+  // d. distinct weights, descending
+  for (int h = tid; h < kWideFinHash; h += NT) {
+    const uint32_t k = F.u.mg.hkey[h];
+    if (k != 0u) F.u.mg.sortk[atomicAdd(&F.cnt, 1u)] = ((uint64_t)k << 32) | (uint64_t)h;
+  }
+  __syncthreads();
+  const int R = (int)F.cnt;
+  if (R == 0) return 0xffffffffu;
+  {
+    const int n2 = next_pow2(R);
+    for (int i = R + tid; i < n2; i += NT) F.u.mg.sortk[i] = 0ull;
+    __syncthreads();
+    for (int k = 2; k <= n2; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < n2; i += NT) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const uint64_t x = F.u.mg.sortk[i], y = F.u.mg.sortk[ixj];
+            const bool desc = (i & k) == 0;
+            if (desc ? (x < y) : (x > y)) { F.u.mg.sortk[i] = y; F.u.mg.sortk[ixj] = x; }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+  {
+    // runs in rank order: read everything first, the arrays overlap
+    constexpr int kPer = kWideRunCap / NT;
+    float rx[kPer];
+    uint32_t rm[kPer], ri[kPer];
+    #pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int r = q * NT + tid;
+      if (r < R) {
+        const uint64_t k = F.u.mg.sortk[r];
+        const uint32_t h = (uint32_t)k;
+        rx[q] = __uint_as_float((uint32_t)(k >> 32));
+        rm[q] = F.u.mg.hcnt[h];
+        ri[q] = F.u.mg.hmin[h];
+      }
+    }
+    __syncthreads();
+    #pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int r = q * NT + tid;
+      if (r < R) { F.u.fo.rx[r] = rx[q]; F.u.fo.rm[r] = rm[q]; F.u.fo.ri[r] = ri[q]; }
+    }
+    __syncthreads();
+  }
+
+  // e. cum_p += w / total in rank order (from 0.0), up to the cutoff
+  auto q_of = [&](int r) { return F.u.fo.rx[r] / total; };
+  auto m_of = [&](int r) { return F.u.fo.rm[r]; };
+  const float cum_end = fold::fold_runs<NT>(F.fl, F.pe, R, 0.0f, q_of, m_of,
+                                            [&](int r, float v) { F.u.fo.st[r] = v; });
+  __syncthreads();
+  int rstar = R - 1;
+  uint32_t cstar = F.u.fo.rm[R - 1];
+  if (cfg.cutoff < 1.f) {
+    uint32_t first = 0xffffffffu;
+    for (int r = tid; r < R; r += NT) {
+      const float end = r + 1 < R ? F.u.fo.st[r + 1] : cum_end;
+      if (end >= cfg.cutoff) first = min(first, (uint32_t)r);
+    }
+    first = ~block_max_u32<NT>(~first, F.fl.wcnt);
+    if (first == 0xffffffffu) {
+      // the cutoff is not reached inside the superset: that is the whole
+      // nucleus only when the superset holds every positive weight
+      if (w_lo > cfg.min_p) {
+        path = kWideNoCutoff;
+        return 0xffffffffu;
+      }
+    } else {
+      rstar = (int)first;
+      cstar = fold::run_find<false>(F.u.fo.st[rstar], q_of(rstar), F.u.fo.rm[rstar], cfg.cutoff, nullptr);
+      if (cstar == fold::kNone) return 0xffffffffu;
+    }
+  }
+  // f. the candidate total: the weights of the ranks before m_end (from -0.0)
+  auto m2_of = [&](int r) { return r == rstar ? cstar : F.u.fo.rm[r]; };
+  const float ct = fold::fold_runs<NT>(F.fl, F.pe, rstar + 1, -0.0f, [&](int r) { return F.u.fo.rx[r]; }, m2_of,
+                                       [&](int r, float v) { F.u.fo.st2[r] = v; });
+  __syncthreads();
+  if (!(ct > 0.f) || !finitef_(ct)) return 0xffffffffu;
+  // g. the inverse CDF: the first rank whose running weight passes target
+  const float target = clamp_uniform(cfg.u) * ct;
+  uint32_t pr = 0xffffffffu;
+  for (int r = tid; r <= rstar; r += NT) {
+    const float end = r < rstar ? F.u.fo.st2[r + 1] : ct;
+    if (target < end) pr = min(pr, (uint32_t)r);
+  }
+  pr = ~block_max_u32<NT>(~pr, F.fl.wcnt);
+  int rp = rstar;
+  uint32_t cp = cstar;  // gpu.rs:899: the last candidate
+  if (pr != 0xffffffffu) {
+    const uint32_t c = fold::run_find<true>(F.u.fo.st2[pr], F.u.fo.rx[pr], m2_of((int)pr), target, nullptr);
+    if (c != fold::kNone) { rp = (int)pr; cp = c; }
+  }
+  // h. the drawn index: the cp-th smallest index among the weights equal
+  //    to the run's (equal weights rank by index)
+  const uint32_t first_idx = F.u.fo.ri[rp];
+  path = kWideDone;
+  if (cp == 1u) return first_idx;
+  const uint32_t key = __float_as_uint(F.u.fo.rx[rp]);
+  __syncthreads();
+  for (int c = tid; c < kWideRunCap; c += NT) F.u.cntc[c] = 0u;
+  __syncthreads();
+  if (nch > kWideRunCap) {
+    path = kWideDrawFail;
+    return 0xffffffffu;
+  }
+  wide_for_each_run(F, a, row, [&](int c, uint64_t e) {
+    if ((uint32_t)(e >> 32) == key) F.u.cntc[c] = (uint32_t)(e >> 16) & 0xffffu;
+  });
+  if (tid == 0) {
+    uint32_t seen = 0u;
+    F.csel = 0xffffffffu;
+    for (int c = 0; c < nch; ++c) {
+      const uint32_t k = F.u.cntc[c];
+      if (k != 0u && seen + k >= cp) { F.csel = (uint32_t)c; F.rsel = cp - seen; break; }
+      seen += k;
+    }
+    F.tok = 0xffffffffu;
+    F.cnt = 0u;
+  }
+  __syncthreads();
+  const uint32_t csel = F.csel, want = F.rsel;
+  if (csel == 0xffffffffu) {
+    path = kWideDrawFail;
+    return 0xffffffffu;
+  }
+  // the want-th weight equal to key in chunk csel, in index order
+  const int c0 = (int)csel * a.chunk;
+  const int len = min(a.chunk, a.V - c0);
+  const float* srow = a.ws_s + (int64_t)row * a.V + c0;
+  const uint32_t wid = (uint32_t)tid >> 6;
+  for (int base = 0; base < len; base += NT) {
+    const int i = base + tid;
+    bool eq = false;
+    if (i < len) {
+      float x = exact_expf(srow[i] - M);
+      x = x < cfg.min_p ? 0.f : x;
+      eq = __float_as_uint(x) == key;
+    }
+    const uint64_t bm = __ballot(eq);
+    if ((tid & 63) == 0) F.fl.wcnt[wid] = (uint32_t)__popcll(bm);
+    __syncthreads();
+    uint32_t before = F.cnt;
+    for (uint32_t v = 0; v < wid; ++v) before += F.fl.wcnt[v];
+    if (eq && before + lanes_below(bm) + 1u == want) F.tok = (uint32_t)(c0 + i);
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t s = 0u;
+      for (int v = 0; v < NT / 64; ++v) s += F.fl.wcnt[v];
+      F.cnt += s;
+    }
+    __syncthreads();
+    if (F.tok != 0xffffffffu) break;
+  }
+  if (F.tok == 0xffffffffu) path = kWideDrawFail;
+  return F.tok;
+}
+
+// The second kernel of the chunked path: grid (chunks, rows).  Top-p rows
+// take the wide pass on every chunk; every other row is finished by its
+// chunk-0 workgroup (finish_lean, else finish_row).
+__global__ void __launch_bounds__(NT) finish_grid_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int chunk = blockIdx.x, row = blockIdx.y;
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  if (cfg.cls != kTopP) {
+    if (chunk != 0) return;
+    FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
+    if (finish_lean(fs, a, row, cfg)) return;
+    __syncthreads();
+    finish_row(fs, a, row, cfg);
+    return;
+  }
+  WideChunkLds& L = *reinterpret_cast<WideChunkLds*>(lds_raw);
+  const WideRow wr = a.wrow[row];
+  const bool valid = wr.valid != 0u;
+  const float M = wr.M, w_lo = wr.w_lo;
+  if (valid) wide_chunk_work(L, lds_raw, a, row, chunk, cfg, M, w_lo, a.wstat[(int64_t)row * a.n_chunks + chunk].pred);
+  // the last workgroup of the row finishes it (as select_finish_kernel)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  uint32_t* counter = a.done + row;
+  if (threadIdx.x == 0) {
+    __threadfence();
+    L.last = atomicAdd(counter, 1u) == (uint32_t)(a.n_chunks - 1) ? 1u : 0u;
+    if (L.last) {
+      __threadfence();
+      *counter = 0u;
+    }
+  }
+  __syncthreads();
+  if (L.last == 0u) return;
+  uint32_t token = 0xffffffffu;
+  uint32_t path = kWideNoStats;
+  if (valid) token = wide_finish(lds_raw, a, row, cfg, M, w_lo, path);
+  if (threadIdx.x == 0) a.diag[row] = path;
+  __syncthreads();
+  FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
+  if (token == 0xffffffffu) {
+    finish_row(fs, a, row, cfg);
+    return;
+  }
+  if (threadIdx.x == 0) a.out_tokens[row] = token;
+  if (a.n_lp > 0 || a.out_token_lp) finish_logprobs(fs, a, row, cfg, token, M, false, 0);
+}
+
+size_t finish_grid_lds(int chunk) {
+  size_t b = sizeof(FinLds);
+  b = b > wide_chunk_lds(chunk) ? b : wide_chunk_lds(chunk);
+  b = b > wide_fin_lds(chunk) ? b : wide_fin_lds(chunk);
+  return (b + 15) & ~(size_t)15;
 }
 
 // ==========================================================================
@@ -4023,6 +4722,22 @@ int choose_chunk(int B, int V, int n_lp, int vec_ok, bool hist) {
   return wg_large >= 512 ? kChunk : kChunkSmall;
 }
 
+// Raises a kernel's dynamic LDS limit to at least `bytes` on the current
+// device (once per device and size; the attribute is per device).
+hipError_t ensure_lds(const void* fn, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& have = done[{fn, dev}];
+  if (have >= bytes) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess) have = bytes;
+  return e;
+}
+
 hipError_t record(const LaunchEvents* le, int i, hipStream_t stream) {
   return le ? hipEventRecord(le->ev[i], stream) : hipSuccess;
 }
@@ -4065,13 +4780,8 @@ hipError_t launch_fused_t(const SampleArgs& a, hipStream_t stream) {
   size_t body = sel > sizeof(FinLds) ? sel : sizeof(FinLds);
   body = (body + 15) & ~(size_t)15;
   const size_t lds = body + 16;
-  static size_t attr = 0;  // largest dynamic LDS size set so far
-  if (lds > attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)select_finish_kernel<DT, NL, MASK>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr = lds;
-  }
+  hipError_t e = ensure_lds((const void*)select_finish_kernel<DT, NL, MASK>, lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((select_finish_kernel<DT, NL, MASK>), dim3(a.n_chunks, a.B), dim3(NT), lds, stream, a,
                      (uint32_t)body);
   return hipGetLastError();
@@ -4094,13 +4804,8 @@ hipError_t launch_select_d(const SampleArgs& a, hipStream_t stream) {
 template <bool MASK>
 hipError_t launch_rows(const SampleArgs& a, hipStream_t stream) {
   const size_t lds = row_lds_bytes(a.V);
-  static size_t attr = 0;  // largest dynamic LDS size set so far
-  if (lds > attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)row_kernel<MASK>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return e;
-    attr = lds;
-  }
+  hipError_t e = ensure_lds((const void*)row_kernel<MASK>, lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(row_kernel<MASK>, dim3(a.B), dim3(kRowThreads), lds, stream, a.logits, a.row_stride, a.V, a);
   return hipGetLastError();
 }
@@ -4129,7 +4834,10 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t stream, const LaunchEv
     e = a.mask ? launch_select_d<HI_ROCM_DTYPE_F32, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_F32, false>(a, stream);
   if (e == hipSuccess) e = record(le, 1, stream);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(finish_kernel, dim3(a.B), dim3(NT), 0, stream, a);
+  const size_t lds = finish_grid_lds(a.chunk);
+  e = ensure_lds((const void*)finish_grid_kernel, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(finish_grid_kernel, dim3(a.n_chunks, a.B), dim3(NT), lds, stream, a);
   e = hipGetLastError();
   return e == hipSuccess ? record(le, 2, stream) : e;
 }
@@ -4147,8 +4855,7 @@ size_t debug_fold_lds(int R) { return sizeof(fold::WgLds<NT>) + (size_t)R + 1; }
 hipError_t launch_debug_fold(const float* x, const uint32_t* m, int R, float a0, float* out_start,
                              float* out_final, hipStream_t stream) {
   const size_t lds = debug_fold_lds(R);
-  hipError_t e = hipFuncSetAttribute((const void*)debug_fold_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)lds);
+  hipError_t e = ensure_lds((const void*)debug_fold_kernel, lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(debug_fold_kernel, dim3(1), dim3(NT), lds, stream, x, m, R, a0, out_start, out_final);
   return hipGetLastError();

@@ -223,6 +223,20 @@ class Sampler:
         return out
 
 
+WIDE_PATHS = {0: "other", 1: "wide", 2: "no-stats", 3: "chunk-full", 4: "total", 5: "merge-full",
+              6: "no-cutoff", 7: "draw-fail"}
+
+
+def debug_wide_paths(smp: "Sampler", batch: int, vocab: int,
+                     stream: Optional[torch.cuda.Stream] = None) -> np.ndarray:
+    """How the last ``smp.sample`` call finished each top-p row on the
+    chunked path (``hi_rocm_debug_wide_paths``; codes in WIDE_PATHS)."""
+    out = np.zeros(batch, np.uint32)
+    check(load().hi_rocm_debug_wide_paths(smp.workspace.data_ptr(), smp.workspace.numel(), batch, vocab,
+                                          out.ctypes.data, _stream_ptr(stream)))
+    return out
+
+
 def debug_distribution(logits: torch.Tensor, params: torch.Tensor,
                        hist_offsets=None, hist_ids=None, hist_counts=None, mask_words=None,
                        stream: Optional[torch.cuda.Stream] = None):
@@ -251,5 +265,5 @@ def debug_expf(x: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> t
 __all__ = [
     "RowSampling", "SamplerError", "HiRocmError", "Sampler", "row_params", "params_to_device",
     "argmax_batched_last_token", "sample_batched_last_token", "select_batched_last_token_per_row",
-    "sample_last_row_with_sample", "debug_distribution", "debug_expf",
+    "sample_last_row_with_sample", "debug_distribution", "debug_expf", "debug_wide_paths",
 ]

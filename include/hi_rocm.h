@@ -191,6 +191,15 @@ int hi_rocm_launch_dsv4_indexer_select(const void* scores, int n_blocks, int top
 int hi_rocm_debug_fold(const float* terms, const uint32_t* counts, int runs, float start,
                        float* out_start, float* out_final, void* stream);
 
+/* Debug export: how the last hi_rocm_sample call on this workspace
+ * finished each top-p row without a top-k bound on its chunked path
+ * (u32[batch] to host memory; blocking): 1 = the chunk-parallel wide pass,
+ * 2-7 = a named fallback to the general finish, 0 = not such a row.  The
+ * batch and vocab must be the call's; any stream, the null one included.
+ * No reference counterpart. */
+int hi_rocm_debug_wide_paths(const void* workspace, size_t workspace_bytes, int batch, int vocab,
+                             uint32_t* out_paths, void* stream);
+
 /* Debug export: y[i] = the device weight function exp(x[i]) for n floats
  * (device arrays).  Bit-identical to host glibc expf.  No reference
  * counterpart; the reference's closest check is crates/hi-cuda/src/

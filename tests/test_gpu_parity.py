@@ -43,7 +43,7 @@ def dev(x):
     return torch.from_numpy(x).to("cuda")
 
 
-def run_gpu(w: Workload, token_logprobs=True, repeat=1):
+def run_gpu(w: Workload, token_logprobs=True, repeat=1, paths=None):
     torch = _torch()
     from hi_amd import sampler as S
     logits = dev(w.logits)
@@ -60,6 +60,8 @@ def run_gpu(w: Workload, token_logprobs=True, repeat=1):
                          token_logprobs=token_logprobs)
         torch.cuda.synchronize()
         outs.append({k: v.cpu().numpy() for k, v in out.items()})
+    if paths is not None:
+        paths.append(S.debug_wide_paths(smp, w.batch, w.vocab))
     for o in outs:
         o["tokens"] = o["tokens"].view(np.uint32)
         if "logprob_ids" in o:
@@ -297,9 +299,20 @@ def test_reference_host_grid_per_row(hip, oracle):
 def test_config_parity(hip, oracle, cfg):
     w = CONFIGS[cfg]()
     say(f"config {cfg}: {w.name} B={w.batch} V={w.vocab}")
-    got = run_gpu(w)
+    paths = []
+    got = run_gpu(w, paths=paths)
     want = run_oracle(oracle, w)
     compare(w, got, want, w.name)
+    if cfg in (2, 5):
+        # every top-p row with a finite logit takes the chunk-parallel wide
+        # pass (not the general finish)
+        from hi_amd.sampler import WIDE_PATHS
+        topp = (w.params["temperature"] > 0) & (w.params["top_p"] < 1)
+        if w.mask_words is not None:
+            topp &= w.mask_words.any(axis=1)
+        got_paths = [WIDE_PATHS[int(p)] for p in paths[0][topp]]
+        say(f"wide paths: {dict(zip(*np.unique(got_paths, return_counts=True)))}")
+        assert all(p == "wide" for p in got_paths), got_paths
 
 
 def test_config3_deterministic(hip):

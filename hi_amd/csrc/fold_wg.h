@@ -89,7 +89,7 @@ __device__ __forceinline__ void run_maps(float x, uint32_t m, int e, Map& mp, Ma
 // binade below its predicted one (seg_alt), for a start value that lags
 // the prediction.  Ends with a barrier.
 template <int NTH, typename TermF, typename MultF, bool ALT = false>
-__device__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, int R, double base, TermF term, MultF mult) {
+__device__ __forceinline__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, int R, double base, TermF term, MultF mult) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   int r0, r1;
   block_of<NTH>(pos, R, r0, r1);
@@ -265,7 +265,7 @@ __device__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, int R, double bas
 // The chain from the exact value `a` before run pos (thread 0).  Ends with
 // a barrier; L.acc holds the value after the last applied part.
 template <int NTH, typename TermF, typename MultF>
-__device__ void fold_chain(WgLds<NTH>& L, int pos, int R, float a, TermF term, MultF mult) {
+__device__ __forceinline__ void fold_chain(WgLds<NTH>& L, int pos, int R, float a, TermF term, MultF mult) {
   if (threadIdx.x == 0) {
     const uint32_t nb = L.nb;
     uint32_t fail = nb + 1u, resume = (uint32_t)R;
@@ -300,7 +300,7 @@ __device__ void fold_chain(WgLds<NTH>& L, int pos, int R, float a, TermF term, M
 // out(r, v): the exact fold value v before run r, for every run the chain
 // applied.
 template <int NTH, typename TermF, typename MultF, typename OutF>
-__device__ void fold_emit(WgLds<NTH>& L, const uint8_t* pe, int pos, int R, TermF term, MultF mult, OutF out) {
+__device__ __forceinline__ void fold_emit(WgLds<NTH>& L, const uint8_t* pe, int pos, int R, TermF term, MultF mult, OutF out) {
   int r0, r1;
   block_of<NTH>(pos, R, r0, r1);
   const uint32_t fail = L.fail;
@@ -323,7 +323,7 @@ __device__ void fold_emit(WgLds<NTH>& L, const uint8_t* pe, int pos, int R, Term
 // The fold of runs [0, R) from a0; out(r, v) receives the value before each
 // run.  Returns the final value (uniform).  pe: LDS, R + 1 bytes.
 template <int NTH, typename TermF, typename MultF, typename OutF>
-__device__ float fold_runs(WgLds<NTH>& L, uint8_t* pe, int R, float a0, TermF term, MultF mult, OutF out) {
+__device__ __forceinline__ float fold_runs(WgLds<NTH>& L, uint8_t* pe, int R, float a0, TermF term, MultF mult, OutF out) {
   int pos = 0;
   float a = a0;
   while (pos < R) {

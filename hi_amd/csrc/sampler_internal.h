@@ -99,23 +99,19 @@ struct WideRow {
 };
 static_assert(sizeof(WideStat) == 144, "WideStat layout");
 
-// Per (row, chunk) result of the wide pass for a top-p row: the plan of the
-// chunk's part of the vocabulary-order weight fold (segments of one binade
-// and the boundary terms between them) and the number of distinct-weight
-// runs of the nucleus superset it wrote.
-constexpr int kFoldSegs = 12;
+// Per (row, chunk) result of the wide pass for a top-p row: the maps of
+// the chunk's weights in the vocabulary-order fold for a start value in
+// binade e0, e0 + 1 or e0 + 2 (exact while the sum stays in that binade),
+// and the number of distinct-weight runs of the nucleus superset it wrote.
 struct ChunkFold {
-  uint32_t nseg;             // segments; 0: the plan did not fit (the finish refolds the chunk)
-  uint32_t nonempty;         // bit k: segment k has terms
+  uint32_t e0;
   uint32_t nruns;            // superset runs written; kFoldNone: the chunk's table overflowed
   uint32_t has_end;          // chunk 0: `end` is the exact fold of its weights from -0.0
   float end;
-  uint32_t pad[3];
-  uint32_t seg_e[kFoldSegs];
-  fold::Map seg_map[kFoldSegs];
-  fold::Map seg_alt[kFoldSegs];  // the same terms in the binade below seg_e
-  float bnd_x[kFoldSegs];
+  fold::Map map[3];
+  uint32_t pad[2];
 };
+static_assert(sizeof(ChunkFold) == 48, "ChunkFold layout");
 constexpr uint32_t kFoldNone = 0xffffffffu;
 
 struct SampleArgs {

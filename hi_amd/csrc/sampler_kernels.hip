@@ -176,12 +176,15 @@ __device__ __forceinline__ RowCfg load_cfg(const ParamsView& pv, int row, int V,
   c.freq = finitef_(c.freq) ? c.freq : 0.f;
   c.pres = finitef_(c.pres) ? c.pres : 0.f;
   c.wide = c.cls == kTopK && c.k_eff > kLeanK;
-  c.k_sel = (c.cls == kTopK && !c.wide) ? max(c.k_eff, n_lp) : n_lp;
+  // top-k rows keep their top k as candidates in the streaming pass; beyond
+  // what the ranked finish holds (kBuf) they keep their scaled logits
+  const bool ranked_k = c.cls == kTopK && c.k_eff <= kBuf;
+  c.k_sel = ranked_k ? max(c.k_eff, n_lp) : n_lp;
   // Logprobs need the normaliser to ~1e-7 relative: its largest terms are
   // summed in double from the candidates, so every chunk keeps a few.
   if (need_lse) c.k_sel = max(c.k_sel, kLseTop);
   if (c.k_sel > V) c.k_sel = V;
-  c.store_s = c.cls == kTopP || c.cls == kTempOnly || c.wide;
+  c.store_s = c.cls == kTopP || c.cls == kTempOnly || (c.wide && !ranked_k);
   // Every caller's row is uniform over the workgroup: the float fields are
   // kept in scalar registers (as vector values they would hold vector
   // registers for the whole kernel, or be spilled to scratch memory)
@@ -635,6 +638,62 @@ __device__ __forceinline__ void sort_ranked(FinLds& fs, int n) {
   }
 }
 
+// Calls f(key) with the candidate key (processed-logit key, index) of every
+// logit of `row` this thread owns, recomputing the processed logits: tiles
+// of 2048 logits with an LDS count table of the row's history (cnt has
+// 2048 entries).  All threads call it.
+template <typename F>
+__device__ __forceinline__ void for_each_row_key(const SampleArgs& a, int row, const RowCfg& cfg, uint32_t* cnt,
+                                                 F f) {
+  constexpr int T = 2048;
+  const int tid = threadIdx.x;
+  uint32_t h0 = 0, h1 = 0;
+  if (a.hoff) { h0 = a.hoff[row]; h1 = a.hoff[row + 1]; }
+  const int64_t rbase = (int64_t)row * a.row_stride;
+  for (int t0 = 0; t0 < a.V; t0 += T) {
+    const int t1 = min(t0 + T, a.V);
+    __syncthreads();
+    for (int i = tid; i < T; i += NT) cnt[i] = 0u;
+    __syncthreads();
+    for (uint32_t h = h0 + tid; h < h1; h += NT) {
+      const uint32_t id = a.hids[h];
+      if (id >= (uint32_t)t0 && id < (uint32_t)t1) atomicAdd(&cnt[id - t0], a.hcnt[h]);
+    }
+    __syncthreads();
+    for (int e = t0 + tid; e < t1; e += NT) {
+      float l = load_raw(a.logits, a.dtype, rbase + e);
+      if (!allowed(a, row, (uint32_t)e)) l = -__builtin_inff();
+      l = apply_penalties(l, cnt[e - t0], cfg);
+      f(cand_key(lkey(l), (uint32_t)e));
+    }
+  }
+  __syncthreads();
+}
+
+// The exact top kk candidate keys of the whole row into fs.buf[0, kk),
+// from the logits themselves (for a row whose chunks' candidates may miss
+// part of its top kk).  Returns the kk-th key; *below gets the largest key
+// left out.
+__device__ __forceinline__ uint64_t row_select_exact(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg,
+                                                     int kk, uint64_t* below) {
+  const int tid = threadIdx.x;
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(fs.mass);
+  static_assert(sizeof(fs.mass) >= 2048 * sizeof(uint32_t), "count table fits");
+  uint64_t thr = 0ull;
+  if (kk < a.V)
+    thr = radix_select_top(fs.hist, fs.sel, (uint32_t)kk, 64,
+                           [&](auto cb) { for_each_row_key(a, row, cfg, cnt, cb); });
+  if (tid == 0) fs.counter = 0u;
+  __syncthreads();
+  uint64_t umax = 0ull;
+  for_each_row_key(a, row, cfg, cnt, [&](uint64_t x) {
+    if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
+    else if (x > umax) umax = x;
+  });
+  *below = block_max_u64<NT>(umax, fs.red64);
+  return thr;
+}
+
 // Number of candidates the chunks of `row` wrote.
 __device__ __forceinline__ int candidate_count(const SampleArgs& a, int row) {
   const ChunkStat* stats = a.stats + (int64_t)row * a.n_chunks;
@@ -652,7 +711,7 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
   const int nch = a.n_chunks;
   const ChunkStat* stats = a.stats + (int64_t)row * nch;
   const int n_total = candidate_count(a, row);
-  const int kk = min(kk_req, n_total);
+  int kk = min(kk_req, n_total);
   if (kk <= 0) return 0;
   auto s_of = [&](uint64_t x) { return key_to_s(cand_skey(x), cfg.t_eff); };
   // 1. candidates into LDS: all of them when they fit, else those at or above
@@ -722,6 +781,26 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
     below_max = max(below_max, block_max_u64<NT>(umax, fs.red64));
   }
   thr = thr > t0 ? thr : t0;
+  // the candidates hold the row's top kk only if the kk-th key is above
+  // every key a truncated chunk left out; else select from the logits
+  {
+    uint32_t ub = 0u;
+    for (int c = tid; c < nch; c += NT)
+      if (stats[c].trunc) ub = max(ub, stats[c].unkept_key);
+    ub = block_max_u32<NT>(ub, fs.redu);
+    uint64_t mn = ~0ull;
+    for (int i = tid; i < kk; i += NT) mn = fs.buf[i] < mn ? fs.buf[i] : mn;
+    mn = block_min_u64<NT>(mn, fs.red64);
+    const uint64_t kth = kk < n_total ? thr : mn;
+    if (ub != 0u && cand_skey(kth) <= ub) {
+      kk = min(kk_req, a.V);
+      uint64_t bm;
+      thr = row_select_exact(fs, a, row, cfg, kk, &bm);
+      below_max = bm;
+      t0 = 0ull;
+      in_lds = false;
+    }
+  }
   // 3. weights; the smallest selected weight is w_b
   uint32_t wmin_bits = 0xffffffffu;
   for (int i = tid; i < kk; i += NT) {
@@ -795,7 +874,8 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
           for (uint32_t h = h0; h < h1; ++h) if (a.hids[h] == (uint32_t)e) cnt += a.hcnt[h];
           l = apply_penalties(l, cnt, cfg);
           const uint32_t kl = lkey(l);
-          if (cand_key(kl, (uint32_t)e) >= cs.min_kept) continue;  // already a candidate
+          const uint64_t ck = cand_key(kl, (uint32_t)e);
+          if (ck >= cs.min_kept || ck >= thr) continue;  // a candidate, or selected
           const float sx = key_to_s(kl, cfg.t_eff);
           const float w = exact_expf(sx - M);
           if (w == w_b) add_ext(w, (uint32_t)e, sx);
@@ -1151,7 +1231,7 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
     token = a.pv.greedy_rule == kGreedyFiniteLane ? am_fin : am_ieee;
   } else if (!finitef_(M)) {
     token = cfg.cls == kTempOnly ? am_fin : row_argmax_total(fs, a, row, cfg);
-  } else if (cfg.cls == kTopK && !cfg.wide) {
+  } else if (cfg.cls == kTopK && !cfg.store_s) {
     ranked_k = rank_candidates(fs, a, row, cfg, cfg.k_sel, M);
     token = draw_topk(fs, cfg, cfg.k_eff, u);
     if (token == 0xffffffffu) token = row_argmax_total(fs, a, row, cfg);
@@ -3231,7 +3311,7 @@ __device__ __forceinline__ void select_chunk(const SampleArgs& a, int row, int c
 }
 
 // The streaming select pass: workgroup (chunk, row).
-__device__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg);
+__device__ __forceinline__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg);
 
 template <int DT, int NL, bool MASK>
 __global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
@@ -3382,7 +3462,8 @@ struct WideChunkLds {
   uint32_t hkey[kWideChunkHash];
   uint32_t hcnt[kWideChunkHash];
   uint32_t hmin[kWideChunkHash];
-  uint32_t nrun, ovf, last;
+  uint32_t nrun, ovf, last, fu;
+  float fend;
 };
 constexpr size_t kWideChunkHead = (sizeof(WideChunkLds) + 15) & ~(size_t)15;
 // Weights sit in LDS with one pad word per 16, so that threads reading
@@ -3419,8 +3500,8 @@ struct WideFinLds {
   } u;
   uint8_t pe[kWideRunCap + 4];
   uint32_t noff[NT + 1];
-  uint32_t cnt, fail_c, rsel, csel, tok;
-  float acc;
+  uint32_t cnt, fail_c, rsel, csel, tok, fu;
+  float acc, acc2;
 };
 // The refold arrays (weights, then fold binades) start after the chain's
 // plans, inside or past the union.
@@ -3428,7 +3509,7 @@ __host__ __device__ inline size_t wide_fin_w_off() {
   return (offsetof(WideFinLds, u) + sizeof(ChunkFold) * kWideBatch + 15) & ~(size_t)15;
 }
 __host__ __device__ inline size_t wide_fin_lds(int chunk) {
-  const size_t r = wide_fin_w_off() + wide_w_bytes(chunk) + (size_t)chunk + 16;
+  const size_t r = wide_fin_w_off() + wide_w_bytes(chunk);
   return r > sizeof(WideFinLds) ? r : sizeof(WideFinLds);
 }
 
@@ -3458,7 +3539,7 @@ __device__ __forceinline__ bool wide_insert(uint32_t* hkey, uint32_t* hcnt, uint
 // row: M, the superset bound w_lo and the predicted fold value before each
 // chunk (WideRow, WideStat::pred).  The masses use approximate exp; they
 // only size the superset and predict binades.
-__device__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg) {
+__device__ __forceinline__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg) {
   const int tid = threadIdx.x;
   const int nch = a.n_chunks;
   const ChunkStat* stats = a.stats + (int64_t)row * nch;
@@ -3486,7 +3567,7 @@ __device__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const 
   for (int cb = 0; cb < nch; cb += kSurvCap) {
     const int nb = min(kSurvCap, nch - cb);
     for (int i = tid; i < nb; i += NT) {
-      const WideStat& ws = wst[cb + i];
+      const WideStat ws = wst[cb + i];
       const float lb = (M - ws.ms) * 1.4426950408889634f;  // log2 of M's weight over the chunk max's
       const float r = __builtin_amdgcn_exp2f(-lb);
       double cm = 0.0;
@@ -3528,53 +3609,162 @@ __device__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const 
   }
 }
 
+// w[wide_pad(i)] = the weight of scaled logit s[i] (exact expf; min-p
+// zeros it), i < len: all of a thread's loads of a block are issued before
+// any is used.
+__device__ __forceinline__ void wide_weights(const float* s, int len, float M, float min_p, float* w) {
+  constexpr int kB = 8;
+  for (int base = 0; base < len; base += kB * NT) {
+    float v[kB];
+    #pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = base + k * NT + (int)threadIdx.x;
+      v[k] = i < len ? s[i] : -__builtin_inff();
+    }
+    #pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = base + k * NT + (int)threadIdx.x;
+      const float x = exact_expf(v[k] - M);
+      if (i < len) w[wide_pad(i)] = x < min_p ? 0.f : x;  // min-p: excluded like a zero weight
+    }
+  }
+}
+
+// Map of one term in binade e (exact_fold.h): n ulps, plus one above half
+// an ulp, plus one on an exact half when that makes the sum even.
+__device__ __forceinline__ fold::Map term_map(float x, int e) {
+  const fold::Inc c = fold::classify(x, e);
+  const uint32_t base = c.n + (c.cls == 2u ? 1u : 0u);
+  const uint32_t odd = c.n & 1u;
+  fold::Map m;
+  m.t0 = base + ((c.cls == 1u && odd) ? 1u : 0u);
+  m.t1 = base + ((c.cls == 1u && !odd) ? 1u : 0u);
+  return m;
+}
+
+// Exclusive scan of maps over the workgroup in thread order; *tot gets the
+// composition of all.  Two barriers.
+__device__ __forceinline__ fold::Map block_map_scan(fold::Map m, fold::Map* wm, fold::Map* tot) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  fold::Map inc = m;
+  #pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    fold::Map o;
+    o.t0 = (uint32_t)__shfl_up((int)inc.t0, (unsigned)d, 64);
+    o.t1 = (uint32_t)__shfl_up((int)inc.t1, (unsigned)d, 64);
+    if (lane >= d) inc = fold::compose(o, inc);
+  }
+  fold::Map ex;
+  ex.t0 = (uint32_t)__shfl_up((int)inc.t0, 1u, 64);
+  ex.t1 = (uint32_t)__shfl_up((int)inc.t1, 1u, 64);
+  if (lane == 0) ex = fold::map_identity();
+  __syncthreads();
+  if (lane == 63) wm[wid] = inc;
+  __syncthreads();
+  fold::Map before = fold::map_identity(), all = fold::map_identity();
+  #pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    if (w < wid) before = fold::compose(before, wm[w]);
+    all = fold::compose(all, wm[w]);
+  }
+  *tot = all;
+  return fold::compose(before, ex);
+}
+
+// The exact sequential f32 fold of w[wide_pad(0 .. len)) (LDS) from a0, by
+// the workgroup.  Thread t holds a block of consecutive terms; in the
+// current binade every block is one map, so a scan gives each block's
+// exact start until the first block whose terms leave the binade.  That
+// thread adds its terms (and, while crossings come close together, the
+// next blocks' terms) as real f32 additions, and the scan resumes after
+// them in the new binade.  Returns the sum (uniform).
+__device__ __forceinline__ float exact_chunk_fold(const float* w, int len, float a0, fold::Map* wm, float* shf,
+                                                  uint32_t* red) {
+  constexpr int kSeqBlocks = 4;  // blocks one thread adds after a crossing
+  const int tid = threadIdx.x;
+  const int J = (len + NT - 1) / NT;
+  const int r0 = min(tid * J, len), r1 = min(r0 + J, len);
+  float a = a0;
+  int pos = 0;
+  while (pos < NT) {
+    const int e = fold::binade(a);
+    const uint32_t A = fold::to_A(a);
+    fold::Map m = fold::map_identity();
+    if (tid >= pos)
+      for (int r = r0; r < r1; ++r) m = fold::compose(m, term_map(w[wide_pad(r)], e));
+    fold::Map tot;
+    const fold::Map ex = block_map_scan(m, wm, &tot);
+    const uint32_t p = A & 1u;
+    if ((uint64_t)A + fold::apply(tot, p) < fold::kTop) {
+      a = fold::from_A(A + fold::apply(tot, p), e);
+      break;
+    }
+    const uint64_t At = (uint64_t)A + fold::apply(ex, p);
+    const bool cross = tid >= pos && (At >= fold::kTop || At + fold::apply(m, (uint32_t)At & 1u) >= fold::kTop);
+    uint32_t first = ~block_max_u32<NT>(cross ? ~(uint32_t)tid : 0u, red);
+    if (first == 0xffffffffu) first = (uint32_t)pos;  // (not reached: the total leaves the binade)
+    if (tid == (int)first) {
+      // At < kTop: the blocks before this one stayed in the binade
+      float x = fold::from_A((uint32_t)At, e);
+      const int stop = min(len, (tid + kSeqBlocks) * J);
+      for (int r = r0; r < stop; ++r) x = fold::fadd(x, w[wide_pad(r)]);
+      shf[0] = x;
+    }
+    __syncthreads();
+    a = shf[0];
+    pos = (int)first + kSeqBlocks;
+    __syncthreads();
+  }
+  return a;
+}
+
 // Steps 2-3 for one (chunk, row), with the row's M, w_lo and the chunk's
 // predicted start S.
-__device__ void wide_chunk_work(WideChunkLds& L, unsigned char* lds_raw, const SampleArgs& a, int row, int chunk,
+__device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* lds_raw, const SampleArgs& a, int row, int chunk,
                                 const RowCfg& cfg, float M, float w_lo, double S) {
   const int tid = threadIdx.x;
   const int c0 = chunk * a.chunk;
   const int len = min(a.chunk, a.V - c0);
   float* w = reinterpret_cast<float*>(lds_raw + wide_w_off(a.chunk));
-  uint8_t* pe = lds_raw + wide_pe_off(a.chunk);
   const float* srow = a.ws_s + (int64_t)row * a.V + c0;
-  for (int i = tid; i < len; i += NT) {
-    const float x = exact_expf(srow[i] - M);
-    w[wide_pad(i)] = x < cfg.min_p ? 0.f : x;  // min-p: excluded like a zero weight
-  }
+  wide_weights(srow, len, M, cfg.min_p, w);
   for (int h = tid; h < kWideChunkHash; h += NT) { L.hkey[h] = 0u; L.hcnt[h] = 0u; L.hmin[h] = 0xffffffffu; }
   if (tid == 0) { L.nrun = 0u; L.ovf = 0u; }
   __syncthreads();
-  // the chunk's part of the vocabulary-order fold: chunk 0 starts from
-  // the known -0.0 and folds exactly; the others plan from a predicted start
-  ChunkFold* cf = a.wfold + (int64_t)row * a.n_chunks + chunk;
-  auto tf = [&](int r) { return w[wide_pad(r)]; };
-  auto mf = [](int) { return 1u; };
-  if (chunk == 0) {
-    const float end = fold::fold_runs<NT>(L.fl, pe, len, -0.0f, tf, mf, [](int, float) {});
-    if (tid == 0) { cf->has_end = 1u; cf->end = end; cf->nseg = 1u; }
-  } else {
-    if (tid == 0) cf->has_end = 0u;
-    fold::fold_plan<NT, decltype(tf), decltype(mf), true>(L.fl, pe, 0, len, S, tf, mf);
+  // the weights for the finish's exact refolds
+  {
+    float* wg = a.ws_w + (int64_t)row * a.V + c0;
+    for (int i = tid; i < len; i += NT) wg[i] = w[wide_pad(i)];
   }
-  const uint32_t nb = L.fl.nb;
-  const uint32_t nseg = nb + 1u;
-  if (chunk != 0 && tid < 64) {
-    const uint32_t k = (uint32_t)tid;
-    bool ne = false;
-    if (k < nseg && nseg <= (uint32_t)kFoldSegs) {
-      const int first = k == 0 ? 0 : (int)L.fl.bnd_run[k - 1] + 1;
-      const int last = k < nb ? (int)L.fl.bnd_run[k] - 1 : len - 1;
-      ne = first <= last;
-      cf->seg_e[k] = L.fl.seg_e[k];
-      cf->seg_map[k] = L.fl.seg_map[k];
-      cf->seg_alt[k] = L.fl.seg_alt[k];
-      if (k < nb) cf->bnd_x[k] = w[wide_pad((int)L.fl.bnd_run[k])];
+  // the chunk's part of the vocabulary-order fold: chunk 0 starts from the
+  // known -0.0 and folds exactly; the others give their maps in the
+  // binades around the predicted start
+  ChunkFold* cf = a.wfold + (int64_t)row * a.n_chunks + chunk;
+  if (chunk == 0) {
+    const float end = exact_chunk_fold(w, len, -0.0f, L.fl.wmap, &L.fend, L.fl.wcnt);
+    if (tid == 0) { cf->has_end = 1u; cf->end = end; cf->e0 = 1u; }
+  } else {
+    const int ep = fold::binade((float)S);
+    const int e0 = ep > 1 ? ep - 1 : 1;
+    const int J = (len + NT - 1) / NT;
+    const int r0 = min(tid * J, len), r1 = min(r0 + J, len);
+    fold::Map m0 = fold::map_identity(), m1 = m0, m2 = m0;
+    for (int r = r0; r < r1; ++r) {
+      const float x = w[wide_pad(r)];
+      m0 = fold::compose(m0, term_map(x, e0));
+      m1 = fold::compose(m1, term_map(x, e0 + 1));
+      m2 = fold::compose(m2, term_map(x, e0 + 2));
     }
-    const uint64_t nem = __ballot(ne);
+    fold::Map t0, t1, t2;
+    block_map_scan(m0, L.fl.wmap, &t0);
+    block_map_scan(m1, L.fl.wmap, &t1);
+    block_map_scan(m2, L.fl.wmap, &t2);
     if (tid == 0) {
-      cf->nseg = nseg <= (uint32_t)kFoldSegs ? nseg : 0u;
-      cf->nonempty = (uint32_t)nem;
+      cf->has_end = 0u;
+      cf->e0 = (uint32_t)e0;
+      cf->map[0] = t0;
+      cf->map[1] = t1;
+      cf->map[2] = t2;
     }
   }
   // the superset's distinct weights
@@ -3601,22 +3791,30 @@ __device__ void wide_chunk_work(WideChunkLds& L, unsigned char* lds_raw, const S
 }
 
 // The exact fold value after chunk c's weights, from `acc` before them:
-// reads the chunk's scaled logits again (the chain's fallback when the
-// chunk's predicted binades missed).  All threads call it.
-__device__ float wide_refold(WideFinLds& F, unsigned char* lds_raw, const SampleArgs& a, int row, int c, float M,
-                             const RowCfg& cfg, float acc) {
+// reads the chunk's weights back (the chain's path when a chunk's sum
+// leaves its binades).  All threads call it.
+__device__ __forceinline__ float wide_refold(WideFinLds& F, unsigned char* lds_raw, const SampleArgs& a, int row,
+                                             int c, float acc) {
   const int c0 = c * a.chunk;
   const int len = min(a.chunk, a.V - c0);
   float* w = reinterpret_cast<float*>(lds_raw + wide_fin_w_off());
-  uint8_t* pe = lds_raw + wide_fin_w_off() + wide_w_bytes(a.chunk);
-  const float* srow = a.ws_s + (int64_t)row * a.V + c0;
-  for (int i = threadIdx.x; i < len; i += NT) {
-    const float x = exact_expf(srow[i] - M);
-    w[wide_pad(i)] = x < cfg.min_p ? 0.f : x;
+  const float* wg = a.ws_w + (int64_t)row * a.V + c0;
+  constexpr int kB = 8;
+  for (int base = 0; base < len; base += kB * NT) {
+    float v[kB];
+    #pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = base + k * NT + (int)threadIdx.x;
+      v[k] = i < len ? wg[i] : 0.f;
+    }
+    #pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = base + k * NT + (int)threadIdx.x;
+      if (i < len) w[wide_pad(i)] = v[k];
+    }
   }
   __syncthreads();
-  return fold::fold_runs<NT>(F.fl, pe, len, acc, [&](int r) { return w[wide_pad(r)]; }, [](int) { return 1u; },
-                             [](int, float) {});
+  return exact_chunk_fold(w, len, acc, F.fl.wmap, &F.acc2, F.fl.wcnt);
 }
 
 // Calls f(c, e) for every superset run entry e of chunk c of `row`, in
@@ -3650,7 +3848,7 @@ __device__ __forceinline__ void wide_for_each_run(WideFinLds& W, const SampleArg
 // Step 4: the row finish by the last workgroup.  Returns the token, or
 // 0xffffffff when the row must take finish_row (nothing written); `path`
 // gets the WidePath code.
-__device__ uint32_t wide_finish(unsigned char* lds_raw, const SampleArgs& a, int row, const RowCfg& cfg, float M,
+__device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const SampleArgs& a, int row, const RowCfg& cfg, float M,
                                 float w_lo, uint32_t& path) {
   WideFinLds& F = *reinterpret_cast<WideFinLds*>(lds_raw);
   const int tid = threadIdx.x;
@@ -3680,22 +3878,15 @@ __device__ uint32_t wide_finish(unsigned char* lds_raw, const SampleArgs& a, int
         for (int cc = c; cc < cb + nb; ++cc) {
           const ChunkFold& cf = F.u.ch.batch[cc - cb];
           if (cf.has_end) { x = cf.end; continue; }  // chunk 0, from -0.0
-          if (cf.nseg == 0u) { fail = (uint32_t)cc; break; }
+          const int ey = fold::binade(x);
+          const int k = ey - (int)cf.e0;
+          bool ok = k >= 0 && k < 3;
           float y = x;
-          bool ok = true;
-          for (uint32_t k = 0; k < cf.nseg; ++k) {
-            if ((cf.nonempty >> k) & 1u) {
-              const int e = (int)cf.seg_e[k];
-              const int ey = fold::binade(y);
-              const uint32_t A = fold::to_A(y);
-              // in the predicted binade, or (a start that lags the
-              // prediction) in the one below
-              const fold::Map mp = ey == e ? cf.seg_map[k] : cf.seg_alt[k];
-              const uint32_t t = fold::apply(mp, A & 1u);
-              if ((ey != e && (ey != e - 1 || e <= 1)) || (uint64_t)A + t >= fold::kTop) { ok = false; break; }
-              y = fold::from_A(A + t, ey);
-            }
-            if (k + 1u < cf.nseg) y = fold::fadd(y, cf.bnd_x[k]);
+          if (ok) {
+            const uint32_t A = fold::to_A(x);
+            const uint32_t t = fold::apply(cf.map[k], A & 1u);
+            ok = (uint64_t)A + t < fold::kTop;
+            y = fold::from_A(A + t, ey);
           }
           if (!ok) { fail = (uint32_t)cc; break; }
           x = y;
@@ -3708,7 +3899,7 @@ __device__ uint32_t wide_finish(unsigned char* lds_raw, const SampleArgs& a, int
       const uint32_t fail = F.fail_c;
       __syncthreads();
       if (fail == 0xffffffffu) break;
-      acc = wide_refold(F, lds_raw, a, row, (int)fail, M, cfg, acc);
+      acc = wide_refold(F, lds_raw, a, row, (int)fail, acc);
       c = (int)fail + 1;
     }
     __syncthreads();

@@ -523,6 +523,33 @@ def test_top_k_clustered_in_one_chunk(hip, oracle, n_lp):
     compare(w, got, want, f"clustered n_lp={n_lp}")
 
 
+@pytest.mark.parametrize("k", [256, 1024])
+def test_top_k_beyond_chunk_candidates(hip, oracle, k):
+    """A chunk that holds more of the row's top k than it keeps as
+    candidates (its survivor bound sits above the row's k-th key): the
+    finish must notice and select the row's top k from the logits.  Also
+    4096 tied logits in one chunk (ties rank by index), a top k spread over
+    a few chunks, and plain rows; top-k 256 (the lean path's largest) and
+    1024 (the ranked finish's largest)."""
+    from hi_amd.sampler import row_params
+    rng = np.random.default_rng(77 + k)
+    B, V = 6, 151936
+    x = rng.normal(0, 1.0, (B, V)).astype(F32)
+    hot = rng.random(4096) < 0.6
+    x[0, 4096:8192] += (hot * 20.0 + rng.normal(0, 0.5, 4096)).astype(F32)
+    x[1, 0:20000:7] += F32(15.0)
+    x[2, 4096:8192] = F32(5.0)
+    p = row_params(B, temperature=0.9, top_p=0.95, top_k=k)
+    p["top_p"][4] = 1.0
+    u = rng.random(B).astype(F32)
+    for n_lp in (0, 20):
+        w = Workload(f"beyond-candidates k={k} n_lp={n_lp}", x, p, u, n_logprobs=n_lp)
+        say(f"{w.name}")
+        got = run_gpu(w)
+        want = run_oracle(oracle, w)
+        compare(w, got, want, w.name)
+
+
 @pytest.mark.parametrize("V", [37, 1000, 8192, 8193, 20011, 70000])
 def test_edge_mixed_batches(hip, oracle, V):
     rng = np.random.default_rng(V)

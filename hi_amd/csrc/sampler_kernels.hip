@@ -600,6 +600,17 @@ __device__ __forceinline__ void for_each_candidate(const SampleArgs& a, int row,
   }
 }
 
+// One compare-exchange step of a descending bitonic sort over element
+// indices i (this value) and i ^ j (the partner's value y / q), in stage k:
+// the lower index of a pair keeps the larger key when (i & k) == 0.
+__device__ __forceinline__ void bitonic_keep(uint64_t& x, uint32_t& p, uint64_t y, uint32_t q, int i, int j, int k) {
+  const bool keep_max = ((i & k) == 0) == ((i & j) == 0);
+  if (keep_max ? (y > x) : (y < x)) {
+    x = y;
+    p = q;
+  }
+}
+
 // Descending sort of fs.buf[0..n) carrying fs.pay; n <= kBuf.
 __device__ __forceinline__ void sort_ranked(FinLds& fs, int n) {
   const int tid = threadIdx.x;
@@ -617,25 +628,59 @@ __device__ __forceinline__ void sort_ranked(FinLds& fs, int n) {
     __syncthreads();
     return;
   }
-  const int n2 = next_pow2(n);
-  for (int i = n + tid; i < n2; i += NT) { fs.buf[i] = 0ull; fs.pay[i] = 0u; }
+  // Bitonic network over kBuf elements (zero keys pad, and sort last), four
+  // consecutive elements per thread in registers: distances 1 and 2 inside
+  // the thread, 4 .. 128 across the lanes of a wave (shuffles), 256 and 512
+  // across waves through LDS.
+  static_assert(kBuf == 4 * NT, "four elements per thread");
+  uint64_t x[4];
+  uint32_t p[4];
+  #pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 4 * tid + r;
+    x[r] = i < n ? fs.buf[i] : 0ull;
+    p[r] = i < n ? fs.pay[i] : 0u;
+  }
   __syncthreads();
-  for (int k = 2; k <= n2; k <<= 1) {
+  #pragma unroll
+  for (int k = 2; k <= kBuf; k <<= 1) {
+    #pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < n2; i += NT) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const uint64_t x = fs.buf[i], y = fs.buf[ixj];
-          const bool desc = (i & k) == 0;
-          if (desc ? (x < y) : (x > y)) {
-            fs.buf[i] = y; fs.buf[ixj] = x;
-            const uint32_t t = fs.pay[i]; fs.pay[i] = fs.pay[ixj]; fs.pay[ixj] = t;
-          }
+      if (j >= 256) {
+        #pragma unroll
+        for (int r = 0; r < 4; ++r) { fs.buf[4 * tid + r] = x[r]; fs.pay[4 * tid + r] = p[r]; }
+        __syncthreads();
+        #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 4 * tid + r;
+          bitonic_keep(x[r], p[r], fs.buf[i ^ j], fs.pay[i ^ j], i, j, k);
         }
+        __syncthreads();
+      } else if (j >= 4) {
+        const int o = j >> 2;  // partner lane: lane ^ o (same wave: 4 * 64 = 256 elements)
+        #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint64_t y = shfl_xor_u64(x[r], o);
+          const uint32_t q = (uint32_t)__shfl_xor((int)p[r], o, 64);
+          bitonic_keep(x[r], p[r], y, q, 4 * tid + r, j, k);
+        }
+      } else {
+        // partners inside the thread: (0, j) and (1 or 2, 1 + j or 3)
+        uint64_t y[4];
+        uint32_t q[4];
+        #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          y[r] = j == 1 ? x[r ^ 1] : x[r ^ 2];
+          q[r] = j == 1 ? p[r ^ 1] : p[r ^ 2];
+        }
+        #pragma unroll
+        for (int r = 0; r < 4; ++r) bitonic_keep(x[r], p[r], y[r], q[r], 4 * tid + r, j, k);
       }
-      __syncthreads();
     }
   }
+  #pragma unroll
+  for (int r = 0; r < 4; ++r) { fs.buf[4 * tid + r] = x[r]; fs.pay[4 * tid + r] = p[r]; }
+  __syncthreads();
 }
 
 // Calls f(key) with the candidate key (processed-logit key, index) of every
@@ -909,60 +954,9 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
   return kk;
 }
 
-// Reference steps 7-10 (gpu.rs:831-899) over the first k entries of the rank
-// order in fs.buf (top-k rows).  Returns the token, or 0xffffffff for "fall
-// back to argmax_host".
-__device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int k, float u) {
-  const int tid = threadIdx.x;
-  for (int i = tid; i < k; i += NT) {
-    const float w = rank_w(fs.buf[i]);
-    fs.fa[i] = (w < cfg.min_p) ? 0.f : w;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float total = -0.0f;  // gpu.rs:834-836: kept mass in rank order
-    for (int i = 0; i < k; ++i) total += fs.fa[i];
-    fs.fval0 = total;
-  }
-  __syncthreads();
-  const float total = fs.fval0;
-  if (total <= 0.f || !finitef_(total)) return 0xffffffffu;
-  for (int i = tid; i < k; i += NT) fs.fb[i] = fs.fa[i] / total;
-  __syncthreads();
-  if (tid == 0) {
-    float cum_p = 0.f;
-    int m_end = 0;  // candidates: positive weights in [0, m_end)
-    bool any = false;
-    for (int i = 0; i < k; ++i) {
-      if (fs.fa[i] <= 0.f) continue;
-      any = true;
-      m_end = i + 1;
-      cum_p += fs.fb[i];
-      if (cfg.cutoff < 1.f && cum_p >= cfg.cutoff) break;
-    }
-    uint32_t tok = 0xffffffffu;
-    if (any) {
-      float ct = -0.0f;
-      for (int i = 0; i < m_end; ++i) if (fs.fa[i] > 0.f) ct += fs.fa[i];
-      if (ct > 0.f && finitef_(ct)) {
-        const float target = clamp_uniform(u) * ct;
-        float cum = 0.f;
-        int last = -1, pick = -1;
-        for (int i = 0; i < m_end; ++i) {
-          if (fs.fa[i] <= 0.f) continue;
-          last = i;
-          cum += fs.fa[i];
-          if (target < cum) { pick = i; break; }
-        }
-        if (pick < 0) pick = last;
-        tok = cand_idx(fs.buf[pick]);
-      }
-    }
-    fs.token = tok;
-  }
-  __syncthreads();
-  return fs.token;
-}
+// Reference steps 7-10 over the first k entries of the rank order in fs.buf
+// (top-k rows); defined with the wave folds below.
+__device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int k);
 
 // Serial f32 fold of a global float array in index order (Rust's Sum: a fold
 // from -0.0), by thread 0, staged through LDS tiles.  Valid in all threads.
@@ -1233,7 +1227,7 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
     token = cfg.cls == kTempOnly ? am_fin : row_argmax_total(fs, a, row, cfg);
   } else if (cfg.cls == kTopK && !cfg.store_s) {
     ranked_k = rank_candidates(fs, a, row, cfg, cfg.k_sel, M);
-    token = draw_topk(fs, cfg, cfg.k_eff, u);
+    token = draw_topk(fs, cfg, min(cfg.k_eff, ranked_k));
     if (token == 0xffffffffu) token = row_argmax_total(fs, a, row, cfg);
   } else if (cfg.cls == kTempOnly) {
     token = draw_temp_only(fs, a, row, M, u, am_fin);
@@ -1450,6 +1444,93 @@ __device__ __forceinline__ float wave_fold_f32_until(float v, float start, int n
   return p;
 }
 
+// Reference steps 7-10 (gpu.rs:831-899) over the rank order keys[0, k)
+// (LDS, k <= 64 * DM), by every wave from registers: entry m * 64 + lane
+// sits in lane `lane` of slot m.  Returns the drawn entry, or -1 for the
+// reference's argmax_host fallback (no positive weight, or a total or
+// candidate total that is not positive and finite).  All waves return the
+// same, with no barrier.
+template <int DM>
+__device__ __forceinline__ int wave_draw(const uint64_t* keys, int k, const RowCfg& cfg) {
+  const uint32_t lane = threadIdx.x & 63u;
+  float fa[DM], pa[DM];
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const float w = i < k ? rank_w(keys[i]) : 0.f;
+    fa[m] = w < cfg.min_p ? 0.f : w;  // min-p: excluded like w <= 0 (gpu.rs:847-849)
+  }
+  // the weights are in rank order, so the positive ones are a prefix
+  // [0, last_pos] (min-p and underflow zeros sit at the end)
+  int last_pos = -1;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const uint64_t pm = __ballot(i < k && fa[m] > 0.f);
+    if (pm != 0ull) last_pos = m * 64 + 63 - __clzll((unsigned long long)pm);
+  }
+  if (last_pos < 0) return -1;  // no candidate: argmax_host fallback
+  // P_i: the sequential sum of fa[0..i]: the total of gpu.rs:834-836 (the
+  // kept weights in rank order; the zeros after last_pos add nothing) and,
+  // at positive entries, the candidate total and CDF of gpu.rs:874-896
+  const int kp = last_pos + 1;
+  float P = -0.0f;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    if (m * 64 < kp) {
+      pa[m] = wave_fold_f32(fa[m], P, min(64, kp - m * 64));
+      P = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), min(63, kp - 1 - m * 64)));
+    } else {
+      pa[m] = P;
+    }
+  }
+  const float total = P;
+  if (!(total > 0.f) || !finitef_(total)) return -1;  // argmax_host fallback
+  // the nucleus: cum_p over w / total of the positive entries (gpu.rs:843-856),
+  // folded only as far as the first one that reaches the cutoff
+  int cut = -1;  // first positive entry where cum_p reaches the cutoff
+  if (cfg.cutoff < 1.f) {
+    float Q = 0.f;
+    #pragma unroll
+    for (int m = 0; m < DM; ++m) {
+      if (cut < 0 && m * 64 < kp) {
+        const int i = m * 64 + (int)lane;
+        const bool pos = i < kp;
+        const float fb = pos ? fa[m] / total : 0.f;
+        int first;
+        const float q = wave_fold_f32_until(fb, Q, min(64, kp - m * 64), pos, cfg.cutoff, first);
+        if (first >= 0) cut = m * 64 + first;
+        else Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(q), min(63, kp - 1 - m * 64)));
+      }
+    }
+  }
+  const int m_end = cut >= 0 ? cut + 1 : last_pos + 1;
+  const int me = m_end - 1;
+  float ct = 0.f;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m)
+    if ((me >> 6) == m) ct = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), me & 63));
+  if (!(ct > 0.f) || !finitef_(ct)) return -1;
+  // inverse CDF: the first candidate whose cumulative weight passes target
+  const float target = clamp_uniform(cfg.u) * ct;
+  int pick = -1;
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    const uint64_t hit = __ballot(i < m_end && fa[m] > 0.f && target < pa[m]);
+    if (pick < 0 && hit != 0ull) pick = m * 64 + __ffsll((unsigned long long)hit) - 1;
+  }
+  return pick < 0 ? me : pick;
+}
+
+// Reference steps 7-10 (gpu.rs:831-899) over the first k <= kBuf entries of
+// the rank order in fs.buf (top-k rows).  Returns the token, or 0xffffffff
+// for "fall back to argmax_host".
+__device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int k) {
+  const int pick = wave_draw<kBuf / 64>(fs.buf, k, cfg);
+  return pick < 0 ? 0xffffffffu : cand_idx(fs.buf[pick]);
+}
+
 // Steps 4-9 of the lean finish over the candidates fs.cbig[0, n) of `row`
 // (candidate keys, any order; n >= 1).  M is the row max of s; ub_key bounds
 // the processed-logit keys of the row's logits that are not candidates (0:
@@ -1571,76 +1652,8 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   __syncthreads();
 
   // 8. the draw, by every wave from registers (gpu.rs:831-899)
-  const int k = min(cfg.k_eff, kk);
-  constexpr int DM = kLeanK / 64;
-  float fa[DM], pa[DM], fb[DM], qa[DM];
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int i = m * 64 + (int)lane;
-    const float w = i < k ? rank_w(fs.cbig[i]) : 0.f;
-    fa[m] = w < cfg.min_p ? 0.f : w;  // min-p: excluded like w <= 0 (gpu.rs:847-849)
-  }
-  // the weights are in rank order, so the positive ones are a prefix
-  // [0, last_pos] (min-p and underflow zeros sit at the end)
-  int last_pos = -1;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int i = m * 64 + (int)lane;
-    const uint64_t pm = __ballot(i < k && fa[m] > 0.f);
-    if (pm != 0ull) last_pos = m * 64 + 63 - __clzll((unsigned long long)pm);
-  }
-  if (last_pos < 0) return false;  // no candidate: argmax_host fallback
-  // P_i: the sequential sum of fa[0..i]: the total of gpu.rs:834-836 (the
-  // kept weights in rank order; the zeros after last_pos add nothing) and,
-  // at positive entries, the candidate total and CDF of gpu.rs:874-896
-  const int kp = last_pos + 1;
-  float P = -0.0f;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    if (m * 64 < kp) {
-      pa[m] = wave_fold_f32(fa[m], P, min(64, kp - m * 64));
-      P = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), min(63, kp - 1 - m * 64)));
-    } else {
-      pa[m] = P;
-    }
-  }
-  const float total = P;
-  if (!(total > 0.f) || !finitef_(total)) return false;  // argmax_host fallback
-  // the nucleus: cum_p over w / total of the positive entries (gpu.rs:843-856),
-  // folded only as far as the first one that reaches the cutoff
-  int cut = -1;        // first positive entry where cum_p reaches the cutoff
-  if (cfg.cutoff < 1.f) {
-    float Q = 0.f;
-    #pragma unroll
-    for (int m = 0; m < DM; ++m) {
-      if (cut < 0 && m * 64 < kp) {
-        const int i = m * 64 + (int)lane;
-        const bool pos = i < kp;
-        fb[m] = pos ? fa[m] / total : 0.f;
-        int first;
-        qa[m] = wave_fold_f32_until(fb[m], Q, min(64, kp - m * 64), pos, cfg.cutoff, first);
-        if (first >= 0) cut = m * 64 + first;
-        else Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(qa[m]), min(63, kp - 1 - m * 64)));
-      }
-    }
-  }
-  const int m_end = cut >= 0 ? cut + 1 : last_pos + 1;
-  const int me = m_end - 1;
-  float ct = 0.f;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m)
-    if ((me >> 6) == m) ct = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pa[m]), me & 63));
-  if (!(ct > 0.f) || !finitef_(ct)) return false;
-  // inverse CDF: the first candidate whose cumulative weight passes target
-  const float target = clamp_uniform(cfg.u) * ct;
-  int pick = -1;
-  #pragma unroll
-  for (int m = 0; m < DM; ++m) {
-    const int i = m * 64 + (int)lane;
-    const uint64_t hit = __ballot(i < m_end && fa[m] > 0.f && target < pa[m]);
-    if (pick < 0 && hit != 0ull) pick = m * 64 + __ffsll((unsigned long long)hit) - 1;
-  }
-  if (pick < 0) pick = me;
+  const int pick = wave_draw<kLeanK / 64>(fs.cbig, min(cfg.k_eff, kk), cfg);
+  if (pick < 0) return false;  // argmax_host fallback
   const uint32_t token = cand_idx(fs.cbig[pick]);
   if (tid == 0) a.out_tokens[row] = token;
   if (!want_lp) return true;
@@ -4093,12 +4106,22 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   return F.tok;
 }
 
-// The second kernel of the chunked path: grid (chunks, rows).  Top-p rows
-// take the wide pass on every chunk; every other row is finished by its
-// chunk-0 workgroup (finish_lean, else finish_row).
+// The second kernel of the chunked path: one workgroup per (row, chunk),
+// on a 1-D grid whose first B workgroups are chunk 0 of rows 0 .. B-1 and
+// the rest chunks 1 .. of each row in turn.  Top-p rows take the wide pass
+// on every chunk; every other row is finished by its chunk-0 workgroup
+// (finish_lean, else finish_row) and its other workgroups exit at once.
+// Workgroups go to the XCDs and their shader engines round-robin by linear
+// id, so the B finishing workgroups, being consecutive, spread over the
+// whole chip (on a (chunks, rows) grid they would share a few engines).
 __global__ void __launch_bounds__(NT) finish_grid_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  const int chunk = blockIdx.x, row = blockIdx.y;
+  int row = (int)blockIdx.x, chunk = 0;
+  if (row >= a.B) {
+    const int rest = row - a.B, per = a.n_chunks - 1;
+    row = rest / per;
+    chunk = 1 + rest % per;
+  }
   const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
   if (cfg.cls != kTopP) {
     if (chunk != 0) return;
@@ -5025,10 +5048,12 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t stream, const LaunchEv
     e = a.mask ? launch_select_d<HI_ROCM_DTYPE_F32, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_F32, false>(a, stream);
   if (e == hipSuccess) e = record(le, 1, stream);
   if (e != hipSuccess) return e;
+  const int64_t n_wg = (int64_t)a.n_chunks * a.B;
+  if (n_wg * NT >= ((int64_t)1 << 32)) return hipErrorInvalidConfiguration;  // 1-D grid of work-items
   const size_t lds = finish_grid_lds(a.chunk);
   e = ensure_lds((const void*)finish_grid_kernel, lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(finish_grid_kernel, dim3(a.n_chunks, a.B), dim3(NT), lds, stream, a);
+  hipLaunchKernelGGL(finish_grid_kernel, dim3((unsigned)n_wg), dim3(NT), lds, stream, a);
   e = hipGetLastError();
   return e == hipSuccess ? record(le, 2, stream) : e;
 }

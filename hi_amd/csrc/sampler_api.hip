@@ -9,9 +9,10 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <map>
 #include <mutex>
 #include <string>
-#include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "hi_rocm.h"
@@ -32,24 +33,29 @@ int hip_fail(hipError_t e, const char* where) {
 }
 
 // Library-owned workspace for the workspace-free reference mirrors: one
-// buffer per device, grown on demand, never shrunk.
+// buffer per (device, stream), grown on demand, never shrunk, like the
+// reference's thread-local buffer pool (crates/hi-cuda/src/runtime.rs:
+// 218-231).  Calls on one stream are ordered by the stream, so a buffer is
+// never used by two kernels at once; calls on different streams (from any
+// thread) use different buffers.  Growing waits for the buffer's own stream
+// only.
 struct DeviceWorkspace {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::unordered_map<int, DeviceWorkspace> g_ws;
+std::map<std::pair<int, uintptr_t>, DeviceWorkspace> g_ws;
 
-int internal_workspace(size_t bytes, void** out) {
+int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  DeviceWorkspace& ws = g_ws[dev];
+  DeviceWorkspace& ws = g_ws[{dev, (uintptr_t)stream}];
   if (ws.bytes < bytes) {
     if (ws.ptr) {
-      e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+      e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
       e = hipFree(ws.ptr);
       if (e != hipSuccess) return hip_fail(e, "hipFree");
       ws.ptr = nullptr;
@@ -58,8 +64,8 @@ int internal_workspace(size_t bytes, void** out) {
     e = hipMalloc(&ws.ptr, bytes);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(sampler workspace)");
     // the per-row chunk counters start at zero; the kernels leave them so
-    e = hipMemset(ws.ptr, 0, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMemset(sampler workspace)");
+    e = hipMemsetAsync(ws.ptr, 0, bytes, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync(sampler workspace)");
     ws.bytes = bytes;
   }
   *out = ws.ptr;
@@ -129,7 +135,7 @@ int run_with_internal_ws(hi_rocm::SampleArgs& a, hipStream_t stream) {
   if (a.B > hi_rocm::kDoneRows) return fail(HI_ROCM_ERR_UNSUPPORTED, "batch above 65536 rows");
   const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(a.B, a.V);
   void* ws = nullptr;
-  int rc = internal_workspace(L.total, &ws);
+  int rc = internal_workspace(L.total, stream, &ws);
   if (rc != HI_ROCM_OK) return rc;
   carve(a, ws, L);
   hipError_t e = hi_rocm::launch_sample(a, stream, next_events());
@@ -244,12 +250,14 @@ int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* o
   return run_with_internal_ws(a, (hipStream_t)stream);
 }
 
-int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs) {
-  if (max_batch <= 0 || vocab <= 0 || n_logprobs < 0 || n_logprobs > HI_ROCM_MAX_LOGPROBS)
+int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs, void* stream) {
+  if (max_batch <= 0 || vocab <= 0 || n_logprobs < 0 || n_logprobs > HI_ROCM_MAX_LOGPROBS ||
+      stream == nullptr)
     return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sampler_reserve: invalid arguments");
   if (!vocab_ok(vocab)) return fail(HI_ROCM_ERR_UNSUPPORTED, "vocabulary too large");
+  if (max_batch > hi_rocm::kDoneRows) return fail(HI_ROCM_ERR_UNSUPPORTED, "batch above 65536 rows");
   void* ws = nullptr;
-  return internal_workspace(hi_rocm::workspace_layout(max_batch, vocab).total, &ws);
+  return internal_workspace(hi_rocm::workspace_layout(max_batch, vocab).total, (hipStream_t)stream, &ws);
 }
 
 int hi_rocm_sampler_workspace_bytes(int max_batch, int vocab, int n_logprobs, size_t* out_bytes) {
@@ -380,7 +388,7 @@ int hi_rocm_debug_distribution(const void* logits, int dtype, int batch, int voc
   a.mask = mask_words;
   const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(batch, vocab);
   void* ws = nullptr;
-  rc = internal_workspace(L.total, &ws);
+  rc = internal_workspace(L.total, (hipStream_t)stream, &ws);
   if (rc != HI_ROCM_OK) return rc;
   carve(a, ws, L);
   hipError_t e = hi_rocm::launch_debug_distribution(a, out_processed, out_probs, (hipStream_t)stream);

@@ -11,6 +11,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <map>
 #include <optional>
 #include <stdexcept>
 #include <string>
@@ -51,21 +52,46 @@ void status_check(int rc, const char* what) {
   if (rc != HI_ROCM_OK) throw SamplerError(std::string(what) + ": " + hi_rocm_last_error());
 }
 
-// A device buffer freed on scope exit (DeviceBuffer::alloc in runtime.rs).
+// Device staging for the per-call arrays (tokens, samples, row parameters):
+// one buffer per (thread, device), grown on demand and kept, in the manner
+// of the reference's thread-local buffer pool (runtime.rs:218-231).  Every
+// Sampler call ends by synchronising its stream, so a thread's buffer is
+// idle between calls and growing it needs no further wait.  The buffers
+// are not freed at thread exit (the HIP runtime may be gone by then).
 struct DeviceBuffer {
-  void* ptr = nullptr;
-  explicit DeviceBuffer(size_t bytes, const char* what) {
-    hip_check(hipMalloc(&ptr, bytes > 0 ? bytes : 1), what);
-  }
-  ~DeviceBuffer() {
-    if (ptr) (void)hipFree(ptr);
-  }
-  DeviceBuffer(const DeviceBuffer&) = delete;
-  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  void* ptr;
 };
 
+struct Staging {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+thread_local std::map<int, Staging> t_staging;
+
+constexpr size_t kSlot = 256;  // slot alignment
+
+size_t slot_bytes(size_t bytes) { return (bytes + kSlot - 1) & ~(kSlot - 1); }
+
+// `count` slots of `bytes` each in this thread's staging buffer.
+std::vector<DeviceBuffer> staging(size_t count, size_t bytes, const char* what) {
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), what);
+  Staging& st = t_staging[dev];
+  const size_t per = slot_bytes(bytes > 0 ? bytes : 1), need = per * count;
+  if (st.bytes < need) {
+    if (st.ptr) hip_check(hipFree(st.ptr), what);
+    st.ptr = nullptr;
+    st.bytes = 0;
+    hip_check(hipMalloc(&st.ptr, need), what);
+    st.bytes = need;
+  }
+  std::vector<DeviceBuffer> v;
+  for (size_t i = 0; i < count; ++i) v.push_back({(char*)st.ptr + i * per});
+  return v;
+}
+
 template <typename T>
-void upload(DeviceBuffer& b, const std::vector<T>& v, hipStream_t s, const char* what) {
+void upload(const DeviceBuffer& b, const std::vector<T>& v, hipStream_t s, const char* what) {
   hip_check(hipMemcpyAsync(b.ptr, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, s), what);
 }
 
@@ -85,7 +111,7 @@ class Sampler {
 
   // gpu.rs:15542-15559
   uint32_t argmax_last_row(const DeviceLogits& logits) {
-    DeviceBuffer token(sizeof(uint32_t), "allocating CUDA argmax token");
+    const DeviceBuffer token = staging(1, sizeof(uint32_t), "allocating CUDA argmax token")[0];
     status_check(hi_rocm_launch_argmax_last_row(logits.data, token.ptr, (int)logits.rows,
                                                 (int)logits.cols, stream_),
                  "argmax launch");
@@ -99,7 +125,7 @@ class Sampler {
     if (logits.rows == 0 || logits.cols == 0)
       throw SamplerError("CUDA sampled token selection requires non-empty logits, got " +
                          std::to_string(logits.rows) + "x" + std::to_string(logits.cols));
-    DeviceBuffer token(sizeof(uint32_t), "allocating CUDA sampled token");
+    const DeviceBuffer token = staging(1, sizeof(uint32_t), "allocating CUDA sampled token")[0];
     status_check(hi_rocm_launch_sample_last_row(logits.data, token.ptr, (int)logits.rows,
                                                 (int)logits.cols, temperature, top_p,
                                                 top_k_i32(top_k), sample, stream_),
@@ -115,7 +141,8 @@ class Sampler {
       throw SamplerError("CUDA batched argmax logits rows " + std::to_string(logits.rows) +
                          " do not match batch " + std::to_string(batch_count) + " x seq " +
                          std::to_string(seq_len));
-    DeviceBuffer tokens(batch_count * sizeof(uint32_t), "allocating CUDA batched argmax tokens");
+    const DeviceBuffer tokens =
+        staging(1, batch_count * sizeof(uint32_t), "allocating CUDA batched argmax tokens")[0];
     status_check(hi_rocm_launch_argmax_batched_last_token(logits.data, tokens.ptr,
                                                           (int)batch_count, (int)seq_len,
                                                           (int)logits.cols, stream_),
@@ -140,9 +167,8 @@ class Sampler {
           "CUDA batched sampled token selection requires non-empty logits, got batch=" +
           std::to_string(batch_count) + ", seq_len=" + std::to_string(seq_len) +
           ", cols=" + std::to_string(logits.cols));
-    DeviceBuffer tokens(batch_count * sizeof(uint32_t), "allocating CUDA batched sampled tokens");
-    DeviceBuffer sample_buffer(batch_count * sizeof(float),
-                               "allocating CUDA batched sampler samples");
+    const auto bufs = staging(2, batch_count * sizeof(uint32_t), "allocating CUDA batched sampled tokens");
+    const DeviceBuffer tokens = bufs[0], sample_buffer = bufs[1];
     upload(sample_buffer, samples, stream_, "copying CUDA batched sampler samples");
     status_check(hi_rocm_launch_sample_batched_last_token(
                      logits.data, tokens.ptr, sample_buffer.ptr, (int)batch_count, (int)seq_len,
@@ -193,11 +219,9 @@ class Sampler {
         top_ks.push_back(r.top_k ? (int32_t)*r.top_k : 0);
       }
     }
-    DeviceBuffer tokens(batch_count * sizeof(uint32_t), "allocating CUDA per-row selected tokens");
-    DeviceBuffer sample_buffer(batch_count * 4, "allocating CUDA per-row samples");
-    DeviceBuffer temperature_buffer(batch_count * 4, "allocating CUDA per-row temperatures");
-    DeviceBuffer top_p_buffer(batch_count * 4, "allocating CUDA per-row top_p values");
-    DeviceBuffer top_k_buffer(batch_count * 4, "allocating CUDA per-row top_k values");
+    const auto bufs = staging(5, batch_count * 4, "allocating CUDA per-row selected tokens");
+    const DeviceBuffer tokens = bufs[0], sample_buffer = bufs[1], temperature_buffer = bufs[2],
+                       top_p_buffer = bufs[3], top_k_buffer = bufs[4];
     upload(sample_buffer, samples, stream_, "copying CUDA per-row samples");
     upload(temperature_buffer, temperatures, stream_, "copying CUDA per-row temperatures");
     upload(top_p_buffer, top_ps, stream_, "copying CUDA per-row top_p values");

@@ -116,12 +116,14 @@ int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* o
                                                      int gpu_ranked, void* stream);
 
 /* The mirrors above take no workspace, like the reference.  They use a
- * per-device workspace that the library grows on demand (hipMalloc).  Call
- * this once, before any stream capture, with the largest shape to be
- * sampled so that no allocation happens afterwards. No reference
- * counterpart (the reference pre-warms its buffer pool instead,
+ * workspace per (device, stream) that the library grows on demand
+ * (hipMalloc; growing waits for that stream), so calls on different
+ * streams, from any threads, never share one.  Call this once per stream,
+ * before any stream capture, with the largest shape to be sampled on it so
+ * that no allocation happens afterwards.  No reference counterpart (the
+ * reference pre-warms its buffer pool instead,
  * crates/hi-cuda/src/runtime.rs:240-262). */
-int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs);
+int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs, void* stream);
 
 /* ---- extended pipeline (the decode-step API; proposal of the survey's
  *      boundary section, no single reference counterpart) ---- */

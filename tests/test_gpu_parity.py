@@ -217,6 +217,58 @@ def test_uniform_launchers_every_chunk_shape(hip, oracle, B, V):
     assert int(out[0].item()) & 0xffffffff == oracle.ranked_sample(x[B - 1], 0.9, 0.8, 50, float(u[0]))
 
 
+def test_concurrent_streams_and_threads(hip, oracle):
+    """The workspace-free mirrors from two host threads, each on its own
+    stream, calling at the same time: every call equals the oracle (each
+    (device, stream) has its own library workspace)."""
+    import threading
+    torch = _torch()
+    lib = hip.load()
+    jobs = []
+    for seed, (B, V) in enumerate(((64, 151936), (8, 100003))):
+        rng = np.random.default_rng(1000 + seed)
+        x = (rng.standard_normal((B, V)) * 3.0).astype(F32)
+        u = rng.random(B).astype(F32)
+        t = rng.uniform(0.5, 1.5, B).astype(F32)
+        tp = np.where(rng.random(B) < 0.5, np.float32(np.inf), np.float32(0.9)).astype(F32)
+        tk = rng.choice(np.array([0, 40, 300], np.int32), B)
+        tk[np.isinf(tp)] = np.maximum(tk[np.isinf(tp)], 40)  # every row ranked
+        want = [oracle.ranked_sample(x[b], float(t[b]), float(tp[b]), int(tk[b]) or None, float(u[b]))
+                for b in range(B)]
+        jobs.append(dict(B=B, V=V, x=dev(x), u=dev(u), t=dev(t), tp=dev(tp), tk=dev(tk), want=want,
+                         out=torch.zeros(B, dtype=torch.int32, device="cuda"), stream=torch.cuda.Stream()))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(j):
+        try:
+            for it in range(12):
+                j["out"].zero_()  # on the default stream; joined below
+                torch.cuda.current_stream().synchronize()
+                rc = lib.hi_rocm_launch_select_batched_last_token_per_row(
+                    j["x"].data_ptr(), j["out"].data_ptr(), j["u"].data_ptr(), j["t"].data_ptr(),
+                    j["tp"].data_ptr(), j["tk"].data_ptr(), j["B"], 1, j["V"], 1, j["stream"].cuda_stream)
+                if rc != 0:
+                    errors.append((j["B"], it, "rc", rc))
+                    return
+                j["stream"].synchronize()
+                got = j["out"].cpu().numpy().view(np.uint32).tolist()
+                if got != j["want"]:
+                    errors.append((j["B"], it, [b for b in range(j["B"]) if got[b] != j["want"][b]][:8]))
+                    return
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append((j["B"], repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(j,)) for j in jobs]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=100)
+    say(f"concurrent mirror calls: errors={errors}")
+    assert not any(th.is_alive() for th in threads)
+    assert not errors, errors
+
+
 def _finite_lane_rows(V, B, rng):
     """Rows whose finite-lane argmax (kernels.cu:7775-7801) depends on the
     tie order: tied maxima at residues 1 and 2, at indices 5 and 300, three

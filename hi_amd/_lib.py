@@ -46,6 +46,8 @@ SIGNATURES = {
     "hi_rocm_launch_sample_batched_last_token": (_i, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _i, _vp]),
     "hi_rocm_launch_select_batched_last_token_per_row": (
         _i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "hi_rocm_launch_select_batched_last_token_per_row_noalloc": (
+        _i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "hi_rocm_sampler_reserve": (_i, [_i, _i, _i, _vp]),
     "hi_rocm_profile_begin": (_i, [_i]),
     "hi_rocm_profile_end": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),

@@ -224,22 +224,22 @@ int hi_rocm_launch_sample_batched_last_token(const void* logits, void* output_to
   return run_with_internal_ws(a, (hipStream_t)stream);
 }
 
-int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* output_tokens,
-                                                     const void* samples,
-                                                     const void* temperatures,
-                                                     const void* top_ps, const void* top_ks,
-                                                     int batch_count, int seq_len, int cols,
-                                                     int gpu_ranked, void* stream) {
-  (void)gpu_ranked;
+}  // extern "C"
+
+namespace {
+
+// Argument checks and kernel arguments of the per-row mirror
+// (kernels.cu:14850-14880); `what` names the entry point in messages.
+int per_row_args(const void* logits, void* output_tokens, const void* samples, const void* temperatures,
+                 const void* top_ps, const void* top_ks, int batch_count, int seq_len, int cols, void* stream,
+                 const char* what, hi_rocm::SampleArgs& a) {
   if (logits == nullptr || output_tokens == nullptr || samples == nullptr ||
       temperatures == nullptr || top_ps == nullptr || top_ks == nullptr || batch_count <= 0 ||
       seq_len <= 0 || cols <= 0 || stream == nullptr)
-    return fail(HI_ROCM_ERR_ARGS,
-                "hi_rocm_launch_select_batched_last_token_per_row: invalid arguments");
+    return fail(HI_ROCM_ERR_ARGS, std::string(what) + ": invalid arguments");
   if (!vocab_ok(cols)) return fail(HI_ROCM_ERR_UNSUPPORTED, "vocabulary too large");
   const float* first = (const float*)logits + (int64_t)(seq_len - 1) * cols;
-  hi_rocm::SampleArgs a = base_args(first, HI_ROCM_DTYPE_F32, batch_count, cols,
-                                    (int64_t)seq_len * cols);
+  a = base_args(first, HI_ROCM_DTYPE_F32, batch_count, cols, (int64_t)seq_len * cols);
   a.pv.mode = hi_rocm::kParamsSoA;
   a.pv.temps = (const float*)temperatures;
   a.pv.top_ps = (const float*)top_ps;
@@ -247,6 +247,24 @@ int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* o
   a.pv.uniforms = (const float*)samples;
   a.pv.greedy_rule = hi_rocm::kGreedyIeee;  // kernels.cu:8058-8061
   a.out_tokens = (uint32_t*)output_tokens;
+  return HI_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* output_tokens,
+                                                     const void* samples,
+                                                     const void* temperatures,
+                                                     const void* top_ps, const void* top_ks,
+                                                     int batch_count, int seq_len, int cols,
+                                                     int gpu_ranked, void* stream) {
+  (void)gpu_ranked;
+  hi_rocm::SampleArgs a;
+  const int rc = per_row_args(logits, output_tokens, samples, temperatures, top_ps, top_ks, batch_count,
+                              seq_len, cols, stream, "hi_rocm_launch_select_batched_last_token_per_row", a);
+  if (rc != HI_ROCM_OK) return rc;
   return run_with_internal_ws(a, (hipStream_t)stream);
 }
 
@@ -433,6 +451,83 @@ int hi_rocm_launch_dsv4_indexer_select(const void* scores, int n_blocks, int top
                                               (uint8_t*)marks, (int32_t*)sel_out,
                                               (hipStream_t)stream);
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "indexer select launch");
+}
+
+}  // extern "C"
+
+// ---- the per-row mirror without allocation ------------------------------
+//
+// For callers that cannot call hipMalloc (code under stream capture, tight
+// serving loops): the workspace is a file-scope device array of fixed size,
+// one copy per GPU, held by every GPU the library runs on until the process
+// ends.  Every call on a GPU uses that GPU's copy, so calls that overlap on
+// one GPU (two streams, two threads) race; callers serialise them.
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = HI_ROCM_NOALLOC_SCRATCH_BYTES;  // per GPU
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// The per-row chunk counters of a call start at zero (the kernels leave
+// them so, but the array keeps whatever the last call left): a fill kernel,
+// not a memset node, so that the call can be captured in a graph.
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) p[i] = 0u;
+}
+
+std::mutex g_scratch_mutex;
+std::map<int, void*> g_scratch_ptr;  // device -> address of its `scratch`
+
+// The device address of the current device's `scratch`, looked up once per
+// device (the array's name in host code is not that address).
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  auto it = g_scratch_ptr.find(dev);
+  if (it == g_scratch_ptr.end()) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) return fail(HI_ROCM_ERR_HIP, "hipGetSymbolAddress(scratch): null address");
+    it = g_scratch_ptr.emplace(dev, ptr).first;
+  }
+  *out = it->second;
+  return HI_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hi_rocm_launch_select_batched_last_token_per_row_noalloc(
+    const void* logits, void* output_tokens, const void* samples, const void* temperatures, const void* top_ps,
+    const void* top_ks, int batch_count, int seq_len, int cols, int gpu_ranked, void* stream) {
+  (void)gpu_ranked;
+  static const char* kWhat = "hi_rocm_launch_select_batched_last_token_per_row_noalloc";
+  hi_rocm::SampleArgs a;
+  int rc = per_row_args(logits, output_tokens, samples, temperatures, top_ps, top_ks, batch_count, seq_len,
+                        cols, stream, kWhat, a);
+  if (rc != HI_ROCM_OK) return rc;
+  if (batch_count > hi_rocm::kDoneRows) return fail(HI_ROCM_ERR_UNSUPPORTED, "batch above 65536 rows");
+  const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(batch_count, cols);
+  if (L.total > kNoAllocScratchBytes)
+    return fail(HI_ROCM_ERR_UNSUPPORTED,
+                std::string(kWhat) + ": batch " + std::to_string(batch_count) + " x vocab " + std::to_string(cols) +
+                    " needs " + std::to_string(L.total) + " bytes of workspace, above the " +
+                    std::to_string(kNoAllocScratchBytes) + "-byte static scratch");
+  void* ptr = nullptr;
+  rc = scratch_address(&ptr);
+  if (rc != HI_ROCM_OK) return rc;
+  carve(a, ptr, L);
+  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((batch_count + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, a.done, batch_count);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "scratch counter reset");
+  e = hi_rocm::launch_sample(a, (hipStream_t)stream, next_events());
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "sampler launch");
 }
 
 }  // extern "C"

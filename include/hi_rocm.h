@@ -115,6 +115,24 @@ int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* o
                                                      int batch_count, int seq_len, int cols,
                                                      int gpu_ranked, void* stream);
 
+/* hi_rocm_launch_select_batched_last_token_per_row without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under stream capture, serving loops that forbid hipMalloc).  Same
+ * arguments, checks and results as the mirror above; its workspace is a
+ * static device array of HI_ROCM_NOALLOC_SCRATCH_BYTES per GPU (held by
+ * every GPU the library runs on until the process ends), so shapes whose
+ * workspace (hi_rocm_sampler_workspace_bytes) exceeds it are rejected with
+ * HI_ROCM_ERR_UNSUPPORTED -- e.g. up to 16 rows at vocabulary 151,936.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one
+ * GPU (several streams or threads) race and must be serialised. */
+#define HI_ROCM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int hi_rocm_launch_select_batched_last_token_per_row_noalloc(const void* logits, void* output_tokens,
+                                                             const void* samples,
+                                                             const void* temperatures,
+                                                             const void* top_ps, const void* top_ks,
+                                                             int batch_count, int seq_len, int cols,
+                                                             int gpu_ranked, void* stream);
+
 /* The mirrors above take no workspace, like the reference.  They use a
  * workspace per (device, stream) that the library grows on demand
  * (hipMalloc; growing waits for that stream), so calls on different

@@ -1,0 +1,78 @@
+"""The allocation-free per-row mirror against the allocating one.
+
+hi_rocm_launch_select_batched_last_token_per_row_noalloc keeps its
+workspace in a static device array; two calls in a row (the second on a
+smaller batch and vocabulary, so stale records of the first call are left
+in the array) must equal hi_rocm_launch_select_batched_last_token_per_row on
+the same inputs, bit for bit.  After the first call on the device (which
+places the array), the device's free memory must not change across calls,
+and shapes beyond the array are rejected.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+
+
+def _inputs(torch, rng, B, V):
+    x = (rng.standard_normal((B, V)) * 3.0).astype(F32)
+    u = rng.random(B).astype(F32)
+    t = rng.uniform(0.4, 1.6, B).astype(F32)
+    t[::7] = 0.0  # greedy rows
+    tp = np.where(rng.random(B) < 0.5, np.float32(np.inf), np.float32(0.9)).astype(F32)
+    tk = rng.choice(np.array([0, 1, 40, 300, 2000], np.int32), B)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    return [dev(x), dev(u), dev(t), dev(tp), dev(tk)]
+
+
+def _call(lib, fn, args, B, V, stream, out=None):
+    x, u, t, tp, tk = args
+    import torch
+    if out is None:
+        out = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    rc = getattr(lib, fn)(x.data_ptr(), out.data_ptr(), u.data_ptr(), t.data_ptr(), tp.data_ptr(),
+                          tk.data_ptr(), B, 1, V, 1, stream.cuda_stream)
+    return rc, out
+
+
+def test_noalloc_matches_allocating_mirror(hip):
+    import torch
+    lib = hip.load()
+    stream = torch.cuda.Stream()
+    rng = np.random.default_rng(2024)
+    shapes = [(16, 151936), (5, 70001)]
+    inputs = [_inputs(torch, rng, B, V) for B, V in shapes]
+    # set-up: the first call on the device looks up the array's address, and
+    # the runtime places the array on the device then; later calls must not
+    # change the free memory
+    rc, _ = _call(lib, "hi_rocm_launch_select_batched_last_token_per_row_noalloc", inputs[1], *shapes[1], stream)
+    hip.check(rc)
+    stream.synchronize()
+    outs = [torch.full((B,), -1, dtype=torch.int32, device="cuda") for B, _ in shapes]
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    got = []
+    for (B, V), args, out in zip(shapes, inputs, outs):
+        print(f"noalloc call B={B} V={V}", flush=True)
+        rc, out = _call(lib, "hi_rocm_launch_select_batched_last_token_per_row_noalloc", args, B, V, stream, out)
+        hip.check(rc)
+        stream.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    got = [o.cpu().numpy().copy() for o in outs]
+    assert free1 == free0, (free0, free1)
+    for (B, V), args, g in zip(shapes, inputs, got):
+        rc, out = _call(lib, "hi_rocm_launch_select_batched_last_token_per_row", args, B, V, stream)
+        hip.check(rc)
+        stream.synchronize()
+        want = out.cpu().numpy()
+        assert np.array_equal(g, want), (B, V, np.flatnonzero(g != want)[:8])
+        assert (g >= 0).all() and (g < V).all()
+    # a shape whose workspace exceeds the static array is rejected
+    B, V = 32, 151936
+    big = _inputs(torch, rng, B, V)
+    rc, _ = _call(lib, "hi_rocm_launch_select_batched_last_token_per_row_noalloc", big, B, V, stream)
+    assert rc == 2, rc
+    assert b"static scratch" in lib.hi_rocm_last_error()

@@ -1,6 +1,7 @@
 """Compile the hi-rocm HIP library in-tree (``hi_amd/libhi_rocm.so``) for gfx950."""
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -9,7 +10,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libhi_rocm.so")
-SOURCES = ["sampler_kernels.hip", "index_select.hip", "sampler_api.hip", "sampler_host.hip"]
+SOURCES = ["sampler_kernels.hip", "index_select.hip", "sampler_api.hip", "sampler_host.hip", "decode_step.hip"]
 
 # -ffp-contract=off: every f32/f64 operation that decides a token is a
 # separate IEEE rounding (fused operations are written out explicitly).
@@ -41,11 +42,16 @@ def build(verbose: bool = False) -> str:
     objs = []
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
-    for src in SOURCES:
+    def compile_one(src):
         obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         cmd = [cc, *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-c",
                os.path.join(CSRC, src), "-o", obj]
-        res = subprocess.run(cmd, capture_output=True, text=True)
+        return src, obj, subprocess.run(cmd, capture_output=True, text=True)
+
+    # the sources compile independently: one hipcc process each, at once
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+        results = list(pool.map(compile_one, SOURCES))
+    for src, obj, res in results:
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
         if verbose and res.stderr.strip():

@@ -32,6 +32,16 @@ int hip_fail(hipError_t e, const char* where) {
   return HI_ROCM_ERR_HIP;
 }
 
+}  // namespace
+
+namespace hi_rocm {
+// The calling thread's message for hi_rocm_last_error, from other sources.
+int api_fail(int code, const char* msg) { return fail(code, msg); }
+int api_hip_fail(hipError_t e, const char* where) { return hip_fail(e, where); }
+}  // namespace hi_rocm
+
+namespace {
+
 // Library-owned workspace for the workspace-free reference mirrors: one
 // buffer per (device, stream), grown on demand, never shrunk, like the
 // reference's thread-local buffer pool (crates/hi-cuda/src/runtime.rs:

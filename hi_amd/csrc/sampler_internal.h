@@ -231,6 +231,11 @@ hipError_t launch_debug_fold(const float* x, const uint32_t* m, int R, float a0,
 hipError_t launch_debug_distribution(const SampleArgs& a, float* out_proc, float* out_probs,
                                      hipStream_t stream);
 
+// Status helpers of the C ABI (sampler_api.hip): set the calling thread's
+// hi_rocm_last_error message and return the status code.
+int api_fail(int code, const char* msg);
+int api_hip_fail(hipError_t e, const char* where);
+
 // Exact top-k block selection of the DSV4 indexer (index_select.hip).
 hipError_t launch_index_select(const float* scores, int n, int top_k, uint8_t* marks, int32_t* sel,
                                hipStream_t stream);

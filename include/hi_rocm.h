@@ -115,6 +115,46 @@ int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* o
                                                      int batch_count, int seq_len, int cols,
                                                      int gpu_ranked, void* stream);
 
+/* ---- decode-step upkeep on the device (the reference keeps these on the
+ *      host: generated tokens in a Vec, crates/hi-cuda/src/lib.rs:4342, and
+ *      one StdRng draw per request per step, lib.rs:6415-6429) ---- */
+
+/* Per-request token history for the penalties (occurrence counts over the
+ * prompt and the generated tokens, crates/hi-mlx/src/generate.rs:52-73).
+ * Request slot r owns `capacity` entries of slot_ids / slot_counts (device
+ * u32[batch][capacity]) in first-occurrence order; lens[r] (device u32[batch])
+ * of them are in use.  Appends the pairs (rows[j], tokens[j]), j < n, in order
+ * (rows null: pair j is slot j, n <= batch); rows[j] outside [0, batch) are
+ * skipped; HI_ROCM_HISTORY_RESET as a token empties the slot (a new request).
+ * A new id that finds its slot full is dropped and counted in *overflow
+ * (device u32, may be null).  No allocation: graph-capturable. */
+#define HI_ROCM_HISTORY_RESET 0xffffffffu
+int hi_rocm_history_append(uint32_t* slot_ids, uint32_t* slot_counts, uint32_t* lens, int batch, int capacity,
+                           const int32_t* rows, const uint32_t* tokens, int n, uint32_t* overflow, void* stream);
+
+/* The compact CSR that hi_rocm_sample reads (hist_offsets u32[batch + 1],
+ * hist_ids / hist_counts u32[batch * capacity] at most), from the slots. */
+int hi_rocm_history_pack(const uint32_t* slot_ids, const uint32_t* slot_counts, const uint32_t* lens, int batch,
+                         int capacity, uint32_t* out_offsets, uint32_t* out_ids, uint32_t* out_counts, void* stream);
+
+/* Host: the ChaCha12 key of rand 0.8's StdRng::seed_from_u64(seed)
+ * (rand_core 0.6's PCG32 expansion; key: u32[8]).  lib.rs:4865 seeds each
+ * sampled request this way. */
+int hi_rocm_rng_key_from_seed(uint64_t seed, uint32_t* key);
+
+/* One uniform per request (lib.rs:6415-6429 continuous_sampling_values):
+ * request b with sampled[b] != 0 (sampled null: every request) draws
+ * gen_range(0.0f32..1.0f32) from its StdRng -- keystream word
+ * words_used[b] of ChaCha12 under keys[b] (u32[batch][8]) -- and advances
+ * words_used[b] (device u64[batch]); the others get 0.  Device arrays;
+ * graph-capturable. */
+int hi_rocm_rng_uniforms(const uint32_t* keys, uint64_t* words_used, const uint8_t* sampled, float* out_uniforms,
+                         int batch, void* stream);
+
+/* Host: one ChaCha block (RFC 8439 block function) of `rounds` rounds with
+ * state words 12-15 given; for the known-answer tests. */
+int hi_rocm_debug_chacha_block(const uint32_t* key, const uint32_t* words12_15, int rounds, uint32_t* out);
+
 /* hi_rocm_launch_select_batched_last_token_per_row without any allocation.
  * No counterpart in the reference: it is for callers that cannot allocate
  * (code under stream capture, serving loops that forbid hipMalloc).  Same

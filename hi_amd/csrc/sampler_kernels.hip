@@ -39,6 +39,7 @@
 #include "hi_rocm.h"
 #include "exact_expf.h"
 #include "fold_wg.h"
+#include "wave_ops.h"
 #include "sampler_internal.h"
 
 namespace hi_rocm {
@@ -233,13 +234,6 @@ constexpr int kDppMirror = 0x140;      // row_mirror
 constexpr int kDppShr1 = 0x111;        // row_shr:1 (+1, +3, +7 for :2, :4, :8)
 constexpr int kDppBcast15 = 0x142;     // row_bcast:15
 constexpr int kDppBcast31 = 0x143;     // row_bcast:31
-
-// v moved by CTRL; lanes of rows outside ROW_MASK (or with no source lane
-// when BC) get `old`.
-template <int CTRL, int ROW_MASK = 0xf, bool BC = false>
-__device__ __forceinline__ uint32_t dpp32(uint32_t old, uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xf, BC);
-}
 
 // Reduction of a 32-bit value under a commutative, associative op with
 // identity `id`.
@@ -1396,29 +1390,6 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
 
 constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
 constexpr int kSpecChunks = 40;   // rows of up to this many chunks load their candidates early
-
-// Sequential f32 sums over the wave's lanes: lane l < n returns
-// ((start + v_0) + v_1) + ... + v_l, the reference's left-to-right fold
-// (gpu.rs:834-836, 851, 878, 889-896); lanes from n on hold partial sums.
-// Lane 0 holds start + v_0 from the outset; each step adds v to the running
-// sums moved one lane up (wave_shr:1 filling lane 0 with zero, which the
-// compiler fuses into the add).  After step s lanes [0, s] hold their
-// final sums and later steps leave them unchanged, so steps run in groups
-// of 8 (n - 1 steps are needed).  No lane's sum is -0 (the terms and
-// `start` are not negative), so 0 + x == x at lane 0.
-__device__ __forceinline__ float wave_fold_u(float u) {
-  return __uint_as_float(dpp32<0x138, 0xf, true>(0u, __float_as_uint(u)));
-}
-__device__ __forceinline__ float wave_fold_f32(float v, float start, int n) {
-  const float u = (threadIdx.x & 63u) == 0u ? start + v : v;
-  float p = u;
-  #pragma unroll 1
-  for (int s = 1; s < n; s += 8) {
-    #pragma unroll
-    for (int i = 0; i < 8; ++i) p = wave_fold_u(p) + u;
-  }
-  return p;
-}
 
 // wave_fold_f32 that stops once a lane at or below the last final one has
 // hit set and p >= cutoff; returns the first such lane (-1: none, all n

@@ -115,6 +115,17 @@ int hi_rocm_launch_select_batched_last_token_per_row(const void* logits, void* o
                                                      int batch_count, int seq_len, int cols,
                                                      int gpu_ranked, void* stream);
 
+/* kernels.cu:8482 hi_cuda_launch_moe_topk_router (kernel kernels.cu:536-684):
+ * scores f32[rows][experts], output_ids u32[rows][top_k], output_weights
+ * f32[rows][top_k], selection_bias f32[experts] or null (sigmoid gating
+ * ranks on score + bias, weights stay bias-free).  Same checks (status 1)
+ * and semantics; one wave per row; experts <= 2048 (status 2 above).  The
+ * exponential is glibc's expf, as everywhere in this library, where the
+ * reference calls CUDA's expf. */
+int hi_rocm_launch_moe_topk_router(const void* scores, void* output_ids, void* output_weights,
+                                   const void* selection_bias, int rows, int experts, int top_k,
+                                   int norm_topk, int gating_sigmoid, float weights_scale, void* stream);
+
 /* ---- decode-step upkeep on the device (the reference keeps these on the
  *      host: generated tokens in a Vec, crates/hi-cuda/src/lib.rs:4342, and
  *      one StdRng draw per request per step, lib.rs:6415-6429) ---- */

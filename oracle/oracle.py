@@ -77,9 +77,9 @@ _lib = None
 
 def build(force: bool = False) -> str:
     """Compile liboracle.so with the committed Makefile."""
-    if force or not os.path.exists(_LIB_PATH):
-        subprocess.run(["make", "-s", "-B" if force else "", "-C", _HERE], check=True,
-                       stdout=subprocess.DEVNULL)
+    # make rebuilds when sampler_oracle.c is newer than the library
+    args = ["make", "-s"] + (["-B"] if force else []) + ["-C", _HERE]
+    subprocess.run(args, check=True, stdout=subprocess.DEVNULL)
     return _LIB_PATH
 
 
@@ -120,6 +120,10 @@ def lib() -> ctypes.CDLL:
                                          ctypes.c_void_p, ctypes.c_void_p]
         L.hro_fold_f32.restype = ctypes.c_float
         L.hro_fold_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+        L.hro_moe_router.restype = None
+        L.hro_moe_router.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_float]
         _lib = L
     return _lib
 
@@ -270,3 +274,16 @@ def indexer_select(scores, top_k):
     if took < 0:
         raise ValueError("indexer_select: n and top_k must be positive")
     return sel[:took], marks
+
+
+def moe_router(scores, top_k, bias=None, norm_topk=False, gating_sigmoid=False, weights_scale=1.0):
+    """MoE router top-k (kernels.cu:536-684, glibc expf): ids u32 and weights
+    f32, each [rows, top_k]."""
+    x = np.ascontiguousarray(scores, dtype=np.float32)
+    rows, experts = x.shape
+    ids = np.zeros((rows, top_k), np.uint32)
+    w = np.zeros((rows, top_k), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    lib().hro_moe_router(_ptr(x), _ptr(ids), _ptr(w), _ptr(b), rows, experts, int(top_k), int(bool(norm_topk)),
+                         int(bool(gating_sigmoid)), float(weights_scale))
+    return ids, w

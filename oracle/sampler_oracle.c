@@ -664,3 +664,106 @@ int64_t hro_indexer_select(const float* scores, int64_t n, int64_t top_k, uint8_
   qsort(sel, (size_t)take, sizeof(int32_t), hro_int_cmp);
   return take;
 }
+
+/* ---- MoE router top-k (kernels.cu:536-684 moe_topk_router_kernel) ----
+ * The reference's per-row loops restated literally, one row at a time,
+ * with glibc expf in place of CUDA's expf (which cannot be reproduced
+ * here).  scores [rows][experts]; ids u32 / weights f32 [rows][top_k];
+ * bias f32[experts] or NULL. */
+void hro_moe_router(const float* scores, uint32_t* output_ids, float* output_weights,
+                    const float* selection_bias, int rows, int experts, int top_k, int norm_topk,
+                    int gating_sigmoid, float weights_scale) {
+  for (int row = 0; row < rows; ++row) {
+    const float* row_scores = scores + (int64_t)row * experts;
+    uint32_t* row_ids = output_ids + (int64_t)row * top_k;
+    float* row_weights = output_weights + (int64_t)row * top_k;
+    if (gating_sigmoid) {
+      /* kernels.cu:556-604 */
+      float previous_key = INFINITY;
+      int previous_id = -1;
+      float selected_sum = 0.0f;
+      for (int rank = 0; rank < top_k; ++rank) {
+        int best_id = -1;
+        float best_key = -INFINITY, best_weight = 0.0f;
+        for (int expert = 0; expert < experts; ++expert) {
+          float score = 1.0f / (1.0f + expf(-row_scores[expert]));
+          if (!isfinite(score)) score = 0.0f;
+          float key = score;
+          if (selection_bias != NULL) key += selection_bias[expert];
+          const int eligible = previous_id < 0 || key < previous_key ||
+                               (key == previous_key && expert > previous_id);
+          if (!eligible) continue;
+          if (best_id < 0 || key > best_key || (key == best_key && expert < best_id)) {
+            best_id = expert;
+            best_key = key;
+            best_weight = score;
+          }
+        }
+        if (best_id < 0) {
+          best_id = rank < experts ? rank : experts - 1;
+          best_key = -INFINITY;
+          best_weight = 0.0f;
+        }
+        row_ids[rank] = (uint32_t)best_id;
+        row_weights[rank] = best_weight;
+        selected_sum += best_weight;
+        previous_id = best_id;
+        previous_key = best_key;
+      }
+      if (norm_topk && top_k > 1 && selected_sum > 1.0e-7f && isfinite(selected_sum))
+        for (int rank = 0; rank < top_k; ++rank) row_weights[rank] /= selected_sum;
+      if (weights_scale != 1.0f)
+        for (int rank = 0; rank < top_k; ++rank) row_weights[rank] *= weights_scale;
+      continue;
+    }
+    /* kernels.cu:606-684 */
+    float max_score = -INFINITY;
+    for (int expert = 0; expert < experts; ++expert)
+      if (row_scores[expert] > max_score) max_score = row_scores[expert];
+    float denom = 0.0f;
+    int fallback = !isfinite(max_score);
+    if (!fallback) {
+      for (int expert = 0; expert < experts; ++expert) denom += expf(row_scores[expert] - max_score);
+      fallback = denom <= 0.0f || !isfinite(denom);
+    }
+    if (fallback) {
+      const float weight = (norm_topk && top_k > 1) ? 1.0f / (float)top_k : 1.0f / (float)experts;
+      for (int rank = 0; rank < top_k; ++rank) {
+        row_ids[rank] = (uint32_t)rank;
+        row_weights[rank] = weight;
+      }
+      continue;
+    }
+    float previous_weight = INFINITY;
+    int previous_id = -1;
+    float selected_sum = 0.0f;
+    for (int rank = 0; rank < top_k; ++rank) {
+      int best_id = -1;
+      float best_weight = -1.0f;
+      for (int expert = 0; expert < experts; ++expert) {
+        float weight = expf(row_scores[expert] - max_score) / denom;
+        if (!isfinite(weight)) weight = 0.0f;
+        const int eligible = previous_id < 0 || weight < previous_weight ||
+                             (weight == previous_weight && expert > previous_id);
+        if (!eligible) continue;
+        if (best_id < 0 || weight > best_weight || (weight == best_weight && expert < best_id)) {
+          best_id = expert;
+          best_weight = weight;
+        }
+      }
+      if (best_id < 0) {
+        best_id = rank < experts ? rank : experts - 1;
+        best_weight = 0.0f;
+      }
+      row_ids[rank] = (uint32_t)best_id;
+      row_weights[rank] = best_weight;
+      selected_sum += best_weight;
+      previous_id = best_id;
+      previous_weight = best_weight;
+    }
+    if (norm_topk && top_k > 1 && selected_sum > 1.0e-7f && isfinite(selected_sum))
+      for (int rank = 0; rank < top_k; ++rank) row_weights[rank] /= selected_sum;
+    if (weights_scale != 1.0f)
+      for (int rank = 0; rank < top_k; ++rank) row_weights[rank] *= weights_scale;
+  }
+}

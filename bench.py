@@ -225,12 +225,13 @@ def time_graph_b1(torch, w, steps, warmup):
     return graph_us, in_graph_us, eager_us
 
 
-def time_indexer_select(torch, shapes=((1162, 512), (65536, 2048)), launches=200):
+def time_indexer_select(torch, shapes=((1162, 512), (65536, 2048)), launches=200, cpu=True):
     """DSV4 indexer block selection (hi_rocm_launch_dsv4_indexer_select):
     us per launch over back-to-back launches on one stream, bracketed by HIP
     events on that stream.  Algorithmic bytes per launch: n scores f32 read,
     n marks u8 and min(k, n) int32 indices written.  One workgroup per
-    launch, so the bound is latency, not HBM."""
+    launch, so the bound is latency, not HBM.  CPU baseline: the host
+    selection the reference's CPU path runs, on the same scores."""
     import ctypes
     from hi_amd import _lib
     from hi_amd.workloads import indexer_test_scores
@@ -256,9 +257,68 @@ def time_indexer_select(torch, shapes=((1162, 512), (65536, 2048)), launches=200
         e1.synchronize()
         us = e0.elapsed_time(e1) * 1000.0 / launches
         alg = n * 4 + n + min(n, k) * 4
-        out.append({"n_blocks": n, "top_k": k, "us_per_launch": us, "algorithmic_bytes": alg,
-                    "gbs": alg / us / 1e3})
+        rec = {"n_blocks": n, "top_k": k, "us_per_launch": us, "algorithmic_bytes": alg, "gbs": alg / us / 1e3}
+        if cpu:
+            # the reference's host path (dsv4_cpu.rs:3258-3270: rank by
+            # total_cmp, keep the first k, sort the kept indices), restated
+            # in C with qsort, one thread
+            from oracle import oracle
+            oracle.build()
+            xs = x.cpu().numpy()
+            calls, t0 = 0, time.perf_counter()
+            while calls < 3 or time.perf_counter() - t0 < 0.5:
+                oracle.indexer_select(xs, k)
+                calls += 1
+            rec["cpu_baseline"] = {"us_per_call": (time.perf_counter() - t0) / calls * 1e6, "cores": 1,
+                                   "kind": "port", "sample": f"{calls} calls on the same scores"}
+        out.append(rec)
     return out
+
+
+def time_router(torch, rows=4096, experts=256, top_k=8, launches=100, cpu=True):
+    """MoE router top-k (hi_rocm_launch_moe_topk_router), DeepSeek-V3-style
+    sigmoid gating with a selection bias and normalised weights: us per
+    launch over back-to-back launches between HIP events on the launch
+    stream.  Algorithmic bytes: scores read once, ids and weights written.
+    CPU baseline: the oracle's literal restatement of the reference kernel's
+    per-row loops (one thread), on a bounded sample of the rows."""
+    import ctypes
+    from hi_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(3)
+    xs = rng.standard_normal((rows, experts)).astype(np.float32)
+    bs = (rng.standard_normal(experts) * 0.1).astype(np.float32)
+    x, b = torch.from_numpy(xs).cuda(), torch.from_numpy(bs).cuda()
+    ids = torch.empty((rows, top_k), dtype=torch.int32, device="cuda")
+    w = torch.empty((rows, top_k), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    args = (x.data_ptr(), ids.data_ptr(), w.data_ptr(), b.data_ptr(), rows, experts, top_k, 1, 1, 2.5,
+            ctypes.c_void_p(stream.cuda_stream))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for _ in range(10):
+            _lib.check(lib.hi_rocm_launch_moe_topk_router(*args))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(launches):
+            _lib.check(lib.hi_rocm_launch_moe_topk_router(*args))
+        e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / launches
+    alg = rows * experts * 4 + experts * 4 + rows * top_k * 8
+    rec = {"rows": rows, "experts": experts, "top_k": top_k, "gating": "sigmoid+bias, normalised",
+           "us_per_launch": us, "rows_per_s": rows / (us * 1e-6), "algorithmic_bytes": alg, "gbs": alg / us / 1e3}
+    if cpu:
+        from oracle import oracle
+        oracle.build()
+        n, t0 = 0, time.perf_counter()
+        while n < rows and (n < 64 or time.perf_counter() - t0 < 1.0):
+            oracle.moe_router(xs[n:n + 64], top_k, bias=bs, norm_topk=True, gating_sigmoid=True, weights_scale=2.5)
+            n += 64
+        dt = time.perf_counter() - t0
+        rec["cpu_baseline"] = {"rows_per_s": n / dt, "cores": 1, "kind": "port",
+                               "sample": f"{n} of the {rows} rows"}
+    return rec
 
 
 def cpu_baseline(w, budget_s=15.0):
@@ -398,7 +458,8 @@ def main():
     from hi_amd.workloads import config2, config4, config5
     res["other_configs"] = {f"c{i}": time_config(torch, mk(), args.steps, args.warmup)
                             for i, mk in ((2, config2), (4, config4), (5, config5))}
-    res["dsv4_indexer_select"] = time_indexer_select(torch)
+    res["dsv4_indexer_select"] = time_indexer_select(torch, cpu=not args.no_cpu_baseline)
+    res["moe_router"] = time_router(torch, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w3, args.cpu_budget)
         res["cpu_baseline_all_cores"] = cpu_baseline_all_cores(w3)

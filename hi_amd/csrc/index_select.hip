@@ -33,6 +33,7 @@
 #include <stdint.h>
 
 #include "sampler_internal.h"
+#include "wave_ops.h"
 
 namespace hi_rocm {
 namespace {
@@ -162,13 +163,210 @@ index_select_kernel(const float* __restrict__ scores, int n, int take, uint8_t* 
   }
 }
 
+// The same three steps with every key held in registers: wave w owns the
+// contiguous span [w * 64 * PER, (w + 1) * 64 * PER), lane l its elements
+// span + j * 64 + l (j < PER), loaded once with all loads in flight (the
+// loop form above reloads the scores on every pass and waits on each load).
+// The descent takes 12, 10 and 10 bits: float keys crowd into few values of
+// their top 8 bits (sign and exponent), and lanes of one wave adding to the
+// same LDS bin are serialised, so the first digit reaches 3 mantissa bits
+// into one shared 4096-bin histogram.  For n <= 1024 * PER.
+constexpr int kRegBins = 4096;
+
+struct RegSelLds {
+  uint32_t hist[kRegBins];
+  uint32_t wsum[kSelWaves];
+  uint32_t span_gt[kSelWaves];
+  uint32_t span_eq[kSelWaves];
+  uint32_t digit, above, count;
+};
+
+// The bin of hist[0, 1024 * BPT) that holds the need-th largest key
+// (thread t owns bins [t * BPT, t * BPT + BPT)), with the keys in the bins
+// above it and in it.  Ends with a barrier; every thread reads the result.
+template <int BPT>
+__device__ __forceinline__ void reg_find_bin(RegSelLds& L, uint32_t need) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  uint32_t c[BPT], tot = 0u;
+  #pragma unroll
+  for (int q = 0; q < BPT; ++q) {
+    c[q] = L.hist[tid * BPT + q];
+    tot += c[q];
+  }
+  uint32_t sfx = tot;  // this lane and the lanes above it in the wave
+  #pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = (uint32_t)__shfl_down((int)sfx, (unsigned)d, 64);
+    if (lane + d < 64) sfx += y;
+  }
+  if (lane == 0) L.wsum[wid] = sfx;
+  __syncthreads();
+  uint32_t above = sfx - tot;
+  for (int w = wid + 1; w < kSelWaves; ++w) above += L.wsum[w];
+  #pragma unroll
+  for (int q = BPT - 1; q >= 0; --q) {
+    if (above < need && above + c[q] >= need) {
+      L.digit = (uint32_t)(tid * BPT + q);
+      L.above = above;
+      L.count = c[q];
+    }
+    above += c[q];
+  }
+  __syncthreads();
+}
+
+template <int PER>
+__global__ void __launch_bounds__(kSelThreads)
+index_select_reg_kernel(const float* __restrict__ scores, int n, int take, uint8_t* __restrict__ marks,
+                        int32_t* __restrict__ sel, int vec) {
+  static_assert(PER % 4 == 0, "four consecutive elements per lane and group");
+  constexpr int G = PER / 4;  // groups of 256 elements per wave
+  __shared__ RegSelLds L;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = tid >> 6;
+  const int s0 = wid * 64 * PER;
+  // lane l holds elements s0 + g * 256 + 4 * l + q, q < 4 (16-byte loads
+  // and 4-byte mark stores when `vec`: aligned pointers and n a multiple of
+  // 4; otherwise element by element)
+  uint32_t key[PER];
+  if (vec) {
+    // every load issued before any is used: out-of-range groups load
+    // element 0 and are masked afterwards
+    float4 v[G];
+    #pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int i0 = s0 + g * 256 + 4 * lane;
+      v[g] = *reinterpret_cast<const float4*>(scores + (i0 < n ? i0 : 0));
+    }
+    #pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const bool in = s0 + g * 256 + 4 * lane < n;
+      key[4 * g + 0] = in ? total_key(v[g].x) : 0u;
+      key[4 * g + 1] = in ? total_key(v[g].y) : 0u;
+      key[4 * g + 2] = in ? total_key(v[g].z) : 0u;
+      key[4 * g + 3] = in ? total_key(v[g].w) : 0u;
+    }
+  } else {
+    float v[PER];
+    #pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = s0 + (j >> 2) * 256 + 4 * lane + (j & 3);
+      v[j] = scores[i < n ? i : 0];
+    }
+    #pragma unroll
+    for (int j = 0; j < PER; ++j) key[j] = s0 + (j >> 2) * 256 + 4 * lane + (j & 3) < n ? total_key(v[j]) : 0u;
+  }
+  auto idx = [&](int j) { return s0 + (j >> 2) * 256 + 4 * lane + (j & 3); };
+  // 1. radix descent over bits [31:20], [19:10], [9:0] (keys past n never count)
+  uint32_t prefix = 0u;
+  int shift = 32;
+  uint32_t need = (uint32_t)take;
+  #pragma unroll 1
+  for (int pass = 0; pass < 3; ++pass) {
+    const int dshift = pass == 0 ? 20 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 0 ? 4095u : 1023u;
+    const int nb = pass == 0 ? kRegBins : 1024;
+    for (int i = tid; i < nb; i += kSelThreads) L.hist[i] = 0u;
+    __syncthreads();
+    #pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (idx(j) < n && (pass == 0 || (key[j] >> shift) == prefix)) atomicAdd(&L.hist[(key[j] >> dshift) & dmask], 1u);
+    __syncthreads();
+    if (pass == 0) reg_find_bin<kRegBins / kSelThreads>(L, need);
+    else reg_find_bin<1>(L, need);
+    const uint32_t d = L.digit;
+    need -= L.above;
+    const bool whole = L.count == need;
+    prefix = pass == 0 ? d : ((prefix << 10) | d);
+    shift = dshift;
+    __syncthreads();  // L is rewritten by the next pass
+    if (whole) break;
+  }
+  // 2. per-wave counts (per-lane counters, one reduction)
+  uint32_t gt = 0u, eq = 0u;
+  #pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const bool in = idx(j) < n;
+    const uint32_t hi = key[j] >> shift;
+    gt += (in && hi > prefix) ? 1u : 0u;
+    eq += (in && hi == prefix) ? 1u : 0u;
+  }
+  uint32_t packed = (eq << 16) | gt;  // per lane <= PER each
+  #pragma unroll
+  for (int o = 32; o > 0; o >>= 1) packed += (uint32_t)__shfl_xor((int)packed, o, 64);
+  if (lane == 0) {
+    L.span_gt[wid] = packed & 0xffffu;
+    L.span_eq[wid] = packed >> 16;
+  }
+  __syncthreads();
+  uint32_t gt_run = 0u, eq_run = 0u;
+  #pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    gt_run += w < wid ? L.span_gt[w] : 0u;
+    eq_run += w < wid ? L.span_eq[w] : 0u;
+  }
+  // 3. marks and ascending output, a group of 256 elements at a time: the
+  //    (greater, equal) counts before each element come from one exclusive
+  //    scan of the lanes' packed counts
+  #pragma unroll
+  for (int g = 0; g < G; ++g) {
+    uint32_t cg = 0u, ce = 0u;
+    bool is_gt[4], is_eq[4];
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool in = idx(4 * g + q) < n;
+      const uint32_t hi = key[4 * g + q] >> shift;
+      is_gt[q] = in && hi > prefix;
+      is_eq[q] = in && hi == prefix;
+      cg += is_gt[q] ? 1u : 0u;
+      ce += is_eq[q] ? 1u : 0u;
+    }
+    const uint32_t mine = (ce << 16) | cg;
+    const uint32_t incl = wave_incl_scan_u32(mine);
+    const uint32_t excl = incl - mine;
+    uint32_t G0 = gt_run + (excl & 0xffffu), E0 = eq_run + (excl >> 16);
+    uint32_t mk = 0u;
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool keep = is_gt[q] || (is_eq[q] && E0 < need);
+      const uint32_t slot = G0 + min(E0, need);
+      if (keep && slot < (uint32_t)take) sel[slot] = idx(4 * g + q);
+      mk |= (keep ? 1u : 0u) << (8 * q);
+      G0 += is_gt[q] ? 1u : 0u;
+      E0 += is_eq[q] ? 1u : 0u;
+    }
+    const int i0 = idx(4 * g);
+    if (vec && i0 < n) {
+      *reinterpret_cast<uint32_t*>(marks + i0) = mk;
+    } else {
+      #pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (i0 + q < n) marks[i0 + q] = (uint8_t)(mk >> (8 * q));
+    }
+    const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    gt_run += tot & 0xffffu;
+    eq_run += tot >> 16;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_index_select(const float* scores, int n, int top_k, uint8_t* marks, int32_t* sel,
                                hipStream_t stream) {
   const int take = top_k < n ? top_k : n;
-  hipLaunchKernelGGL(index_select_kernel, dim3(1), dim3(kSelThreads), 0, stream, scores, n, take,
-                     marks, sel);
+  const int vec = ((uintptr_t)scores % 16 == 0) && ((uintptr_t)marks % 4 == 0) && (n % 4 == 0);
+  if (n <= kSelThreads * 4)
+    hipLaunchKernelGGL(index_select_reg_kernel<4>, dim3(1), dim3(kSelThreads), 0, stream, scores, n, take, marks, sel,
+                       vec);
+  else if (n <= kSelThreads * 16)
+    hipLaunchKernelGGL(index_select_reg_kernel<16>, dim3(1), dim3(kSelThreads), 0, stream, scores, n, take, marks,
+                       sel, vec);
+  else if (n <= kSelThreads * 64)
+    hipLaunchKernelGGL(index_select_reg_kernel<64>, dim3(1), dim3(kSelThreads), 0, stream, scores, n, take, marks,
+                       sel, vec);
+  else
+    hipLaunchKernelGGL(index_select_kernel, dim3(1), dim3(kSelThreads), 0, stream, scores, n, take, marks, sel);
   return hipGetLastError();
 }
 

@@ -457,6 +457,9 @@ int hi_rocm_launch_dsv4_indexer_select(const void* scores, int n_blocks, int top
   if (scores == nullptr || marks == nullptr || sel_out == nullptr || n_blocks <= 0 || top_k <= 0 ||
       stream == nullptr)
     return fail(HI_ROCM_ERR_ARGS, "hi_rocm_launch_dsv4_indexer_select: invalid arguments");
+  // the kernels' span and loop arithmetic is in int: keep it clear of overflow
+  if (n_blocks > INT32_MAX - (1 << 20))
+    return fail(HI_ROCM_ERR_UNSUPPORTED, "hi_rocm_launch_dsv4_indexer_select: n_blocks above 2^31 - 2^20");
   hipError_t e = hi_rocm::launch_index_select((const float*)scores, n_blocks, top_k,
                                               (uint8_t*)marks, (int32_t*)sel_out,
                                               (hipStream_t)stream);

@@ -227,13 +227,6 @@ __device__ __forceinline__ float apply_penalties_norep(float l, uint32_t cnt, co
 // every lane.  The scan is the Hillis-Steele sequence row_shr:1,2,4,8
 // followed by the same two row broadcasts.  Each step is one VALU
 // instruction with no LDS round trip.
-constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
-constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
-constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
-constexpr int kDppMirror = 0x140;      // row_mirror
-constexpr int kDppShr1 = 0x111;        // row_shr:1 (+1, +3, +7 for :2, :4, :8)
-constexpr int kDppBcast15 = 0x142;     // row_bcast:15
-constexpr int kDppBcast31 = 0x143;     // row_bcast:31
 
 // Reduction of a 32-bit value under a commutative, associative op with
 // identity `id`.
@@ -296,16 +289,6 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   }));
 }
 
-// Inclusive prefix sum over the wave in lane order.
-__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
-  v += dpp32<kDppShr1, 0xf, true>(0u, v);
-  v += dpp32<kDppShr1 + 1, 0xf, true>(0u, v);
-  v += dpp32<kDppShr1 + 3, 0xf, true>(0u, v);
-  v += dpp32<kDppShr1 + 7, 0xf, true>(0u, v);
-  v += dpp32<kDppBcast15, 0xa>(0u, v);
-  v += dpp32<kDppBcast31, 0xc>(0u, v);
-  return v;
-}
 __device__ __forceinline__ uint32_t wave_last_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }

@@ -5,6 +5,15 @@
 
 namespace hi_rocm {
 
+// DPP controls (gfx9 encodings)
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+constexpr int kDppShr1 = 0x111;        // row_shr:1 (+1, +3, +7 for :2, :4, :8)
+constexpr int kDppBcast15 = 0x142;     // row_bcast:15
+constexpr int kDppBcast31 = 0x143;     // row_bcast:31
+
 // v moved by CTRL; lanes of rows outside ROW_MASK (or with no source lane
 // when BC) get `old`.
 template <int CTRL, int ROW_MASK = 0xf, bool BC = false>
@@ -33,6 +42,17 @@ __device__ __forceinline__ float wave_fold_f32(float v, float start, int n) {
     for (int i = 0; i < 8; ++i) p = wave_fold_u(p) + u;
   }
   return p;
+}
+
+// Inclusive prefix sum over the wave in lane order.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  v += dpp32<kDppShr1, 0xf, true>(0u, v);
+  v += dpp32<kDppShr1 + 1, 0xf, true>(0u, v);
+  v += dpp32<kDppShr1 + 3, 0xf, true>(0u, v);
+  v += dpp32<kDppShr1 + 7, 0xf, true>(0u, v);
+  v += dpp32<kDppBcast15, 0xa>(0u, v);
+  v += dpp32<kDppBcast31, 0xc>(0u, v);
+  return v;
 }
 
 }  // namespace hi_rocm

@@ -24,6 +24,8 @@ def launch_dsv4_indexer_select(scores: torch.Tensor, n_blocks: int, top_k: int,
     (int32, ascending) and 1/0 per block into ``marks`` (uint8)."""
     if n_blocks <= 0 or n_blocks > 2**31 - 1:
         raise ValueError("dsv4 indexer select blocks out of range")
+    if n_blocks > 2**31 - 1 - 2**20:
+        raise ValueError("dsv4 indexer select: n_blocks above 2^31 - 2^20 is not supported")
     if top_k <= 0 or top_k > 2**31 - 1:
         raise ValueError("dsv4 indexer select top_k out of range")
     if scores.dtype != torch.float32 or not scores.is_cuda or not scores.is_contiguous():

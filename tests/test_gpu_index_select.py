@@ -129,3 +129,25 @@ def test_python_front_end(env):
         launch_dsv4_indexer_select(torch.from_numpy(x).cuda(), 1162, 512,
                                    torch.empty(10, dtype=torch.uint8, device="cuda"),
                                    torch.empty(512, dtype=torch.int32, device="cuda"))
+
+
+def test_unaligned_buffers(env):
+    """Scores and marks that start off a 16-byte / 4-byte boundary, and n not
+    a multiple of 4: the element-by-element load and store path."""
+    torch, lib, oracle = env
+    rng = np.random.default_rng(9)
+    s = ctypes.c_void_p(_STREAM[0].cuda_stream)
+    for n, k in ((4096, 300), (65536, 2048), (65535, 2048), (16385, 100)):
+        x = rng.standard_normal(n).astype(np.float32)
+        big = torch.from_numpy(np.concatenate([[np.float32(7)], x])).cuda()
+        marks_big = torch.full((n + 1,), 0xAB, dtype=torch.uint8, device="cuda")
+        d_sel = torch.full((min(k, n),), -7, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        say(f"indexer select: unaligned n={n} k={k}")
+        assert lib.hi_rocm_launch_dsv4_indexer_select(big.data_ptr() + 4, n, k, marks_big.data_ptr() + 1,
+                                                      d_sel.data_ptr(), s) == 0
+        torch.cuda.synchronize()
+        want_sel, want_marks = oracle.indexer_select(x, k)
+        assert np.array_equal(d_sel.cpu().numpy(), want_sel)
+        m = marks_big.cpu().numpy()
+        assert m[0] == 0xAB and np.array_equal(m[1:], want_marks)

@@ -553,6 +553,7 @@ struct FinLds {
   float fval0, fval1;
   uint64_t below;   // largest candidate left out of the selection
   uint32_t wmin;    // bits of the smallest selected weight
+  uint64_t thr;     // the selection threshold of a one-wave select
 };
 constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
 
@@ -1178,7 +1179,7 @@ __device__ __forceinline__ uint32_t row_argmax_total(FinLds& fs, const SampleArg
   return 0xffffffffu - (uint32_t)best;
 }
 
-__device__ void finish_logprobs(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t token,
+__device__ __forceinline__ void finish_logprobs(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t token,
                                 float M, bool eos, int ranked_k);
 
 __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg) {
@@ -1223,7 +1224,7 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
 // max of s; fs.buf / fs.pay hold the first ranked_k entries of the rank
 // order (0: none yet).  The normaliser sums the candidates of every chunk
 // in double and the other logits from each chunk's mass.
-__device__ void finish_logprobs(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t token,
+__device__ __forceinline__ void finish_logprobs(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t token,
                                 float M, bool eos, int ranked_k) {
   const int tid = threadIdx.x;
   const int V = a.V;
@@ -1371,6 +1372,74 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
   return prefix;
 }
 
+// block_select_skip for n <= 64 * PER items, by one wave: the keys in
+// registers, a 256-bin histogram in `hist` that only this wave touches, and
+// no barrier (LDS operations of one wave complete in order).  Same result.
+template <int PER>
+__device__ __forceinline__ uint64_t wave_select_skip(const uint64_t* items, int n, uint32_t k, uint32_t* hist,
+                                                     uint64_t lo, uint64_t hi_b) {
+  const int lane = threadIdx.x & 63;
+  uint64_t x[PER];
+  uint64_t mn = ~0ull, mx = 0ull;
+  #pragma unroll
+  for (int m = 0; m < PER; ++m) {
+    const int i = m * 64 + lane;
+    x[m] = i < n ? items[i] : 0ull;
+    if (i < n) {
+      mn = x[m] < mn ? x[m] : mn;
+      mx = x[m] > mx ? x[m] : mx;
+    }
+  }
+  if (lo > hi_b) {
+    mn = wave_min_u64(mn);
+    mx = wave_max_u64(mx);
+  } else {
+    mn = lo;
+    mx = hi_b;
+  }
+  if (mn == mx) return mx;
+  int hi = 64 - __clzll(mn ^ mx);
+  uint64_t prefix = hi >= 64 ? 0ull : (mx >> hi) << hi;
+  uint32_t remaining = k;
+  #pragma unroll 1
+  while (hi > 0) {
+    const int db = hi >= 8 ? 8 : hi;
+    const int lo_bit = hi - db;
+    const uint64_t hp = hi >= 64 ? 0ull : (prefix >> hi);
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) hist[lane * 4 + q] = 0u;
+    #pragma unroll
+    for (int m = 0; m < PER; ++m)
+      if (m * 64 + lane < n && (hi >= 64 || (x[m] >> hi) == hp))
+        atomicAdd(&hist[(uint32_t)(x[m] >> lo_bit) & ((1u << db) - 1u)], 1u);
+    // lane l owns bins 255-4l .. 252-4l (descending)
+    uint32_t loc[4], lsum = 0u;
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) { loc[q] = hist[255 - 4 * lane - q]; lsum += loc[q]; }
+    const uint32_t inc = wave_incl_scan_u32(lsum);
+    const uint32_t above = inc - lsum;
+    const bool mine = above < remaining && remaining <= above + lsum;
+    uint32_t d = 0u, acc_b = 0u, cnt = 0u;
+    if (mine) {
+      uint32_t acc = above;
+      #pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (remaining <= acc + loc[q] && acc < remaining) { d = 255u - 4u * (uint32_t)lane - (uint32_t)q; acc_b = acc; cnt = loc[q]; }
+        acc += loc[q];
+      }
+    }
+    const int owner = __ffsll((unsigned long long)__ballot(mine)) - 1;
+    d = (uint32_t)__builtin_amdgcn_readlane((int)d, owner);
+    acc_b = (uint32_t)__builtin_amdgcn_readlane((int)acc_b, owner);
+    cnt = (uint32_t)__builtin_amdgcn_readlane((int)cnt, owner);
+    prefix |= (uint64_t)d << lo_bit;
+    remaining -= acc_b;
+    hi = lo_bit;
+    if (cnt == remaining) break;
+  }
+  return prefix;
+}
+
 constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
 constexpr int kSpecChunks = 40;   // rows of up to this many chunks load their candidates early
 
@@ -1495,7 +1564,7 @@ __device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int
 // general finish; all threads return the same.
 __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, int n,
                                             float M, uint32_t ub_key, double part, uint32_t above = 0u,
-                                            uint64_t lo = ~0ull, uint64_t hi = 0ull) {
+                                            uint64_t lo = ~0ull, uint64_t hi = 0ull, bool one_wave_select = true) {
   const int tid = threadIdx.x;
   const uint32_t lane = (uint32_t)tid & 63u;
   const bool want_lp = a.n_lp > 0 || a.out_token_lp != nullptr;
@@ -1511,8 +1580,19 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   const int kk = min(cfg.k_sel, n);
   uint64_t thr = 0ull;
   if (tid == 0) { fs.counter = 0u; fs.below = 0ull; fs.wmin = 0xffffffffu; }
-  if (n > kk) thr = block_select_skip(fs.cbig, n, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b, lo, hi);
-  else __syncthreads();  // the counters above are set
+  if (one_wave_select && n > kk && n <= 1024) {
+    // one wave selects; the barrier publishes the threshold
+    if (tid < 64) {
+      const uint64_t t = wave_select_skip<16>(fs.cbig, n, (uint32_t)kk, fs.hist, lo, hi);
+      if (tid == 0) fs.thr = t;
+    }
+    __syncthreads();
+    thr = fs.thr;
+  } else if (n > kk) {
+    thr = block_select_skip(fs.cbig, n, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b, lo, hi);
+  } else {
+    __syncthreads();  // the counters above are set
+  }
   // the caller's candidates hold the row's top kk only if the kk-th key is
   // above `above` (the largest key the caller may have left out)
   if (n > kk && cand_skey(thr) <= above) return false;
@@ -4794,7 +4874,9 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   __syncthreads();
   const float M = key_to_s(cand_skey(top), cfg.t_eff);
   // key bounds for the selection: every candidate's key is at least Tm
-  return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm, (uint64_t)Tm << 32, top);
+  // (the 16-wave row kernel keeps the workgroup select: the one-wave select's
+  // registers cost its stream more than the select saves)
+  return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm, (uint64_t)Tm << 32, top, false);
 }
 
 // The general path of a row (see the section comment), on the first NT

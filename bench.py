@@ -159,17 +159,36 @@ def pmc_probe(torch, w, steps, copy_mib=512):
     print(json.dumps({"pmc_probe": w.name, "steps": steps, "copy_bytes": n * 4}))
 
 
+def source_hash():
+    """SHA-256 of the library's HIP sources and headers (hi_amd/csrc, include),
+    which identifies the build a counter summary was measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    for d in (os.path.join(ROOT, "hi_amd", "csrc"), os.path.join(ROOT, "include")):
+        for name in sorted(os.listdir(d)):
+            if name.endswith((".hip", ".h")):
+                h.update(name.encode())
+                with open(os.path.join(d, name), "rb") as f:
+                    h.update(f.read())
+    return h.hexdigest()
+
+
 def traffic_from_profile():
-    """HBM bytes per launch of the C3 step's kernel, measured by the
-    committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by a
-    copy of known size), or None when no summary is present."""
+    """HBM bytes per launch of the C3 step's kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy of
+    known size), with the source hash the summary was measured on.  Returns
+    (bytes or None, summary hash or None): the caller reports the bytes only
+    when the hash is this build's."""
     path = os.path.join(ROOT, "profiles", "row_kernel_c3_hbm_traffic.md")
     if not os.path.exists(path):
-        return None
+        return None, None
+    traffic = tag = None
     for line in open(path):
         if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1].strip())
-    return None
+            traffic = float(line.split(":", 1)[1].strip())
+        if line.startswith("source_hash:"):
+            tag = line.split(":", 1)[1].strip()
+    return traffic, tag
 
 
 def time_graph_b1(torch, w, steps, warmup):
@@ -409,7 +428,7 @@ def main():
     pass_us, _ = time_parts(torch, w3, args.steps)
     w1 = config1()
     b1_graph_us, b1_in_graph_us, b1_eager_us = time_graph_b1(torch, w1, max(args.steps, 100), 20)
-    b1_pass_us, b1_finish_us = time_parts(torch, w1, max(args.steps, 100))
+    b1_pass_us, _ = time_parts(torch, w1, max(args.steps, 100))
     # the dominant kernel of the C3 step: at B >= 192 (no logprobs) the step
     # is one row_kernel launch, which reads every algorithmic byte and also
     # finishes the rows.  Its average duration is the timed region's (K
@@ -418,6 +437,8 @@ def main():
     # overhead and are reported beside it.
     kernel_us = ms * 1000.0
     kernel_gbs = alg_bytes / (kernel_us * 1e-6) / 1e9
+    traffic, traffic_tag = traffic_from_profile()
+    traffic_current = traffic is not None and traffic_tag == source_hash()
 
     res = {
         "metric": METRIC,
@@ -443,13 +464,17 @@ def main():
         "b1_us_per_step_in_graph": b1_in_graph_us,
         "b1_us_per_step_eager": b1_eager_us,
         "b1_workload": w1.name,
-        "b1_kernel_us": {"select_pass": b1_pass_us, "finish": b1_finish_us},
+        # C1 runs as one fused launch (select_finish_kernel): the library's
+        # first event interval is that launch, the second holds no kernel
+        "b1_kernel_us": {"select_finish_kernel": b1_pass_us},
         "step_hbm_fraction": achieved / HBM_PEAK_GBS,
         # one row_kernel launch per C3 step; the library's third event follows
         # the second directly there, so only the first interval is a kernel
         "step_kernel_us": {"row_kernel": pass_us},
         "roofline": {"bound": "hbm", "achieved": kernel_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": kernel_gbs / HBM_PEAK_GBS, "traffic": traffic_from_profile(),
+                     "frac": kernel_gbs / HBM_PEAK_GBS, "traffic": traffic if traffic_current else None,
+                     "traffic_summary": {"file": "profiles/row_kernel_c3_hbm_traffic.md", "bytes": traffic,
+                                         "source_hash": traffic_tag, "matches_this_build": traffic_current},
                      "kernel": "hi_rocm::row_kernel<false> (C3: one workgroup per row, whole step)",
                      "kernel_avg_us": kernel_us,
                      "kernel_avg_us_library_events": pass_us,

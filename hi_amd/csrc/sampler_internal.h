@@ -144,6 +144,7 @@ struct SampleArgs {
   uint32_t* done;      // [kDoneRows] chunks of the row finished (zero between launches)
   WideStat* wstat;     // [B][n_chunks]
   ChunkFold* wfold;    // [B][n_chunks]
+  fold::Map* wbmap;    // [B][n_chunks][3][kScanThreads]: per-thread block maps of each ChunkFold binade
   WideRow* wrow;       // [B]
   uint32_t* diag;      // [B] how the wide pass finished each top-p row (WidePath)
 };
@@ -169,7 +170,7 @@ constexpr int kFusedMaxRows = kFusedMaxWorkgroups;
 constexpr int kDoneRows = 65536;
 
 struct WorkspaceLayout {
-  size_t stats, cand, ws_s, ws_w, ws_list, done, wstat, wfold, wrow, diag, total;
+  size_t stats, cand, ws_s, ws_w, ws_list, done, wstat, wfold, wbmap, wrow, diag, total;
   int64_t slots;       // (row, chunk) records reserved
   int64_t list_stride;
 };
@@ -203,6 +204,7 @@ inline WorkspaceLayout workspace_layout(int max_batch, int V) {
   L.stats = off; off = align(off + (size_t)L.slots * sizeof(ChunkStat));
   L.wstat = off; off = align(off + (size_t)L.slots * sizeof(WideStat));
   L.wfold = off; off = align(off + (size_t)L.slots * sizeof(ChunkFold));
+  L.wbmap = off; off = align(off + (size_t)L.slots * 3 * kScanThreads * sizeof(fold::Map));
   L.wrow = off; off = align(off + (size_t)max_batch * sizeof(WideRow));
   L.diag = off; off = align(off + (size_t)max_batch * sizeof(uint32_t));
   L.cand = off; off = align(off + (size_t)L.slots * kFast * sizeof(uint64_t));

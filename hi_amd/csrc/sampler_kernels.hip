@@ -3802,6 +3802,11 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
       m1 = fold::compose(m1, term_map(x, e0 + 1));
       m2 = fold::compose(m2, term_map(x, e0 + 2));
     }
+    // each thread's block maps, for the finish's crossing search
+    fold::Map* bm = a.wbmap + ((int64_t)row * a.n_chunks + chunk) * 3 * NT;
+    bm[tid] = m0;
+    bm[NT + tid] = m1;
+    bm[2 * NT + tid] = m2;
     fold::Map t0, t1, t2;
     block_map_scan(m0, L.fl.wmap, &t0);
     block_map_scan(m1, L.fl.wmap, &t1);
@@ -3862,6 +3867,83 @@ __device__ __forceinline__ float wide_refold(WideFinLds& F, unsigned char* lds_r
   }
   __syncthreads();
   return exact_chunk_fold(w, len, acc, F.fl.wmap, &F.acc2, F.fl.wcnt);
+}
+
+// The exact fold value after chunk c's weights from the exact value `acc`
+// before them, when the chunk's sum leaves the binade it starts in: wave 0
+// finds the crossing block from the chunk's stored block maps (a scan of the
+// maps over the blocks; block b holds the chunk's terms [b * J, b * J + J),
+// J = ceil(len / NT)), adds that block's terms one by one as real f32
+// additions, and repeats in the new binade.  Returns kNone's float bits
+// (NaN) when a binade falls outside the three stored ones; the caller then
+// refolds the chunk.  Wave 0 only; the result is in lane 0 and every lane.
+__device__ __forceinline__ float wide_cross_wave(const SampleArgs& a, int row, int c, float acc, bool& ok) {
+  constexpr int PB = NT / 64;  // blocks per lane
+  const int lane = threadIdx.x & 63;
+  const ChunkFold cf = a.wfold[(int64_t)row * a.n_chunks + c];
+  const fold::Map* bm = a.wbmap + ((int64_t)row * a.n_chunks + c) * 3 * NT;
+  const int c0 = c * a.chunk;
+  const int len = min(a.chunk, a.V - c0);
+  const int J = (len + NT - 1) / NT;
+  const float* wg = a.ws_w + (int64_t)row * a.V + c0;
+  float x = acc;
+  int bstart = 0;
+  ok = true;
+  while (bstart < NT) {
+    const int ey = fold::binade(x);
+    const int k = ey - (int)cf.e0;
+    if (k < 0 || k >= 3) { ok = false; return x; }
+    // this lane's blocks 4 * lane .. (those before bstart count as identity)
+    fold::Map bl[PB];
+    fold::Map mine = fold::map_identity();
+    #pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const int b = PB * lane + q;
+      bl[q] = b >= bstart ? bm[k * NT + b] : fold::map_identity();
+      mine = fold::compose(mine, bl[q]);
+    }
+    fold::Map inc = mine;
+    #pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      fold::Map o;
+      o.t0 = (uint32_t)__shfl_up((int)inc.t0, (unsigned)d, 64);
+      o.t1 = (uint32_t)__shfl_up((int)inc.t1, (unsigned)d, 64);
+      if (lane >= d) inc = fold::compose(o, inc);
+    }
+    fold::Map ex;
+    ex.t0 = (uint32_t)__shfl_up((int)inc.t0, 1u, 64);
+    ex.t1 = (uint32_t)__shfl_up((int)inc.t1, 1u, 64);
+    if (lane == 0) ex = fold::map_identity();
+    const uint32_t A = fold::to_A(x), p = A & 1u;
+    const uint64_t cross = __ballot((uint64_t)A + fold::apply(inc, p) >= fold::kTop);
+    if (cross == 0ull) {
+      const fold::Map all = {(uint32_t)__builtin_amdgcn_readlane((int)inc.t0, 63),
+                             (uint32_t)__builtin_amdgcn_readlane((int)inc.t1, 63)};
+      return fold::from_A(A + fold::apply(all, p), ey);
+    }
+    const int fl = __ffsll((unsigned long long)cross) - 1;
+    // in lane fl: the block where the sum leaves the binade, and the value before it
+    uint32_t Ab = A + fold::apply(ex, p);  // A before this lane's blocks (< kTop: earlier lanes stayed)
+    int blk = PB * lane + PB - 1;
+    bool found = false;
+    #pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const uint32_t t = fold::apply(bl[q], Ab & 1u);
+      if (!found && (uint64_t)Ab + t >= fold::kTop) { blk = PB * lane + q; found = true; }
+      if (!found) Ab += t;
+    }
+    blk = __builtin_amdgcn_readlane(blk, fl);
+    Ab = (uint32_t)__builtin_amdgcn_readlane((int)Ab, fl);
+    // the crossing block's terms as real additions (lane 0; the rest wait)
+    float y = fold::from_A(Ab, ey);
+    if (lane == 0) {
+      const int r0 = min(blk * J, len), r1 = min(r0 + J, len);
+      for (int r = r0; r < r1; ++r) y = fold::fadd(y, wg[r]);
+    }
+    x = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 0));
+    bstart = blk + 1;
+  }
+  return x;
 }
 
 // Calls f(c, e) for every superset run entry e of chunk c of `row`, in
@@ -3946,7 +4028,18 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
       const uint32_t fail = F.fail_c;
       __syncthreads();
       if (fail == 0xffffffffu) break;
-      acc = wide_refold(F, lds_raw, a, row, (int)fail, acc);
+      // the chunk whose sum leaves its binade: the crossing from the block
+      // maps (wave 0), else an exact refold of its weights
+      if (tid < 64) {
+        bool okw = true;
+        const float y = wide_cross_wave(a, row, (int)fail, acc, okw);
+        if (tid == 0) { F.acc = y; F.fail_c = okw ? 1u : 0u; }
+      }
+      __syncthreads();
+      const bool crossed = F.fail_c != 0u;
+      const float ycross = F.acc;
+      __syncthreads();
+      acc = crossed ? ycross : wide_refold(F, lds_raw, a, row, (int)fail, acc);
       c = (int)fail + 1;
     }
     __syncthreads();

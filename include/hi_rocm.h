@@ -173,7 +173,7 @@ int hi_rocm_debug_chacha_block(const uint32_t* key, const uint32_t* words12_15, 
  * static device array of HI_ROCM_NOALLOC_SCRATCH_BYTES per GPU (held by
  * every GPU the library runs on until the process ends), so shapes whose
  * workspace (hi_rocm_sampler_workspace_bytes) exceeds it are rejected with
- * HI_ROCM_ERR_UNSUPPORTED -- e.g. up to 16 rows at vocabulary 151,936.
+ * HI_ROCM_ERR_UNSUPPORTED -- e.g. up to 15 rows at vocabulary 151,936.
  * Every call on a GPU shares that GPU's array: calls that overlap on one
  * GPU (several streams or threads) race and must be serialised. */
 #define HI_ROCM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)

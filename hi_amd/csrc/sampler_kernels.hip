@@ -1,31 +1,49 @@
 // hi-rocm batched token sampler: CDNA4 (gfx950) kernels.
 //
-// Two kernels per decode step.  Logits [B, V] stay in HBM; the scan grid is
-// (chunks per row, B) workgroups of 256 threads (4 wave64s):
+// Logits [B, V] (f32 or bf16) stay in HBM and are read once, with 128-bit
+// (f32) or 64-bit (bf16) loads.  launch_sample() picks one of four shapes:
 //
-//   scan   every workgroup streams one chunk of one row exactly once with
-//          128-bit loads, all issued before any use (4 KiB per wave in
-//          flight; 4096-logit chunks, 1024 when the batch is small).  Per element: allowed-token mask, penalties from an LDS
-//          count table built from the row's history, temperature.  The
-//          workgroup then reduces its statistics (max, three argmax
-//          variants) and selects the chunk's exact top-k' by (scaled logit
-//          desc, index asc): a bound from the per-thread maxima pre-filters
-//          the chunk to about 1.3 k' elements, and an 8-bit LDS radix
-//          descent finishes the selection.
-//   finish a second launch, one workgroup per row, merges the chunk
-//          candidates, ranks them with the glibc-exact weight function and
-//          runs the reference's sequential f32 folds and inverse-CDF draw
-//          (crates/hi-cuda/src/gpu.rs:753-900).
+//   row_kernel          B >= 192, V <= 2^18, no logprobs: one 1024-thread
+//                       workgroup per row streams the row in 16384-logit
+//                       tiles (two in flight), keeps per-wave candidate lists
+//                       against a running bound, and finishes the row itself
+//                       (one launch per step).  Rows the fast path cannot
+//                       resolve take row_general, out of line.
+//   select_finish       small grids (<= 512 workgroups): one workgroup per
+//                       (row, chunk) of 4096 or 16384 logits selects the
+//                       chunk's candidates; the last workgroup of a row
+//                       (per-row counter) finishes it (one launch).
+//   select + finish     larger grids: the same select kernel, then
+//                       finish_grid_kernel on a 1-D grid whose first B
+//                       workgroups finish the rows (spread over every XCD)
+//                       and whose other workgroups run the wide pass of
+//                       top-p rows.
+//   scan + finish       more than 256 logprobs, or rows not aligned for
+//                       vector loads: scan_generic_kernel, then
+//                       finish_kernel, one workgroup per row.
 //
-// Rows without top-k (top-p / min-p only, temperature-only) and rows with
-// top_k > 1024 also keep their scaled logits in the workspace; their finish
-// re-reads the row from there (served mostly by L2 / MALL).
+// Per element: allowed-token mask, penalties from an LDS count table of the
+// row's history, temperature.  Candidates are 64-bit keys (processed logit,
+// index) so that one integer compare ranks them; selections are MSD radix
+// descents over LDS histograms with DPP scans and ballots.
 //
-// Every operation that decides a token mirrors the reference bit for bit:
-// IEEE f32 division and addition in the reference's order, no contraction
-// (the library is built with -ffp-contract=off), and exact_expf() equal to
-// host glibc expf.  Selections use integer histograms and prefix scans in a
-// fixed order, so results are deterministic run to run.
+// Finishes: the lean finish (greedy; top-k <= 256) ranks by counting and
+// runs the reference's sequential f32 folds on every wave from registers
+// (wave_draw); top-k rows up to 1024 rank their candidates (register
+// bitonic sort) and draw the same way; top-p rows without top-k take the
+// wide pass: exact weights per chunk, the vocabulary-order normaliser as an
+// exact parallel emulation of the f32 fold (exact_fold.h / fold_wg.h: per
+// binade integer maps, one real add per binade crossing), the nucleus from
+// a mass histogram as a superset of distinct weights, and the rank-order
+// folds over those runs in closed form.  finish_row is the general
+// fallback and reproduces the reference step by step.
+//
+// Every operation that decides a token mirrors the reference bit for bit
+// (crates/hi-cuda/src/gpu.rs:753-900): IEEE f32 division and addition in
+// the reference's order, no contraction (the library is built with
+// -ffp-contract=off), and exact_expf() equal to host glibc expf.
+// Selections use integer histograms and prefix scans in a fixed order, so
+// results are deterministic run to run.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <float.h>
@@ -3607,32 +3625,32 @@ __device__ __forceinline__ void wide_row_prepare(SelLds& L, const SampleArgs& a,
     if (tid == 0) { wr->valid = 0u; wr->M = M; wr->w_lo = 0.f; }
     return;
   }
-  // chunk masses relative to M: in fixed point per binade of their lower
-  // end (for w_lo), and in double per chunk (for the predictions)
-  double* cmass = reinterpret_cast<double*>(L.surv[1]);  // up to kSurvCap chunks at a time
+  // chunk masses relative to M, in fixed point (2^-32): per binade of their
+  // lower end (for w_lo) and per chunk (for the predictions); one (chunk,
+  // bin) pair per thread step, so the whole workgroup works on every chunk
+  unsigned long long* cmass = reinterpret_cast<unsigned long long*>(L.surv[1]);  // up to kSurvCap chunks at a time
   double S = 0.0;  // thread 0: the running prediction
   for (int cb = 0; cb < nch; cb += kSurvCap) {
     const int nb = min(kSurvCap, nch - cb);
-    for (int i = tid; i < nb; i += NT) {
-      const WideStat ws = wst[cb + i];
+    for (int i = tid; i < nb; i += NT) cmass[i] = 0ull;
+    __syncthreads();
+    for (int it = tid; it < nb * kWideBins; it += NT) {
+      const int i = it / kWideBins, j = it % kWideBins;
+      const WideStat& ws = wst[cb + i];
       const float lb = (M - ws.ms) * 1.4426950408889634f;  // log2 of M's weight over the chunk max's
-      const float r = __builtin_amdgcn_exp2f(-lb);
-      double cm = 0.0;
-      for (int j = 0; j < kWideBins; ++j) {
-        const float m = ws.hist[j] * r;
-        if (!(m > 0.f)) continue;
-        cm += (double)m;
-        int g = j == kWideBins - 1 ? kWideGBins - 1 : (int)floorf((float)(j + 1) + lb);
-        g = g < kWideGBins ? g : kWideGBins - 1;
-        atomicAdd(&gmass[g], (unsigned long long)((double)m * 4294967296.0));
-      }
-      cmass[i] = cm;
+      const float m = ws.hist[j] * __builtin_amdgcn_exp2f(-lb);
+      if (!(m > 0.f)) continue;
+      const unsigned long long fx = (unsigned long long)((double)m * 4294967296.0);
+      int g = j == kWideBins - 1 ? kWideGBins - 1 : (int)floorf((float)(j + 1) + lb);
+      g = g < kWideGBins ? g : kWideGBins - 1;
+      atomicAdd(&gmass[g], fx);
+      atomicAdd(&cmass[i], fx);
     }
     __syncthreads();
     if (tid == 0) {
       for (int i = 0; i < nb; ++i) {
         wst[cb + i].pred = S;
-        S += cmass[i];
+        S += (double)cmass[i] * (1.0 / 4294967296.0);
       }
     }
     __syncthreads();

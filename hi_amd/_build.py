@@ -11,7 +11,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libhi_rocm.so")
 SOURCES = ["sampler_kernels.hip", "index_select.hip", "sampler_api.hip", "sampler_host.hip", "decode_step.hip",
-           "moe_router.hip"]
+           "moe_router.hip", "spec_verify.hip"]
 
 # -ffp-contract=off: every f32/f64 operation that decides a token is a
 # separate IEEE rounding (fused operations are written out explicitly).

@@ -50,6 +50,7 @@ SIGNATURES = {
         _i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "hi_rocm_sampler_reserve": (_i, [_i, _i, _i, _vp]),
     "hi_rocm_launch_moe_topk_router": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
+    "hi_rocm_spec_verify_greedy": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hi_rocm_history_append": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _vp]),
     "hi_rocm_history_pack": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp]),
     "hi_rocm_rng_key_from_seed": (_i, [ctypes.c_uint64, _vp]),

@@ -126,6 +126,20 @@ int hi_rocm_launch_moe_topk_router(const void* scores, void* output_ids, void* o
                                    const void* selection_bias, int rows, int experts, int top_k,
                                    int norm_topk, int gating_sigmoid, float weights_scale, void* stream);
 
+/* Greedy speculative-decoding verification (gpu.rs:10725-10762
+ * speculative_greedy_next_tokens_paged_with_page_table, batched): logits
+ * f32[batch][max_draft + 1][vocab] (row i of a request predicts the token
+ * after its i-th verify input), draft_tokens u32[batch][max_draft],
+ * draft_len i32[batch] (null: every request drafted max_draft tokens).
+ * Writes out_greedy u32[batch][max_draft + 1] (each row's argmax by the
+ * host rule of gpu.rs:6406-6435: first maximum by '>', a NaN at index 0
+ * keeps index 0), and per request the accepted prefix: out_tokens
+ * u32[batch][max_draft + 1] receives greedy[0 ..= accepted] and out_count
+ * i32[batch] its length.  Device arrays; no allocation. */
+int hi_rocm_spec_verify_greedy(const void* logits, int batch, int max_draft, int vocab, const void* draft_tokens,
+                               const void* draft_len, void* out_greedy, void* out_tokens, void* out_count,
+                               void* stream);
+
 /* ---- decode-step upkeep on the device (the reference keeps these on the
  *      host: generated tokens in a Vec, crates/hi-cuda/src/lib.rs:4342, and
  *      one StdRng draw per request per step, lib.rs:6415-6429) ---- */

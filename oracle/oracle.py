@@ -120,6 +120,10 @@ def lib() -> ctypes.CDLL:
                                          ctypes.c_void_p, ctypes.c_void_p]
         L.hro_fold_f32.restype = ctypes.c_float
         L.hro_fold_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+        L.hro_spec_verify_greedy.restype = None
+        L.hro_spec_verify_greedy.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_void_p]
         L.hro_moe_router.restype = None
         L.hro_moe_router.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -287,3 +291,19 @@ def moe_router(scores, top_k, bias=None, norm_topk=False, gating_sigmoid=False, 
     lib().hro_moe_router(_ptr(x), _ptr(ids), _ptr(w), _ptr(b), rows, experts, int(top_k), int(bool(norm_topk)),
                          int(bool(gating_sigmoid)), float(weights_scale))
     return ids, w
+
+
+def spec_verify_greedy(logits, draft, draft_len=None):
+    """Greedy speculative verification (gpu.rs:10725-10762): logits
+    [B, K+1, V] f32, draft [B, K] u32.  Returns (greedy [B, K+1],
+    tokens [B, K+1] (valid up to count), count [B])."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    B, K1, V = x.shape
+    K = K1 - 1
+    d = np.ascontiguousarray(draft, dtype=np.uint32).reshape(B, K) if K > 0 else np.zeros((B, 1), np.uint32)
+    dl = None if draft_len is None else np.ascontiguousarray(draft_len, dtype=np.int32)
+    g = np.zeros((B, K1), np.uint32)
+    t = np.zeros((B, K1), np.uint32)
+    c = np.zeros(B, np.int32)
+    lib().hro_spec_verify_greedy(_ptr(x), B, K, V, _ptr(d), _ptr(dl), _ptr(g), _ptr(t), _ptr(c))
+    return g, t, c

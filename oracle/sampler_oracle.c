@@ -767,3 +767,39 @@ void hro_moe_router(const float* scores, uint32_t* output_ids, float* output_wei
       for (int rank = 0; rank < top_k; ++rank) row_weights[rank] *= weights_scale;
   }
 }
+
+/* ---- greedy speculative verification (gpu.rs:10725-10762) ----
+ * argmax_rows (gpu.rs:6421-6434) per verify row, then the accepted prefix.
+ * logits [batch][K+1][V]; draft [batch][K]; draft_len[batch] or NULL;
+ * greedy / out_tokens [batch][K+1]; out_count[batch]. */
+void hro_spec_verify_greedy(const float* logits, int batch, int K, int V, const uint32_t* draft,
+                            const int32_t* draft_len, uint32_t* greedy, uint32_t* out_tokens,
+                            int32_t* out_count) {
+  for (int b = 0; b < batch; ++b) {
+    for (int r = 0; r <= K; ++r) {
+      const float* row = logits + ((int64_t)b * (K + 1) + r) * V;
+      int64_t best = 0;
+      float best_val = row[0];
+      for (int64_t idx = 0; idx < V; ++idx) {
+        if (row[idx] > best_val) {
+          best_val = row[idx];
+          best = idx;
+        }
+      }
+      greedy[(int64_t)b * (K + 1) + r] = (uint32_t)best;
+    }
+    int k = draft_len ? draft_len[b] : K;
+    if (k < 0) k = 0;
+    if (k > K) k = K;
+    const uint32_t* g = greedy + (int64_t)b * (K + 1);
+    int accepted = k;
+    for (int i = 0; i < k; ++i) {
+      if (draft[(int64_t)b * K + i] != g[i]) {
+        accepted = i;
+        break;
+      }
+    }
+    for (int i = 0; i <= accepted; ++i) out_tokens[(int64_t)b * (K + 1) + i] = g[i];
+    out_count[b] = accepted + 1;
+  }
+}

@@ -469,6 +469,80 @@ int hi_rocm_launch_dsv4_indexer_select(const void* scores, int n_blocks, int top
 
 }  // extern "C"
 
+// ---- LM-head projection + bias + softcap fused into the first pass -------
+
+namespace {
+
+int lm_args(const void* hidden, const void* weight, const float* bias, float softcap, int batch, int hidden_dim,
+            int vocab, const char* what, hi_rocm::LmArgs& a) {
+  if (hidden == nullptr || weight == nullptr || batch <= 0 || hidden_dim <= 0 || vocab <= 0)
+    return fail(HI_ROCM_ERR_ARGS, std::string(what) + ": invalid arguments");
+  if (batch > hi_rocm::kLmRows || hidden_dim % 32 != 0 || (uintptr_t)hidden % 16 != 0 || (uintptr_t)weight % 16 != 0)
+    return fail(HI_ROCM_ERR_UNSUPPORTED,
+                std::string(what) + ": needs batch <= 32, hidden_dim a multiple of 32, 16-byte aligned bf16 arrays");
+  const int tiles = (vocab + hi_rocm::kLmTile - 1) / hi_rocm::kLmTile;
+  if (hi_rocm::lm_finish_lds(tiles) > 160 * 1024)
+    return fail(HI_ROCM_ERR_UNSUPPORTED, std::string(what) + ": vocabulary above the fused finish's LDS");
+  memset(&a, 0, sizeof(a));
+  a.hidden = (const __bf16*)hidden;
+  a.weight = (const __bf16*)weight;
+  a.bias = bias;
+  a.cap = softcap;
+  a.B = batch;
+  a.H = hidden_dim;
+  a.V = vocab;
+  a.n_chunks = tiles;
+  return HI_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hi_rocm_lm_head_workspace_bytes(int batch, int vocab, size_t* out_bytes) {
+  if (batch <= 0 || vocab <= 0 || out_bytes == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_lm_head_workspace_bytes: invalid arguments");
+  *out_bytes = hi_rocm::lm_workspace_bytes(batch, vocab);
+  return HI_ROCM_OK;
+}
+
+int hi_rocm_lm_head_logits(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
+                           int hidden_dim, int vocab, float* out_logits, void* stream) {
+  hi_rocm::LmArgs a;
+  int rc = lm_args(hidden, weight, bias, softcap, batch, hidden_dim, vocab, "hi_rocm_lm_head_logits", a);
+  if (rc != HI_ROCM_OK) return rc;
+  if (out_logits == nullptr || stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_lm_head_logits: invalid arguments");
+  a.out_logits = out_logits;
+  const hipError_t e = hi_rocm::launch_lm_logits(a, (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "lm head launch");
+}
+
+int hi_rocm_sample_lm_head(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
+                           int hidden_dim, int vocab, const hi_rocm_row_params* params, const float* uniforms,
+                           uint32_t* out_tokens, void* workspace, size_t workspace_bytes, void* stream) {
+  hi_rocm::LmArgs a;
+  int rc = lm_args(hidden, weight, bias, softcap, batch, hidden_dim, vocab, "hi_rocm_sample_lm_head", a);
+  if (rc != HI_ROCM_OK) return rc;
+  if (params == nullptr || uniforms == nullptr || out_tokens == nullptr || stream == nullptr)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sample_lm_head: invalid arguments");
+  const size_t need = hi_rocm::lm_workspace_bytes(batch, vocab);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sample_lm_head: workspace too small");
+  a.pv.mode = hi_rocm::kParamsRows;
+  a.pv.rows = params;
+  a.pv.uniforms = uniforms;
+  a.pv.greedy_rule = hi_rocm::kGreedyIeee;
+  const size_t recs = ((size_t)batch * a.n_chunks * 32 + 255) & ~(size_t)255;
+  a.lm_recs = (hi_rocm::LmTileRec*)workspace;
+  a.lm_cand = (uint64_t*)((char*)workspace + recs);
+  a.out_tokens = out_tokens;
+  const hipError_t e = hi_rocm::launch_lm_sample(a, (hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "lm head sample launch");
+}
+
+}  // extern "C"
+
 // ---- the per-row mirror without allocation ------------------------------
 //
 // For callers that cannot call hipMalloc (code under stream capture, tight

@@ -238,6 +238,30 @@ hipError_t launch_debug_distribution(const SampleArgs& a, float* out_proc, float
 int api_fail(int code, const char* msg);
 int api_hip_fail(hipError_t e, const char* where);
 
+// The LM-head projection + bias + softcap fused into the sampler's first
+// pass (sampler_kernels.hip).
+constexpr int kLmTile = 1024;    // vocabulary columns per workgroup (chunk)
+constexpr int kLmRows = 32;      // rows per call
+constexpr int kLmMaxK = 64;      // largest top-k of the fused finish
+struct LmTileRec;
+struct LmArgs {
+  const __bf16* hidden;   // [B][H]
+  const __bf16* weight;   // [V][H]
+  const float* bias;      // [V] or null
+  float cap;              // softcap (<= 0: none)
+  int B, H, V;
+  int n_chunks;           // tiles: ceil(V / kLmTile)
+  float* out_logits;      // the twin: [B][V]
+  ParamsView pv;
+  LmTileRec* lm_recs;     // [B][n_chunks]
+  uint64_t* lm_cand;      // [B][n_chunks][kLmMaxK]
+  uint32_t* out_tokens;   // [B]
+};
+hipError_t launch_lm_logits(const LmArgs& a, hipStream_t stream);
+hipError_t launch_lm_sample(const LmArgs& a, hipStream_t stream);
+size_t lm_workspace_bytes(int B, int V);
+size_t lm_finish_lds(int n_tiles);
+
 // Exact top-k block selection of the DSV4 indexer (index_select.hip).
 hipError_t launch_index_select(const float* scores, int n, int top_k, uint8_t* marks, int32_t* sel,
                                hipStream_t stream);

@@ -57,6 +57,7 @@
 #include "hi_rocm.h"
 #include "exact_expf.h"
 #include "fold_wg.h"
+#include "softcap.h"
 #include "wave_ops.h"
 #include "sampler_internal.h"
 
@@ -1393,16 +1394,16 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
 // block_select_skip for n <= 64 * PER items, by one wave: the keys in
 // registers, a 256-bin histogram in `hist` that only this wave touches, and
 // no barrier (LDS operations of one wave complete in order).  Same result.
-template <int PER>
-__device__ __forceinline__ uint64_t wave_select_skip(const uint64_t* items, int n, uint32_t k, uint32_t* hist,
-                                                     uint64_t lo, uint64_t hi_b) {
+template <int PER, typename LoadF>
+__device__ __forceinline__ uint64_t wave_select_skip_f(LoadF item, int n, uint32_t k, uint32_t* hist,
+                                                       uint64_t lo, uint64_t hi_b) {
   const int lane = threadIdx.x & 63;
   uint64_t x[PER];
   uint64_t mn = ~0ull, mx = 0ull;
   #pragma unroll
   for (int m = 0; m < PER; ++m) {
     const int i = m * 64 + lane;
-    x[m] = i < n ? items[i] : 0ull;
+    x[m] = i < n ? item(i) : 0ull;
     if (i < n) {
       mn = x[m] < mn ? x[m] : mn;
       mx = x[m] > mx ? x[m] : mx;
@@ -1456,6 +1457,11 @@ __device__ __forceinline__ uint64_t wave_select_skip(const uint64_t* items, int 
     if (cnt == remaining) break;
   }
   return prefix;
+}
+template <int PER>
+__device__ __forceinline__ uint64_t wave_select_skip(const uint64_t* items, int n, uint32_t k, uint32_t* hist,
+                                                     uint64_t lo, uint64_t hi_b) {
+  return wave_select_skip_f<PER>([&](int i) { return items[i]; }, n, k, hist, lo, hi_b);
 }
 
 constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
@@ -4452,6 +4458,311 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
   }
 }
 
+// ==========================================================================
+// LM-head projection + bias + final softcap fused into the first pass
+// ==========================================================================
+//
+// gpu.rs:20999-21009 output_logits_f32_device: logits = hidden . W^T, plus
+// the optional bias, then the final softcap (gpu.rs:23232-23249); the
+// sampler then reads the logits back.  Here each workgroup owns a tile of
+// kLmTile vocabulary columns for every row: 16 waves, each 64 columns, run
+// bf16 MFMAs (16x16x32, f32 accumulation) over the hidden dimension, add the
+// bias, apply the softcap (softcap.h), and keep the tile's processed logits
+// in LDS.  The fused kernel then records, per (row, tile), what the finish
+// needs -- the maximum, both argmaxes, and the tile's top-k candidates --
+// so the logits never reach HBM.  The twin kernel runs the same code and
+// writes the logits instead: the fused path's logits are bit-identical to
+// the twin's by construction (same tiles, same MFMA order, same epilogue).
+//
+// MFMA 16x16x32 bf16 operand layout (lane l = 16 * g + r): A row r, K
+// elements 8g .. 8g + 7; B column r, the same K elements; D rows 4g .. 4g + 3
+// of column r.
+typedef __bf16 lm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float lm_f32x4 __attribute__((ext_vector_type(4)));
+
+struct LmTileRec {
+  uint32_t max_lk;       // largest processed-logit key (lkey) of the tile
+  uint32_t am_ieee_i;    // IEEE '>' argmax (0xffffffff: no value above -inf)
+  float am_ieee_v;
+  uint32_t tot_key;      // largest total_cmp key (biased to unsigned)
+  uint32_t tot_i;        // its lowest index
+  uint32_t n_cand;       // candidates written (the tile's top k)
+  uint64_t unkept;       // largest candidate key of the tile not written
+};
+static_assert(sizeof(LmTileRec) == 32, "LmTileRec layout");
+
+__device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* tile) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int H = a.H;
+  const int v0 = tile0 + wid * 64;
+  lm_f32x4 acc[2][4];
+  #pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+    #pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = lm_f32x4{0.f, 0.f, 0.f, 0.f};
+  const lm_bf16x8 zero = {};
+  const __bf16* hrow[2];
+  bool hok[2];
+  #pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int m = mt * 16 + r;
+    hok[mt] = m < a.B;
+    hrow[mt] = a.hidden + (int64_t)(hok[mt] ? m : 0) * H + 8 * g;
+  }
+  const __bf16* wrow[4];
+  bool wok[4];
+  #pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int v = v0 + nt * 16 + r;
+    wok[nt] = v < a.V;
+    wrow[nt] = a.weight + (int64_t)(wok[nt] ? v : 0) * H + 8 * g;
+  }
+  // one K step ahead in registers
+  lm_bf16x8 ac[2], bc[4];
+  #pragma unroll
+  for (int mt = 0; mt < 2; ++mt) ac[mt] = hok[mt] ? *reinterpret_cast<const lm_bf16x8*>(hrow[mt]) : zero;
+  #pragma unroll
+  for (int nt = 0; nt < 4; ++nt) bc[nt] = wok[nt] ? *reinterpret_cast<const lm_bf16x8*>(wrow[nt]) : zero;
+  for (int k0 = 0; k0 < H; k0 += 32) {
+    lm_bf16x8 an[2], bn[4];
+    const bool more = k0 + 32 < H;
+    #pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+      an[mt] = (more && hok[mt]) ? *reinterpret_cast<const lm_bf16x8*>(hrow[mt] + k0 + 32) : zero;
+    #pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      bn[nt] = (more && wok[nt]) ? *reinterpret_cast<const lm_bf16x8*>(wrow[nt] + k0 + 32) : zero;
+    #pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+      #pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mt], bc[nt], acc[mt][nt], 0, 0, 0);
+    #pragma unroll
+    for (int mt = 0; mt < 2; ++mt) ac[mt] = an[mt];
+    #pragma unroll
+    for (int nt = 0; nt < 4; ++nt) bc[nt] = bn[nt];
+  }
+  // epilogue: bias, softcap; tile[m * kLmTile + column]
+  #pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+    #pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      #pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = mt * 16 + 4 * g + j;
+        const int v = v0 + nt * 16 + r;
+        if (m >= a.B || v >= a.V) continue;
+        float x = acc[mt][nt][j];
+        if (a.bias) x = x + a.bias[v];
+        if (a.cap > 0.f) x = softcap_f32(x, a.cap);
+        tile[m * kLmTile + (v - tile0)] = x;
+      }
+}
+
+// The twin: the same tiles, written to logits [B][V].
+__global__ void __launch_bounds__(1024) lm_logits_kernel(LmArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* tile = reinterpret_cast<float*>(lds_raw);
+  const int tile0 = blockIdx.x * kLmTile;
+  lm_gemm_tile(a, tile0, tile);
+  __syncthreads();
+  const int len = min(kLmTile, a.V - tile0);
+  for (int i = threadIdx.x; i < a.B * kLmTile; i += 1024) {
+    const int m = i / kLmTile, c = i % kLmTile;
+    if (c < len) a.out_logits[(int64_t)m * a.V + tile0 + c] = tile[i];
+  }
+}
+
+// Whether the fused finish takes a row: greedy, or top-k up to kLmMaxK
+// (with temperature, top-p, min-p), no penalties (the fused entry point
+// takes no history).
+__device__ __forceinline__ bool lm_row_ok(const RowCfg& c) {
+  return c.cls == kGreedy || (c.cls == kTopK && c.k_eff <= kLmMaxK);
+}
+
+// The fused pass: per (row, tile) records and candidates.  Wave w takes the
+// rows w, w + 16 of the tile.
+__global__ void __launch_bounds__(1024) lm_select_kernel(LmArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* tile = reinterpret_cast<float*>(lds_raw);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(lds_raw + (size_t)kLmRows * kLmTile * sizeof(float));
+  const int t = blockIdx.x, tile0 = t * kLmTile;
+  lm_gemm_tile(a, tile0, tile);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int len = min(kLmTile, a.V - tile0);
+  uint32_t* h = hist + wid * 256;
+  for (int m = wid; m < a.B; m += 16) {
+    const RowCfg cfg = load_cfg(a.pv, m, a.V, 0, 0);
+    const float* row = tile + m * kLmTile;
+    uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu;
+    uint64_t am = 0ull;
+    for (int i = lane; i < len; i += 64) {
+      const float l = row[i];
+      const uint32_t e = (uint32_t)(tile0 + i);
+      mk = max(mk, lkey(l));
+      if (l > -__builtin_inff()) {  // IEEE '>' from -inf: NaN and -inf never win
+        const uint64_t k = cand_key(okey(l), e);
+        am = k > am ? k : am;
+      }
+      const uint32_t tot = (uint32_t)total_key(l) ^ 0x80000000u;
+      if (tot > tk || (tot == tk && e < ti)) { tk = tot; ti = e; }
+    }
+    // wave reductions
+    mk = wave_max_u32(mk);
+    am = wave_max_u64(am);
+    {
+      const uint64_t tot64 = ((uint64_t)tk << 32) | (uint64_t)(0xffffffffu - ti);
+      const uint64_t best = wave_max_u64(lane < len ? tot64 : 0ull);
+      tk = (uint32_t)(best >> 32);
+      ti = 0xffffffffu - (uint32_t)best;
+    }
+    LmTileRec rec;
+    rec.max_lk = mk;
+    rec.am_ieee_i = am ? cand_idx(am) : 0xffffffffu;
+    rec.am_ieee_v = am ? okey_inv(cand_skey(am)) : -__builtin_inff();
+    rec.tot_key = tk;
+    rec.tot_i = ti;
+    rec.n_cand = 0u;
+    rec.unkept = 0ull;
+    uint64_t* cand = a.lm_cand + ((int64_t)m * a.n_chunks + t) * kLmMaxK;
+    if (cfg.cls == kTopK && cfg.k_eff <= kLmMaxK) {
+      const int k = cfg.k_eff;
+      auto item = [&](int i) { return cand_key(lkey(row[i]), (uint32_t)(tile0 + i)); };
+      uint64_t thr = 0ull;
+      if (len > k) thr = wave_select_skip_f<kLmTile / 64>(item, len, (uint32_t)k, h, ~0ull, 0ull);
+      uint32_t pos = 0u;
+      uint64_t below = 0ull;
+      for (int i0 = 0; i0 < len; i0 += 64) {
+        const int i = i0 + lane;
+        const uint64_t x = i < len ? item(i) : 0ull;
+        const bool keep = i < len && x >= thr;
+        const uint64_t bm = __ballot(keep);
+        if (keep) cand[pos + (uint32_t)__popcll(bm & ((1ull << lane) - 1ull))] = x;
+        pos += (uint32_t)__popcll(bm);
+        if (i < len && !keep) below = x > below ? x : below;
+      }
+      rec.n_cand = pos;
+      rec.unkept = wave_max_u64(below);
+    }
+    if (lane == 0) a.lm_recs[(int64_t)m * a.n_chunks + t] = rec;
+  }
+}
+
+// The fused finish: one workgroup per row (gpu.rs:753-900 on the row's
+// candidates, as the lean finish does).  out_tokens[row] = 0xffffffff for a
+// row the fused path does not take (its class, or a tie it cannot resolve
+// without the logits: the caller samples that row from the twin's logits).
+__global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
+  uint64_t* cands = reinterpret_cast<uint64_t*>(lds_raw + ((sizeof(FinLds) + 15) & ~(size_t)15));
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, 0, 0);
+  if (!lm_row_ok(cfg)) {
+    if (tid == 0) a.out_tokens[row] = 0xffffffffu;
+    return;
+  }
+  // merge the tile records
+  uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu, ai = 0xffffffffu, n_total_mine = 0u;
+  float av = -__builtin_inff();
+  uint64_t unk = 0ull;
+  for (int c = tid; c < a.n_chunks; c += NT) {
+    const LmTileRec r = a.lm_recs[(int64_t)row * a.n_chunks + c];
+    mk = max(mk, r.max_lk);
+    if (r.tot_key > tk || (r.tot_key == tk && r.tot_i < ti)) { tk = r.tot_key; ti = r.tot_i; }
+    if (r.am_ieee_i != 0xffffffffu && (ai == 0xffffffffu || r.am_ieee_v > av || (r.am_ieee_v == av && r.am_ieee_i < ai))) {
+      av = r.am_ieee_v; ai = r.am_ieee_i;
+    }
+    unk = r.unkept > unk ? r.unkept : unk;
+    n_total_mine += r.n_cand;
+  }
+  mk = block_max_u32<NT>(mk, fs.redu);
+  unk = block_max_u64<NT>(unk, fs.red64);
+  {
+    const uint64_t tb = block_max_u64<NT>(((uint64_t)tk << 32) | (uint64_t)(0xffffffffu - ti), fs.red64b);
+    tk = (uint32_t)(tb >> 32);
+    ti = 0xffffffffu - (uint32_t)tb;
+  }
+  {
+    // IEEE argmax: (value key, -index) over the tiles that have one
+    const uint64_t k = ai == 0xffffffffu ? 0ull : cand_key(okey(av), ai);
+    const uint64_t kb = block_max_u64<NT>(k, fs.red64);
+    ai = kb ? cand_idx(kb) : 0xffffffffu;
+  }
+  const uint32_t host_argmax = ti;  // argmax_host (gpu.rs:739-751)
+  if (cfg.cls == kGreedy) {
+    if (tid == 0) a.out_tokens[row] = ai == 0xffffffffu ? 0u : ai;
+    return;
+  }
+  const float M = mk > kKeyNegInf ? okey_inv(mk) / cfg.t_eff : -__builtin_inff();
+  if (!finitef_(M)) {
+    if (tid == 0) a.out_tokens[row] = host_argmax;
+    return;
+  }
+  // gather every tile's candidates (prefix offsets over the records)
+  if (tid == 0) fs.counter = 0u;
+  __syncthreads();
+  for (int c = tid; c < a.n_chunks; c += NT) {
+    const LmTileRec r = a.lm_recs[(int64_t)row * a.n_chunks + c];
+    const uint32_t o = atomicAdd(&fs.counter, r.n_cand);
+    const uint64_t* src = a.lm_cand + ((int64_t)row * a.n_chunks + c) * kLmMaxK;
+    for (uint32_t j = 0; j < r.n_cand; ++j) cands[o + j] = src[j];
+  }
+  __syncthreads();
+  const int n = (int)fs.counter;
+  const int kk = min(cfg.k_eff, n);
+  uint64_t thr = 0ull;
+  if (n > kk) thr = block_select_skip(cands, n, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b);
+  else __syncthreads();
+  // the selection (order does not matter: it is ranked below) and the
+  // largest candidate left out
+  if (tid == 0) fs.counter = 0u;
+  __syncthreads();
+  uint64_t below = 0ull;
+  for (int j = tid; j < n; j += NT) {
+    const uint64_t x = cands[j];
+    if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
+    else below = x > below ? x : below;
+  }
+  below = block_max_u64<NT>(below, fs.red64);
+  __syncthreads();
+  // weights; the smallest selected weight; a tie with the largest key left
+  // out (in a tile or among the candidates) is unresolved
+  if (tid == 0) fs.wmin = 0xffffffffu;
+  __syncthreads();
+  for (int j = tid; j < kk; j += NT) {
+    const uint64_t x = fs.buf[j];
+    const float w = exact_expf(key_to_s(cand_skey(x), cfg.t_eff) - M);
+    fs.pay[j] = cand_skey(x);
+    fs.buf[j] = rank_key(w, cand_idx(x));
+    atomicMin(&fs.wmin, __float_as_uint(w));
+  }
+  __syncthreads();
+  const float w_b = __uint_as_float(fs.wmin);
+  const uint64_t xk64 = below > unk ? below : unk;
+  const uint32_t xk = xk64 ? cand_skey(xk64) : 0u;
+  if (w_b > 0.f && xk > kKeyNegInf && exact_expf(key_to_s(xk, cfg.t_eff) - M) == w_b) {
+    if (tid == 0) a.out_tokens[row] = 0xfffffffeu;
+    return;
+  }
+  sort_ranked(fs, kk);
+  const int pick = wave_draw<kLmMaxK / 64>(fs.buf, kk, cfg);
+  if (tid == 0) a.out_tokens[row] = pick < 0 ? host_argmax : cand_idx(fs.buf[pick]);
+}
+
+size_t lm_workspace_bytes(int B, int V) {
+  const int64_t tiles = (V + kLmTile - 1) / kLmTile;
+  const size_t recs = ((size_t)B * tiles * sizeof(LmTileRec) + 255) & ~(size_t)255;
+  return recs + (size_t)B * tiles * kLmMaxK * sizeof(uint64_t);
+}
+
+size_t lm_select_lds() { return (size_t)kLmRows * kLmTile * sizeof(float) + 16 * 256 * sizeof(uint32_t); }
+size_t lm_finish_lds(int n_tiles) {
+  return ((sizeof(FinLds) + 15) & ~(size_t)15) + (size_t)n_tiles * kLmMaxK * sizeof(uint64_t);
+}
+
 // --------------------------------------------------------------------------
 // launch wrappers (called from the host API)
 
@@ -5239,6 +5550,28 @@ hipError_t launch_debug_distribution(const SampleArgs& a, float* out_proc, float
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(debug_probs_kernel, dim3(a.B), dim3(1024), 0, stream, b, (const float*)out_proc, out_probs);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_logits(const LmArgs& a, hipStream_t stream) {
+  const size_t lds = (size_t)kLmRows * kLmTile * sizeof(float);
+  hipError_t e = ensure_lds((const void*)lm_logits_kernel, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(lm_logits_kernel, dim3((unsigned)a.n_chunks), dim3(1024), lds, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_sample(const LmArgs& a, hipStream_t stream) {
+  const size_t l1 = lm_select_lds();
+  hipError_t e = ensure_lds((const void*)lm_select_kernel, l1);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(lm_select_kernel, dim3((unsigned)a.n_chunks), dim3(1024), l1, stream, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t l2 = lm_finish_lds(a.n_chunks);
+  e = ensure_lds((const void*)lm_finish_kernel, l2);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(lm_finish_kernel, dim3((unsigned)a.B), dim3(NT), l2, stream, a);
   return hipGetLastError();
 }
 

@@ -126,6 +126,28 @@ int hi_rocm_launch_moe_topk_router(const void* scores, void* output_ids, void* o
                                    const void* selection_bias, int rows, int experts, int top_k,
                                    int norm_topk, int gating_sigmoid, float weights_scale, void* stream);
 
+/* LM-head projection + bias + final softcap fused into the sampler's first
+ * pass (gpu.rs:20999-21009 output_logits_f32_device: project, add the bias,
+ * apply_final_logit_softcap gpu.rs:23232-23249; then the sampler).
+ *   hidden  bf16[batch][hidden_dim], weight bf16[vocab][hidden_dim] (both
+ *           16-byte aligned), bias f32[vocab] or null, softcap > 0 applies
+ *           cap * tanh(x / cap) (tanh defined in hi_amd/csrc/softcap.h; the
+ *           reference uses CUDA's tanhf), batch <= 32, hidden_dim % 32 == 0.
+ * hi_rocm_lm_head_logits writes the logits f32[batch][vocab] (the unfused
+ * twin).  hi_rocm_sample_lm_head samples from the same logits without
+ * writing them: per-row params as hi_rocm_sample (greedy, or top-k <= 64
+ * with temperature / top-p / min-p; no penalties, mask or logprobs) and one
+ * uniform per row; out_tokens[b] = 0xffffffff for a row of another class and
+ * 0xfffffffe for a row whose k-th weight ties a logit outside the tile
+ * candidates (rare): sample those rows with hi_rocm_sample on the twin's
+ * logits.  Workspace: hi_rocm_lm_head_workspace_bytes. */
+int hi_rocm_lm_head_workspace_bytes(int batch, int vocab, size_t* out_bytes);
+int hi_rocm_lm_head_logits(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
+                           int hidden_dim, int vocab, float* out_logits, void* stream);
+int hi_rocm_sample_lm_head(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
+                           int hidden_dim, int vocab, const hi_rocm_row_params* params, const float* uniforms,
+                           uint32_t* out_tokens, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Greedy speculative-decoding verification (gpu.rs:10725-10762
  * speculative_greedy_next_tokens_paged_with_page_table, batched): logits
  * f32[batch][max_draft + 1][vocab] (row i of a request predicts the token

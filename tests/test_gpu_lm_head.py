@@ -1,0 +1,103 @@
+"""GPU checks of the LM-head projection fused into the sampler's first pass
+(hi_rocm_sample_lm_head; reference gpu.rs:20999-21009 + the softcap of
+gpu.rs:23232-23249 + the sampler).
+
+* The unfused twin (hi_rocm_lm_head_logits) against a float64 product of
+  the same bf16 operands, with bias and softcap: this checks the MFMA
+  operand layout and the epilogue (tolerance: f32 accumulation, 1e-5 of
+  the magnitude sum, and the softcap's tanh to 2e-6).
+* The fused tokens against the sampler oracle run on the twin's logits,
+  row by row, bit-exact (the fused pass computes the same logits by
+  construction and never writes them); rows of classes the fused finish
+  does not take report 0xffffffff.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+
+
+def _bf16(torch, shape, scale, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
+    return x.cuda(), x.float().numpy().astype(np.float64)
+
+
+def _twin(hip, torch, h, w, bias, cap, B, H, V):
+    lib = hip.load()
+    out = torch.zeros((B, V), dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    hip.check(lib.hi_rocm_lm_head_logits(h.data_ptr(), w.data_ptr(), 0 if bias is None else bias.data_ptr(),
+                                         cap, B, H, V, out.data_ptr(), s.cuda_stream))
+    s.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("B,H,V,cap", [(5, 64, 2000, 0.0), (32, 256, 3001, 5.0), (17, 4096, 1024, 30.0)])
+def test_twin_logits_match_float64(hip, B, H, V, cap):
+    import torch
+    h, hn = _bf16(torch, (B, H), 1.0, 1)
+    w, wn = _bf16(torch, (V, H), 1.0 / np.sqrt(H), 2)
+    bn = (np.random.default_rng(3).standard_normal(V) * 0.5).astype(F32)
+    bias = torch.from_numpy(bn).cuda()
+    print(f"lm head twin B={B} H={H} V={V} cap={cap}", flush=True)
+    got = _twin(hip, torch, h, w, bias, cap, B, H, V).astype(np.float64)
+    acc = hn @ wn.T
+    mag = np.abs(hn) @ np.abs(wn).T
+    pre = acc + bn
+    if cap > 0:
+        want = cap * np.tanh(pre / cap)
+        # d(cap tanh(x/cap))/dx <= 1: the accumulation error carries through
+        tol = 1e-5 * mag + 2e-6 * np.abs(want) + 1e-6
+    else:
+        want = pre
+        tol = 1e-5 * mag + 1e-6
+    bad = np.abs(got - want) > tol
+    assert not bad.any(), (np.argwhere(bad)[:5], got[bad][:5], want[bad][:5])
+
+
+def test_fused_tokens_match_oracle_on_twin_logits(hip, oracle):
+    import torch
+    from hi_amd import sampler as S
+    from hi_amd._lib import ROW_PARAMS_DTYPE
+    lib = hip.load()
+    B, H, V, cap = 32, 512, 50000, 8.0
+    h, _ = _bf16(torch, (B, H), 1.0, 11)
+    w, _ = _bf16(torch, (V, H), 3.0 / np.sqrt(H), 12)
+    bias = torch.from_numpy((np.random.default_rng(13).standard_normal(V) * 0.3).astype(F32)).cuda()
+    logits = _twin(hip, torch, h, w, bias, cap, B, H, V)
+    rng = np.random.default_rng(14)
+    params = np.zeros(B, ROW_PARAMS_DTYPE)
+    params["temperature"] = rng.uniform(0.5, 1.3, B)
+    params["top_p"] = rng.choice(np.array([1.0, 0.9, 0.5], F32), B)
+    params["top_k"] = rng.choice(np.array([1, 5, 20, 40, 64], np.int32), B)
+    params["min_p"] = np.where(rng.random(B) < 0.3, F32(0.05), F32(0.0))
+    params["temperature"][:4] = 0.0           # greedy
+    params["top_k"][4] = 0                     # top-p only: not taken by the fused finish
+    params["top_p"][4] = 0.9
+    u = rng.random(B).astype(F32)
+    want = oracle.sample_rows(logits, params, u)["tokens"]
+    ws_n = ctypes.c_size_t()
+    hip.check(lib.hi_rocm_lm_head_workspace_bytes(B, V, ctypes.byref(ws_n)))
+    ws = torch.zeros(ws_n.value, dtype=torch.uint8, device="cuda")
+    dp = S.params_to_device(params)
+    du = torch.from_numpy(u).cuda()
+    out = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for rep in range(2):
+        hip.check(lib.hi_rocm_sample_lm_head(h.data_ptr(), w.data_ptr(), bias.data_ptr(), cap, B, H, V,
+                                             dp.data_ptr(), du.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                             ws_n.value, s.cuda_stream))
+        s.synchronize()
+        got = out.cpu().numpy().view(np.uint32)
+        print(f"lm head fused rep {rep}: {got[:8].tolist()}", flush=True)
+        assert got[4] == 0xFFFFFFFF
+        ok = np.arange(B) != 4
+        assert not (got[ok] == 0xFFFFFFFE).any(), "unresolved tie rows"
+        assert np.array_equal(got[ok], want[ok]), (np.flatnonzero(got[ok] != want[ok])[:8])

@@ -340,6 +340,63 @@ def time_router(torch, rows=4096, experts=256, top_k=8, launches=100, cpu=True):
     return rec
 
 
+def time_lm_head(torch, B=32, H=4096, V=151936, cap=30.0, launches=20):
+    """The LM-head projection + softcap fused into the sampler's first pass
+    (hi_rocm_sample_lm_head) against the unfused pair (hi_rocm_lm_head_logits
+    writing the logits, then hi_rocm_sample on them), both timed by HIP events
+    on the launch stream over back-to-back calls.  Rows: top-k 40, top-p 0.9,
+    T 0.8.  Algorithmic bytes per call: the bf16 weight V*H*2 and hidden
+    B*H*2 read, tokens written (the projection reads every weight once)."""
+    import ctypes
+    from hi_amd import _lib
+    from hi_amd import sampler as S
+    lib = _lib.load()
+    g = torch.Generator(device="cpu").manual_seed(5)
+    h = (torch.randn((B, H), generator=g)).to(torch.bfloat16).cuda()
+    w = (torch.randn((V, H), device="cuda") * (1.0 / H ** 0.5)).to(torch.bfloat16)
+    params = np.zeros(B, _lib.ROW_PARAMS_DTYPE)
+    params["temperature"] = 0.8
+    params["top_p"] = 0.9
+    params["top_k"] = 40
+    dp = S.params_to_device(params)
+    du = torch.from_numpy(np.random.default_rng(6).random(B).astype(np.float32)).cuda()
+    n = ctypes.c_size_t()
+    _lib.check(lib.hi_rocm_lm_head_workspace_bytes(B, V, ctypes.byref(n)))
+    ws = torch.zeros(n.value, dtype=torch.uint8, device="cuda")
+    tok = torch.empty(B, dtype=torch.int32, device="cuda")
+    logits = torch.empty((B, V), dtype=torch.float32, device="cuda")
+    smp = S.Sampler(B, V, 0)
+    stream = torch.cuda.Stream()
+    s = ctypes.c_void_p(stream.cuda_stream)
+
+    def fused():
+        _lib.check(lib.hi_rocm_sample_lm_head(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, dp.data_ptr(),
+                                              du.data_ptr(), tok.data_ptr(), ws.data_ptr(), n.value, s))
+
+    def unfused():
+        _lib.check(lib.hi_rocm_lm_head_logits(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, logits.data_ptr(), s))
+        smp.sample(logits, dp, du, out={"tokens": tok}, stream=stream)
+
+    res = {"batch": B, "hidden": H, "vocab": V, "softcap": cap, "rows": "top-k 40, top-p 0.9, T 0.8"}
+    torch.cuda.synchronize()
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(launches):
+                fn()
+            e1.record(stream)
+        e1.synchronize()
+        res[f"{name}_us"] = e0.elapsed_time(e1) * 1000.0 / launches
+    alg = V * H * 2 + B * H * 2 + B * 4
+    res["algorithmic_bytes"] = alg
+    res["fused_gbs"] = alg / res["fused_us"] / 1e3
+    res["fused_hbm_frac"] = res["fused_gbs"] / HBM_PEAK_GBS
+    return res
+
+
 def cpu_baseline(w, budget_s=15.0):
     """The oracle (a C restatement of the reference CPU sampler plus the
     extension stages), single thread, rows processed serially like the
@@ -485,6 +542,7 @@ def main():
                             for i, mk in ((2, config2), (4, config4), (5, config5))}
     res["dsv4_indexer_select"] = time_indexer_select(torch, cpu=not args.no_cpu_baseline)
     res["moe_router"] = time_router(torch, cpu=not args.no_cpu_baseline)
+    res["lm_head_fused"] = time_lm_head(torch)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w3, args.cpu_budget)
         res["cpu_baseline_all_cores"] = cpu_baseline_all_cores(w3)

@@ -240,9 +240,11 @@ int api_hip_fail(hipError_t e, const char* where);
 
 // The LM-head projection + bias + softcap fused into the sampler's first
 // pass (sampler_kernels.hip).
-constexpr int kLmTile = 1024;    // vocabulary columns per workgroup (chunk)
+constexpr int kLmTile = 256;     // vocabulary columns per workgroup (chunk)
+constexpr int kLmThreads = 256;  // 4 waves of 64 columns
 constexpr int kLmRows = 32;      // rows per call
 constexpr int kLmMaxK = 64;      // largest top-k of the fused finish
+constexpr int kLmMaxTiles = 4096;  // tiles per row the fused finish holds (V <= 1,048,576)
 struct LmTileRec;
 struct LmArgs {
   const __bf16* hidden;   // [B][H]
@@ -260,7 +262,7 @@ struct LmArgs {
 hipError_t launch_lm_logits(const LmArgs& a, hipStream_t stream);
 hipError_t launch_lm_sample(const LmArgs& a, hipStream_t stream);
 size_t lm_workspace_bytes(int B, int V);
-size_t lm_finish_lds(int n_tiles);
+size_t lm_recs_bytes(int B, int n_tiles);
 
 // Exact top-k block selection of the DSV4 indexer (index_select.hip).
 hipError_t launch_index_select(const float* scores, int n, int top_k, uint8_t* marks, int32_t* sel,

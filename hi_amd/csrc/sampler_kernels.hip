@@ -1312,15 +1312,16 @@ __device__ __forceinline__ void finish_logprobs(FinLds& fs, const SampleArgs& a,
 
 constexpr int kFinPer = kGather / NT;  // candidates each thread gathers
 
-// Threshold T such that exactly k of items[0, n) (unique keys, LDS) are
+// Threshold T such that exactly k of item(0 .. n-1) (unique keys) are
 // >= T, 1 <= k <= n: an 8-bit MSD radix select over the workgroup that
 // starts below the common high bits of the keys' bounds lo <= key <= hi
 // (lo > hi: the bounds are the keys' own minimum and maximum, found here).
 // Two 256-bin histograms (hist[0, 512)) alternate, so a pass takes two
 // barriers: counts, then the chosen bin.  All threads call it.
-__device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int n, uint32_t k, uint32_t* hist,
-                                                      uint32_t* sel, uint64_t* reda, uint64_t* redb,
-                                                      uint64_t lo = ~0ull, uint64_t hi_b = 0ull) {
+template <typename LoadF>
+__device__ __forceinline__ uint64_t block_select_skip_f(LoadF item, int n, uint32_t k, uint32_t* hist, uint32_t* sel,
+                                                        uint64_t* reda, uint64_t* redb, uint64_t lo = ~0ull,
+                                                        uint64_t hi_b = 0ull) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
   uint64_t mn = lo, mx = hi_b;
@@ -1329,7 +1330,7 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
     mn = ~0ull;
     mx = 0ull;
     for (int i = tid; i < n; i += NT) {
-      const uint64_t x = items[i];
+      const uint64_t x = item(i);
       mn = x < mn ? x : mn;
       mx = x > mx ? x : mx;
     }
@@ -1358,7 +1359,7 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
     uint32_t* o = hist + (cur ^ 1) * 256;  // the next pass's bins: last read before the previous barrier
     for (int b = tid; b < 256; b += NT) o[b] = 0u;
     for (int i = tid; i < n; i += NT) {
-      const uint64_t x = items[i];
+      const uint64_t x = item(i);
       if (hi >= 64 || (x >> hi) == hp) atomicAdd(&h[(uint32_t)(x >> lo_bit) & ((1u << db) - 1u)], 1u);
     }
     __syncthreads();
@@ -1389,6 +1390,13 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
     if (done) break;
   }
   return prefix;
+}
+
+// block_select_skip_f over items[0, n) (LDS or global memory).
+__device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int n, uint32_t k, uint32_t* hist,
+                                                      uint32_t* sel, uint64_t* reda, uint64_t* redb,
+                                                      uint64_t lo = ~0ull, uint64_t hi_b = 0ull) {
+  return block_select_skip_f([&](int i) { return items[i]; }, n, k, hist, sel, reda, redb, lo, hi_b);
 }
 
 // block_select_skip for n <= 64 * PER items, by one wave: the keys in
@@ -4465,7 +4473,7 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
 // gpu.rs:20999-21009 output_logits_f32_device: logits = hidden . W^T, plus
 // the optional bias, then the final softcap (gpu.rs:23232-23249); the
 // sampler then reads the logits back.  Here each workgroup owns a tile of
-// kLmTile vocabulary columns for every row: 16 waves, each 64 columns, run
+// kLmTile vocabulary columns for every row: 4 waves, each 64 columns, run
 // bf16 MFMAs (16x16x32, f32 accumulation) over the hidden dimension, add the
 // bias, apply the softcap (softcap.h), and keep the tile's processed logits
 // in LDS.  The fused kernel then records, per (row, tile), what the finish
@@ -4488,60 +4496,89 @@ struct LmTileRec {
   uint32_t tot_i;        // its lowest index
   uint32_t n_cand;       // candidates written (the tile's top k)
   uint64_t unkept;       // largest candidate key of the tile not written
+  uint64_t top;          // largest candidate key of the tile (top-k rows)
 };
-static_assert(sizeof(LmTileRec) == 32, "LmTileRec layout");
+static_assert(sizeof(LmTileRec) == 40, "LmTileRec layout");
 
+// Loads of one K block for a lane: 16 bytes at element `off` of each operand
+// row (rows past the batch or the vocabulary read row 0 and are dropped in
+// the epilogue, so every load is unconditional).
+__device__ __forceinline__ lm_bf16x8 lm_ld(const __bf16* p) { return *reinterpret_cast<const lm_bf16x8*>(p); }
+
+// The logits of vocabulary columns [tile0, tile0 + kLmTile) for rows
+// [0, B), processed (bias, softcap), into tile[m * kLmTile + column].  Wave w
+// owns 64 columns as four 16-column MFMA tiles, times two 16-row tiles.
+// K runs in blocks of 64: lane (g, r) loads 32 contiguous bytes of its row at
+// element 16g and gives the first half to one MFMA and the second to the
+// next, so each row's 128-byte line is used whole by one load pair (the two
+// operands share the K order, which is all the product needs); one block is
+// in flight while the previous one multiplies.  A trailing 32-element block
+// (H % 64 == 32) takes the plain layout, element 8g.
 __device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* tile) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int H = a.H;
+  const int H = a.H, H64 = a.H & ~63;
   const int v0 = tile0 + wid * 64;
   lm_f32x4 acc[2][4];
   #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
     #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = lm_f32x4{0.f, 0.f, 0.f, 0.f};
-  const lm_bf16x8 zero = {};
   const __bf16* hrow[2];
-  bool hok[2];
   #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     const int m = mt * 16 + r;
-    hok[mt] = m < a.B;
-    hrow[mt] = a.hidden + (int64_t)(hok[mt] ? m : 0) * H + 8 * g;
+    hrow[mt] = a.hidden + (int64_t)(m < a.B ? m : 0) * H;
   }
   const __bf16* wrow[4];
-  bool wok[4];
   #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int v = v0 + nt * 16 + r;
-    wok[nt] = v < a.V;
-    wrow[nt] = a.weight + (int64_t)(wok[nt] ? v : 0) * H + 8 * g;
+    wrow[nt] = a.weight + (int64_t)(v < a.V ? v : 0) * H;
   }
-  // one K step ahead in registers
-  lm_bf16x8 ac[2], bc[4];
-  #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) ac[mt] = hok[mt] ? *reinterpret_cast<const lm_bf16x8*>(hrow[mt]) : zero;
-  #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) bc[nt] = wok[nt] ? *reinterpret_cast<const lm_bf16x8*>(wrow[nt]) : zero;
-  for (int k0 = 0; k0 < H; k0 += 32) {
-    lm_bf16x8 an[2], bn[4];
-    const bool more = k0 + 32 < H;
+  lm_bf16x8 ac[2][2], bc[4][2];
+  if (H64 > 0) {
     #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-      an[mt] = (more && hok[mt]) ? *reinterpret_cast<const lm_bf16x8*>(hrow[mt] + k0 + 32) : zero;
+    for (int mt = 0; mt < 2; ++mt) { ac[mt][0] = lm_ld(hrow[mt] + 16 * g); ac[mt][1] = lm_ld(hrow[mt] + 16 * g + 8); }
     #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-      bn[nt] = (more && wok[nt]) ? *reinterpret_cast<const lm_bf16x8*>(wrow[nt] + k0 + 32) : zero;
+    for (int nt = 0; nt < 4; ++nt) { bc[nt][0] = lm_ld(wrow[nt] + 16 * g); bc[nt][1] = lm_ld(wrow[nt] + 16 * g + 8); }
+  }
+  for (int k0 = 0; k0 < H64; k0 += 64) {
+    lm_bf16x8 an[2][2], bn[4][2];
+    const int kn = k0 + 64 < H64 ? k0 + 64 : k0;  // the last block reloads itself (unused)
+    #pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      bn[nt][0] = lm_ld(wrow[nt] + kn + 16 * g);
+      bn[nt][1] = lm_ld(wrow[nt] + kn + 16 * g + 8);
+    }
+    #pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      an[mt][0] = lm_ld(hrow[mt] + kn + 16 * g);
+      an[mt][1] = lm_ld(hrow[mt] + kn + 16 * g + 8);
+    }
+    #pragma unroll
+    for (int h = 0; h < 2; ++h)
+      #pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        #pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mt][h], bc[nt][h], acc[mt][nt], 0, 0, 0);
+    #pragma unroll
+    for (int mt = 0; mt < 2; ++mt) { ac[mt][0] = an[mt][0]; ac[mt][1] = an[mt][1]; }
+    #pragma unroll
+    for (int nt = 0; nt < 4; ++nt) { bc[nt][0] = bn[nt][0]; bc[nt][1] = bn[nt][1]; }
+  }
+  if (H64 < H) {
+    lm_bf16x8 at[2], bt[4];
+    #pragma unroll
+    for (int mt = 0; mt < 2; ++mt) at[mt] = lm_ld(hrow[mt] + H64 + 8 * g);
+    #pragma unroll
+    for (int nt = 0; nt < 4; ++nt) bt[nt] = lm_ld(wrow[nt] + H64 + 8 * g);
     #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
       #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mt], bc[nt], acc[mt][nt], 0, 0, 0);
-    #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) ac[mt] = an[mt];
-    #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) bc[nt] = bn[nt];
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at[mt], bt[nt], acc[mt][nt], 0, 0, 0);
   }
   // epilogue: bias, softcap; tile[m * kLmTile + column]
   #pragma unroll
@@ -4561,14 +4598,14 @@ __device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* 
 }
 
 // The twin: the same tiles, written to logits [B][V].
-__global__ void __launch_bounds__(1024) lm_logits_kernel(LmArgs a) {
+__global__ void __launch_bounds__(kLmThreads) lm_logits_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* tile = reinterpret_cast<float*>(lds_raw);
   const int tile0 = blockIdx.x * kLmTile;
   lm_gemm_tile(a, tile0, tile);
   __syncthreads();
   const int len = min(kLmTile, a.V - tile0);
-  for (int i = threadIdx.x; i < a.B * kLmTile; i += 1024) {
+  for (int i = threadIdx.x; i < a.B * kLmTile; i += kLmThreads) {
     const int m = i / kLmTile, c = i % kLmTile;
     if (c < len) a.out_logits[(int64_t)m * a.V + tile0 + c] = tile[i];
   }
@@ -4582,8 +4619,11 @@ __device__ __forceinline__ bool lm_row_ok(const RowCfg& c) {
 }
 
 // The fused pass: per (row, tile) records and candidates.  Wave w takes the
-// rows w, w + 16 of the tile.
-__global__ void __launch_bounds__(1024) lm_select_kernel(LmArgs a) {
+// rows w, w + kLmThreads / 64, ... of the tile.  A top-k row's tile writes
+// its k largest candidate keys to slots [0, k); a tile shorter than k
+// writes all of its keys and zeros after them (no candidate key is zero:
+// its low word is 0xffffffff - index).
+__global__ void __launch_bounds__(kLmThreads) lm_select_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* tile = reinterpret_cast<float*>(lds_raw);
   uint32_t* hist = reinterpret_cast<uint32_t*>(lds_raw + (size_t)kLmRows * kLmTile * sizeof(float));
@@ -4593,7 +4633,7 @@ __global__ void __launch_bounds__(1024) lm_select_kernel(LmArgs a) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int len = min(kLmTile, a.V - tile0);
   uint32_t* h = hist + wid * 256;
-  for (int m = wid; m < a.B; m += 16) {
+  for (int m = wid; m < a.B; m += kLmThreads / 64) {
     const RowCfg cfg = load_cfg(a.pv, m, a.V, 0, 0);
     const float* row = tile + m * kLmTile;
     uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu;
@@ -4626,6 +4666,7 @@ __global__ void __launch_bounds__(1024) lm_select_kernel(LmArgs a) {
     rec.tot_i = ti;
     rec.n_cand = 0u;
     rec.unkept = 0ull;
+    rec.top = 0ull;
     uint64_t* cand = a.lm_cand + ((int64_t)m * a.n_chunks + t) * kLmMaxK;
     if (cfg.cls == kTopK && cfg.k_eff <= kLmMaxK) {
       const int k = cfg.k_eff;
@@ -4633,7 +4674,7 @@ __global__ void __launch_bounds__(1024) lm_select_kernel(LmArgs a) {
       uint64_t thr = 0ull;
       if (len > k) thr = wave_select_skip_f<kLmTile / 64>(item, len, (uint32_t)k, h, ~0ull, 0ull);
       uint32_t pos = 0u;
-      uint64_t below = 0ull;
+      uint64_t below = 0ull, top = 0ull;
       for (int i0 = 0; i0 < len; i0 += 64) {
         const int i = i0 + lane;
         const uint64_t x = i < len ? item(i) : 0ull;
@@ -4642,9 +4683,12 @@ __global__ void __launch_bounds__(1024) lm_select_kernel(LmArgs a) {
         if (keep) cand[pos + (uint32_t)__popcll(bm & ((1ull << lane) - 1ull))] = x;
         pos += (uint32_t)__popcll(bm);
         if (i < len && !keep) below = x > below ? x : below;
+        top = x > top ? x : top;
       }
+      for (int j = (int)pos + lane; j < k; j += 64) cand[j] = 0ull;
       rec.n_cand = pos;
       rec.unkept = wave_max_u64(below);
+      rec.top = wave_max_u64(top);
     }
     if (lane == 0) a.lm_recs[(int64_t)m * a.n_chunks + t] = rec;
   }
@@ -4652,12 +4696,12 @@ __global__ void __launch_bounds__(1024) lm_select_kernel(LmArgs a) {
 
 // The fused finish: one workgroup per row (gpu.rs:753-900 on the row's
 // candidates, as the lean finish does).  out_tokens[row] = 0xffffffff for a
-// row the fused path does not take (its class, or a tie it cannot resolve
-// without the logits: the caller samples that row from the twin's logits).
+// row the fused path does not take (its class), 0xfffffffe for a tie it
+// cannot resolve without the logits: the caller samples such a row from the
+// twin's logits.
 __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
-  uint64_t* cands = reinterpret_cast<uint64_t*>(lds_raw + ((sizeof(FinLds) + 15) & ~(size_t)15));
   const int row = blockIdx.x, tid = threadIdx.x;
   const RowCfg cfg = load_cfg(a.pv, row, a.V, 0, 0);
   if (!lm_row_ok(cfg)) {
@@ -4665,18 +4709,18 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     return;
   }
   // merge the tile records
-  uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu, ai = 0xffffffffu, n_total_mine = 0u;
+  uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu, ai = 0xffffffffu;
   float av = -__builtin_inff();
   uint64_t unk = 0ull;
   for (int c = tid; c < a.n_chunks; c += NT) {
     const LmTileRec r = a.lm_recs[(int64_t)row * a.n_chunks + c];
+    fs.cbig[c] = r.top;
     mk = max(mk, r.max_lk);
     if (r.tot_key > tk || (r.tot_key == tk && r.tot_i < ti)) { tk = r.tot_key; ti = r.tot_i; }
     if (r.am_ieee_i != 0xffffffffu && (ai == 0xffffffffu || r.am_ieee_v > av || (r.am_ieee_v == av && r.am_ieee_i < ai))) {
       av = r.am_ieee_v; ai = r.am_ieee_i;
     }
     unk = r.unkept > unk ? r.unkept : unk;
-    n_total_mine += r.n_cand;
   }
   mk = block_max_u32<NT>(mk, fs.redu);
   unk = block_max_u64<NT>(unk, fs.red64);
@@ -4701,38 +4745,68 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     if (tid == 0) a.out_tokens[row] = host_argmax;
     return;
   }
-  // gather every tile's candidates (prefix offsets over the records)
+  // The k-th largest tile top L bounds the row's k-th key from below (the
+  // tops are k distinct keys), and only the tiles whose top is >= L -- k of
+  // them, or every tile when there are fewer than k -- can hold keys >= L:
+  // at most k * k <= kGather candidates, gathered into LDS.
+  static_assert(kLmMaxTiles <= kGather, "tile tops fit the gather buffer");
+  const int k = cfg.k_eff;
+  const int nt = a.n_chunks;
+  const uint64_t L = nt > k ? block_select_skip(fs.cbig, nt, (uint32_t)k, fs.hist, fs.sel, fs.red64, fs.red64b) : 0ull;
   if (tid == 0) fs.counter = 0u;
   __syncthreads();
-  for (int c = tid; c < a.n_chunks; c += NT) {
-    const LmTileRec r = a.lm_recs[(int64_t)row * a.n_chunks + c];
-    const uint32_t o = atomicAdd(&fs.counter, r.n_cand);
-    const uint64_t* src = a.lm_cand + ((int64_t)row * a.n_chunks + c) * kLmMaxK;
-    for (uint32_t j = 0; j < r.n_cand; ++j) cands[o + j] = src[j];
+  uint64_t out_max = 0ull;  // the largest key left out of the scan (a tile top below L)
+  uint64_t* list = fs.buf;  // tiles to scan
+  for (int c = tid; c < nt; c += NT) {
+    const uint64_t t = fs.cbig[c];
+    if (t >= L) list[atomicAdd(&fs.counter, 1u)] = (uint64_t)c;
+    else out_max = t > out_max ? t : out_max;
+  }
+  __syncthreads();
+  const int n_list = (int)fs.counter;
+  __syncthreads();
+  if (tid == 0) fs.counter = 0u;
+  __syncthreads();
+  const uint64_t* cb = a.lm_cand + (int64_t)row * nt * kLmMaxK;
+  static_assert(kLmMaxK * kLmMaxK == kGather && kGather % NT == 0, "scan fits the gather buffer");
+  uint64_t xs[kGather / NT];
+  #pragma unroll
+  for (int q = 0; q < kGather / NT; ++q) {
+    const int i = tid + q * NT;
+    const int li = i / kLmMaxK, sl = i % kLmMaxK;
+    const uint64_t c = list[li < n_list ? li : 0];
+    xs[q] = cb[c * kLmMaxK + sl];  // unconditional: the slot exists
+  }
+  uint64_t below = 0ull;
+  #pragma unroll
+  for (int q = 0; q < kGather / NT; ++q) {
+    const int i = tid + q * NT;
+    const uint64_t x = xs[q];
+    if (i / kLmMaxK < n_list && i % kLmMaxK < k && x != 0ull) {
+      if (x >= L) fs.cbig[atomicAdd(&fs.counter, 1u)] = x;
+      else below = x > below ? x : below;
+    }
   }
   __syncthreads();
   const int n = (int)fs.counter;
-  const int kk = min(cfg.k_eff, n);
-  uint64_t thr = 0ull;
-  if (n > kk) thr = block_select_skip(cands, n, (uint32_t)kk, fs.hist, fs.sel, fs.red64, fs.red64b);
-  else __syncthreads();
+  const uint64_t thr = n > k ? block_select_skip(fs.cbig, n, (uint32_t)k, fs.hist, fs.sel, fs.red64, fs.red64b) : 0ull;
   // the selection (order does not matter: it is ranked below) and the
   // largest candidate left out
   if (tid == 0) fs.counter = 0u;
   __syncthreads();
-  uint64_t below = 0ull;
   for (int j = tid; j < n; j += NT) {
-    const uint64_t x = cands[j];
+    const uint64_t x = fs.cbig[j];
     if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
     else below = x > below ? x : below;
   }
+  below = below > out_max ? below : out_max;
   below = block_max_u64<NT>(below, fs.red64);
   __syncthreads();
   // weights; the smallest selected weight; a tie with the largest key left
   // out (in a tile or among the candidates) is unresolved
   if (tid == 0) fs.wmin = 0xffffffffu;
   __syncthreads();
-  for (int j = tid; j < kk; j += NT) {
+  for (int j = tid; j < k; j += NT) {
     const uint64_t x = fs.buf[j];
     const float w = exact_expf(key_to_s(cand_skey(x), cfg.t_eff) - M);
     fs.pay[j] = cand_skey(x);
@@ -4747,21 +4821,21 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     if (tid == 0) a.out_tokens[row] = 0xfffffffeu;
     return;
   }
-  sort_ranked(fs, kk);
-  const int pick = wave_draw<kLmMaxK / 64>(fs.buf, kk, cfg);
+  sort_ranked(fs, k);
+  const int pick = wave_draw<kLmMaxK / 64>(fs.buf, k, cfg);
   if (tid == 0) a.out_tokens[row] = pick < 0 ? host_argmax : cand_idx(fs.buf[pick]);
 }
 
+size_t lm_recs_bytes(int B, int n_tiles) { return ((size_t)B * n_tiles * sizeof(LmTileRec) + 255) & ~(size_t)255; }
 size_t lm_workspace_bytes(int B, int V) {
-  const int64_t tiles = (V + kLmTile - 1) / kLmTile;
-  const size_t recs = ((size_t)B * tiles * sizeof(LmTileRec) + 255) & ~(size_t)255;
-  return recs + (size_t)B * tiles * kLmMaxK * sizeof(uint64_t);
+  const int tiles = (V + kLmTile - 1) / kLmTile;
+  return lm_recs_bytes(B, tiles) + (size_t)B * tiles * kLmMaxK * sizeof(uint64_t);
 }
 
-size_t lm_select_lds() { return (size_t)kLmRows * kLmTile * sizeof(float) + 16 * 256 * sizeof(uint32_t); }
-size_t lm_finish_lds(int n_tiles) {
-  return ((sizeof(FinLds) + 15) & ~(size_t)15) + (size_t)n_tiles * kLmMaxK * sizeof(uint64_t);
+size_t lm_select_lds() {
+  return (size_t)kLmRows * kLmTile * sizeof(float) + (kLmThreads / 64) * 256 * sizeof(uint32_t);
 }
+size_t lm_finish_lds() { return (sizeof(FinLds) + 15) & ~(size_t)15; }
 
 // --------------------------------------------------------------------------
 // launch wrappers (called from the host API)
@@ -5557,7 +5631,7 @@ hipError_t launch_lm_logits(const LmArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)kLmRows * kLmTile * sizeof(float);
   hipError_t e = ensure_lds((const void*)lm_logits_kernel, lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(lm_logits_kernel, dim3((unsigned)a.n_chunks), dim3(1024), lds, stream, a);
+  hipLaunchKernelGGL(lm_logits_kernel, dim3((unsigned)a.n_chunks), dim3(kLmThreads), lds, stream, a);
   return hipGetLastError();
 }
 
@@ -5565,10 +5639,10 @@ hipError_t launch_lm_sample(const LmArgs& a, hipStream_t stream) {
   const size_t l1 = lm_select_lds();
   hipError_t e = ensure_lds((const void*)lm_select_kernel, l1);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(lm_select_kernel, dim3((unsigned)a.n_chunks), dim3(1024), l1, stream, a);
+  hipLaunchKernelGGL(lm_select_kernel, dim3((unsigned)a.n_chunks), dim3(kLmThreads), l1, stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t l2 = lm_finish_lds(a.n_chunks);
+  const size_t l2 = lm_finish_lds();
   e = ensure_lds((const void*)lm_finish_kernel, l2);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(lm_finish_kernel, dim3((unsigned)a.B), dim3(NT), l2, stream, a);

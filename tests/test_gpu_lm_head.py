@@ -38,7 +38,8 @@ def _twin(hip, torch, h, w, bias, cap, B, H, V):
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("B,H,V,cap", [(5, 64, 2000, 0.0), (32, 256, 3001, 5.0), (17, 4096, 1024, 30.0)])
+@pytest.mark.parametrize("B,H,V,cap", [(5, 64, 2000, 0.0), (32, 256, 3001, 5.0), (17, 4096, 1024, 30.0),
+                                       (9, 96, 777, 2.0)])
 def test_twin_logits_match_float64(hip, B, H, V, cap):
     import torch
     h, hn = _bf16(torch, (B, H), 1.0, 1)
@@ -61,17 +62,21 @@ def test_twin_logits_match_float64(hip, B, H, V, cap):
     assert not bad.any(), (np.argwhere(bad)[:5], got[bad][:5], want[bad][:5])
 
 
-def test_fused_tokens_match_oracle_on_twin_logits(hip, oracle):
+# (32, 512, 50000): more tiles than k (the tile-top bound); (20, 96, 3000):
+# fewer tiles than most k (every tile scanned) and a trailing 32-wide K
+# block; (8, 64, 50): one tile shorter than k (zero-padded slots).
+@pytest.mark.parametrize("B,H,V,cap,seed", [(32, 512, 50000, 8.0, 11), (20, 96, 3000, 0.0, 21), (8, 64, 50, 3.0, 31)])
+def test_fused_tokens_match_oracle_on_twin_logits(hip, oracle, B, H, V, cap, seed):
     import torch
     from hi_amd import sampler as S
     from hi_amd._lib import ROW_PARAMS_DTYPE
     lib = hip.load()
-    B, H, V, cap = 32, 512, 50000, 8.0
-    h, _ = _bf16(torch, (B, H), 1.0, 11)
-    w, _ = _bf16(torch, (V, H), 3.0 / np.sqrt(H), 12)
-    bias = torch.from_numpy((np.random.default_rng(13).standard_normal(V) * 0.3).astype(F32)).cuda()
+    print(f"lm head fused B={B} H={H} V={V} cap={cap}", flush=True)
+    h, _ = _bf16(torch, (B, H), 1.0, seed)
+    w, _ = _bf16(torch, (V, H), 3.0 / np.sqrt(H), seed + 1)
+    bias = torch.from_numpy((np.random.default_rng(seed + 2).standard_normal(V) * 0.3).astype(F32)).cuda()
     logits = _twin(hip, torch, h, w, bias, cap, B, H, V)
-    rng = np.random.default_rng(14)
+    rng = np.random.default_rng(seed + 3)
     params = np.zeros(B, ROW_PARAMS_DTYPE)
     params["temperature"] = rng.uniform(0.5, 1.3, B)
     params["top_p"] = rng.choice(np.array([1.0, 0.9, 0.5], F32), B)

@@ -482,7 +482,7 @@ int lm_args(const void* hidden, const void* weight, const float* bias, float sof
                 std::string(what) + ": needs batch <= 32, hidden_dim a multiple of 32, 16-byte aligned bf16 arrays");
   const int tiles = (vocab + hi_rocm::kLmTile - 1) / hi_rocm::kLmTile;
   if (tiles > hi_rocm::kLmMaxTiles)
-    return fail(HI_ROCM_ERR_UNSUPPORTED, std::string(what) + ": vocabulary above 1,048,576");
+    return fail(HI_ROCM_ERR_UNSUPPORTED, std::string(what) + ": vocabulary above 524,288");
   memset(&a, 0, sizeof(a));
   a.hidden = (const __bf16*)hidden;
   a.weight = (const __bf16*)weight;
@@ -535,7 +535,7 @@ int hi_rocm_sample_lm_head(const void* hidden, const void* weight, const float* 
   a.pv.greedy_rule = hi_rocm::kGreedyIeee;
   const size_t recs = hi_rocm::lm_recs_bytes(batch, a.n_chunks);
   a.lm_recs = (hi_rocm::LmTileRec*)workspace;
-  a.lm_cand = (uint64_t*)((char*)workspace + recs);
+  a.lm_logits = (float*)((char*)workspace + recs);
   a.out_tokens = out_tokens;
   const hipError_t e = hi_rocm::launch_lm_sample(a, (hipStream_t)stream);
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "lm head sample launch");

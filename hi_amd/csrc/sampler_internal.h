@@ -240,11 +240,11 @@ int api_hip_fail(hipError_t e, const char* where);
 
 // The LM-head projection + bias + softcap fused into the sampler's first
 // pass (sampler_kernels.hip).
-constexpr int kLmTile = 256;     // vocabulary columns per workgroup (chunk)
-constexpr int kLmThreads = 256;  // 4 waves of 64 columns
+constexpr int kLmTile = 128;     // vocabulary columns per workgroup (chunk)
+constexpr int kLmThreads = 128;  // 2 waves of 64 columns
 constexpr int kLmRows = 32;      // rows per call
 constexpr int kLmMaxK = 64;      // largest top-k of the fused finish
-constexpr int kLmMaxTiles = 4096;  // tiles per row the fused finish holds (V <= 1,048,576)
+constexpr int kLmMaxTiles = 4096;  // tiles per row the fused finish holds (V <= 524,288)
 struct LmTileRec;
 struct LmArgs {
   const __bf16* hidden;   // [B][H]
@@ -256,7 +256,7 @@ struct LmArgs {
   float* out_logits;      // the twin: [B][V]
   ParamsView pv;
   LmTileRec* lm_recs;     // [B][n_chunks]
-  uint64_t* lm_cand;      // [B][n_chunks][kLmMaxK]
+  float* lm_logits;       // [B][V]: the tiles of top-k rows
   uint32_t* out_tokens;   // [B]
 };
 hipError_t launch_lm_logits(const LmArgs& a, hipStream_t stream);

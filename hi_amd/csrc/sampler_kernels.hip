@@ -1402,10 +1402,14 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
 // block_select_skip for n <= 64 * PER items, by one wave: the keys in
 // registers, a 256-bin histogram in `hist` that only this wave touches, and
 // no barrier (LDS operations of one wave complete in order).  Same result.
+//
+// kmax > k asks for a threshold that keeps at least k and at most kmax
+// keys (the radix passes stop at the first digit that allows it).
 template <int PER, typename LoadF>
 __device__ __forceinline__ uint64_t wave_select_skip_f(LoadF item, int n, uint32_t k, uint32_t* hist,
-                                                       uint64_t lo, uint64_t hi_b) {
+                                                       uint64_t lo, uint64_t hi_b, uint32_t kmax = 0u) {
   const int lane = threadIdx.x & 63;
+  const uint32_t kcap = kmax > k ? kmax : k;
   uint64_t x[PER];
   uint64_t mn = ~0ull, mx = 0ull;
   #pragma unroll
@@ -1459,10 +1463,13 @@ __device__ __forceinline__ uint64_t wave_select_skip_f(LoadF item, int n, uint32
     d = (uint32_t)__builtin_amdgcn_readlane((int)d, owner);
     acc_b = (uint32_t)__builtin_amdgcn_readlane((int)acc_b, owner);
     cnt = (uint32_t)__builtin_amdgcn_readlane((int)cnt, owner);
+    // keys at or above the boundary bin's lower edge (with kcap == k this
+    // is the exact stop: the bin holds exactly the keys still needed)
+    const uint32_t kept = (k - remaining) + acc_b + cnt;
     prefix |= (uint64_t)d << lo_bit;
     remaining -= acc_b;
     hi = lo_bit;
-    if (cnt == remaining) break;
+    if (kept <= kcap) break;
   }
   return prefix;
 }
@@ -4473,7 +4480,7 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
 // gpu.rs:20999-21009 output_logits_f32_device: logits = hidden . W^T, plus
 // the optional bias, then the final softcap (gpu.rs:23232-23249); the
 // sampler then reads the logits back.  Here each workgroup owns a tile of
-// kLmTile vocabulary columns for every row: 4 waves, each 64 columns, run
+// kLmTile vocabulary columns for every row: 2 waves, each 64 columns, run
 // bf16 MFMAs (16x16x32, f32 accumulation) over the hidden dimension, add the
 // bias, apply the softcap (softcap.h), and keep the tile's processed logits
 // in LDS.  The fused kernel then records, per (row, tile), what the finish
@@ -4494,11 +4501,10 @@ struct LmTileRec {
   float am_ieee_v;
   uint32_t tot_key;      // largest total_cmp key (biased to unsigned)
   uint32_t tot_i;        // its lowest index
-  uint32_t n_cand;       // candidates written (the tile's top k)
-  uint64_t unkept;       // largest candidate key of the tile not written
-  uint64_t top;          // largest candidate key of the tile (top-k rows)
+  uint32_t pad;
+  uint64_t top;          // largest candidate key of the tile
 };
-static_assert(sizeof(LmTileRec) == 40, "LmTileRec layout");
+static_assert(sizeof(LmTileRec) == 32, "LmTileRec layout");
 
 // Loads of one K block for a lane: 16 bytes at element `off` of each operand
 // row (rows past the batch or the vocabulary read row 0 and are dropped in
@@ -4511,13 +4517,22 @@ __device__ __forceinline__ lm_bf16x8 lm_ld(const __bf16* p) { return *reinterpre
 // K runs in blocks of 64: lane (g, r) loads 32 contiguous bytes of its row at
 // element 16g and gives the first half to one MFMA and the second to the
 // next, so each row's 128-byte line is used whole by one load pair (the two
-// operands share the K order, which is all the product needs); one block is
-// in flight while the previous one multiplies.  A trailing 32-element block
-// (H % 64 == 32) takes the plain layout, element 8g.
+// operands share the K order, which is all the product needs).  Two slots
+// of registers hold blocks: a slot multiplies, then refills with the block
+// two ahead, so about two blocks are always in flight; with the kernels
+// held to 3 waves per SIMD (168 registers), every workgroup of a
+// 151936-column head is resident at once.  Each wave starts at its own
+// block (wave index mod the block count) and wraps around, so the waves'
+// reads at any moment are spread over the rows' whole length instead of
+// all sitting at one offset (about 10% more HBM throughput than a common
+// start).  A trailing 32-element block (H % 64 == 32) takes the plain
+// layout, element 8g, last.  The order is fixed per (tile, wave), so every
+// kernel built on this function produces the same bits.
+constexpr int kLmDepth = 2;  // K blocks in flight
 __device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* tile) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int H = a.H, H64 = a.H & ~63;
+  const int H = a.H, nb = a.H >> 6;
   const int v0 = tile0 + wid * 64;
   lm_f32x4 acc[2][4];
   #pragma unroll
@@ -4536,44 +4551,41 @@ __device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* 
     const int v = v0 + nt * 16 + r;
     wrow[nt] = a.weight + (int64_t)(v < a.V ? v : 0) * H;
   }
-  lm_bf16x8 ac[2][2], bc[4][2];
-  if (H64 > 0) {
+  const int rot = nb > 0 ? (int)(((uint32_t)tile0 / 64u + (uint32_t)wid) % (uint32_t)nb) : 0;
+  auto blk = [&](int i) { const int b = i + rot; return (b >= nb ? b - nb : b) * 64 + 16 * g; };
+  lm_bf16x8 ab[kLmDepth][2][2], bb[kLmDepth][4][2];
+  auto load = [&](lm_bf16x8 (&ar)[2][2], lm_bf16x8 (&br)[4][2], int off) {
     #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) { ac[mt][0] = lm_ld(hrow[mt] + 16 * g); ac[mt][1] = lm_ld(hrow[mt] + 16 * g + 8); }
+    for (int nt = 0; nt < 4; ++nt) { br[nt][0] = lm_ld(wrow[nt] + off); br[nt][1] = lm_ld(wrow[nt] + off + 8); }
     #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) { bc[nt][0] = lm_ld(wrow[nt] + 16 * g); bc[nt][1] = lm_ld(wrow[nt] + 16 * g + 8); }
-  }
-  for (int k0 = 0; k0 < H64; k0 += 64) {
-    lm_bf16x8 an[2][2], bn[4][2];
-    const int kn = k0 + 64 < H64 ? k0 + 64 : k0;  // the last block reloads itself (unused)
+    for (int mt = 0; mt < 2; ++mt) { ar[mt][0] = lm_ld(hrow[mt] + off); ar[mt][1] = lm_ld(hrow[mt] + off + 8); }
+  };
+  #pragma unroll
+  for (int s = 0; s < kLmDepth; ++s)
+    if (s < nb) load(ab[s], bb[s], blk(s));
+  for (int i = 0; i < nb; i += kLmDepth) {
     #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      bn[nt][0] = lm_ld(wrow[nt] + kn + 16 * g);
-      bn[nt][1] = lm_ld(wrow[nt] + kn + 16 * g + 8);
-    }
-    #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      an[mt][0] = lm_ld(hrow[mt] + kn + 16 * g);
-      an[mt][1] = lm_ld(hrow[mt] + kn + 16 * g + 8);
-    }
-    #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+    for (int s = 0; s < kLmDepth; ++s) {
+      if (i + s < nb) {
         #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mt][h], bc[nt][h], acc[mt][nt], 0, 0, 0);
-    #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) { ac[mt][0] = an[mt][0]; ac[mt][1] = an[mt][1]; }
-    #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) { bc[nt][0] = bn[nt][0]; bc[nt][1] = bn[nt][1]; }
+        for (int h = 0; h < 2; ++h)
+          #pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+            #pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+              acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab[s][mt][h], bb[s][nt][h], acc[mt][nt], 0, 0, 0);
+      }
+      const int il = i + s + kLmDepth;
+      if (il < nb) load(ab[s], bb[s], blk(il));
+    }
   }
-  if (H64 < H) {
+  if ((nb << 6) < H) {
+    const int off = (nb << 6) + 8 * g;
     lm_bf16x8 at[2], bt[4];
     #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) at[mt] = lm_ld(hrow[mt] + H64 + 8 * g);
+    for (int mt = 0; mt < 2; ++mt) at[mt] = lm_ld(hrow[mt] + off);
     #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) bt[nt] = lm_ld(wrow[nt] + H64 + 8 * g);
+    for (int nt = 0; nt < 4; ++nt) bt[nt] = lm_ld(wrow[nt] + off);
     #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
       #pragma unroll
@@ -4598,7 +4610,7 @@ __device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* 
 }
 
 // The twin: the same tiles, written to logits [B][V].
-__global__ void __launch_bounds__(kLmThreads) lm_logits_kernel(LmArgs a) {
+__global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) lm_logits_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* tile = reinterpret_cast<float*>(lds_raw);
   const int tile0 = blockIdx.x * kLmTile;
@@ -4618,77 +4630,92 @@ __device__ __forceinline__ bool lm_row_ok(const RowCfg& c) {
   return c.cls == kGreedy || (c.cls == kTopK && c.k_eff <= kLmMaxK);
 }
 
-// The fused pass: per (row, tile) records and candidates.  Wave w takes the
-// rows w, w + kLmThreads / 64, ... of the tile.  A top-k row's tile writes
-// its k largest candidate keys to slots [0, k); a tile shorter than k
-// writes all of its keys and zeros after them (no candidate key is zero:
-// its low word is 0xffffffff - index).
-__global__ void __launch_bounds__(kLmThreads) lm_select_kernel(LmArgs a) {
+// IEEE '>' argmax key of a value above -inf: -0 counts as +0 (the two are
+// equal under '>', so the lowest index among them wins).
+__device__ __forceinline__ uint64_t ieee_key(float l, uint32_t e) { return cand_key(okey(l == 0.f ? 0.f : l), e); }
+
+// The fused pass: per (row, tile) records.  Wave w takes the rows w,
+// w + kLmThreads / 64, ... of the tile.  A top-k row also leaves the tile's
+// logits in the workspace, where the finish reads the few tiles that can
+// hold the row's top k (greedy rows leave nothing but the records).
+__global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) lm_select_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* tile = reinterpret_cast<float*>(lds_raw);
-  uint32_t* hist = reinterpret_cast<uint32_t*>(lds_raw + (size_t)kLmRows * kLmTile * sizeof(float));
   const int t = blockIdx.x, tile0 = t * kLmTile;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  // lane m holds row m's k (0: greedy or not taken), loaded before the
+  // product so that its latency hides there
+  uint32_t my_k = 0u;
+  if (lane < a.B) {
+    const RowCfg cfg = load_cfg(a.pv, lane, a.V, 0, 0);
+    my_k = (cfg.cls == kTopK && cfg.k_eff <= kLmMaxK) ? (uint32_t)cfg.k_eff : 0u;
+  }
   lm_gemm_tile(a, tile0, tile);
   __syncthreads();
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int len = min(kLmTile, a.V - tile0);
-  uint32_t* h = hist + wid * 256;
+  constexpr int PER = kLmTile / 64;
   for (int m = wid; m < a.B; m += kLmThreads / 64) {
-    const RowCfg cfg = load_cfg(a.pv, m, a.V, 0, 0);
+    const uint32_t k = (uint32_t)__builtin_amdgcn_readlane((int)my_k, m);
     const float* row = tile + m * kLmTile;
-    uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu;
-    uint64_t am = 0ull;
-    for (int i = lane; i < len; i += 64) {
-      const float l = row[i];
-      const uint32_t e = (uint32_t)(tile0 + i);
-      mk = max(mk, lkey(l));
-      if (l > -__builtin_inff()) {  // IEEE '>' from -inf: NaN and -inf never win
-        const uint64_t k = cand_key(okey(l), e);
-        am = k > am ? k : am;
+    // the largest candidate key; values that are not finite or are -0 take
+    // the exact record path below
+    uint64_t top = 0ull;
+    bool special = false;
+    #pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int i = q * 64 + lane;
+      if (i < len) {
+        const float l = row[i];
+        const uint64_t x = cand_key(lkey(l), (uint32_t)(tile0 + i));
+        top = x > top ? x : top;
+        special |= !finitef_(l) || __float_as_uint(l) == 0x80000000u;
       }
-      const uint32_t tot = (uint32_t)total_key(l) ^ 0x80000000u;
-      if (tot > tk || (tot == tk && e < ti)) { tk = tot; ti = e; }
     }
-    // wave reductions
-    mk = wave_max_u32(mk);
-    am = wave_max_u64(am);
-    {
+    top = wave_max_u64(top);
+    LmTileRec rec;
+    if (!__any(special)) {
+      // every value finite and no -0: lkey, the IEEE key and total_cmp order
+      // the tile alike, so the maximum key gives all three argmaxes
+      const uint32_t i0 = cand_idx(top);
+      const float l0 = okey_inv(cand_skey(top));
+      rec.max_lk = cand_skey(top);
+      rec.am_ieee_i = i0;
+      rec.am_ieee_v = l0;
+      rec.tot_key = (uint32_t)total_key(l0) ^ 0x80000000u;
+      rec.tot_i = i0;
+    } else {
+      uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu;
+      uint64_t am = 0ull;
+      for (int i = lane; i < len; i += 64) {
+        const float l = row[i];
+        const uint32_t e = (uint32_t)(tile0 + i);
+        mk = max(mk, lkey(l));
+        if (l > -__builtin_inff()) {  // IEEE '>' from -inf: NaN and -inf never win
+          const uint64_t kk = ieee_key(l, e);
+          am = kk > am ? kk : am;
+        }
+        const uint32_t tot = (uint32_t)total_key(l) ^ 0x80000000u;
+        if (tot > tk || (tot == tk && e < ti)) { tk = tot; ti = e; }
+      }
+      mk = wave_max_u32(mk);
+      am = wave_max_u64(am);
       const uint64_t tot64 = ((uint64_t)tk << 32) | (uint64_t)(0xffffffffu - ti);
       const uint64_t best = wave_max_u64(lane < len ? tot64 : 0ull);
-      tk = (uint32_t)(best >> 32);
-      ti = 0xffffffffu - (uint32_t)best;
+      rec.max_lk = mk;
+      rec.am_ieee_i = am ? cand_idx(am) : 0xffffffffu;
+      rec.am_ieee_v = am ? okey_inv(cand_skey(am)) : -__builtin_inff();
+      rec.tot_key = (uint32_t)(best >> 32);
+      rec.tot_i = 0xffffffffu - (uint32_t)best;
     }
-    LmTileRec rec;
-    rec.max_lk = mk;
-    rec.am_ieee_i = am ? cand_idx(am) : 0xffffffffu;
-    rec.am_ieee_v = am ? okey_inv(cand_skey(am)) : -__builtin_inff();
-    rec.tot_key = tk;
-    rec.tot_i = ti;
-    rec.n_cand = 0u;
-    rec.unkept = 0ull;
-    rec.top = 0ull;
-    uint64_t* cand = a.lm_cand + ((int64_t)m * a.n_chunks + t) * kLmMaxK;
-    if (cfg.cls == kTopK && cfg.k_eff <= kLmMaxK) {
-      const int k = cfg.k_eff;
-      auto item = [&](int i) { return cand_key(lkey(row[i]), (uint32_t)(tile0 + i)); };
-      uint64_t thr = 0ull;
-      if (len > k) thr = wave_select_skip_f<kLmTile / 64>(item, len, (uint32_t)k, h, ~0ull, 0ull);
-      uint32_t pos = 0u;
-      uint64_t below = 0ull, top = 0ull;
-      for (int i0 = 0; i0 < len; i0 += 64) {
-        const int i = i0 + lane;
-        const uint64_t x = i < len ? item(i) : 0ull;
-        const bool keep = i < len && x >= thr;
-        const uint64_t bm = __ballot(keep);
-        if (keep) cand[pos + (uint32_t)__popcll(bm & ((1ull << lane) - 1ull))] = x;
-        pos += (uint32_t)__popcll(bm);
-        if (i < len && !keep) below = x > below ? x : below;
-        top = x > top ? x : top;
+    rec.pad = 0u;
+    rec.top = top;
+    if (k > 0u) {
+      float* dst = a.lm_logits + (int64_t)m * a.V + tile0;
+      #pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int i = q * 64 + lane;
+        if (i < len) dst[i] = row[i];
       }
-      for (int j = (int)pos + lane; j < k; j += 64) cand[j] = 0ull;
-      rec.n_cand = pos;
-      rec.unkept = wave_max_u64(below);
-      rec.top = wave_max_u64(top);
     }
     if (lane == 0) a.lm_recs[(int64_t)m * a.n_chunks + t] = rec;
   }
@@ -4711,7 +4738,6 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
   // merge the tile records
   uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu, ai = 0xffffffffu;
   float av = -__builtin_inff();
-  uint64_t unk = 0ull;
   for (int c = tid; c < a.n_chunks; c += NT) {
     const LmTileRec r = a.lm_recs[(int64_t)row * a.n_chunks + c];
     fs.cbig[c] = r.top;
@@ -4720,10 +4746,8 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     if (r.am_ieee_i != 0xffffffffu && (ai == 0xffffffffu || r.am_ieee_v > av || (r.am_ieee_v == av && r.am_ieee_i < ai))) {
       av = r.am_ieee_v; ai = r.am_ieee_i;
     }
-    unk = r.unkept > unk ? r.unkept : unk;
   }
   mk = block_max_u32<NT>(mk, fs.redu);
-  unk = block_max_u64<NT>(unk, fs.red64);
   {
     const uint64_t tb = block_max_u64<NT>(((uint64_t)tk << 32) | (uint64_t)(0xffffffffu - ti), fs.red64b);
     tk = (uint32_t)(tb >> 32);
@@ -4731,7 +4755,7 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
   }
   {
     // IEEE argmax: (value key, -index) over the tiles that have one
-    const uint64_t k = ai == 0xffffffffu ? 0ull : cand_key(okey(av), ai);
+    const uint64_t k = ai == 0xffffffffu ? 0ull : ieee_key(av, ai);
     const uint64_t kb = block_max_u64<NT>(k, fs.red64);
     ai = kb ? cand_idx(kb) : 0xffffffffu;
   }
@@ -4747,19 +4771,20 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
   }
   // The k-th largest tile top L bounds the row's k-th key from below (the
   // tops are k distinct keys), and only the tiles whose top is >= L -- k of
-  // them, or every tile when there are fewer than k -- can hold keys >= L:
-  // at most k * k <= kGather candidates, gathered into LDS.
+  // them, or every tile when there are fewer than k -- can hold the row's
+  // top k.  Their keys >= L are gathered into LDS; when more than kGather
+  // are, the select runs over the listed tiles in global memory instead.
   static_assert(kLmMaxTiles <= kGather, "tile tops fit the gather buffer");
   const int k = cfg.k_eff;
   const int nt = a.n_chunks;
   const uint64_t L = nt > k ? block_select_skip(fs.cbig, nt, (uint32_t)k, fs.hist, fs.sel, fs.red64, fs.red64b) : 0ull;
   if (tid == 0) fs.counter = 0u;
   __syncthreads();
-  uint64_t out_max = 0ull;  // the largest key left out of the scan (a tile top below L)
-  uint64_t* list = fs.buf;  // tiles to scan
+  uint64_t out_max = 0ull;  // the largest key of the tiles not scanned
+  uint32_t* list = fs.aux;  // tiles to scan (at most kLmMaxK)
   for (int c = tid; c < nt; c += NT) {
     const uint64_t t = fs.cbig[c];
-    if (t >= L) list[atomicAdd(&fs.counter, 1u)] = (uint64_t)c;
+    if (t >= L) list[atomicAdd(&fs.counter, 1u)] = (uint32_t)c;
     else out_max = t > out_max ? t : out_max;
   }
   __syncthreads();
@@ -4767,44 +4792,70 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
   __syncthreads();
   if (tid == 0) fs.counter = 0u;
   __syncthreads();
-  const uint64_t* cb = a.lm_cand + (int64_t)row * nt * kLmMaxK;
-  static_assert(kLmMaxK * kLmMaxK == kGather && kGather % NT == 0, "scan fits the gather buffer");
-  uint64_t xs[kGather / NT];
-  #pragma unroll
-  for (int q = 0; q < kGather / NT; ++q) {
-    const int i = tid + q * NT;
-    const int li = i / kLmMaxK, sl = i % kLmMaxK;
-    const uint64_t c = list[li < n_list ? li : 0];
-    xs[q] = cb[c * kLmMaxK + sl];  // unconditional: the slot exists
-  }
+  const float* lg = a.lm_logits + (int64_t)row * a.V;
+  const int n_items = n_list * kLmTile;
+  // item i: column i % kLmTile of listed tile i / kLmTile (0 past the
+  // vocabulary: below every key)
+  auto item = [&](int i) -> uint64_t {
+    const uint32_t v = list[i / kLmTile] * kLmTile + (uint32_t)(i % kLmTile);
+    return v < (uint32_t)a.V ? cand_key(lkey(lg[v]), v) : 0ull;
+  };
+  constexpr int kScanPer = kLmMaxK * kLmTile / NT;
+  static_assert(kScanPer * NT == kLmMaxK * kLmTile, "scan split");
   uint64_t below = 0ull;
-  #pragma unroll
-  for (int q = 0; q < kGather / NT; ++q) {
-    const int i = tid + q * NT;
-    const uint64_t x = xs[q];
-    if (i / kLmMaxK < n_list && i % kLmMaxK < k && x != 0ull) {
-      if (x >= L) fs.cbig[atomicAdd(&fs.counter, 1u)] = x;
-      else below = x > below ? x : below;
+  bool over = false;
+  {
+    float xs[kScanPer];
+    #pragma unroll
+    for (int q = 0; q < kScanPer; ++q) {
+      const int i = tid + q * NT;
+      const int li = i / kLmTile;
+      const uint32_t v = list[li < n_list ? li : 0] * kLmTile + (uint32_t)(i % kLmTile);
+      xs[q] = lg[v < (uint32_t)a.V ? v : 0u];  // unconditional: the address is valid
+    }
+    #pragma unroll
+    for (int q = 0; q < kScanPer; ++q) {
+      const int i = tid + q * NT;
+      const int li = i / kLmTile;
+      const uint32_t v = list[li < n_list ? li : 0] * kLmTile + (uint32_t)(i % kLmTile);
+      if (li < n_list && v < (uint32_t)a.V) {
+        const uint64_t x = cand_key(lkey(xs[q]), v);
+        if (x >= L) {
+          const uint32_t o = atomicAdd(&fs.counter, 1u);
+          if (o < (uint32_t)kGather) fs.cbig[o] = x;
+          else over = true;
+        } else {
+          below = x > below ? x : below;
+        }
+      }
     }
   }
-  __syncthreads();
-  const int n = (int)fs.counter;
-  const uint64_t thr = n > k ? block_select_skip(fs.cbig, n, (uint32_t)k, fs.hist, fs.sel, fs.red64, fs.red64b) : 0ull;
+  over = __syncthreads_or(over);
+  const int n = over ? n_items : (int)fs.counter;
+  uint64_t thr = 0ull;
+  if (over) thr = block_select_skip_f(item, n_items, (uint32_t)k, fs.hist, fs.sel, fs.red64, fs.red64b);
+  else if (n > k) thr = block_select_skip(fs.cbig, n, (uint32_t)k, fs.hist, fs.sel, fs.red64, fs.red64b);
   // the selection (order does not matter: it is ranked below) and the
   // largest candidate left out
   if (tid == 0) fs.counter = 0u;
   __syncthreads();
   for (int j = tid; j < n; j += NT) {
-    const uint64_t x = fs.cbig[j];
+    const uint64_t x = over ? item(j) : fs.cbig[j];
     if (x >= thr) fs.buf[atomicAdd(&fs.counter, 1u)] = x;
     else below = x > below ? x : below;
   }
   below = below > out_max ? below : out_max;
   below = block_max_u64<NT>(below, fs.red64);
   __syncthreads();
-  // weights; the smallest selected weight; a tie with the largest key left
-  // out (in a tile or among the candidates) is unresolved
-  if (tid == 0) fs.wmin = 0xffffffffu;
+  // weights; the smallest selected weight w_b and key S.  The selection
+  // ranks by (key desc, index asc), the reference by (weight desc, index
+  // asc): they agree unless keys with weight w_b sit on both sides of the
+  // cut with different keys.  When the largest key left out (in a tile or
+  // among the candidates) has weight w_b, the row is resolved only if that
+  // key is S, no selected key of weight w_b differs from S, and the key
+  // just below S weighs less than w_b (so no key left out below S can
+  // weigh w_b); else the tie is unresolved.
+  if (tid == 0) { fs.wmin = 0xffffffffu; fs.token = 0xffffffffu; }
   __syncthreads();
   for (int j = tid; j < k; j += NT) {
     const uint64_t x = fs.buf[j];
@@ -4812,14 +4863,23 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     fs.pay[j] = cand_skey(x);
     fs.buf[j] = rank_key(w, cand_idx(x));
     atomicMin(&fs.wmin, __float_as_uint(w));
+    atomicMin(&fs.token, cand_skey(x));
   }
   __syncthreads();
   const float w_b = __uint_as_float(fs.wmin);
-  const uint64_t xk64 = below > unk ? below : unk;
-  const uint32_t xk = xk64 ? cand_skey(xk64) : 0u;
+  const uint32_t S = fs.token;
+  const uint32_t xk = below ? cand_skey(below) : 0u;
   if (w_b > 0.f && xk > kKeyNegInf && exact_expf(key_to_s(xk, cfg.t_eff) - M) == w_b) {
-    if (tid == 0) a.out_tokens[row] = 0xfffffffeu;
-    return;
+    if (tid == 0) fs.flag = 0u;
+    __syncthreads();
+    for (int j = tid; j < k; j += NT)
+      if (fs.pay[j] != S && exact_expf(key_to_s(fs.pay[j], cfg.t_eff) - M) == w_b) fs.flag = 1u;
+    __syncthreads();
+    const bool lone = xk == S && fs.flag == 0u && !(exact_expf(key_to_s(S - 1u, cfg.t_eff) - M) == w_b);
+    if (!lone) {
+      if (tid == 0) a.out_tokens[row] = 0xfffffffeu;
+      return;
+    }
   }
   sort_ranked(fs, k);
   const int pick = wave_draw<kLmMaxK / 64>(fs.buf, k, cfg);
@@ -4829,12 +4889,10 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
 size_t lm_recs_bytes(int B, int n_tiles) { return ((size_t)B * n_tiles * sizeof(LmTileRec) + 255) & ~(size_t)255; }
 size_t lm_workspace_bytes(int B, int V) {
   const int tiles = (V + kLmTile - 1) / kLmTile;
-  return lm_recs_bytes(B, tiles) + (size_t)B * tiles * kLmMaxK * sizeof(uint64_t);
+  return lm_recs_bytes(B, tiles) + (size_t)B * V * sizeof(float);
 }
 
-size_t lm_select_lds() {
-  return (size_t)kLmRows * kLmTile * sizeof(float) + (kLmThreads / 64) * 256 * sizeof(uint32_t);
-}
+size_t lm_select_lds() { return (size_t)kLmRows * kLmTile * sizeof(float); }
 size_t lm_finish_lds() { return (sizeof(FinLds) + 15) & ~(size_t)15; }
 
 // --------------------------------------------------------------------------

@@ -106,3 +106,48 @@ def test_fused_tokens_match_oracle_on_twin_logits(hip, oracle, B, H, V, cap, see
         ok = np.arange(B) != 4
         assert not (got[ok] == 0xFFFFFFFE).any(), "unresolved tie rows"
         assert np.array_equal(got[ok], want[ok]), (np.flatnonzero(got[ok] != want[ok])[:8])
+
+
+def test_fused_duplicate_vocabulary_rows(hip, oracle):
+    """Every weight row repeated 48 times in a row: tiles of ties, where no
+    logit threshold keeps between k and 64 keys (top-k 50 and 64 take the
+    exact one-wave select), and top-k cuts inside a run of equal logits (the
+    finish resolves them by index, as the reference's (weight, index) rank
+    does).  With T <= 1 neighbouring logits keep distinct weights and every
+    row resolves; with T > 1 a cut whose next lower logit weighs the same
+    may report 0xfffffffe, and any token reported is the oracle's."""
+    import torch
+    from hi_amd import sampler as S
+    from hi_amd._lib import ROW_PARAMS_DTYPE
+    lib = hip.load()
+    B, H, V, cap = 12, 128, 6000, 4.0
+    g = torch.Generator(device="cpu").manual_seed(41)
+    base = (torch.randn(((V + 47) // 48, H), generator=g) * (2.0 / np.sqrt(H))).to(torch.bfloat16)
+    w = base.repeat_interleave(48, dim=0)[:V].contiguous().cuda()
+    h = torch.randn((B, H), generator=g).to(torch.bfloat16).cuda()
+    logits = _twin(hip, torch, h, w, None, cap, B, H, V)
+    rng = np.random.default_rng(42)
+    params = np.zeros(B, ROW_PARAMS_DTYPE)
+    params["temperature"] = rng.uniform(0.55, 1.0, B)
+    params["temperature"][-3:] = [1.3, 1.7, 2.5]
+    params["top_p"] = 1.0
+    params["top_k"] = np.array([50, 64, 40, 5, 64, 50, 1, 20, 64, 50, 33, 48], np.int32)
+    params["temperature"][0] = 0.0
+    u = rng.random(B).astype(F32)
+    want = oracle.sample_rows(logits, params, u)["tokens"]
+    ws_n = ctypes.c_size_t()
+    hip.check(lib.hi_rocm_lm_head_workspace_bytes(B, V, ctypes.byref(ws_n)))
+    ws = torch.zeros(ws_n.value, dtype=torch.uint8, device="cuda")
+    dp = S.params_to_device(params)
+    du = torch.from_numpy(u).cuda()
+    out = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    print(f"lm head fused duplicate rows B={B} H={H} V={V}", flush=True)
+    torch.cuda.synchronize()
+    hip.check(lib.hi_rocm_sample_lm_head(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, dp.data_ptr(),
+                                         du.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_n.value, s.cuda_stream))
+    s.synchronize()
+    got = out.cpu().numpy().view(np.uint32)
+    print(f"got {got.tolist()}\nwant {want.tolist()}", flush=True)
+    assert np.array_equal(got[:-3], want[:-3])
+    assert ((got[-3:] == want[-3:]) | (got[-3:] == 0xFFFFFFFE)).all()

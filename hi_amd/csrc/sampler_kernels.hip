@@ -4735,6 +4735,10 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     if (tid == 0) a.out_tokens[row] = 0xffffffffu;
     return;
   }
+  // warm the exponential's table (its first use, in the weights below,
+  // would otherwise wait on a cold miss); the loads overlap the records'
+  uint64_t warm = 0ull;
+  if (tid < 32) warm = exp2_tab32((uint32_t)tid);
   // merge the tile records
   uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu, ai = 0xffffffffu;
   float av = -__builtin_inff();
@@ -4747,17 +4751,28 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
       av = r.am_ieee_v; ai = r.am_ieee_i;
     }
   }
-  mk = block_max_u32<NT>(mk, fs.redu);
+  asm volatile("" ::"v"(warm));
   {
-    const uint64_t tb = block_max_u64<NT>(((uint64_t)tk << 32) | (uint64_t)(0xffffffffu - ti), fs.red64b);
-    tk = (uint32_t)(tb >> 32);
-    ti = 0xffffffffu - (uint32_t)tb;
-  }
-  {
-    // IEEE argmax: (value key, -index) over the tiles that have one
-    const uint64_t k = ai == 0xffffffffu ? 0ull : ieee_key(av, ai);
-    const uint64_t kb = block_max_u64<NT>(k, fs.red64);
-    ai = kb ? cand_idx(kb) : 0xffffffffu;
+    // the three maxima in one exchange: the logit key, total_cmp's argmax
+    // and the IEEE argmax ((value key, -index) over the tiles that have one)
+    uint64_t m3[3] = {(uint64_t)mk, ((uint64_t)tk << 32) | (uint64_t)(0xffffffffu - ti),
+                      ai == 0xffffffffu ? 0ull : ieee_key(av, ai)};
+    #pragma unroll
+    for (int q = 0; q < 3; ++q) m3[q] = wave_max_u64(m3[q]);
+    const int lane = tid & 63, wid = tid >> 6;
+    if (lane == 0) { fs.red64[wid] = m3[0]; fs.red64b[wid] = m3[1]; fs.mass[wid] = m3[2]; }
+    __syncthreads();
+    #pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+      m3[0] = fs.red64[w] > m3[0] ? fs.red64[w] : m3[0];
+      m3[1] = fs.red64b[w] > m3[1] ? fs.red64b[w] : m3[1];
+      m3[2] = fs.mass[w] > m3[2] ? fs.mass[w] : m3[2];
+    }
+    __syncthreads();
+    mk = (uint32_t)m3[0];
+    tk = (uint32_t)(m3[1] >> 32);
+    ti = 0xffffffffu - (uint32_t)m3[1];
+    ai = m3[2] ? cand_idx(m3[2]) : 0xffffffffu;
   }
   const uint32_t host_argmax = ti;  // argmax_host (gpu.rs:739-751)
   if (cfg.cls == kGreedy) {

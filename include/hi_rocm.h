@@ -132,15 +132,17 @@ int hi_rocm_launch_moe_topk_router(const void* scores, void* output_ids, void* o
  *   hidden  bf16[batch][hidden_dim], weight bf16[vocab][hidden_dim] (both
  *           16-byte aligned), bias f32[vocab] or null, softcap > 0 applies
  *           cap * tanh(x / cap) (tanh defined in hi_amd/csrc/softcap.h; the
- *           reference uses CUDA's tanhf), batch <= 32, hidden_dim % 32 == 0.
+ *           reference uses CUDA's tanhf), batch <= 32, hidden_dim % 32 == 0,
+ *           vocab <= 524288 (status 2 otherwise).
  * hi_rocm_lm_head_logits writes the logits f32[batch][vocab] (the unfused
- * twin).  hi_rocm_sample_lm_head samples from the same logits without
- * writing them: per-row params as hi_rocm_sample (greedy, or top-k <= 64
- * with temperature / top-p / min-p; no penalties, mask or logprobs) and one
- * uniform per row; out_tokens[b] = 0xffffffff for a row of another class and
- * 0xfffffffe for a row whose k-th weight ties a logit outside the tile
- * candidates (rare): sample those rows with hi_rocm_sample on the twin's
- * logits.  Workspace: hi_rocm_lm_head_workspace_bytes. */
+ * twin).  hi_rocm_sample_lm_head samples from the same logits (bit for bit)
+ * without a full logits pass: per-row params as hi_rocm_sample (greedy, or
+ * top-k <= 64 with temperature / top-p / min-p; no penalties, mask or
+ * logprobs) and one uniform per row; out_tokens[b] = 0xffffffff for a row of
+ * another class and 0xfffffffe for a row whose cut falls between distinct
+ * logits of equal weight (rare): sample those rows with hi_rocm_sample on
+ * the twin's logits.  Workspace (device, hi_rocm_lm_head_workspace_bytes):
+ * per-tile records and the tile logits of top-k rows. */
 int hi_rocm_lm_head_workspace_bytes(int batch, int vocab, size_t* out_bytes);
 int hi_rocm_lm_head_logits(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
                            int hidden_dim, int vocab, float* out_logits, void* stream);

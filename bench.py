@@ -347,7 +347,8 @@ def time_lm_head(torch, B=32, H=4096, V=151936, cap=30.0, launches=10, rounds=6)
     on the launch stream over back-to-back calls, in alternating rounds (the
     median round of each is reported: the box's HBM throughput drifts by a
     few percent between rounds).  Rows: top-k 40, top-p 0.9, T 0.8; the
-    fused path is also timed with greedy rows.  Algorithmic bytes per call:
+    fused path is also timed with greedy rows, and the projection alone
+    (hi_rocm_lm_head_logits, the logits written).  Algorithmic bytes per call:
     the bf16 weight V*H*2 and hidden B*H*2 read, tokens written (the
     projection reads every weight once)."""
     import ctypes
@@ -382,7 +383,11 @@ def time_lm_head(torch, B=32, H=4096, V=151936, cap=30.0, launches=10, rounds=6)
         _lib.check(lib.hi_rocm_lm_head_logits(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, logits.data_ptr(), s))
         smp.sample(logits, dp, du, out={"tokens": tok}, stream=stream)
 
-    cases = (("fused", lambda: fused(dp)), ("unfused", unfused), ("fused_greedy", lambda: fused(dg)))
+    def twin():
+        _lib.check(lib.hi_rocm_lm_head_logits(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, logits.data_ptr(), s))
+
+    cases = (("fused", lambda: fused(dp)), ("unfused", unfused), ("fused_greedy", lambda: fused(dg)),
+             ("projection", twin))
     times = {name: [] for name, _ in cases}
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
@@ -406,6 +411,8 @@ def time_lm_head(torch, B=32, H=4096, V=151936, cap=30.0, launches=10, rounds=6)
     res["algorithmic_bytes"] = alg
     res["fused_gbs"] = round(alg / res["fused_us"] / 1e3, 1)
     res["fused_hbm_frac"] = round(res["fused_gbs"] / HBM_PEAK_GBS, 4)
+    res["projection_gbs"] = round(alg / res["projection_us"] / 1e3, 1)
+    res["projection_hbm_frac"] = round(res["projection_gbs"] / HBM_PEAK_GBS, 4)
     return res
 
 

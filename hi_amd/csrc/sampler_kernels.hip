@@ -1317,11 +1317,14 @@ constexpr int kFinPer = kGather / NT;  // candidates each thread gathers
 // starts below the common high bits of the keys' bounds lo <= key <= hi
 // (lo > hi: the bounds are the keys' own minimum and maximum, found here).
 // Two 256-bin histograms (hist[0, 512)) alternate, so a pass takes two
-// barriers: counts, then the chosen bin.  All threads call it.
+// barriers: counts, then the chosen bin.  All threads call it.  kmax > k
+// asks for a threshold that keeps at least k and at most kmax keys (the
+// passes stop at the first digit that allows it).
 template <typename LoadF>
 __device__ __forceinline__ uint64_t block_select_skip_f(LoadF item, int n, uint32_t k, uint32_t* hist, uint32_t* sel,
                                                         uint64_t* reda, uint64_t* redb, uint64_t lo = ~0ull,
-                                                        uint64_t hi_b = 0ull) {
+                                                        uint64_t hi_b = 0ull, uint32_t kmax = 0u) {
+  const uint32_t kcap = kmax > k ? kmax : k;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
   uint64_t mn = lo, mx = hi_b;
@@ -1382,12 +1385,14 @@ __device__ __forceinline__ uint64_t block_select_skip_f(LoadF item, int n, uint3
       }
     }
     __syncthreads();
+    // keys at or above the chosen bin's lower edge (with kcap == k the
+    // exact stop: the bin holds exactly the keys still needed)
+    const uint32_t kept = (k - remaining) + sel[1] + sel[2];
     prefix |= (uint64_t)sel[0] << lo_bit;
     remaining -= sel[1];
-    const bool done = sel[2] == remaining;
     hi = lo_bit;
     cur ^= 1;
-    if (done) break;
+    if (kept <= kcap) break;
   }
   return prefix;
 }
@@ -4813,15 +4818,18 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     if (tid == 0) a.out_tokens[row] = host_argmax;
     return;
   }
-  // The k-th largest tile top L bounds the row's k-th key from below (the
-  // tops are k distinct keys), and only the tiles whose top is >= L -- k of
-  // them, or every tile when there are fewer than k -- can hold the row's
-  // top k.  Their keys >= L are gathered into LDS; when more than kGather
-  // are, the select runs over the listed tiles in global memory instead.
+  // A threshold L with between k and kLmMaxK tile tops at or above it
+  // bounds the row's k-th key from below (those tops are k distinct keys),
+  // and only the tiles whose top is >= L -- at most kLmMaxK of them, or
+  // every tile when there are fewer than k -- can hold the row's top k.
+  // Their keys >= L are gathered into LDS; when more than kGather are, the
+  // select runs over the listed tiles in global memory instead.
   static_assert(kLmMaxTiles <= kGather, "tile tops fit the gather buffer");
   const int k = cfg.k_eff;
   const int nt = a.n_chunks;
-  const uint64_t L = nt > k ? block_select_skip(fs.cbig, nt, (uint32_t)k, fs.hist, fs.sel, fs.red64, fs.red64b) : 0ull;
+  const uint64_t L = nt > kLmMaxK ? block_select_skip_f([&](int i) { return fs.cbig[i]; }, nt, (uint32_t)k, fs.hist,
+                                                        fs.sel, fs.red64, fs.red64b, ~0ull, 0ull, (uint32_t)kLmMaxK)
+                                  : 0ull;
   if (tid == 0) fs.counter = 0u;
   __syncthreads();
   uint64_t out_max = 0ull;  // the largest key of the tiles not scanned

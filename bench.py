@@ -482,6 +482,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run C3 steps then a plain copy of known size, for rocprofv3 --pmc")
+    ap.add_argument("--lm-head-only", action="store_true",
+                    help="time only the LM-head projection, fused and unfused (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}): the sampler's rows are "
@@ -493,6 +495,9 @@ def main():
     from hi_amd.workloads import config1, config3
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.lm_head_only:
+        print(json.dumps({"lm_head_fused": time_lm_head(torch)}))
+        return
     w3 = config3()
     if args.pmc_probe:
         pmc_probe(torch, w3, args.steps)

@@ -4743,15 +4743,14 @@ __global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu
     }
     rec.pad = 0u;
     rec.top = top;
-    if (k > 0u) {
-      float* dst = a.lm_logits + (int64_t)m * a.V + tile0;
-      #pragma unroll
-      for (int q = 0; q < PER; ++q) {
-        const int i = q * 64 + lane;
-        if (i < len) dst[i] = row[i];
-      }
-    }
     if (lane == 0) a.lm_recs[(int64_t)m * a.n_chunks + t] = rec;
+  }
+  // the tile logits of top-k rows, row after row as the twin writes them
+  // (a wave covers half a row, so the row's k is uniform over the wave)
+  for (int i = threadIdx.x; i < a.B * kLmTile; i += kLmThreads) {
+    const int m = i / kLmTile, c = i % kLmTile;
+    const uint32_t k = (uint32_t)__builtin_amdgcn_readlane((int)my_k, m);
+    if (k > 0u && c < len) a.lm_logits[(int64_t)m * a.V + tile0 + c] = tile[i];
   }
 }
 

@@ -152,3 +152,42 @@ def test_fused_duplicate_vocabulary_rows(hip, oracle):
     resolved = got != 0xFFFFFFFE
     assert np.array_equal(got[resolved], want[resolved])
     assert resolved.sum() >= 8, got
+
+
+def test_fused_clustered_tiles(hip, oracle):
+    """Weight rows equal to one of 400 base rows per 128-column tile plus 1%
+    noise: every column of a high tile outranks the low tiles, so the
+    tiles kept by the tile-top bound hold far more than 4096 keys above it
+    and the finish selects over global memory."""
+    import torch
+    from hi_amd import sampler as S
+    from hi_amd._lib import ROW_PARAMS_DTYPE
+    lib = hip.load()
+    B, H, V, cap = 8, 64, 128 * 400, 0.0
+    g = torch.Generator(device="cpu").manual_seed(51)
+    base = torch.randn((400, H), generator=g) * (2.0 / np.sqrt(H))
+    w = (base.repeat_interleave(128, dim=0) + 0.01 * torch.randn((V, H), generator=g)).to(torch.bfloat16).cuda()
+    h = torch.randn((B, H), generator=g).to(torch.bfloat16).cuda()
+    logits = _twin(hip, torch, h, w, None, cap, B, H, V)
+    rng = np.random.default_rng(52)
+    params = np.zeros(B, ROW_PARAMS_DTYPE)
+    params["temperature"] = rng.uniform(0.6, 1.0, B)
+    params["top_p"] = 1.0
+    params["top_k"] = np.array([64, 64, 40, 64, 50, 64, 1, 64], np.int32)
+    u = rng.random(B).astype(F32)
+    want = oracle.sample_rows(logits, params, u)["tokens"]
+    ws_n = ctypes.c_size_t()
+    hip.check(lib.hi_rocm_lm_head_workspace_bytes(B, V, ctypes.byref(ws_n)))
+    ws = torch.zeros(ws_n.value, dtype=torch.uint8, device="cuda")
+    dp = S.params_to_device(params)
+    du = torch.from_numpy(u).cuda()
+    out = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    print(f"lm head fused clustered tiles B={B} H={H} V={V}", flush=True)
+    torch.cuda.synchronize()
+    hip.check(lib.hi_rocm_sample_lm_head(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, dp.data_ptr(),
+                                         du.data_ptr(), out.data_ptr(), ws.data_ptr(), ws_n.value, s.cuda_stream))
+    s.synchronize()
+    got = out.cpu().numpy().view(np.uint32)
+    print(f"got {got.tolist()}\nwant {want.tolist()}", flush=True)
+    assert np.array_equal(got, want)

@@ -2496,11 +2496,13 @@ constexpr uint32_t kSelHistCap = 1024;     // distinct history tokens per chunk 
 constexpr int kSelHistPer = 8;             // history entries each thread loads up front
 constexpr int kSelOb = (int)kSelHistCap / NT;  // out-of-band history items per thread
 constexpr int kLaneSurv = 6;               // streamed survivors a lane takes per round (lean path)
+constexpr int kWideCopies = 8;             // copies of the mass histogram (lane % 8 picks one)
 
 struct SelLds {
   uint64_t surv[NT / 64][kSurvCap];
   uint32_t hist[256];
-  float whist[kWideBins];     // top-p rows: the chunk's mass histogram (WideStat)
+  float whist[kWideBins * kWideCopies];  // top-p rows: the chunk's mass histogram (WideStat),
+                                         // kWideCopies interleaved copies
   uint32_t sel[4];
   uint32_t hw[NT / 64];       // history tokens among each wave's logits
   uint32_t wcnt[NT / 64];
@@ -2714,12 +2716,26 @@ __device__ __forceinline__ SelNeeds sel_needs(const SampleArgs& a, const RowCfg&
 }
 
 // Adds one processed logit v (NaN: absent) to a top-p row's chunk mass
-// histogram: w' = exp((v - m) / T) = 2^r, bin floor(-r), clamped.
+// histogram: w' = exp((v - m) / T) = 2^r, bin floor(-r), clamped.  Lane l
+// adds to copy l % kWideCopies: the lanes of a wave that hit one bin (a
+// row's logits fill a few bins) then conflict kWideCopies times less.  The
+// masses are approximate (the wide pass keeps a margin), so the order of
+// the additions does not matter.
 __device__ __forceinline__ void wide_hist_add(float* whist, float v, float m, float a2) {
   if (!finitef_(v)) return;
   const float r = (v - m) * a2;
   const int j = -r < (float)(kWideBins - 1) ? (int)(-r) : kWideBins - 1;
-  atomicAdd(&whist[j], __builtin_amdgcn_exp2f(r));
+  atomicAdd(&whist[j * kWideCopies + (int)(threadIdx.x & (kWideCopies - 1))], __builtin_amdgcn_exp2f(r));
+}
+__device__ __forceinline__ void wide_hist_clear(float* whist) {
+  for (int i = threadIdx.x; i < kWideBins * kWideCopies; i += NT) whist[i] = 0.f;
+}
+// Bin b (b < kWideBins) summed over the copies.
+__device__ __forceinline__ float wide_hist_bin(const float* whist, int b) {
+  float s = 0.f;
+  #pragma unroll
+  for (int c = 0; c < kWideCopies; ++c) s += whist[b * kWideCopies + c];
+  return s;
 }
 
 // Exact pass over the chunk from global memory, element by element.  Used
@@ -2795,7 +2811,7 @@ __device__ __forceinline__ void select_exact(SelLds& L, const SampleArgs& a, con
     bs.lse_m = lm;
     bs.lse_sum = nd.lse ? rest : 0.f;
   }
-  if (nd.whist && tid < kWideBins) L.whist[tid] = 0.f;
+  if (nd.whist) wide_hist_clear(L.whist);
   __syncthreads();
   if (cfg.store_s) {
     float* srow = a.ws_s + (int64_t)row * a.V + c0;
@@ -2809,7 +2825,7 @@ __device__ __forceinline__ void select_exact(SelLds& L, const SampleArgs& a, con
   if (nd.whist) {
     __syncthreads();
     WideStat* ws = a.wstat + slot;
-    if (tid < kWideBins) ws->hist[tid] = L.whist[tid];
+    if (tid < kWideBins) ws->hist[tid] = wide_hist_bin(L.whist, tid);
     if (tid == 0) {
       ws->ms = finitef_(lmax) ? lmax / cfg.t_eff : lmax;
       ws->valid = 1u;
@@ -3149,7 +3165,7 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
     if (prefix <= kKeyNegInf) flag = 1u;
   }
   if (lane == 0u) { L.wmax[wid] = wm; L.wkey[wid] = tkey; L.wflag[wid] = flag; }
-  if (nd.whist && tid < kWideBins) L.whist[tid] = 0.f;
+  if (nd.whist) wide_hist_clear(L.whist);
   __syncthreads();
   float m = L.wmax[0];
   uint32_t tk = L.wkey[0];
@@ -3297,7 +3313,7 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
   }
   if (nd.whist) {
     WideStat* ws = a.wstat + slot;
-    if (lane < (uint32_t)kWideBins) ws->hist[lane] = L.whist[lane];
+    if (lane < (uint32_t)kWideBins) ws->hist[lane] = wide_hist_bin(L.whist, (int)lane);
     if (lane == 0u) {
       ws->ms = m / cfg.t_eff;
       ws->valid = 1u;

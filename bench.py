@@ -347,7 +347,7 @@ def time_lm_head(torch, B=32, H=4096, V=151936, cap=30.0, launches=10, rounds=6)
     on the launch stream over back-to-back calls, in alternating rounds (the
     median round of each is reported: the box's HBM throughput drifts by a
     few percent between rounds).  Rows: top-k 40, top-p 0.9, T 0.8; the
-    fused path is also timed with greedy rows, and the projection alone
+    fused and unfused paths are also timed with greedy rows, and the projection alone
     (hi_rocm_lm_head_logits, the logits written).  Algorithmic bytes per call:
     the bf16 weight V*H*2 and hidden B*H*2 read, tokens written (the
     projection reads every weight once)."""
@@ -379,15 +379,15 @@ def time_lm_head(torch, B=32, H=4096, V=151936, cap=30.0, launches=10, rounds=6)
         _lib.check(lib.hi_rocm_sample_lm_head(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, params_dev.data_ptr(),
                                               du.data_ptr(), tok.data_ptr(), ws.data_ptr(), n.value, s))
 
-    def unfused():
+    def unfused(params_dev):
         _lib.check(lib.hi_rocm_lm_head_logits(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, logits.data_ptr(), s))
-        smp.sample(logits, dp, du, out={"tokens": tok}, stream=stream)
+        smp.sample(logits, params_dev, du, out={"tokens": tok}, stream=stream)
 
     def twin():
         _lib.check(lib.hi_rocm_lm_head_logits(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, logits.data_ptr(), s))
 
-    cases = (("fused", lambda: fused(dp)), ("unfused", unfused), ("fused_greedy", lambda: fused(dg)),
-             ("projection", twin))
+    cases = (("fused", lambda: fused(dp)), ("unfused", lambda: unfused(dp)), ("fused_greedy", lambda: fused(dg)),
+             ("unfused_greedy", lambda: unfused(dg)), ("projection", twin))
     times = {name: [] for name, _ in cases}
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):

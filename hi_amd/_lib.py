@@ -58,6 +58,7 @@ SIGNATURES = {
     "hi_rocm_history_pack": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp]),
     "hi_rocm_rng_key_from_seed": (_i, [ctypes.c_uint64, _vp]),
     "hi_rocm_rng_uniforms": (_i, [_vp, _vp, _vp, _vp, _i, _vp]),
+    "hi_rocm_decode_step_advance": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "hi_rocm_debug_chacha_block": (_i, [_vp, _vp, _i, _vp]),
     "hi_rocm_profile_begin": (_i, [_i]),
     "hi_rocm_profile_end": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),

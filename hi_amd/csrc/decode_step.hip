@@ -188,6 +188,19 @@ __global__ void __launch_bounds__(256)
   words_used[b] = k + 1u;
 }
 
+// The next step's graph inputs from this step's samples
+// (upload_batch_graph_inputs, gpu.rs:10200-10245, on the device): rows
+// below n_active decode their sampled token at the next position; pad rows
+// decode token 0 at position 0.
+__global__ void __launch_bounds__(256)
+    step_advance_kernel(const uint32_t* sampled, uint32_t* tokens, uint32_t* positions, int n_active, int bucket) {
+  const int r = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (r >= bucket) return;
+  const bool live = r < n_active;
+  tokens[r] = live ? sampled[r] : 0u;
+  positions[r] = live ? positions[r] + 1u : 0u;
+}
+
 }  // namespace
 }  // namespace hi_rocm
 
@@ -244,6 +257,17 @@ int hi_rocm_rng_uniforms(const uint32_t* keys, uint64_t* words_used, const uint8
                      words_used, sampled, out_uniforms, batch);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? HI_ROCM_OK : hi_rocm::api_hip_fail(e, "rng uniforms launch");
+}
+
+int hi_rocm_decode_step_advance(const uint32_t* sampled, uint32_t* tokens, uint32_t* positions, int n_active,
+                                int bucket, void* stream) {
+  if (sampled == nullptr || tokens == nullptr || positions == nullptr || bucket <= 0 || n_active < 0 ||
+      n_active > bucket || stream == nullptr)
+    return hi_rocm::api_fail(HI_ROCM_ERR_ARGS, "hi_rocm_decode_step_advance: invalid arguments");
+  hipLaunchKernelGGL(hi_rocm::step_advance_kernel, dim3((bucket + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                     sampled, tokens, positions, n_active, bucket);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? HI_ROCM_OK : hi_rocm::api_hip_fail(e, "decode step advance launch");
 }
 
 int hi_rocm_debug_chacha_block(const uint32_t* key, const uint32_t* words12_15, int rounds, uint32_t* out) {

@@ -200,6 +200,15 @@ int hi_rocm_rng_key_from_seed(uint64_t seed, uint32_t* key);
 int hi_rocm_rng_uniforms(const uint32_t* keys, uint64_t* words_used, const uint8_t* sampled, float* out_uniforms,
                          int batch, void* stream);
 
+/* The next decode step's token and position inputs from this step's
+ * samples, on the device (upload_batch_graph_inputs, gpu.rs:10200-10245,
+ * copies them from the host every step): for r < n_active, tokens[r] =
+ * sampled[r] and positions[r] += 1; pad rows n_active <= r < bucket get
+ * token 0 at position 0.  Device u32 arrays of `bucket` entries (sampled
+ * may be hi_rocm_sample's out_tokens); graph-capturable, no allocation. */
+int hi_rocm_decode_step_advance(const uint32_t* sampled, uint32_t* tokens, uint32_t* positions, int n_active,
+                                int bucket, void* stream);
+
 /* Host: one ChaCha block (RFC 8439 block function) of `rounds` rounds with
  * state words 12-15 given; for the known-answer tests. */
 int hi_rocm_debug_chacha_block(const uint32_t* key, const uint32_t* words12_15, int rounds, uint32_t* out);

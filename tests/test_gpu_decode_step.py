@@ -176,3 +176,98 @@ def test_rng_uniforms_match_stdrng(hip):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (step, got, want)
     u = used.cpu().numpy()
     assert u[1] == 0 and u[0] == 40 and u[3] == (1 << 32) * 16 - 2 + 40
+
+
+def test_decode_step_graph_loop(hip, oracle):
+    """A whole decode step's upkeep captured once and replayed: uniforms from
+    each request's StdRng, the sampler on the packed history, the sampled
+    tokens appended, the history packed, and the next step's token and
+    position inputs written from the samples (hi_rocm_decode_step_advance,
+    the device form of upload_batch_graph_inputs).  Between replays only the
+    logits change, as a forward pass would write them; every replay must
+    equal the host chain: StdRng uniforms, the oracle on the host-built
+    history, the host history and the reference's pad-row rule."""
+    import torch
+    from hi_amd import sampler as S
+    from hi_amd._lib import ROW_PARAMS_DTYPE
+    lib = hip.load()
+    rng = np.random.default_rng(91)
+    B, n_active, cap, V = 6, 5, 64, 3000
+    seeds = [11, 12, 13, 14, 15, 0]
+    sampled = np.array([1, 1, 0, 1, 1, 0], np.uint8)  # request 2 greedy, row 5 a pad row
+    keys = np.zeros((B, 8), np.uint32)
+    for b, sd in enumerate(seeds):
+        k = (ctypes.c_uint32 * 8)()
+        hip.check(lib.hi_rocm_rng_key_from_seed(ctypes.c_uint64(sd), k))
+        keys[b] = list(k)
+    rngs = [D.StdRng(keys[b]) for b in range(B)]
+    params = np.zeros(B, ROW_PARAMS_DTYPE)
+    params["temperature"] = np.where(sampled == 1, 0.85, 0.0)
+    params["top_p"] = 0.95
+    params["top_k"] = 40
+    params["repetition_penalty"] = 1.2
+    params["frequency_penalty"] = 0.3
+    params["presence_penalty"] = 0.2
+    dparams = S.params_to_device(params)
+    dh = DevHistory(torch, lib, hip, B, cap)
+    ref = D.History(B, cap)
+    prompt_rows, prompt_toks = [], []
+    for r in range(n_active):
+        t = rng.integers(0, 60, int(rng.integers(3, 20)))
+        prompt_rows += [r] * len(t)
+        prompt_toks += [int(x) for x in t]
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    dh.append(_t(torch, np.array(prompt_rows, np.int32)), _t(torch, np.array(prompt_toks, np.uint32)),
+              len(prompt_rows), stream)
+    dh.pack(stream)
+    stream.synchronize()
+    ref.append(prompt_rows, prompt_toks)
+    dk = _t(torch, keys.reshape(-1))
+    used = torch.zeros(B, dtype=torch.int64, device="cuda")
+    ds = torch.from_numpy(sampled).to("cuda")
+    unif = torch.zeros(B, dtype=torch.float32, device="cuda")
+    logits = torch.zeros((B, V), dtype=torch.float32, device="cuda")
+    tokens = _t(torch, np.array([7, 8, 9, 10, 11, 0], np.uint32))
+    pos0 = np.array([20, 31, 5, 17, 3, 0], np.uint32)
+    positions = _t(torch, pos0)
+    smp = S.Sampler(B, V, 0)
+    with torch.cuda.stream(stream):
+        out = smp.sample(logits, dparams, unif, dh.offsets, dh.hids, dh.hcnt, stream=stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        cs = torch.cuda.current_stream()
+        hip.check(lib.hi_rocm_rng_uniforms(dk.data_ptr(), used.data_ptr(), ds.data_ptr(), unif.data_ptr(), B,
+                                           cs.cuda_stream))
+        smp.sample(logits, dparams, unif, dh.offsets, dh.hids, dh.hcnt, out=out, stream=cs)
+        dh.append(None, out["tokens"], n_active, cs)
+        dh.pack(cs)
+        hip.check(lib.hi_rocm_decode_step_advance(out["tokens"].data_ptr(), tokens.data_ptr(),
+                                                  positions.data_ptr(), n_active, B, cs.cuda_stream))
+    torch.cuda.synchronize()
+    # capture runs nothing
+    assert int(used.sum().item()) == 0
+    want_pos = pos0.astype(np.int64).copy()
+    for step in range(6):
+        lg = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+        lg[:, :60] += 2.5  # the history tokens compete
+        logits.copy_(torch.from_numpy(lg))
+        torch.cuda.synchronize()
+        u = np.array([rngs[b].uniform_f32() if sampled[b] else 0.0 for b in range(B)], np.float32)
+        offsets, ids, counts = ref.csr()
+        want = oracle.sample_rows(lg, params, u, np.array(offsets, np.uint32), np.array(ids, np.uint32),
+                                  np.array(counts, np.uint32))["tokens"]
+        print(f"decode-step graph replay {step}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(unif.cpu().numpy().view(np.uint32), u.view(np.uint32)), step
+        got = out["tokens"].cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, want), (step, got, want)
+        ref.append(list(range(n_active)), [int(x) for x in got[:n_active]])
+        assert dh.read() == (*ref.csr(), ref.overflow), step
+        want_pos[:n_active] += 1
+        want_pos[n_active:] = 0
+        want_tok = np.concatenate([want[:n_active], np.zeros(B - n_active, np.uint32)])
+        assert np.array_equal(tokens.cpu().numpy().view(np.uint32), want_tok), step
+        assert np.array_equal(positions.cpu().numpy().view(np.uint32), want_pos.astype(np.uint32)), step

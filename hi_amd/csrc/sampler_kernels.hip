@@ -4505,9 +4505,11 @@ __global__ void __launch_bounds__(1024) debug_probs_kernel(SampleArgs a, const f
 // bf16 MFMAs (16x16x32, f32 accumulation) over the hidden dimension, add the
 // bias, apply the softcap (softcap.h), and keep the tile's processed logits
 // in LDS.  The fused kernel then records, per (row, tile), what the finish
-// needs -- the maximum, both argmaxes, and the tile's top-k candidates --
-// so the logits never reach HBM.  The twin kernel runs the same code and
-// writes the logits instead: the fused path's logits are bit-identical to
+// needs -- the maximum, both argmaxes and the largest candidate key -- and
+// leaves the tile's logits in the workspace only for top-k rows, whose
+// finish reads back the few tiles that can hold the row's top k (greedy
+// rows write no logits at all).  The twin kernel runs the same code and
+// writes every logit instead: the fused path's logits are bit-identical to
 // the twin's by construction (same tiles, same MFMA order, same epilogue).
 //
 // MFMA 16x16x32 bf16 operand layout (lane l = 16 * g + r): A row r, K
@@ -4784,10 +4786,6 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     if (tid == 0) a.out_tokens[row] = 0xffffffffu;
     return;
   }
-  // warm the exponential's table (its first use, in the weights below,
-  // would otherwise wait on a cold miss); the loads overlap the records'
-  uint64_t warm = 0ull;
-  if (tid < 32) warm = exp2_tab32((uint32_t)tid);
   // merge the tile records
   uint32_t mk = 0u, tk = 0u, ti = 0xffffffffu, ai = 0xffffffffu;
   float av = -__builtin_inff();
@@ -4800,7 +4798,6 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
       av = r.am_ieee_v; ai = r.am_ieee_i;
     }
   }
-  asm volatile("" ::"v"(warm));
   {
     // the three maxima in one exchange: the logit key, total_cmp's argmax
     // and the IEEE argmax ((value key, -index) over the tiles that have one)

@@ -496,7 +496,8 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.lm_head_only:
-        print(json.dumps({"lm_head_fused": time_lm_head(torch)}))
+        print(json.dumps({"lm_head_fused": time_lm_head(torch),
+                          "lm_head_fused_b64": time_lm_head(torch, B=64, rounds=3)}))
         return
     w3 = config3()
     if args.pmc_probe:
@@ -567,6 +568,7 @@ def main():
     res["dsv4_indexer_select"] = time_indexer_select(torch, cpu=not args.no_cpu_baseline)
     res["moe_router"] = time_router(torch, cpu=not args.no_cpu_baseline)
     res["lm_head_fused"] = time_lm_head(torch)
+    res["lm_head_fused_b64"] = time_lm_head(torch, B=64, rounds=3)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w3, args.cpu_budget)
         res["cpu_baseline_all_cores"] = cpu_baseline_all_cores(w3)

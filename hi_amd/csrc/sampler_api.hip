@@ -479,7 +479,7 @@ int lm_args(const void* hidden, const void* weight, const float* bias, float sof
     return fail(HI_ROCM_ERR_ARGS, std::string(what) + ": invalid arguments");
   if (batch > hi_rocm::kLmRows || hidden_dim % 32 != 0 || (uintptr_t)hidden % 16 != 0 || (uintptr_t)weight % 16 != 0)
     return fail(HI_ROCM_ERR_UNSUPPORTED,
-                std::string(what) + ": needs batch <= 32, hidden_dim a multiple of 32, 16-byte aligned bf16 arrays");
+                std::string(what) + ": needs batch <= 64, hidden_dim a multiple of 32, 16-byte aligned bf16 arrays");
   const int tiles = (vocab + hi_rocm::kLmTile - 1) / hi_rocm::kLmTile;
   if (tiles > hi_rocm::kLmMaxTiles)
     return fail(HI_ROCM_ERR_UNSUPPORTED, std::string(what) + ": vocabulary above 524,288");

@@ -242,7 +242,7 @@ int api_hip_fail(hipError_t e, const char* where);
 // pass (sampler_kernels.hip).
 constexpr int kLmTile = 128;     // vocabulary columns per workgroup (chunk)
 constexpr int kLmThreads = 128;  // 2 waves of 64 columns
-constexpr int kLmRows = 32;      // rows per call
+constexpr int kLmRows = 64;      // rows per call (two groups of 32)
 constexpr int kLmMaxK = 64;      // largest top-k of the fused finish
 constexpr int kLmMaxTiles = 4096;  // tiles per row the fused finish holds (V <= 524,288)
 struct LmTileRec;

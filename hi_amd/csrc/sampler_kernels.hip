@@ -4535,8 +4535,10 @@ static_assert(sizeof(LmTileRec) == 32, "LmTileRec layout");
 __device__ __forceinline__ lm_bf16x8 lm_ld(const __bf16* p) { return *reinterpret_cast<const lm_bf16x8*>(p); }
 
 // The logits of vocabulary columns [tile0, tile0 + kLmTile) for rows
-// [0, B), processed (bias, softcap), into tile[m * kLmTile + column].  Wave w
-// owns 64 columns as four 16-column MFMA tiles, times two 16-row tiles.
+// [0, B), B <= 32 RG, processed (bias, softcap), into tile[m * kLmTile +
+// column].  Wave w owns 64 columns as four 16-column MFMA tiles, times two
+// 16-row tiles for each of the RG groups of 32 rows (every weight block
+// loaded is used by all rows).
 // K runs in blocks of 64: lane (g, r) loads 32 contiguous bytes of its
 // weight row at element 16g and gives the first half to one MFMA and the
 // second to the next, so each row's 128-byte line is used whole by one load
@@ -4553,47 +4555,62 @@ __device__ __forceinline__ lm_bf16x8 lm_ld(const __bf16* p) { return *reinterpre
 // sitting at one offset (about 10% more HBM throughput than a common
 // start).  A trailing 32-element block (H % 64 == 32) takes the plain
 // layout, element 8g, last.  The order is fixed per tile, so every kernel
-// built on this function produces the same bits.
+// built on this function produces the same bits (and a row's logits do not
+// depend on RG or on the other rows).
+template <int RG>
 __device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* tile) {
-  static_assert(kLmThreads == 128 && kLmRows == 32, "hidden block staging: 128 threads x 32 bytes");
-  __shared__ __align__(16) __bf16 a_lds[2][kLmRows * 64];
+  static_assert(kLmThreads == 128, "hidden block staging: 128 threads x 32 bytes per row group");
+  __shared__ __align__(16) __bf16 a_lds[2][RG * 32 * 64];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int H = a.H, nb = a.H >> 6;
   const int v0 = tile0 + wid * 64;
-  lm_f32x4 acc[2][4];
+  lm_f32x4 acc[RG][2][4];
   #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int q = 0; q < RG; ++q)
     #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = lm_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < 2; ++mt)
+      #pragma unroll
+      for (int nt = 0; nt < 4; ++nt) acc[q][mt][nt] = lm_f32x4{0.f, 0.f, 0.f, 0.f};
   const __bf16* wrow[4];
   #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int v = v0 + nt * 16 + r;
     wrow[nt] = a.weight + (int64_t)(v < a.V ? v : 0) * H;
   }
-  // this thread's share of a hidden block: row tid / 4, elements 16 (tid % 4)
-  // .. + 15 of the block, which is MFMA lane (tid % 4, row % 16)'s operand
-  const int am = tid >> 2;
-  const __bf16* arow = a.hidden + (int64_t)(am < a.B ? am : 0) * H + 16 * (tid & 3);
+  // this thread's share of a hidden block: rows 32 q + tid / 4, elements
+  // 16 (tid % 4) .. + 15 of the block, which is MFMA lane (tid % 4, row % 16)'s
+  // operand
+  const __bf16* arow[RG];
+  #pragma unroll
+  for (int q = 0; q < RG; ++q) {
+    const int am = 32 * q + (tid >> 2);
+    arow[q] = a.hidden + (int64_t)(am < a.B ? am : 0) * H + 16 * (tid & 3);
+  }
   const int rot = nb > 0 ? (int)((uint32_t)(tile0 / kLmTile) % (uint32_t)nb) : 0;
   auto blk = [&](int i) { const int b = i + rot; return (b >= nb ? b - nb : b) * 64; };
-  lm_bf16x8 bb[2][4][2], ar[3][2];
+  lm_bf16x8 bb[2][4][2], ar[3][RG][2];
   auto load_w = [&](lm_bf16x8 (&br)[4][2], int i) {
     const int off = blk(i) + 16 * g;
     #pragma unroll
     for (int nt = 0; nt < 4; ++nt) { br[nt][0] = lm_ld(wrow[nt] + off); br[nt][1] = lm_ld(wrow[nt] + off + 8); }
   };
-  auto load_h = [&](lm_bf16x8 (&x)[2], int i) {
+  auto load_h = [&](lm_bf16x8 (&x)[RG][2], int i) {
     const int off = blk(i);
-    x[0] = lm_ld(arow + off);
-    x[1] = lm_ld(arow + off + 8);
+    #pragma unroll
+    for (int q = 0; q < RG; ++q) {
+      x[q][0] = lm_ld(arow[q] + off);
+      x[q][1] = lm_ld(arow[q] + off + 8);
+    }
   };
-  auto stage_h = [&](const lm_bf16x8 (&x)[2], int slot) {
-    lm_bf16x8* d = reinterpret_cast<lm_bf16x8*>(&a_lds[slot][tid * 16]);
-    d[0] = x[0];
-    d[1] = x[1];
+  auto stage_h = [&](const lm_bf16x8 (&x)[RG][2], int slot) {
+    #pragma unroll
+    for (int q = 0; q < RG; ++q) {
+      lm_bf16x8* d = reinterpret_cast<lm_bf16x8*>(&a_lds[slot][(q * kLmThreads + tid) * 16]);
+      d[0] = x[q][0];
+      d[1] = x[q][1];
+    }
   };
   if (nb > 0) { load_w(bb[0], 0); load_h(ar[0], 0); }
   if (nb > 1) { load_w(bb[1], 1); load_h(ar[1], 1); }
@@ -4609,20 +4626,25 @@ __device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* 
       if (j < nb) {
         __syncthreads();  // LDS slot j % 2 written, slot (j + 1) % 2 read by both waves
         if (j + 1 < nb) stage_h(ar[(u + 1) % 3], (u + 1) % 2);
-        lm_bf16x8 af[2][2];
         #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const lm_bf16x8* src = reinterpret_cast<const lm_bf16x8*>(&a_lds[u % 2][((mt * 16 + r) * 4 + g) * 16]);
-          af[mt][0] = src[0];
-          af[mt][1] = src[1];
-        }
-        #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int q = 0; q < RG; ++q) {
+          lm_bf16x8 af[2][2];
           #pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
+          for (int mt = 0; mt < 2; ++mt) {
+            const lm_bf16x8* src =
+                reinterpret_cast<const lm_bf16x8*>(&a_lds[u % 2][(q * kLmThreads + (mt * 16 + r) * 4 + g) * 16]);
+            af[mt][0] = src[0];
+            af[mt][1] = src[1];
+          }
+          #pragma unroll
+          for (int h = 0; h < 2; ++h)
             #pragma unroll
-            for (int nt = 0; nt < 4; ++nt)
-              acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][h], bb[u % 2][nt][h], acc[mt][nt], 0, 0, 0);
+            for (int mt = 0; mt < 2; ++mt)
+              #pragma unroll
+              for (int nt = 0; nt < 4; ++nt)
+                acc[q][mt][nt] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][h], bb[u % 2][nt][h], acc[q][mt][nt], 0, 0, 0);
+        }
         if (j + 2 < nb) load_w(bb[u % 2], j + 2);
         if (j + 3 < nb) load_h(ar[u % 3], j + 3);
       }
@@ -4630,43 +4652,56 @@ __device__ __forceinline__ void lm_gemm_tile(const LmArgs& a, int tile0, float* 
   }
   if ((nb << 6) < H) {
     const int off = (nb << 6) + 8 * g;
-    lm_bf16x8 at[2], bt[4];
-    #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int m = mt * 16 + r;
-      at[mt] = lm_ld(a.hidden + (int64_t)(m < a.B ? m : 0) * H + off);
-    }
+    lm_bf16x8 bt[4];
     #pragma unroll
     for (int nt = 0; nt < 4; ++nt) bt[nt] = lm_ld(wrow[nt] + off);
+    #pragma unroll
+    for (int q = 0; q < RG; ++q) {
+      lm_bf16x8 at[2];
+      #pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int m = 32 * q + mt * 16 + r;
+        at[mt] = lm_ld(a.hidden + (int64_t)(m < a.B ? m : 0) * H + off);
+      }
+      #pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        #pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          acc[q][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at[mt], bt[nt], acc[q][mt][nt], 0, 0, 0);
+    }
+  }
+  // epilogue: bias, softcap; tile[m * kLmTile + column]
+  #pragma unroll
+  for (int q = 0; q < RG; ++q)
     #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
       #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at[mt], bt[nt], acc[mt][nt], 0, 0, 0);
-  }
-  // epilogue: bias, softcap; tile[m * kLmTile + column]
-  #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-    #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-      #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int m = mt * 16 + 4 * g + jj;
-        const int v = v0 + nt * 16 + r;
-        if (m >= a.B || v >= a.V) continue;
-        float x = acc[mt][nt][jj];
-        if (a.bias) x = x + a.bias[v];
-        if (a.cap > 0.f) x = softcap_f32(x, a.cap);
-        tile[m * kLmTile + (v - tile0)] = x;
-      }
+        #pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int m = 32 * q + mt * 16 + 4 * g + jj;
+          const int v = v0 + nt * 16 + r;
+          if (m >= a.B || v >= a.V) continue;
+          float x = acc[q][mt][nt][jj];
+          if (a.bias) x = x + a.bias[v];
+          if (a.cap > 0.f) x = softcap_f32(x, a.cap);
+          tile[m * kLmTile + (v - tile0)] = x;
+        }
 }
 
+// Registers: one row group fits 3 waves per SIMD (every workgroup of a
+// 151936-column head resident at once), two row groups 2.
+template <int RG>
+constexpr int lm_waves_per_eu() { return RG == 1 ? 3 : 2; }
+
 // The twin: the same tiles, written to logits [B][V].
-__global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) lm_logits_kernel(LmArgs a) {
+template <int RG>
+__global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(lm_waves_per_eu<RG>(), 8)))
+    lm_logits_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* tile = reinterpret_cast<float*>(lds_raw);
   const int tile0 = blockIdx.x * kLmTile;
-  lm_gemm_tile(a, tile0, tile);
+  lm_gemm_tile<RG>(a, tile0, tile);
   __syncthreads();
   const int len = min(kLmTile, a.V - tile0);
   for (int i = threadIdx.x; i < a.B * kLmTile; i += kLmThreads) {
@@ -4690,7 +4725,9 @@ __device__ __forceinline__ uint64_t ieee_key(float l, uint32_t e) { return cand_
 // w + kLmThreads / 64, ... of the tile.  A top-k row also leaves the tile's
 // logits in the workspace, where the finish reads the few tiles that can
 // hold the row's top k (greedy rows leave nothing but the records).
-__global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) lm_select_kernel(LmArgs a) {
+template <int RG>
+__global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(lm_waves_per_eu<RG>(), 8)))
+    lm_select_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* tile = reinterpret_cast<float*>(lds_raw);
   const int t = blockIdx.x, tile0 = t * kLmTile;
@@ -4702,7 +4739,7 @@ __global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu
     const RowCfg cfg = load_cfg(a.pv, lane, a.V, 0, 0);
     my_k = (cfg.cls == kTopK && cfg.k_eff <= kLmMaxK) ? (uint32_t)cfg.k_eff : 0u;
   }
-  lm_gemm_tile(a, tile0, tile);
+  lm_gemm_tile<RG>(a, tile0, tile);
   __syncthreads();
   const int len = min(kLmTile, a.V - tile0);
   constexpr int PER = kLmTile / 64;
@@ -4956,7 +4993,7 @@ size_t lm_workspace_bytes(int B, int V) {
   return lm_recs_bytes(B, tiles) + (size_t)B * V * sizeof(float);
 }
 
-size_t lm_select_lds() { return (size_t)kLmRows * kLmTile * sizeof(float); }
+size_t lm_tile_lds(int B) { return (size_t)(B <= 32 ? 32 : kLmRows) * kLmTile * sizeof(float); }
 size_t lm_finish_lds() { return (sizeof(FinLds) + 15) & ~(size_t)15; }
 
 // --------------------------------------------------------------------------
@@ -5749,19 +5786,28 @@ hipError_t launch_debug_distribution(const SampleArgs& a, float* out_proc, float
   return hipGetLastError();
 }
 
-hipError_t launch_lm_logits(const LmArgs& a, hipStream_t stream) {
-  const size_t lds = (size_t)kLmRows * kLmTile * sizeof(float);
-  hipError_t e = ensure_lds((const void*)lm_logits_kernel, lds);
+template <int RG>
+hipError_t launch_lm_logits_rg(const LmArgs& a, hipStream_t stream) {
+  const size_t lds = lm_tile_lds(a.B);
+  hipError_t e = ensure_lds((const void*)lm_logits_kernel<RG>, lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(lm_logits_kernel, dim3((unsigned)a.n_chunks), dim3(kLmThreads), lds, stream, a);
+  hipLaunchKernelGGL(lm_logits_kernel<RG>, dim3((unsigned)a.n_chunks), dim3(kLmThreads), lds, stream, a);
   return hipGetLastError();
 }
 
+hipError_t launch_lm_logits(const LmArgs& a, hipStream_t stream) {
+  return a.B <= 32 ? launch_lm_logits_rg<1>(a, stream) : launch_lm_logits_rg<2>(a, stream);
+}
+
 hipError_t launch_lm_sample(const LmArgs& a, hipStream_t stream) {
-  const size_t l1 = lm_select_lds();
-  hipError_t e = ensure_lds((const void*)lm_select_kernel, l1);
+  const size_t l1 = lm_tile_lds(a.B);
+  const void* sel = a.B <= 32 ? (const void*)lm_select_kernel<1> : (const void*)lm_select_kernel<2>;
+  hipError_t e = ensure_lds(sel, l1);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(lm_select_kernel, dim3((unsigned)a.n_chunks), dim3(kLmThreads), l1, stream, a);
+  if (a.B <= 32)
+    hipLaunchKernelGGL(lm_select_kernel<1>, dim3((unsigned)a.n_chunks), dim3(kLmThreads), l1, stream, a);
+  else
+    hipLaunchKernelGGL(lm_select_kernel<2>, dim3((unsigned)a.n_chunks), dim3(kLmThreads), l1, stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t l2 = lm_finish_lds();

@@ -132,7 +132,7 @@ int hi_rocm_launch_moe_topk_router(const void* scores, void* output_ids, void* o
  *   hidden  bf16[batch][hidden_dim], weight bf16[vocab][hidden_dim] (both
  *           16-byte aligned), bias f32[vocab] or null, softcap > 0 applies
  *           cap * tanh(x / cap) (tanh defined in hi_amd/csrc/softcap.h; the
- *           reference uses CUDA's tanhf), batch <= 32, hidden_dim % 32 == 0,
+ *           reference uses CUDA's tanhf), batch <= 64, hidden_dim % 32 == 0,
  *           vocab <= 524288 (status 2 otherwise).
  * hi_rocm_lm_head_logits writes the logits f32[batch][vocab] (the unfused
  * twin).  hi_rocm_sample_lm_head samples from the same logits (bit for bit)

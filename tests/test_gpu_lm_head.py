@@ -39,7 +39,7 @@ def _twin(hip, torch, h, w, bias, cap, B, H, V):
 
 
 @pytest.mark.parametrize("B,H,V,cap", [(5, 64, 2000, 0.0), (32, 256, 3001, 5.0), (17, 4096, 1024, 30.0),
-                                       (9, 96, 777, 2.0)])
+                                       (9, 96, 777, 2.0), (48, 256, 3001, 5.0), (64, 160, 1500, 0.0)])
 def test_twin_logits_match_float64(hip, B, H, V, cap):
     import torch
     h, hn = _bf16(torch, (B, H), 1.0, 1)
@@ -64,8 +64,10 @@ def test_twin_logits_match_float64(hip, B, H, V, cap):
 
 # (32, 512, 50000): more tiles than k (the tile-top bound); (20, 96, 3000):
 # fewer tiles than most k (every tile scanned) and a trailing 32-wide K
-# block; (8, 64, 50): one tile shorter than k (zero-padded slots).
-@pytest.mark.parametrize("B,H,V,cap,seed", [(32, 512, 50000, 8.0, 11), (20, 96, 3000, 0.0, 21), (8, 64, 50, 3.0, 31)])
+# block; (8, 64, 50): one tile shorter than k; (64, 512, 20000) and
+# (40, 96, 5000): two row groups of 32 per tile.
+@pytest.mark.parametrize("B,H,V,cap,seed", [(32, 512, 50000, 8.0, 11), (20, 96, 3000, 0.0, 21), (8, 64, 50, 3.0, 31),
+                                            (64, 512, 20000, 8.0, 61), (40, 96, 5000, 2.0, 71)])
 def test_fused_tokens_match_oracle_on_twin_logits(hip, oracle, B, H, V, cap, seed):
     import torch
     from hi_amd import sampler as S
@@ -191,3 +193,17 @@ def test_fused_clustered_tiles(hip, oracle):
     got = out.cpu().numpy().view(np.uint32)
     print(f"got {got.tolist()}\nwant {want.tolist()}", flush=True)
     assert np.array_equal(got, want)
+
+
+def test_twin_rows_do_not_depend_on_the_batch(hip):
+    """A row's logits are the same bits whether the call has one row group
+    (20 rows) or two (40 rows, the first 20 the same)."""
+    import torch
+    H, V, cap = 256, 2500, 6.0
+    h, _ = _bf16(torch, (40, H), 1.0, 81)
+    w, _ = _bf16(torch, (V, H), 1.0 / np.sqrt(H), 82)
+    bias = torch.from_numpy((np.random.default_rng(83).standard_normal(V) * 0.5).astype(F32)).cuda()
+    print("lm head twin batch independence", flush=True)
+    big = _twin(hip, torch, h, w, bias, cap, 40, H, V)
+    small = _twin(hip, torch, h[:20].contiguous(), w, bias, cap, 20, H, V)
+    assert np.array_equal(big[:20].view(np.uint32), small.view(np.uint32))

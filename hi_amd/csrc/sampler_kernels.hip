@@ -5026,8 +5026,11 @@ constexpr int kSelChunkSmall = NT * 16;
 //  - History tokens stream like the others (their raw logits).  The history
 //    is ranked in LDS after the first tile (a word of marks per 32 logits
 //    and the number of marked logits before it), and its logits are loaded
-//    while the stream runs; after it their penalties are applied, and list
-//    entries that are history tokens are dropped.
+//    while the stream runs.  Each thread applies the penalties to its own
+//    history entries as soon as its part of the stream ends (the waves
+//    finish up to ~2.5 us apart, in age order per SIMD, so most of that work
+//    hides behind the youngest waves' last tiles) and stores the processed
+//    keys by rank; list entries that are history tokens are dropped.
 //  - Every logit left out has a key at or below the largest wave threshold
 //    Tm, so the union of the lists and the processed history logits above
 //    Tm holds the row's top k whenever its k-th key is above Tm (finish_core
@@ -5059,7 +5062,8 @@ static_assert(kRowKwMax < kRowHW, "a full list holds more than kw entries");
 
 struct RowLds {
   uint64_t wbuf[kRowWaves][kRowCap];   // per-wave candidate lists
-  uint32_t ob_raw[kRowHistCap];        // logit (mask applied) of the history token of rank r
+  uint32_t ob_raw[kRowHistCap];        // key of the processed logit (mask, penalties) of the
+                                       // history token of rank r
   uint32_t ob_cnt[kRowHistCap];        // its summed count
   uint32_t ob_id[kRowHistCap];         // its id
   float xscr[kRowWaves][64 * kRowEl];  // a wave's tile when a branch needs single logits; also
@@ -5382,6 +5386,7 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     #pragma unroll
     for (int r = 0; r < kRowHistPer; ++r) add(hid[r], hcs[r]);
     for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) add(a.hids[h], a.hcnt[h]);
+    __syncthreads();  // the summed counts are complete before any wave's stream ends
   }
   // the history tokens' logits, in flight during the stream: unconditional
   // range-checked loads (an id past the row reads zero and is not stored)
@@ -5406,7 +5411,10 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   if (hist) {
     auto put = [&](uint32_t id, uint32_t raw) {
       const uint2 h = hw[id >> 5];
-      L.ob_raw[h.y + (uint32_t)__popc(h.x & ((1u << (id & 31u)) - 1u))] = raw;
+      const uint32_t rank = h.y + (uint32_t)__popc(h.x & ((1u << (id & 31u)) - 1u));
+      const float l = __uint_as_float(raw);
+      const uint32_t c = L.ob_cnt[rank];
+      L.ob_raw[rank] = lkey(cfg.rep_on ? apply_penalties(l, c, cfg) : apply_penalties_norep(l, c, cfg));
     };
     constexpr uint32_t kNegInfBits = 0xff800000u;
     #pragma unroll
@@ -5471,27 +5479,17 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   const uint32_t r0 = (uint32_t)tid * (uint32_t)kHq;  // this thread's ranks: r0 .. r0 + kHq - 1
   if (r0 < distinct) {
     static_assert(kHq % 4 == 0, "ranks are read four at a time");
-    uint32_t raw[kHq], cnt[kHq], ids[kHq];
+    uint32_t kys[kHq], ids[kHq];
     #pragma unroll
     for (int q = 0; q < kHq; q += 4) {
       const uint4 x = *reinterpret_cast<const uint4*>(&L.ob_raw[r0 + q]);
-      const uint4 c = *reinterpret_cast<const uint4*>(&L.ob_cnt[r0 + q]);
       const uint4 i = *reinterpret_cast<const uint4*>(&L.ob_id[r0 + q]);
-      raw[q] = x.x; raw[q + 1] = x.y; raw[q + 2] = x.z; raw[q + 3] = x.w;
-      cnt[q] = c.x; cnt[q + 1] = c.y; cnt[q + 2] = c.z; cnt[q + 3] = c.w;
+      kys[q] = x.x; kys[q + 1] = x.y; kys[q + 2] = x.z; kys[q + 3] = x.w;
       ids[q] = i.x; ids[q + 1] = i.y; ids[q + 2] = i.z; ids[q + 3] = i.w;
-    }
-    float pl[kHq];
-    if (cfg.rep_on) {
-      #pragma unroll
-      for (int q = 0; q < kHq; ++q) pl[q] = apply_penalties(__uint_as_float(raw[q]), cnt[q], cfg);
-    } else {
-      #pragma unroll
-      for (int q = 0; q < kHq; ++q) pl[q] = apply_penalties_norep(__uint_as_float(raw[q]), cnt[q], cfg);
     }
     #pragma unroll
     for (int q = 0; q < kHq; ++q) {
-      const uint32_t k = lkey(pl[q]);
+      const uint32_t k = kys[q];
       const bool keep = r0 + q < distinct && k > kKeyNegInf && k >= Tm;
       hc[q] = keep ? cand_key(k, ids[q]) : 0ull;
       mine += keep ? 1u : 0u;

@@ -2128,6 +2128,49 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// The largest key prefix with the low 12 bits clear that at least `need`
+// of the wave's group-maximum keys (four per lane) reach, or 0 when none
+// does: it is the need-th largest key with its low 12 bits cleared.  For
+// need <= 16 that key comes from `need` extractions of the wave maximum
+// (each a DPP reduction, the lane holding it moving to its next key); a
+// 20-step bit-by-bit search with a ballot count per step is the general
+// form, and gives the same prefix.  `need` is uniform over the wave.
+__device__ __forceinline__ uint32_t wave_prefix_reach(const uint32_t (&gk)[4], uint32_t need) {
+  if (need <= 16u) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t s0 = gk[0], s1 = gk[1], s2 = gk[2], s3 = gk[3];
+    auto cx = [](uint32_t& p, uint32_t& q) {
+      const uint32_t hi = max(p, q), lo = min(p, q);
+      p = hi;
+      q = lo;
+    };
+    cx(s0, s1); cx(s2, s3); cx(s0, s2); cx(s1, s3); cx(s1, s2);  // s0 >= s1 >= s2 >= s3
+    uint32_t v = 0u;
+    #pragma unroll 1
+    for (uint32_t it = 0; it < need; ++it) {
+      v = wave_max_u32(s0);
+      const uint64_t who = __ballot(s0 == v);
+      if (lane == (uint32_t)(__ffsll((unsigned long long)who) - 1)) {
+        s0 = s1;
+        s1 = s2;
+        s2 = s3;
+        s3 = 0u;
+      }
+    }
+    return v & 0xfffff000u;
+  }
+  uint32_t prefix = 0u;
+  #pragma unroll 1
+  for (int bit = 31; bit >= 12; --bit) {
+    const uint32_t probe = prefix | (1u << bit);
+    uint32_t c = 0u;
+    #pragma unroll
+    for (int g = 0; g < 4; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
+    if (c >= need) prefix = probe;
+  }
+  return prefix;
+}
+
 // Up to NS LDS arrays of candidate keys, read as one list.
 template <int NS>
 struct Segs {
@@ -2901,15 +2944,7 @@ __device__ __forceinline__ bool select_lean(SelLds& L, const SampleArgs& a, cons
   bool inf = false;
   #pragma unroll
   for (int g = 0; g < 4; ++g) { gk[g] = okey(G[g]); inf |= G[g] == __builtin_inff(); }
-  uint32_t prefix = 0u;
-  #pragma unroll 1
-  for (int bit = 31; bit >= 12; --bit) {
-    const uint32_t probe = prefix | (1u << bit);
-    uint32_t c = 0u;
-    #pragma unroll
-    for (int g = 0; g < 4; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
-    if (c >= need) prefix = probe;
-  }
+  const uint32_t prefix = wave_prefix_reach(gk, need);
   const bool bad = !idle && (__ballot(inf) != 0ull || need > 4u * 64u || prefix <= kKeyNegInf);
   if (lane == 0u) { L.wkey[wid] = idle ? 0xffffffffu : prefix; L.wflag[wid] = bad ? 1u : 0u; }
   __syncthreads();
@@ -3152,15 +3187,7 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
       #pragma unroll
       for (int g = 0; g < 4; ++g) gk[g] = okey(G[g]);
     }
-    uint32_t prefix = 0u;
-    #pragma unroll 1
-    for (int bit = 31; bit >= 12; --bit) {
-      const uint32_t probe = prefix | (1u << bit);
-      uint32_t c = 0u;
-      #pragma unroll
-      for (int g = 0; g < 4; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
-      if (c >= k1w) prefix = probe;
-    }
+    const uint32_t prefix = wave_prefix_reach(gk, k1w);
     tkey = prefix;
     if (prefix <= kKeyNegInf) flag = 1u;
   }
@@ -5262,15 +5289,8 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
       #pragma unroll
       for (int g = 0; g < NG; ++g)
         gk[g] = lkey(fmaxf(fmaxf(x[4 * g], x[4 * g + 1]), fmaxf(x[4 * g + 2], x[4 * g + 3])));
-      uint32_t prefix = 0u;
-      #pragma unroll 1
-      for (int bit = 31; bit >= 12; --bit) {
-        const uint32_t probe = prefix | (1u << bit);
-        uint32_t c = 0u;
-        #pragma unroll
-        for (int g = 0; g < NG; ++g) c += (uint32_t)__popcll(__ballot(gk[g] >= probe));
-        if (c >= kw) prefix = probe;
-      }
+      static_assert(NG == 4, "four group maxima per lane");
+      const uint32_t prefix = wave_prefix_reach(gk, kw);
       if (prefix > kKeyNegInf + 1u) set_t(prefix - 1u);
     }
     // any logit above the threshold?  Against a positive threshold the raw

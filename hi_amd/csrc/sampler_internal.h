@@ -19,6 +19,7 @@ constexpr int kFast = 1024;                        // candidates kept per chunk 
 constexpr int kLeanK = 256;                        // largest top-k of the streaming selection
 constexpr int kMaxVocab = 1 << 23;                 // 8,388,608
 constexpr int kLseTop = 16;                        // per-chunk candidates kept for logprobs
+constexpr int kRowGeneralChunk = kScanThreads * 32;  // logits per chunk of the row kernel's general path
 
 enum RowClass : int { kGreedy = 0, kTopK = 1, kTopP = 2, kTempOnly = 3 };
 enum ParamsMode : int { kParamsRows = 0, kParamsSoA = 1, kParamsUniform = 2 };
@@ -195,6 +196,9 @@ inline WorkspaceLayout workspace_layout(int max_batch, int V) {
       const int64_t s = (int64_t)b * ((V + ch - 1) / ch);
       if (s > L.slots) L.slots = s;
     }
+    // the row kernel's general path (8192-logit chunks)
+    const int64_t sg = (int64_t)b * ((V + kRowGeneralChunk - 1) / kRowGeneralChunk);
+    if (sg > L.slots) L.slots = sg;
   }
   L.list_stride = next_pow2_i64(V);
   size_t off = 0;

@@ -5572,9 +5572,15 @@ __device__ __noinline__ void row_general(KernargSampleArgs* ap, int row) {
     #pragma unroll
     for (int i = 0; i < (int)(sizeof(SampleArgs) / 8); ++i) d[i] = w[i];
   }
+  // 8192-logit chunks (the launch's records are not used here): half the
+  // registers of 16384-logit ones, which halves the path's spills (its
+  // scratch is allocated for every wave of the launch, and costs the
+  // launch time even when no row comes here)
+  a.chunk = kRowGeneralChunk;
+  a.n_chunks = (a.V + kRowGeneralChunk - 1) / kRowGeneralChunk;
   const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
   for (int c = 0; c < a.n_chunks; ++c) {
-    select_chunk<HI_ROCM_DTYPE_F32, kSelChunkLarge / NT / 4, MASK>(a, row, c, lds_raw);
+    select_chunk<HI_ROCM_DTYPE_F32, kRowGeneralChunk / NT / 4, MASK>(a, row, c, lds_raw);
     __syncthreads();
   }
   FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);

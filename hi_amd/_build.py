@@ -10,7 +10,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libhi_rocm.so")
-SOURCES = ["sampler_kernels.hip", "index_select.hip", "sampler_api.hip", "sampler_host.hip", "decode_step.hip",
+SOURCES = ["sampler_rows.hip", "sampler_select.hip", "sampler_fused.hip", "sampler_chunked.hip", "lm_head.hip", "sampler_debug.hip",
+           "index_select.hip", "sampler_api.hip", "sampler_host.hip", "decode_step.hip",
            "moe_router.hip", "spec_verify.hip"]
 
 # -ffp-contract=off: every f32/f64 operation that decides a token is a
@@ -37,10 +38,12 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the hi-rocm HIP library cannot be built")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link libhi_rocm.so; returns its path."""
+def build(verbose: bool = False, only=None) -> str:
+    """Compile every HIP source and link libhi_rocm.so; returns its path.
+
+    `only` (a list of source names) recompiles just those and links them with
+    the objects of an earlier build of the others."""
     cc = hipcc()
-    objs = []
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
     def compile_one(src):
@@ -50,14 +53,15 @@ def build(verbose: bool = False) -> str:
         return src, obj, subprocess.run(cmd, capture_output=True, text=True)
 
     # the sources compile independently: one hipcc process each, at once
+    todo = SOURCES if only is None else [s for s in SOURCES if s in only]
     with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        results = list(pool.map(compile_one, SOURCES))
+        results = list(pool.map(compile_one, todo))
     for src, obj, res in results:
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
         if verbose and res.stderr.strip():
             print(res.stderr)
-        objs.append(obj)
+    objs = [os.path.join(build_dir, src.replace(".hip", ".o")) for src in SOURCES]
     tmp = LIB + ".tmp"
     cmd = [cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,0 +1,55 @@
+// hi-rocm: the streaming select pass over (chunk, row) workgroups
+// (select_kernel) and its launcher.
+#include "sampler_wide.h"
+
+namespace hi_rocm {
+
+// The streaming select pass: workgroup (chunk, row).
+template <int DT, int NL, bool MASK>
+__global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int row = blockIdx.y;
+  select_chunk<DT, NL, MASK>(a, row, blockIdx.x, lds_raw);
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  if (cfg.cls != kTopP) return;
+  // top-p rows: the last workgroup of the row merges the chunks' maxima and
+  // mass histograms for the wide pass (as select_finish_kernel's counter)
+  SelLds& L = *reinterpret_cast<SelLds*>(lds_raw);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  uint32_t* counter = a.done + row;
+  if (threadIdx.x == 0) {
+    __threadfence();
+    L.wflag[0] = atomicAdd(counter, 1u) == (uint32_t)(a.n_chunks - 1) ? 1u : 0u;
+    if (L.wflag[0]) {
+      __threadfence();
+      *counter = 0u;
+    }
+  }
+  __syncthreads();
+  if (L.wflag[0] == 0u) return;
+  wide_row_prepare(L, a, row, cfg);
+}
+
+template <int DT, int NL, bool MASK>
+hipError_t launch_select_t(const SampleArgs& a, hipStream_t stream) {
+  constexpr int E = NL * (DT == HI_ROCM_DTYPE_BF16 ? 8 : 4);
+  const size_t lds = kSelHead + (a.hoff ? sel_hist_bytes(NT * E) : 0);
+  hipLaunchKernelGGL((select_kernel<DT, NL, MASK>), dim3(a.n_chunks, a.B), dim3(NT), lds, stream, a);
+  return hipGetLastError();
+}
+
+template <int DT, bool MASK>
+hipError_t launch_select_d(const SampleArgs& a, hipStream_t stream) {
+  constexpr int EPL = DT == HI_ROCM_DTYPE_BF16 ? 8 : 4;
+  if (a.chunk == kSelChunkLarge) return launch_select_t<DT, kSelChunkLarge / NT / EPL, MASK>(a, stream);
+  return launch_select_t<DT, kSelChunkSmall / NT / EPL, MASK>(a, stream);
+}
+
+hipError_t launch_select(const SampleArgs& a, hipStream_t stream) {
+  if (a.dtype == HI_ROCM_DTYPE_BF16)
+    return a.mask ? launch_select_d<HI_ROCM_DTYPE_BF16, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_BF16, false>(a, stream);
+  return a.mask ? launch_select_d<HI_ROCM_DTYPE_F32, true>(a, stream) : launch_select_d<HI_ROCM_DTYPE_F32, false>(a, stream);
+}
+
+}  // namespace hi_rocm

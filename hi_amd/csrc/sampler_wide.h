@@ -1,0 +1,781 @@
+// The wide pass of top-p rows: device code of the chunked path's finish
+// kernel (sampler_chunked.hip), also reached from the select pass.
+#pragma once
+#include "sampler_select.h"
+
+namespace hi_rocm {
+
+// ==========================================================================
+// Wide pass: top-p rows without a top-k bound (gpu.rs:820-899 with
+// top_k unset), chunk-parallel
+// ==========================================================================
+//
+// The reference walks such a row's whole rank order with three sequential
+// f32 folds: the normaliser over every weight in vocabulary order
+// (gpu.rs:837), then cum_p += w / total in rank order up to the cutoff
+// (:843-856), then the candidate total and the inverse CDF (:874-899).  Here
+// the select pass leaves the scaled logits s in ws_s and a mass histogram
+// per chunk (WideStat); then one workgroup per (chunk, row):
+//   1. merges the row's chunk maxima (M) and histograms: a conservative
+//      weight bound w_lo such that the weights >= w_lo hold at least
+//      cutoff + kWideMargin of the mass (every weight of the nucleus is
+//      >= w_lo unless the f32 folds differ from exact sums by more than the
+//      margin, which the finish detects), and the predicted sum before the
+//      chunk;
+//   2. computes its weights w = expf(s - M) exactly (min-p zeros them),
+//      plans its part of the vocabulary-order fold (fold_plan: segments of
+//      one predicted binade and boundary terms) and writes the plan;
+//   3. counts its weights >= w_lo by distinct value in an LDS hash: the
+//      rank order only needs each distinct weight's multiplicity (equal
+//      weights rank by index, and the folds do not see indices);
+//   4. bumps the row's counter; the last workgroup finishes the row:
+//      chains the chunk plans into the exact normaliser (refolding a chunk
+//      whose prediction missed), merges the chunks' runs, sorts them
+//      (weight descending), folds cum_p, the candidate total and the CDF
+//      over the runs with the closed forms for equal terms, and finds the
+//      drawn index among the equal weights of the drawn run.
+// Rows whose chunks took the select pass's exact path, whose tables
+// overflow, or whose nucleus is not inside the superset take finish_row.
+
+constexpr float kWideMargin = 0.005f;  // extra probability mass of the superset
+constexpr int kWideChunkHash = 2048;   // distinct superset weights per chunk
+constexpr int kWideFinHash = 2048;     // distinct superset weights per row
+constexpr int kWideRunCap = kWideFinHash;
+constexpr int kWideBatch = 64;         // chunk plans the chain holds in LDS at a time
+constexpr int kWideGBins = 64;         // threshold bins (binades of w below M)
+
+// LDS of a (chunk, row) workgroup; the chunk's weights and fold binades
+// follow at wide_w_off / wide_pe_off.
+struct WideChunkLds {
+  fold::WgLds<NT> fl;
+  uint32_t hkey[kWideChunkHash];
+  uint32_t hcnt[kWideChunkHash];
+  uint32_t hmin[kWideChunkHash];
+  uint32_t nrun, ovf, last, fu;
+  float fend;
+};
+constexpr size_t kWideChunkHead = (sizeof(WideChunkLds) + 15) & ~(size_t)15;
+// Weights sit in LDS with one pad word per 16, so that threads reading
+// their own 16 consecutive terms hit distinct banks.
+__host__ __device__ inline int wide_pad(int i) { return i + (i >> 4); }
+__host__ __device__ inline size_t wide_w_bytes(int chunk) { return (size_t)wide_pad(chunk) * 4 + 16; }
+__host__ __device__ inline size_t wide_w_off(int) { return kWideChunkHead; }
+__host__ __device__ inline size_t wide_pe_off(int chunk) { return kWideChunkHead + wide_w_bytes(chunk); }
+__host__ __device__ inline size_t wide_chunk_lds(int chunk) { return wide_pe_off(chunk) + (size_t)chunk + 16; }
+
+// LDS of the row finish.  Its phases reuse one union: the chain (chunk
+// plans, and the refold arrays past them), the merge (hash table and sort
+// keys), the draw (runs in rank order and the fold values before them).
+struct WideFinLds {
+  fold::WgLds<NT> fl;
+  union {
+    struct {
+      ChunkFold batch[kWideBatch];
+    } ch;
+    struct {
+      uint32_t hkey[kWideFinHash];
+      uint32_t hcnt[kWideFinHash];
+      uint32_t hmin[kWideFinHash];
+      uint64_t sortk[kWideRunCap];
+    } mg;
+    struct {
+      float rx[kWideRunCap];   // weight of run r (rank order)
+      uint32_t rm[kWideRunCap];  // its multiplicity
+      uint32_t ri[kWideRunCap];  // its smallest index
+      float st[kWideRunCap];   // cum_p before run r
+      float st2[kWideRunCap];  // candidate weight sum before run r
+    } fo;
+    uint32_t cntc[kWideRunCap];  // the drawn weight's multiplicity per chunk
+  } u;
+  uint8_t pe[kWideRunCap + 4];
+  uint32_t noff[NT + 1];
+  uint32_t cnt, fail_c, rsel, csel, tok, fu;
+  float acc, acc2;
+};
+// The refold arrays (weights, then fold binades) start after the chain's
+// plans, inside or past the union.
+__host__ __device__ inline size_t wide_fin_w_off() {
+  return (offsetof(WideFinLds, u) + sizeof(ChunkFold) * kWideBatch + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t wide_fin_lds(int chunk) {
+  const size_t r = wide_fin_w_off() + wide_w_bytes(chunk);
+  return r > sizeof(WideFinLds) ? r : sizeof(WideFinLds);
+}
+
+__device__ __forceinline__ uint32_t wide_hash(uint32_t key, int log2n) {
+  return (key * 0x9E3779B1u) >> (32 - log2n);
+}
+
+// Inserts `count` copies of weight bits `key` with smallest index `idx`
+// into an LDS table of 2^log2n slots (key 0 = empty; weights here are > 0).
+// Returns false when the table is full.
+__device__ __forceinline__ bool wide_insert(uint32_t* hkey, uint32_t* hcnt, uint32_t* hmin, int log2n,
+                                            uint32_t key, uint32_t count, uint32_t idx) {
+  const uint32_t mask = (1u << log2n) - 1u;
+  uint32_t h = wide_hash(key, log2n);
+  for (uint32_t probe = 0; probe <= mask; ++probe, h = (h + 1u) & mask) {
+    const uint32_t old = atomicCAS(&hkey[h], 0u, key);
+    if (old == 0u || old == key) {
+      atomicAdd(&hcnt[h], count);
+      atomicMin(&hmin[h], idx);
+      return true;
+    }
+  }
+  return false;
+}
+
+// Step 1, once per top-p row, by the select pass's last workgroup of the
+// row: M, the superset bound w_lo and the predicted fold value before each
+// chunk (WideRow, WideStat::pred).  The masses use approximate exp; they
+// only size the superset and predict binades.
+__device__ __forceinline__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg) {
+  const int tid = threadIdx.x;
+  const int nch = a.n_chunks;
+  const ChunkStat* stats = a.stats + (int64_t)row * nch;
+  WideStat* wst = a.wstat + (int64_t)row * nch;
+  uint32_t mk = 0u, bad = 0u;
+  for (int c = tid; c < nch; c += NT) {
+    mk = max(mk, okey(stats[c].max_l));
+    bad |= wst[c].valid ^ 1u;
+  }
+  unsigned long long* gmass = reinterpret_cast<unsigned long long*>(L.surv[0]);  // kWideGBins entries
+  if (tid < kWideGBins) gmass[tid] = 0ull;
+  mk = block_max_u32<NT>(mk, L.redu);
+  bad = block_max_u32<NT>(bad, L.redu);
+  const float ml = okey_inv(mk);
+  const float M = finitef_(ml) ? ml / cfg.t_eff : -__builtin_inff();
+  WideRow* wr = a.wrow + row;
+  if (!finitef_(M) || bad) {
+    if (tid == 0) { wr->valid = 0u; wr->M = M; wr->w_lo = 0.f; }
+    return;
+  }
+  // chunk masses relative to M, in fixed point (2^-32): per binade of their
+  // lower end (for w_lo) and per chunk (for the predictions); one (chunk,
+  // bin) pair per thread step, so the whole workgroup works on every chunk
+  unsigned long long* cmass = reinterpret_cast<unsigned long long*>(L.surv[1]);  // up to kSurvCap chunks at a time
+  double S = 0.0;  // thread 0: the running prediction
+  for (int cb = 0; cb < nch; cb += kSurvCap) {
+    const int nb = min(kSurvCap, nch - cb);
+    for (int i = tid; i < nb; i += NT) cmass[i] = 0ull;
+    __syncthreads();
+    for (int it = tid; it < nb * kWideBins; it += NT) {
+      const int i = it / kWideBins, j = it % kWideBins;
+      const WideStat& ws = wst[cb + i];
+      const float lb = (M - ws.ms) * 1.4426950408889634f;  // log2 of M's weight over the chunk max's
+      const float m = ws.hist[j] * __builtin_amdgcn_exp2f(-lb);
+      if (!(m > 0.f)) continue;
+      const unsigned long long fx = (unsigned long long)((double)m * 4294967296.0);
+      int g = j == kWideBins - 1 ? kWideGBins - 1 : (int)floorf((float)(j + 1) + lb);
+      g = g < kWideGBins ? g : kWideGBins - 1;
+      atomicAdd(&gmass[g], fx);
+      atomicAdd(&cmass[i], fx);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int i = 0; i < nb; ++i) {
+        wst[cb + i].pred = S;
+        S += (double)cmass[i] * (1.0 / 4294967296.0);
+      }
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    unsigned long long tot = 0ull;
+    for (int g = 0; g < kWideGBins; ++g) tot += gmass[g];
+    const double frac = (double)cfg.cutoff + (double)kWideMargin;
+    float w_lo = 0.f;
+    if (cfg.cutoff < 1.f && frac < 1.0) {
+      const unsigned long long target = (unsigned long long)(frac * (double)tot);
+      unsigned long long cum = 0ull;
+      for (int g = 0; g < kWideGBins - 1; ++g) {
+        cum += gmass[g];
+        if (cum >= target) { w_lo = __builtin_ldexpf(1.f, -(g + 1)); break; }
+      }
+    }
+    wr->w_lo = fmaxf(w_lo, cfg.min_p);
+    wr->M = M;
+    wr->valid = 1u;
+  }
+}
+
+// w[wide_pad(i)] = the weight of scaled logit s[i] (exact expf; min-p
+// zeros it), i < len: all of a thread's loads of a block are issued before
+// any is used.
+__device__ __forceinline__ void wide_weights(const float* s, int len, float M, float min_p, float* w) {
+  constexpr int kB = 8;
+  for (int base = 0; base < len; base += kB * NT) {
+    float v[kB];
+    #pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = base + k * NT + (int)threadIdx.x;
+      v[k] = i < len ? s[i] : -__builtin_inff();
+    }
+    #pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = base + k * NT + (int)threadIdx.x;
+      const float x = exact_expf(v[k] - M);
+      if (i < len) w[wide_pad(i)] = x < min_p ? 0.f : x;  // min-p: excluded like a zero weight
+    }
+  }
+}
+
+// Map of one term in binade e (exact_fold.h): n ulps, plus one above half
+// an ulp, plus one on an exact half when that makes the sum even.
+__device__ __forceinline__ fold::Map term_map(float x, int e) {
+  const fold::Inc c = fold::classify(x, e);
+  const uint32_t base = c.n + (c.cls == 2u ? 1u : 0u);
+  const uint32_t odd = c.n & 1u;
+  fold::Map m;
+  m.t0 = base + ((c.cls == 1u && odd) ? 1u : 0u);
+  m.t1 = base + ((c.cls == 1u && !odd) ? 1u : 0u);
+  return m;
+}
+
+// Exclusive scan of maps over the workgroup in thread order; *tot gets the
+// composition of all.  Two barriers.
+__device__ __forceinline__ fold::Map block_map_scan(fold::Map m, fold::Map* wm, fold::Map* tot) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  fold::Map inc = m;
+  #pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    fold::Map o;
+    o.t0 = (uint32_t)__shfl_up((int)inc.t0, (unsigned)d, 64);
+    o.t1 = (uint32_t)__shfl_up((int)inc.t1, (unsigned)d, 64);
+    if (lane >= d) inc = fold::compose(o, inc);
+  }
+  fold::Map ex;
+  ex.t0 = (uint32_t)__shfl_up((int)inc.t0, 1u, 64);
+  ex.t1 = (uint32_t)__shfl_up((int)inc.t1, 1u, 64);
+  if (lane == 0) ex = fold::map_identity();
+  __syncthreads();
+  if (lane == 63) wm[wid] = inc;
+  __syncthreads();
+  fold::Map before = fold::map_identity(), all = fold::map_identity();
+  #pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    if (w < wid) before = fold::compose(before, wm[w]);
+    all = fold::compose(all, wm[w]);
+  }
+  *tot = all;
+  return fold::compose(before, ex);
+}
+
+// The exact sequential f32 fold of w[wide_pad(0 .. len)) (LDS) from a0, by
+// the workgroup.  Thread t holds a block of consecutive terms; in the
+// current binade every block is one map, so a scan gives each block's
+// exact start until the first block whose terms leave the binade.  That
+// thread adds its terms (and, while crossings come close together, the
+// next blocks' terms) as real f32 additions, and the scan resumes after
+// them in the new binade.  Returns the sum (uniform).
+__device__ __forceinline__ float exact_chunk_fold(const float* w, int len, float a0, fold::Map* wm, float* shf,
+                                                  uint32_t* red) {
+  constexpr int kSeqBlocks = 4;  // blocks one thread adds after a crossing
+  const int tid = threadIdx.x;
+  const int J = (len + NT - 1) / NT;
+  const int r0 = min(tid * J, len), r1 = min(r0 + J, len);
+  float a = a0;
+  int pos = 0;
+  while (pos < NT) {
+    const int e = fold::binade(a);
+    const uint32_t A = fold::to_A(a);
+    fold::Map m = fold::map_identity();
+    if (tid >= pos)
+      for (int r = r0; r < r1; ++r) m = fold::compose(m, term_map(w[wide_pad(r)], e));
+    fold::Map tot;
+    const fold::Map ex = block_map_scan(m, wm, &tot);
+    const uint32_t p = A & 1u;
+    if ((uint64_t)A + fold::apply(tot, p) < fold::kTop) {
+      a = fold::from_A(A + fold::apply(tot, p), e);
+      break;
+    }
+    const uint64_t At = (uint64_t)A + fold::apply(ex, p);
+    const bool cross = tid >= pos && (At >= fold::kTop || At + fold::apply(m, (uint32_t)At & 1u) >= fold::kTop);
+    uint32_t first = ~block_max_u32<NT>(cross ? ~(uint32_t)tid : 0u, red);
+    if (first == 0xffffffffu) first = (uint32_t)pos;  // (not reached: the total leaves the binade)
+    if (tid == (int)first) {
+      // At < kTop: the blocks before this one stayed in the binade
+      float x = fold::from_A((uint32_t)At, e);
+      const int stop = min(len, (tid + kSeqBlocks) * J);
+      for (int r = r0; r < stop; ++r) x = fold::fadd(x, w[wide_pad(r)]);
+      shf[0] = x;
+    }
+    __syncthreads();
+    a = shf[0];
+    pos = (int)first + kSeqBlocks;
+    __syncthreads();
+  }
+  return a;
+}
+
+// Steps 2-3 for one (chunk, row), with the row's M, w_lo and the chunk's
+// predicted start S.
+__device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* lds_raw, const SampleArgs& a, int row, int chunk,
+                                const RowCfg& cfg, float M, float w_lo, double S) {
+  const int tid = threadIdx.x;
+  const int c0 = chunk * a.chunk;
+  const int len = min(a.chunk, a.V - c0);
+  float* w = reinterpret_cast<float*>(lds_raw + wide_w_off(a.chunk));
+  const float* srow = a.ws_s + (int64_t)row * a.V + c0;
+  wide_weights(srow, len, M, cfg.min_p, w);
+  for (int h = tid; h < kWideChunkHash; h += NT) { L.hkey[h] = 0u; L.hcnt[h] = 0u; L.hmin[h] = 0xffffffffu; }
+  if (tid == 0) { L.nrun = 0u; L.ovf = 0u; }
+  __syncthreads();
+  // the weights for the finish's exact refolds
+  {
+    float* wg = a.ws_w + (int64_t)row * a.V + c0;
+    for (int i = tid; i < len; i += NT) wg[i] = w[wide_pad(i)];
+  }
+  // the chunk's part of the vocabulary-order fold: chunk 0 starts from the
+  // known -0.0 and folds exactly; the others give their maps in the
+  // binades around the predicted start
+  ChunkFold* cf = a.wfold + (int64_t)row * a.n_chunks + chunk;
+  if (chunk == 0) {
+    const float end = exact_chunk_fold(w, len, -0.0f, L.fl.wmap, &L.fend, L.fl.wcnt);
+    if (tid == 0) { cf->has_end = 1u; cf->end = end; cf->e0 = 1u; }
+  } else {
+    const int ep = fold::binade((float)S);
+    const int e0 = ep > 1 ? ep - 1 : 1;
+    const int J = (len + NT - 1) / NT;
+    const int r0 = min(tid * J, len), r1 = min(r0 + J, len);
+    fold::Map m0 = fold::map_identity(), m1 = m0, m2 = m0;
+    for (int r = r0; r < r1; ++r) {
+      const float x = w[wide_pad(r)];
+      m0 = fold::compose(m0, term_map(x, e0));
+      m1 = fold::compose(m1, term_map(x, e0 + 1));
+      m2 = fold::compose(m2, term_map(x, e0 + 2));
+    }
+    // each thread's block maps, for the finish's crossing search
+    fold::Map* bm = a.wbmap + ((int64_t)row * a.n_chunks + chunk) * 3 * NT;
+    bm[tid] = m0;
+    bm[NT + tid] = m1;
+    bm[2 * NT + tid] = m2;
+    fold::Map t0, t1, t2;
+    block_map_scan(m0, L.fl.wmap, &t0);
+    block_map_scan(m1, L.fl.wmap, &t1);
+    block_map_scan(m2, L.fl.wmap, &t2);
+    if (tid == 0) {
+      cf->has_end = 0u;
+      cf->e0 = (uint32_t)e0;
+      cf->map[0] = t0;
+      cf->map[1] = t1;
+      cf->map[2] = t2;
+    }
+  }
+  // the superset's distinct weights
+  constexpr int kLog2 = 11;
+  static_assert((1 << kLog2) == kWideChunkHash, "hash size");
+  bool full = false;
+  for (int i = tid; i < len; i += NT) {
+    const float x = w[wide_pad(i)];
+    if (x > 0.f && x >= w_lo)
+      full |= !wide_insert(L.hkey, L.hcnt, L.hmin, kLog2, __float_as_uint(x), 1u, (uint32_t)i);
+  }
+  if (full) L.ovf = 1u;
+  __syncthreads();
+  uint64_t* out = a.ws_list + (int64_t)row * a.list_stride + (int64_t)chunk * a.chunk;
+  for (int h = tid; h < kWideChunkHash; h += NT) {
+    const uint32_t k = L.hkey[h];
+    if (k != 0u) {
+      const uint32_t p = atomicAdd(&L.nrun, 1u);
+      out[p] = ((uint64_t)k << 32) | ((uint64_t)L.hcnt[h] << 16) | (uint64_t)L.hmin[h];
+    }
+  }
+  __syncthreads();
+  if (tid == 0) cf->nruns = L.ovf ? kFoldNone : L.nrun;
+}
+
+// The exact fold value after chunk c's weights, from `acc` before them:
+// reads the chunk's weights back (the chain's path when a chunk's sum
+// leaves its binades).  All threads call it.
+__device__ __forceinline__ float wide_refold(WideFinLds& F, unsigned char* lds_raw, const SampleArgs& a, int row,
+                                             int c, float acc) {
+  const int c0 = c * a.chunk;
+  const int len = min(a.chunk, a.V - c0);
+  float* w = reinterpret_cast<float*>(lds_raw + wide_fin_w_off());
+  const float* wg = a.ws_w + (int64_t)row * a.V + c0;
+  constexpr int kB = 8;
+  for (int base = 0; base < len; base += kB * NT) {
+    float v[kB];
+    #pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = base + k * NT + (int)threadIdx.x;
+      v[k] = i < len ? wg[i] : 0.f;
+    }
+    #pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int i = base + k * NT + (int)threadIdx.x;
+      if (i < len) w[wide_pad(i)] = v[k];
+    }
+  }
+  __syncthreads();
+  return exact_chunk_fold(w, len, acc, F.fl.wmap, &F.acc2, F.fl.wcnt);
+}
+
+// The exact fold value after chunk c's weights from the exact value `acc`
+// before them, when the chunk's sum leaves the binade it starts in: wave 0
+// finds the crossing block from the chunk's stored block maps (a scan of the
+// maps over the blocks; block b holds the chunk's terms [b * J, b * J + J),
+// J = ceil(len / NT)), adds that block's terms one by one as real f32
+// additions, and repeats in the new binade.  Returns kNone's float bits
+// (NaN) when a binade falls outside the three stored ones; the caller then
+// refolds the chunk.  Wave 0 only; the result is in lane 0 and every lane.
+__device__ __forceinline__ float wide_cross_wave(const SampleArgs& a, int row, int c, float acc, bool& ok) {
+  constexpr int PB = NT / 64;  // blocks per lane
+  const int lane = threadIdx.x & 63;
+  const ChunkFold cf = a.wfold[(int64_t)row * a.n_chunks + c];
+  const fold::Map* bm = a.wbmap + ((int64_t)row * a.n_chunks + c) * 3 * NT;
+  const int c0 = c * a.chunk;
+  const int len = min(a.chunk, a.V - c0);
+  const int J = (len + NT - 1) / NT;
+  const float* wg = a.ws_w + (int64_t)row * a.V + c0;
+  float x = acc;
+  int bstart = 0;
+  ok = true;
+  while (bstart < NT) {
+    const int ey = fold::binade(x);
+    const int k = ey - (int)cf.e0;
+    if (k < 0 || k >= 3) { ok = false; return x; }
+    // this lane's blocks 4 * lane .. (those before bstart count as identity)
+    fold::Map bl[PB];
+    fold::Map mine = fold::map_identity();
+    #pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const int b = PB * lane + q;
+      bl[q] = b >= bstart ? bm[k * NT + b] : fold::map_identity();
+      mine = fold::compose(mine, bl[q]);
+    }
+    fold::Map inc = mine;
+    #pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      fold::Map o;
+      o.t0 = (uint32_t)__shfl_up((int)inc.t0, (unsigned)d, 64);
+      o.t1 = (uint32_t)__shfl_up((int)inc.t1, (unsigned)d, 64);
+      if (lane >= d) inc = fold::compose(o, inc);
+    }
+    fold::Map ex;
+    ex.t0 = (uint32_t)__shfl_up((int)inc.t0, 1u, 64);
+    ex.t1 = (uint32_t)__shfl_up((int)inc.t1, 1u, 64);
+    if (lane == 0) ex = fold::map_identity();
+    const uint32_t A = fold::to_A(x), p = A & 1u;
+    const uint64_t cross = __ballot((uint64_t)A + fold::apply(inc, p) >= fold::kTop);
+    if (cross == 0ull) {
+      const fold::Map all = {(uint32_t)__builtin_amdgcn_readlane((int)inc.t0, 63),
+                             (uint32_t)__builtin_amdgcn_readlane((int)inc.t1, 63)};
+      return fold::from_A(A + fold::apply(all, p), ey);
+    }
+    const int fl = __ffsll((unsigned long long)cross) - 1;
+    // in lane fl: the block where the sum leaves the binade, and the value before it
+    uint32_t Ab = A + fold::apply(ex, p);  // A before this lane's blocks (< kTop: earlier lanes stayed)
+    int blk = PB * lane + PB - 1;
+    bool found = false;
+    #pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const uint32_t t = fold::apply(bl[q], Ab & 1u);
+      if (!found && (uint64_t)Ab + t >= fold::kTop) { blk = PB * lane + q; found = true; }
+      if (!found) Ab += t;
+    }
+    blk = __builtin_amdgcn_readlane(blk, fl);
+    Ab = (uint32_t)__builtin_amdgcn_readlane((int)Ab, fl);
+    // the crossing block's terms as real additions (lane 0; the rest wait)
+    float y = fold::from_A(Ab, ey);
+    if (lane == 0) {
+      const int r0 = min(blk * J, len), r1 = min(r0 + J, len);
+      for (int r = r0; r < r1; ++r) y = fold::fadd(y, wg[r]);
+    }
+    x = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 0));
+    bstart = blk + 1;
+  }
+  return x;
+}
+
+// Calls f(c, e) for every superset run entry e of chunk c of `row`, in
+// parallel: chunks in blocks of NT, their run counts scanned into offsets.
+template <typename F>
+__device__ __forceinline__ void wide_for_each_run(WideFinLds& W, const SampleArgs& a, int row, F f) {
+  const int tid = threadIdx.x;
+  const int nch = a.n_chunks;
+  const ChunkFold* folds = a.wfold + (int64_t)row * nch;
+  for (int cb = 0; cb < nch; cb += NT) {
+    const int c = cb + tid;
+    const uint32_t n = c < nch ? folds[c].nruns : 0u;
+    uint32_t tot;
+    const uint32_t off = block_excl_scan_u32<NT>(n, W.fl.wcnt, &tot);
+    W.noff[tid] = off;
+    if (tid == 0) W.noff[NT] = tot;
+    __syncthreads();
+    for (uint32_t p = (uint32_t)tid; p < tot; p += NT) {
+      int lo = 0, hi = NT - 1;  // the last block whose offset is <= p
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (W.noff[mid] <= p) lo = mid; else hi = mid - 1;
+      }
+      const uint64_t* src = a.ws_list + (int64_t)row * a.list_stride + (int64_t)(cb + lo) * a.chunk;
+      f(cb + lo, src[p - W.noff[lo]]);
+    }
+    __syncthreads();
+  }
+}
+
+// Step 4: the row finish by the last workgroup.  Returns the token, or
+// 0xffffffff when the row must take finish_row (nothing written); `path`
+// gets the WidePath code.
+__device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const SampleArgs& a, int row, const RowCfg& cfg, float M,
+                                float w_lo, uint32_t& path) {
+  WideFinLds& F = *reinterpret_cast<WideFinLds*>(lds_raw);
+  const int tid = threadIdx.x;
+  const int nch = a.n_chunks;
+  const ChunkFold* folds = a.wfold + (int64_t)row * nch;
+
+  // a. the normaliser: the chunk plans chained in vocabulary order
+  //    (Rust's Sum folds from -0.0)
+  float acc = -0.0f;
+  bool ovf = false;
+  for (int cb = 0; cb < nch; cb += kWideBatch) {
+    const int nb = min(kWideBatch, nch - cb);
+    {
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(folds + cb);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(F.u.ch.batch);
+      const int words = nb * (int)(sizeof(ChunkFold) / 4);
+      for (int i = tid; i < words; i += NT) dst[i] = src[i];
+    }
+    __syncthreads();
+    for (int i = tid; i < nb; i += NT)
+      if (F.u.ch.batch[i].nruns == kFoldNone) ovf = true;
+    int c = cb;
+    while (c < cb + nb) {
+      if (tid == 0) {
+        float x = acc;
+        uint32_t fail = 0xffffffffu;
+        for (int cc = c; cc < cb + nb; ++cc) {
+          const ChunkFold& cf = F.u.ch.batch[cc - cb];
+          if (cf.has_end) { x = cf.end; continue; }  // chunk 0, from -0.0
+          const int ey = fold::binade(x);
+          const int k = ey - (int)cf.e0;
+          bool ok = k >= 0 && k < 3;
+          float y = x;
+          if (ok) {
+            const uint32_t A = fold::to_A(x);
+            const uint32_t t = fold::apply(cf.map[k], A & 1u);
+            ok = (uint64_t)A + t < fold::kTop;
+            y = fold::from_A(A + t, ey);
+          }
+          if (!ok) { fail = (uint32_t)cc; break; }
+          x = y;
+        }
+        F.acc = x;
+        F.fail_c = fail;
+      }
+      __syncthreads();
+      acc = F.acc;
+      const uint32_t fail = F.fail_c;
+      __syncthreads();
+      if (fail == 0xffffffffu) break;
+      // the chunk whose sum leaves its binade: the crossing from the block
+      // maps (wave 0), else an exact refold of its weights
+      if (tid < 64) {
+        bool okw = true;
+        const float y = wide_cross_wave(a, row, (int)fail, acc, okw);
+        if (tid == 0) { F.acc = y; F.fail_c = okw ? 1u : 0u; }
+      }
+      __syncthreads();
+      const bool crossed = F.fail_c != 0u;
+      const float ycross = F.acc;
+      __syncthreads();
+      acc = crossed ? ycross : wide_refold(F, lds_raw, a, row, (int)fail, acc);
+      c = (int)fail + 1;
+    }
+    __syncthreads();
+  }
+  ovf = __syncthreads_or(ovf);
+  const float total = acc;
+  path = kWideTotal;
+  if (!(total > 0.f) || !finitef_(total)) return 0xffffffffu;  // argmax_host fallback (finish_row)
+  path = kWideChunkFull;
+  if (ovf) return 0xffffffffu;
+  path = kWideMergeFull;
+
+  // c. merge the chunks' runs by weight
+  constexpr int kLog2 = 11;
+  static_assert((1 << kLog2) == kWideFinHash, "hash size");
+  for (int h = tid; h < kWideFinHash; h += NT) {
+    F.u.mg.hkey[h] = 0u;
+    F.u.mg.hcnt[h] = 0u;
+    F.u.mg.hmin[h] = 0xffffffffu;
+  }
+  if (tid == 0) F.cnt = 0u;
+  __syncthreads();
+  bool full = false;
+  wide_for_each_run(F, a, row, [&](int c, uint64_t e) {
+    full |= !wide_insert(F.u.mg.hkey, F.u.mg.hcnt, F.u.mg.hmin, kLog2, (uint32_t)(e >> 32),
+                         (uint32_t)(e >> 16) & 0xffffu, (uint32_t)(c * a.chunk) + ((uint32_t)e & 0xffffu));
+  });
+  if (__syncthreads_or(full)) return 0xffffffffu;
+  path = kWideDrawFail;
+  // d. distinct weights, descending
+  for (int h = tid; h < kWideFinHash; h += NT) {
+    const uint32_t k = F.u.mg.hkey[h];
+    if (k != 0u) F.u.mg.sortk[atomicAdd(&F.cnt, 1u)] = ((uint64_t)k << 32) | (uint64_t)h;
+  }
+  __syncthreads();
+  const int R = (int)F.cnt;
+  if (R == 0) return 0xffffffffu;
+  {
+    const int n2 = next_pow2(R);
+    for (int i = R + tid; i < n2; i += NT) F.u.mg.sortk[i] = 0ull;
+    __syncthreads();
+    for (int k = 2; k <= n2; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < n2; i += NT) {
+          const int ixj = i ^ j;
+          if (ixj > i) {
+            const uint64_t x = F.u.mg.sortk[i], y = F.u.mg.sortk[ixj];
+            const bool desc = (i & k) == 0;
+            if (desc ? (x < y) : (x > y)) { F.u.mg.sortk[i] = y; F.u.mg.sortk[ixj] = x; }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+  {
+    // runs in rank order: read everything first, the arrays overlap
+    constexpr int kPer = kWideRunCap / NT;
+    float rx[kPer];
+    uint32_t rm[kPer], ri[kPer];
+    #pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int r = q * NT + tid;
+      if (r < R) {
+        const uint64_t k = F.u.mg.sortk[r];
+        const uint32_t h = (uint32_t)k;
+        rx[q] = __uint_as_float((uint32_t)(k >> 32));
+        rm[q] = F.u.mg.hcnt[h];
+        ri[q] = F.u.mg.hmin[h];
+      }
+    }
+    __syncthreads();
+    #pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int r = q * NT + tid;
+      if (r < R) { F.u.fo.rx[r] = rx[q]; F.u.fo.rm[r] = rm[q]; F.u.fo.ri[r] = ri[q]; }
+    }
+    __syncthreads();
+  }
+
+  // e. cum_p += w / total in rank order (from 0.0), up to the cutoff
+  auto q_of = [&](int r) { return F.u.fo.rx[r] / total; };
+  auto m_of = [&](int r) { return F.u.fo.rm[r]; };
+  const float cum_end = fold::fold_runs<NT>(F.fl, F.pe, R, 0.0f, q_of, m_of,
+                                            [&](int r, float v) { F.u.fo.st[r] = v; });
+  __syncthreads();
+  int rstar = R - 1;
+  uint32_t cstar = F.u.fo.rm[R - 1];
+  if (cfg.cutoff < 1.f) {
+    uint32_t first = 0xffffffffu;
+    for (int r = tid; r < R; r += NT) {
+      const float end = r + 1 < R ? F.u.fo.st[r + 1] : cum_end;
+      if (end >= cfg.cutoff) first = min(first, (uint32_t)r);
+    }
+    first = ~block_max_u32<NT>(~first, F.fl.wcnt);
+    if (first == 0xffffffffu) {
+      // the cutoff is not reached inside the superset: that is the whole
+      // nucleus only when the superset holds every positive weight
+      if (w_lo > cfg.min_p) {
+        path = kWideNoCutoff;
+        return 0xffffffffu;
+      }
+    } else {
+      rstar = (int)first;
+      cstar = fold::run_find<false>(F.u.fo.st[rstar], q_of(rstar), F.u.fo.rm[rstar], cfg.cutoff, nullptr);
+      if (cstar == fold::kNone) return 0xffffffffu;
+    }
+  }
+  // f. the candidate total: the weights of the ranks before m_end (from -0.0)
+  auto m2_of = [&](int r) { return r == rstar ? cstar : F.u.fo.rm[r]; };
+  const float ct = fold::fold_runs<NT>(F.fl, F.pe, rstar + 1, -0.0f, [&](int r) { return F.u.fo.rx[r]; }, m2_of,
+                                       [&](int r, float v) { F.u.fo.st2[r] = v; });
+  __syncthreads();
+  if (!(ct > 0.f) || !finitef_(ct)) return 0xffffffffu;
+  // g. the inverse CDF: the first rank whose running weight passes target
+  const float target = clamp_uniform(cfg.u) * ct;
+  uint32_t pr = 0xffffffffu;
+  for (int r = tid; r <= rstar; r += NT) {
+    const float end = r < rstar ? F.u.fo.st2[r + 1] : ct;
+    if (target < end) pr = min(pr, (uint32_t)r);
+  }
+  pr = ~block_max_u32<NT>(~pr, F.fl.wcnt);
+  int rp = rstar;
+  uint32_t cp = cstar;  // gpu.rs:899: the last candidate
+  if (pr != 0xffffffffu) {
+    const uint32_t c = fold::run_find<true>(F.u.fo.st2[pr], F.u.fo.rx[pr], m2_of((int)pr), target, nullptr);
+    if (c != fold::kNone) { rp = (int)pr; cp = c; }
+  }
+  // h. the drawn index: the cp-th smallest index among the weights equal
+  //    to the run's (equal weights rank by index)
+  const uint32_t first_idx = F.u.fo.ri[rp];
+  path = kWideDone;
+  if (cp == 1u) return first_idx;
+  const uint32_t key = __float_as_uint(F.u.fo.rx[rp]);
+  __syncthreads();
+  for (int c = tid; c < kWideRunCap; c += NT) F.u.cntc[c] = 0u;
+  __syncthreads();
+  if (nch > kWideRunCap) {
+    path = kWideDrawFail;
+    return 0xffffffffu;
+  }
+  wide_for_each_run(F, a, row, [&](int c, uint64_t e) {
+    if ((uint32_t)(e >> 32) == key) F.u.cntc[c] = (uint32_t)(e >> 16) & 0xffffu;
+  });
+  if (tid == 0) {
+    uint32_t seen = 0u;
+    F.csel = 0xffffffffu;
+    for (int c = 0; c < nch; ++c) {
+      const uint32_t k = F.u.cntc[c];
+      if (k != 0u && seen + k >= cp) { F.csel = (uint32_t)c; F.rsel = cp - seen; break; }
+      seen += k;
+    }
+    F.tok = 0xffffffffu;
+    F.cnt = 0u;
+  }
+  __syncthreads();
+  const uint32_t csel = F.csel, want = F.rsel;
+  if (csel == 0xffffffffu) {
+    path = kWideDrawFail;
+    return 0xffffffffu;
+  }
+  // the want-th weight equal to key in chunk csel, in index order
+  const int c0 = (int)csel * a.chunk;
+  const int len = min(a.chunk, a.V - c0);
+  const float* srow = a.ws_s + (int64_t)row * a.V + c0;
+  const uint32_t wid = (uint32_t)tid >> 6;
+  for (int base = 0; base < len; base += NT) {
+    const int i = base + tid;
+    bool eq = false;
+    if (i < len) {
+      float x = exact_expf(srow[i] - M);
+      x = x < cfg.min_p ? 0.f : x;
+      eq = __float_as_uint(x) == key;
+    }
+    const uint64_t bm = __ballot(eq);
+    if ((tid & 63) == 0) F.fl.wcnt[wid] = (uint32_t)__popcll(bm);
+    __syncthreads();
+    uint32_t before = F.cnt;
+    for (uint32_t v = 0; v < wid; ++v) before += F.fl.wcnt[v];
+    if (eq && before + lanes_below(bm) + 1u == want) F.tok = (uint32_t)(c0 + i);
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t s = 0u;
+      for (int v = 0; v < NT / 64; ++v) s += F.fl.wcnt[v];
+      F.cnt += s;
+    }
+    __syncthreads();
+    if (F.tok != 0xffffffffu) break;
+  }
+  if (F.tok == 0xffffffffu) path = kWideDrawFail;
+  return F.tok;
+}
+
+// The second kernel of the chunked path: one workgroup per (row, chunk),
+// on a 1-D grid whose first B workgroups are chunk 0 of rows 0 .. B-1 and
+
+}  // namespace hi_rocm

@@ -56,7 +56,14 @@ HI_ROCM_HD inline uint64_t exp2_tab32(uint32_t i) {
 
 HI_ROCM_HD inline double hr_fma(double a, double b, double c) { return __builtin_fma(a, b, c); }
 
-HI_ROCM_HD inline float exact_expf(float x) {
+// The table read through the constant copy (see exp2_tab32); kernels that
+// keep a copy in LDS pass their own reader to exact_expf_t.
+struct Exp2TabConst {
+  HI_ROCM_HD uint64_t operator()(uint32_t i) const { return exp2_tab32(i); }
+};
+
+template <typename Tab>
+HI_ROCM_HD inline float exact_expf_t(float x, const Tab& tab) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
   const double kShift = 0x1.8p+52;
   const double kC0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
@@ -77,7 +84,7 @@ HI_ROCM_HD inline float exact_expf(float x) {
   memcpy(&ki, &kd, 8);
   kd -= kShift;
   const double r = hr_fma(kInvLn2N, xd, -kd);
-  uint64_t t = exp2_tab32((uint32_t)(ki & 31u));
+  uint64_t t = tab((uint32_t)(ki & 31u));
   t += ki << 47;
   double s;
   memcpy(&s, &t, 8);
@@ -88,5 +95,7 @@ HI_ROCM_HD inline float exact_expf(float x) {
   y = y * s;
   return (float)y;
 }
+
+HI_ROCM_HD inline float exact_expf(float x) { return exact_expf_t(x, Exp2TabConst{}); }
 
 }  // namespace hi_rocm

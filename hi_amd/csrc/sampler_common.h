@@ -1512,20 +1512,20 @@ __device__ __forceinline__ float wave_fold_f32_until(float v, float start, int n
   return p;
 }
 
-// Reference steps 7-10 (gpu.rs:831-899) over the rank order keys[0, k)
-// (LDS, k <= 64 * DM), by every wave from registers: entry m * 64 + lane
-// sits in lane `lane` of slot m.  Returns the drawn entry, or -1 for the
-// reference's argmax_host fallback (no positive weight, or a total or
-// candidate total that is not positive and finite).  All waves return the
-// same, with no barrier.
+// Reference steps 7-10 (gpu.rs:831-899) over the rank order held in
+// registers: entry m * 64 + lane of the rank keys sits in lane `lane` of
+// kr[m], entries [0, k) are the kept ones (k <= 64 * DM).  Returns the
+// drawn entry, or -1 for the reference's argmax_host fallback (no positive
+// weight, or a total or candidate total that is not positive and finite).
+// Wave-local: every wave that calls it returns the same, with no barrier.
 template <int DM>
-__device__ __forceinline__ int wave_draw(const uint64_t* keys, int k, const RowCfg& cfg) {
+__device__ __forceinline__ int wave_draw_r(const uint64_t (&kr)[DM], int k, const RowCfg& cfg) {
   const uint32_t lane = threadIdx.x & 63u;
   float fa[DM], pa[DM];
   #pragma unroll
   for (int m = 0; m < DM; ++m) {
     const int i = m * 64 + (int)lane;
-    const float w = i < k ? rank_w(keys[i]) : 0.f;
+    const float w = i < k ? rank_w(kr[m]) : 0.f;
     fa[m] = w < cfg.min_p ? 0.f : w;  // min-p: excluded like w <= 0 (gpu.rs:847-849)
   }
   // the weights are in rank order, so the positive ones are a prefix
@@ -1589,6 +1589,90 @@ __device__ __forceinline__ int wave_draw(const uint64_t* keys, int k, const RowC
     if (pick < 0 && hit != 0ull) pick = m * 64 + __ffsll((unsigned long long)hit) - 1;
   }
   return pick < 0 ? me : pick;
+}
+
+// wave_draw_r over the rank order keys[0, k) in LDS (k <= 64 * DM), by
+// every wave from registers.
+template <int DM>
+__device__ __forceinline__ int wave_draw(const uint64_t* keys, int k, const RowCfg& cfg) {
+  const uint32_t lane = threadIdx.x & 63u;
+  uint64_t kr[DM];
+  #pragma unroll
+  for (int m = 0; m < DM; ++m) {
+    const int i = m * 64 + (int)lane;
+    kr[m] = i < k ? keys[i] : 0ull;
+  }
+  return wave_draw_r<DM>(kr, k, cfg);
+}
+
+// The 64-bit value of lane (lane ^ j), j a power of two below 64: DPP moves
+// within a 16-lane row for j <= 8 (quad_perm; row_shl/row_shr:4 and a
+// select; row_ror:8), ds_swizzle's xor mode across the rows of a 32-lane
+// half for j = 16, ds_bpermute across the halves for j = 32.  j is a
+// constant once the caller's loops are unrolled, so the switch folds.
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t v, int j) {
+  switch (j) {
+    case 1: return dpp32<kDppXor1>(v, v);
+    case 2: return dpp32<kDppXor2>(v, v);
+    case 4: {
+      const uint32_t up = dpp32<0x104>(v, v);  // row_shl:4: lane l gets lane l + 4
+      const uint32_t dn = dpp32<0x114>(v, v);  // row_shr:4: lane l gets lane l - 4
+      return (threadIdx.x & 4u) ? dn : up;
+    }
+    case 8: return dpp32<0x128>(v, v);         // row_ror:8: lane l gets lane (l + 8) mod 16 of its row
+    case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401f);  // and 0x1f, xor 0x10
+    default: return (uint32_t)__shfl_xor((int)v, 32, 64);
+  }
+}
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v, int j) {
+  return ((uint64_t)lane_xor32((uint32_t)(v >> 32), j) << 32) | lane_xor32((uint32_t)v, j);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Descending sort of the wave's 64 * S keys, entry m * 64 + lane in x[m]:
+// a bitonic network whose compare-exchanges between slots stay in a lane's
+// registers and whose exchanges between lanes are lane_xor64 moves.
+template <int S>
+__device__ __forceinline__ void wave_sort_desc(uint64_t (&x)[S]) {
+  const uint32_t lane = threadIdx.x & 63u;
+  constexpr int N = 64 * S;
+  #pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+    #pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= 64) {
+        const int js = j >> 6;
+        #pragma unroll
+        for (int m = 0; m < S; ++m) {
+          if (m & js) continue;
+          // the lower entry of the pair keeps the larger key when (i & k) == 0
+          // (a compile-time choice here)
+          const uint64_t lo = x[m], hi = x[m ^ js];
+          const uint64_t mx = hi > lo ? hi : lo, mn = hi > lo ? lo : hi;
+          const bool desc = ((m * 64) & k) == 0;
+          x[m] = desc ? mx : mn;
+          x[m ^ js] = desc ? mn : mx;
+        }
+      } else {
+        #pragma unroll
+        for (int m = 0; m < S; ++m) {
+          const uint32_t i = (uint32_t)m * 64u + lane;
+          const uint64_t y = lane_xor64(x[m], j);
+          // keep the partner's key when it is larger and this entry keeps
+          // the maximum, or smaller and it keeps the minimum: an all-ones or
+          // all-zero mask, so the exchange is a select with no branch
+          const uint32_t keep_max = (((i & (uint32_t)k) == 0u) == ((i & (uint32_t)j) == 0u)) ? 1u : 0u;
+          const uint32_t gt = y > x[m] ? 1u : 0u;
+          const uint64_t take = 0ull - (uint64_t)(1u ^ gt ^ keep_max);
+          x[m] = (y & take) | (x[m] & ~take);
+        }
+      }
+    }
+  }
 }
 
 // Reference steps 7-10 (gpu.rs:831-899) over the first k <= kBuf entries of

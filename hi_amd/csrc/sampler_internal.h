@@ -160,6 +160,10 @@ enum WidePath : uint32_t {
   kWideMergeFull = 5,     // the row's table of distinct weights overflowed
   kWideNoCutoff = 6,      // the cutoff lies outside the superset
   kWideDrawFail = 7,      // the candidate total or the drawn index could not be resolved
+  // rows of the row kernel
+  kRowPathMinp = 8,       // the min-p support finish
+  kRowPathLists = 9,      // the candidate lists' finish (finish_core)
+  kRowPathGeneral = 10,   // the general path (chunk select and finish)
 };
 
 // Batches whose (chunk, row) grid has at most this many workgroups run the

@@ -58,6 +58,7 @@ constexpr int kRowHistPer = kRowHistCap / kRowThreads;  // history entries per t
 constexpr int kRowMaxV = 1 << 18;
 constexpr int kRowMinBatch = 192;
 constexpr int kRowKwMax = kLeanK / 16 + 16 + 4;       // kw at k = kLeanK (sqrt(256) = 16)
+constexpr int kRowSCap = 512;                         // min-p support entries held in LDS
 static_assert(kRowKwMax < kRowHW, "a full list holds more than kw entries");
 
 struct RowLds {
@@ -74,7 +75,17 @@ struct RowLds {
   uint32_t wcnt[kRowWaves];
   uint32_t redu[kRowWaves];
   uint64_t red64[kRowWaves];
+  // min-p rows: the logits each wave keeps at the end of its stream (list
+  // entries and processed history logits at or above its bound), their
+  // count, the largest processed-logit key seen so far
+  uint64_t sbuf[kRowSCap];
+  uint64_t exptab[32];                 // exact_expf's table (wave 0 copies it at its stream's end)
+  // [kSCnt] entries in sbuf, [kSMax] the largest key seen so far, [kSThr] the
+  // largest list threshold, [kSBad] a list overflowed: one 16-byte read
+  alignas(16) uint32_t sst[4];
+  uint32_t sdone;                      // wave 0's min-p finish: kMinpOk, or why it missed
 };
+enum : int { kSCnt = 0, kSMax = 1, kSThr = 2, kSBad = 3 };
 constexpr size_t kRowHead = (sizeof(RowLds) + 15) & ~(size_t)15;
 static_assert(sizeof(FinLds) <= offsetof(RowLds, wthr), "finish LDS must fit the stream's lists");
 static_assert(offsetof(RowLds, ob_raw) % 16 == 0 && offsetof(RowLds, ob_cnt) % 16 == 0 &&
@@ -182,6 +193,226 @@ __device__ __forceinline__ void row_issue(const SampleArgs& a, int row, RowPipe<
   }
 }
 
+// ---- min-p rows -----------------------------------------------------------
+//
+// With min_p > 0 only the logits whose weight w = expf(s - M) reaches min_p
+// are ever drawn or summed: the reference gives every other one weight 0
+// (gpu.rs:847-849 skips w <= 0; min-p extends that to w < min_p), and the
+// rank order puts them after the others.  Weights are monotone in the
+// processed logit, so that support S is every logit above one key.  At the
+// end of its stream each wave keeps, of its list and of its threads'
+// processed history logits, those whose key reaches a bound below which no
+// weight can reach min_p whatever the final row max (the bound comes from
+// the largest key seen so far, a lower bound of the row max M), and appends
+// them to L.sbuf.  After the barrier one wave computes the exact weights
+// against M, keeps S, sorts it by (w desc, index asc) in registers, and
+// runs the reference's folds: the kept top-k of the rank order is the first
+// min(|S|, k) entries of S.  That needs the lists to have dropped nothing
+// that ranks among them: either their thresholds' weights are below min_p
+// (nothing of S was dropped), or the k-th weight of S is above them.
+
+// Processed-logit key at and above which a weight can reach min_p when the
+// row max is at least the logit of key mk: l_lo = l_m + t ln(min_p) - d, with
+// a margin d far above the rounding of s = l / t, s - M and expf (a weight
+// w >= min_p needs s - M >= ln(min_p) - 2^-22 or so).  Uniform per wave.
+__device__ __forceinline__ uint32_t minp_key_bound(uint32_t mk, float t, float ln_mp) {
+  if (mk <= kKeyNegInf) return kKeyNegInf;
+  const float lm = okey_inv(mk);
+  if (!finitef_(lm)) return 0xffffffffu;  // +inf: the general path takes the row
+  const float span = t * ln_mp;                      // <= 0
+  const float d = t * 0x1p-10f + (fabsf(lm) - span) * 0x1p-18f;
+  const float lo = (lm + span) - d;
+  return lkey(lo);
+}
+
+// With the support known only above the lists' largest threshold (weights
+// there up to wT >= min_p), the kept top k is still exact when the support
+// holds k entries and the k-th weight of the sorted support is above wT:
+// every logit left out then ranks below all of them.
+template <int S>
+__device__ __forceinline__ bool minp_topk_known(const uint64_t (&x)[S], int c, int k, bool complete, float wT) {
+  if (complete) return true;
+  if (c < k) return false;
+  uint64_t v = 0ull;
+  #pragma unroll
+  for (int m = 0; m < S; ++m)
+    if (((k - 1) >> 6) == m) v = readlane64(x[m], (k - 1) & 63);
+  return rank_w(v) > wT;
+}
+
+// exact_expf's table read from an LDS copy: in the tail of a launch a load
+// from global memory waits behind the other workgroups' streams.
+struct Exp2TabLds {
+  const uint64_t* p;
+  __device__ uint64_t operator()(uint32_t i) const { return p[i]; }
+};
+
+// Why the min-p finish left a row to the general finish (0: it did not).
+enum MinpMiss : uint32_t { kMinpOk = 0, kMinpArray = 1, kMinpTopK = 2, kMinpDraw = 3 };
+
+// The wave's sorted support and the draw over its first min(c, k_eff)
+// entries; token gets the drawn index.  Misses: the top k is not known
+// (minp_topk_known), or the reference's argmax fallback (never with a
+// positive row maximum).
+template <int S>
+__device__ __forceinline__ uint32_t minp_draw(uint64_t (&x)[S], int c, const RowCfg& cfg, bool complete, float wT,
+                                              uint32_t& token) {
+  wave_sort_desc<S>(x);
+  if (!minp_topk_known<S>(x, c, cfg.k_eff, complete, wT)) return kMinpTopK;
+  const int pick = wave_draw_r<S>(x, min(c, cfg.k_eff), cfg);
+  if (pick < 0) return kMinpDraw;
+  uint64_t v = 0ull;
+  #pragma unroll
+  for (int m = 0; m < S; ++m)
+    if ((pick >> 6) == m) v = readlane64(x[m], pick & 63);
+  token = cand_idx(v);
+  return kMinpOk;
+}
+
+// The min-p finish on one wave (see above); sc (kRowSCap entries) and hist
+// (256 words) are LDS scratch no other wave uses meanwhile.  Tm is the
+// largest list threshold of the row.  A miss (MinpMiss) sends the row to
+// the candidate lists' finish.
+// The rank (entries above it) of this lane's key among the wave's keys
+// (zero keys count for nothing): over the lanes of km one at a time, or,
+// for many, over all 64 lanes in an unrolled loop of independent compares.
+__device__ __forceinline__ uint32_t wave_rank_desc(uint64_t x, uint64_t km) {
+  uint32_t r = 0u;
+  if (__popcll(km) <= 16) {
+    for (uint64_t mm = km; mm != 0ull; mm &= mm - 1ull)
+      r += readlane64(x, __builtin_ctzll(mm)) > x ? 1u : 0u;
+    return r;
+  }
+  uint32_t r1 = 0u, r2 = 0u, r3 = 0u;
+  #pragma unroll
+  for (int j = 0; j < 64; j += 4) {
+    r += readlane64(x, j) > x ? 1u : 0u;
+    r1 += readlane64(x, j + 1) > x ? 1u : 0u;
+    r2 += readlane64(x, j + 2) > x ? 1u : 0u;
+    r3 += readlane64(x, j + 3) > x ? 1u : 0u;
+  }
+  return (r + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ uint32_t row_minp_finish(const RowLds& L, const RowCfg& cfg, uint64_t* sc, uint32_t* hist,
+                                                    uint32_t& token) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint4 st = *reinterpret_cast<const uint4*>(L.sst);
+  const uint32_t ns = st.x, mk = st.y, Tm = st.z;
+  if (st.w != 0u || ns == 0u || ns > (uint32_t)kRowSCap || mk <= kKeyNegInf || mk >= kKeyPosInf) return kMinpArray;
+  const Exp2TabLds tab{L.exptab};
+  const float M = key_to_s(mk, cfg.t_eff);
+  const uint32_t ke = (uint32_t)cfg.k_eff;
+  if (ns <= 64u) {
+    // one slot: the support stays where it is
+    const uint64_t x = lane < ns ? L.sbuf[lane] : 0ull;
+    uint64_t rk = 0ull;
+    if (x != 0ull) {
+      const float w = exact_expf_t(key_to_s(cand_skey(x), cfg.t_eff) - M, tab);
+      if (w >= cfg.min_p) rk = rank_key(w, cand_idx(x));
+    }
+    // every logit left out of the lists has a key at or below Tm, so a
+    // weight of at most wT: with wT below min_p none of them is in the support
+    const float wT = Tm > kKeyNegInf ? exact_expf_t(key_to_s(Tm, cfg.t_eff) - M, tab) : 0.f;
+    const bool complete = wT < cfg.min_p;
+    const uint64_t km = __ballot(rk != 0ull);
+    const uint32_t c = (uint32_t)__popcll(km);
+    // rank by counting (distinct keys: the ranks of the kept lanes are a
+    // permutation of [0, c)), then each entry moves to the lane of its rank
+    const uint32_t r = wave_rank_desc(rk, km);
+    const int to = rk != 0ull ? (int)(r * 4u) : 63 * 4;  // the other lanes write past c (c < 64) or
+                                                        // nowhere (c == 64: every lane is kept)
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)(uint32_t)rk);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)(uint32_t)(rk >> 32));
+    uint64_t y[1] = {lane < c ? ((uint64_t)hi << 32) | lo : 0ull};
+    if (!minp_topk_known<1>(y, (int)c, cfg.k_eff, complete, wT)) return kMinpTopK;
+    const int pick = wave_draw_r<1>(y, min((int)c, cfg.k_eff), cfg);
+    if (pick < 0) return kMinpDraw;
+    token = cand_idx(readlane64(y[0], pick));
+    return kMinpOk;
+  }
+  const float wT = Tm > kKeyNegInf ? exact_expf_t(key_to_s(Tm, cfg.t_eff) - M, tab) : 0.f;
+  const bool complete = wT < cfg.min_p;
+  constexpr int NS = kRowSCap / 64;
+  uint64_t rk[NS];
+  uint32_t c = 0u;
+  #pragma unroll
+  for (int m = 0; m < NS; ++m) {
+    const uint32_t i = (uint32_t)m * 64u + lane;
+    rk[m] = 0ull;
+    if (m * 64 < (int)ns) {
+      if (i < ns) {
+        const uint64_t x = L.sbuf[i];
+        const float w = exact_expf_t(key_to_s(cand_skey(x), cfg.t_eff) - M, tab);
+        if (w >= cfg.min_p) rk[m] = rank_key(w, cand_idx(x));
+      }
+      c += (uint32_t)__popcll(__ballot(rk[m] != 0ull));
+    }
+  }
+  {
+    // the support gathered into entries [0, c) (every one of them written)
+    uint32_t at = 0u;
+    #pragma unroll
+    for (int m = 0; m < NS; ++m) {
+      if (m * 64 < (int)ns) {
+        const uint64_t bm = __ballot(rk[m] != 0ull);
+        if (rk[m] != 0ull) sc[at + lanes_below(bm)] = rk[m];
+        at += (uint32_t)__popcll(bm);
+      }
+    }
+    wave_lds_sync();
+    #pragma unroll
+    for (int m = 0; m < NS; ++m) {
+      const uint32_t i = (uint32_t)m * 64u + lane;
+      rk[m] = i < c ? sc[i] : 0ull;
+    }
+    wave_lds_sync();
+  }
+  if (c > ke && c > 64u) {
+    // more support than the kept top k: the top k first (a one-wave radix
+    // select over the distinct rank keys: exactly k of them reach thr),
+    // gathered into [0, k)
+    const uint64_t thr = wave_select_skip_f<NS>([&](int i) { return sc[i]; }, (int)c, ke, hist, ~0ull, 0ull);
+    uint32_t at = 0u;
+    wave_lds_sync();
+    #pragma unroll
+    for (int m = 0; m < NS; ++m) {
+      const uint64_t bm = __ballot(rk[m] >= thr);
+      if (rk[m] >= thr) sc[at + lanes_below(bm)] = rk[m];
+      at += (uint32_t)__popcll(bm);
+    }
+    wave_lds_sync();
+    c = ke;
+    #pragma unroll
+    for (int m = 0; m < NS; ++m) {
+      const uint32_t i = (uint32_t)m * 64u + lane;
+      rk[m] = i < c ? sc[i] : 0ull;
+    }
+    wave_lds_sync();
+  }
+  if (c <= 64u) {
+    const uint64_t km = __ballot(rk[0] != 0ull);
+    const uint32_t r = wave_rank_desc(rk[0], km);
+    const int to = rk[0] != 0ull ? (int)(r * 4u) : 63 * 4;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)(uint32_t)rk[0]);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)(uint32_t)(rk[0] >> 32));
+    uint64_t y[1] = {lane < c ? ((uint64_t)hi << 32) | lo : 0ull};
+    if (!minp_topk_known<1>(y, (int)c, cfg.k_eff, complete, wT)) return kMinpTopK;
+    const int pick = wave_draw_r<1>(y, min((int)c, cfg.k_eff), cfg);
+    if (pick < 0) return kMinpDraw;
+    token = cand_idx(readlane64(y[0], pick));
+    return kMinpOk;
+  }
+  if (c <= 128u) {
+    uint64_t y[2] = {rk[0], rk[1]};
+    return minp_draw<2>(y, (int)c, cfg, complete, wT, token);
+  }
+  // c <= k_eff <= kLeanK here
+  static_assert(kLeanK <= 256, "four slots hold the kept top k");
+  uint64_t y[4] = {rk[0], rk[1], rk[2], rk[3]};
+  return minp_draw<4>(y, (int)c, cfg, complete, wT, token);
+}
+
 // The fast path of one row, with its first tiles in flight (row_issue);
 // false sends the row to the general path (all threads return the same).
 template <bool MASK>
@@ -201,6 +432,12 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   // 1. the loads in flight
   const uint32_t h0 = pp.h0, h1 = pp.h1;
   const bool hist = h1 > h0;
+  constexpr uint32_t kFirst = (uint32_t)(kRowHistPer * kRowThreads);
+  // min-p rows take the min-p finish when their history entries sit in
+  // registers (at most kFirst)
+  bool sp = cfg.min_p > 0.f && (!hist || h1 - h0 <= kFirst);
+  uint32_t minp_miss = 0u;  // why the min-p finish missed (diag bits 8-15)
+  const float ln_mp = sp ? logf(cfg.min_p) : 0.f;
   auto& hid = pp.hid;
   auto& hcs = pp.hcs;
   const __amdgpu_buffer_rsrc_t rs = pp.rs;
@@ -319,7 +556,15 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   using Slot1 = std::integral_constant<int, 1>;
   static_assert(kRowDepth == 2, "the stream alternates two slots");
 
-  // 3. the first two tiles
+  // 3. the first two tiles (the min-p state is set before any wave's stream
+  //    can end: the history ranking below has barriers, else one here)
+  if (sp && tid == 0) {
+    L.sst[kSCnt] = 0u;
+    L.sst[kSMax] = kKeyNegInf;
+    L.sst[kSThr] = 0u;
+    L.sst[kSBad] = 0u;
+  }
+  if (sp && !hist) __syncthreads();
   step(Slot0{}, 0, true);
   step(Slot1{}, 1, false);
 
@@ -327,7 +572,6 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   //    were issued before them, so they have arrived): marks and rank
   //    prefix, then the summed count and id of each distinct token by rank,
   //    whose logit is loaded during the stream
-  constexpr uint32_t kFirst = (uint32_t)(kRowHistPer * kRowThreads);
   uint32_t distinct = 0u;
   if (hist) {
     for (int i = tid; i < Wm; i += kRowThreads) hw[i] = make_uint2(0u, 0u);
@@ -350,16 +594,28 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
       wsum += w < Wm ? (uint32_t)__popc(hw[w].x) : 0u;
     }
     wsum = wave_sum_u32(wsum);
-    if (lane == 0u) L.redu[wid] = wsum;
+    // min-p rows append each history token once: with no id repeated in
+    // the list, the entries holding an id below V are as many as the
+    // distinct tokens (else the row takes the candidate lists' finish)
+    uint32_t nv = 0u;
+    #pragma unroll
+    for (int r = 0; r < kRowHistPer; ++r) nv += hid[r] < (uint32_t)V ? 1u : 0u;
+    nv = wave_sum_u32(nv);
+    if (lane == 0u) {
+      L.redu[wid] = wsum;
+      L.red64[wid] = nv;
+    }
     __syncthreads();
-    uint32_t run = 0u;
+    uint32_t run = 0u, valid = 0u;
     #pragma unroll
     for (int v = 0; v < kRowWaves; ++v) {
       const uint32_t c = L.redu[v];
       run += v < wid ? c : 0u;
       distinct += c;
+      valid += (uint32_t)L.red64[v];
     }
     if (distinct > (uint32_t)kRowHistCap) return false;
+    sp = sp && valid == distinct;
     for (int b = 0; b < PB; b += 64) {
       const int w = w0 + b + (int)lane;
       const uint32_t c = w < Wm ? (uint32_t)__popc(hw[w].x) : 0u;
@@ -381,6 +637,22 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) add(a.hids[h], a.hcnt[h]);
     __syncthreads();  // the summed counts are complete before any wave's stream ends
   }
+  if (sp) {
+    // a lower bound of the row max for the waves' end-of-stream bounds: the
+    // largest key of this wave's list after its first two tiles that is not
+    // a history token
+    uint32_t mx = 0u;
+    #pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t i = lane + 64u * (uint32_t)m;
+      const uint64_t x = i < wn ? wl[i] : 0ull;
+      const uint32_t id = min(cand_idx(x), (uint32_t)V - 1u);
+      const bool off = hist && ((hw[id >> 5].x >> (id & 31u)) & 1u);
+      if (x != 0ull && !off) mx = max(mx, cand_skey(x));
+    }
+    mx = wave_max_u32(mx);
+    if (lane == 0u && mx != 0u) atomicMax(&L.sst[kSMax], mx);
+  }
   // the history tokens' logits, in flight during the stream: unconditional
   // range-checked loads (an id past the row reads zero and is not stored)
   uint32_t hraw[kRowHistPer], hmw[kRowHistPer];
@@ -401,18 +673,24 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     L.wbad[wid] = bad ? 1u : 0u;
     L.wcnt[wid] = wn;
   }
+  uint32_t hk[kRowHistPer];  // processed keys of this thread's history entries
+  #pragma unroll
+  for (int r = 0; r < kRowHistPer; ++r) hk[r] = kKeyNegInf;
   if (hist) {
     auto put = [&](uint32_t id, uint32_t raw) {
       const uint2 h = hw[id >> 5];
       const uint32_t rank = h.y + (uint32_t)__popc(h.x & ((1u << (id & 31u)) - 1u));
       const float l = __uint_as_float(raw);
       const uint32_t c = L.ob_cnt[rank];
-      L.ob_raw[rank] = lkey(cfg.rep_on ? apply_penalties(l, c, cfg) : apply_penalties_norep(l, c, cfg));
+      const uint32_t k = lkey(cfg.rep_on ? apply_penalties(l, c, cfg) : apply_penalties_norep(l, c, cfg));
+      L.ob_raw[rank] = k;
+      return k;
     };
     constexpr uint32_t kNegInfBits = 0xff800000u;
     #pragma unroll
     for (int r = 0; r < kRowHistPer; ++r) {
-      if (hid[r] < (uint32_t)V) put(hid[r], MASK && !((hmw[r] >> (hid[r] & 31u)) & 1u) ? kNegInfBits : hraw[r]);
+      if (hid[r] < (uint32_t)V)
+        hk[r] = put(hid[r], MASK && !((hmw[r] >> (hid[r] & 31u)) & 1u) ? kNegInfBits : hraw[r]);
     }
     for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) {
       const uint32_t id = a.hids[h];
@@ -422,11 +700,85 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
       }
     }
   }
+  if (sp) {
+    // min-p rows: this wave's list entries that are not history tokens and
+    // its threads' processed history logits (first occurrences) whose key
+    // reaches the bound of the largest key seen so far go to L.sbuf
+    if (wid == 0 && lane < 32u) L.exptab[lane] = exp2_tab32(lane);
+    if (lane == 0u) {
+      atomicMax(&L.sst[kSThr], T);
+      if (bad) atomicOr(&L.sst[kSBad], 1u);
+    }
+    uint64_t e[2 + kRowHistPer];
+    const uint32_t mprev = L.sst[kSMax];  // a lower bound of the row max
+    #pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t i = lane + 64u * (uint32_t)m;
+      e[m] = i < wn ? wl[i] : 0ull;
+    }
+    if (hist) {
+      uint32_t mk[2];
+      #pragma unroll
+      for (int m = 0; m < 2; ++m) mk[m] = hw[min(cand_idx(e[m]), (uint32_t)V - 1u) >> 5].x;
+      #pragma unroll
+      for (int m = 0; m < 2; ++m)
+        if ((mk[m] >> (cand_idx(e[m]) & 31u)) & 1u) e[m] = 0ull;
+    }
+    #pragma unroll
+    for (int r = 0; r < kRowHistPer; ++r)
+      e[2 + r] = hk[r] > kKeyNegInf ? cand_key(hk[r], hid[r]) : 0ull;
+    uint32_t mx = 0u;
+    #pragma unroll
+    for (int m = 0; m < 2 + kRowHistPer; ++m) mx = max(mx, cand_skey(e[m]));
+    mx = wave_max_u32(mx);
+    if (lane == 0u && mx > mprev) atomicMax(&L.sst[kSMax], mx);
+    const uint32_t mcur = (uint32_t)__builtin_amdgcn_readfirstlane((int)max(mprev, mx));
+    const uint32_t kb = max(minp_key_bound(mcur, cfg.t_eff, ln_mp), kKeyNegInf + 1u);
+    uint64_t bm[2 + kRowHistPer];
+    uint32_t nk = 0u;
+    #pragma unroll
+    for (int m = 0; m < 2 + kRowHistPer; ++m) {
+      bm[m] = __ballot(e[m] != 0ull && cand_skey(e[m]) >= kb);
+      nk += (uint32_t)__popcll(bm[m]);
+    }
+    if (nk != 0u) {
+      uint32_t at = 0u;
+      if (lane == 0u) at = atomicAdd(&L.sst[kSCnt], nk);
+      at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
+      #pragma unroll
+      for (int m = 0; m < 2 + kRowHistPer; ++m) {
+        const uint32_t pos = at + lanes_below(bm[m]);
+        if (((bm[m] >> lane) & 1ull) && pos < (uint32_t)kRowSCap) L.sbuf[pos] = e[m];
+        at += (uint32_t)__popcll(bm[m]);
+      }
+    }
+  }
   __syncthreads();  // lists, thresholds and the history complete
 
   // 6. the rest runs on the first NT threads, one wave per SIMD; the other
   //    waves end here (ended waves no longer count at barriers)
   if (wid >= NT / 64) return true;
+  if (sp) {
+    // wave 0 runs the min-p finish and publishes whether it resolved the
+    // row: the four waves then take the same path (the general finish
+    // below needs all of them)
+    if (wid == 0) {
+      uint32_t tok = 0u;
+      // scratch: waves 0 and 1's tile buffers (the other waves wait below)
+      const uint32_t miss = row_minp_finish(L, cfg, reinterpret_cast<uint64_t*>(L.xscr[0]),
+                                            reinterpret_cast<uint32_t*>(L.xscr[1]), tok);
+      if (lane == 0u) {
+        L.sdone = miss;
+        if (miss == kMinpOk) {
+          a.out_tokens[row] = tok;
+          a.diag[row] = kRowPathMinp;
+        }
+      }
+    }
+    __syncthreads();
+    minp_miss = L.sdone;
+    if (minp_miss == kMinpOk) return true;
+  }
   uint32_t Tm = L.wthr[0];
   uint32_t anybad = L.wbad[0];
   #pragma unroll
@@ -522,7 +874,9 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   // key bounds for the selection: every candidate's key is at least Tm
   // (the 16-wave row kernel keeps the workgroup select: the one-wave select's
   // registers cost its stream more than the select saves)
-  return finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm, (uint64_t)Tm << 32, top, false);
+  const bool ok = finish_core(fs, a, row, cfg, (int)n, M, Tm > kKeyNegInf ? Tm : 0u, 0.0, Tm, (uint64_t)Tm << 32, top, false);
+  if (ok && tid == 0) a.diag[row] = kRowPathLists | (minp_miss << 8);
+  return ok;
 }
 
 // The general path of a row (see the section comment), on the first NT
@@ -556,6 +910,7 @@ __device__ __noinline__ void row_general(KernargSampleArgs* ap, int row) {
     select_chunk<HI_ROCM_DTYPE_F32, kRowGeneralChunk / NT / 4, MASK>(a, row, c, lds_raw);
     __syncthreads();
   }
+  if (threadIdx.x == 0) a.diag[row] = kRowPathGeneral;
   FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
   if (finish_lean(fs, a, row, cfg)) return;
   __syncthreads();

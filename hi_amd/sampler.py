@@ -224,17 +224,31 @@ class Sampler:
 
 
 WIDE_PATHS = {0: "other", 1: "wide", 2: "no-stats", 3: "chunk-full", 4: "total", 5: "merge-full",
-              6: "no-cutoff", 7: "draw-fail"}
+              6: "no-cutoff", 7: "draw-fail", 8: "row-minp", 9: "row-lists", 10: "row-general"}
 
 
 def debug_wide_paths(smp: "Sampler", batch: int, vocab: int,
                      stream: Optional[torch.cuda.Stream] = None) -> np.ndarray:
-    """How the last ``smp.sample`` call finished each top-p row on the
-    chunked path (``hi_rocm_debug_wide_paths``; codes in WIDE_PATHS)."""
+    """How the last ``smp.sample`` call finished each row: top-p rows on the
+    chunked path, every row of the row kernel (``hi_rocm_debug_wide_paths``;
+    codes in WIDE_PATHS)."""
     out = np.zeros(batch, np.uint32)
     check(load().hi_rocm_debug_wide_paths(smp.workspace.data_ptr(), smp.workspace.numel(), batch, vocab,
                                           out.ctypes.data, _stream_ptr(stream)))
-    return out
+    return out & 0xff
+
+
+MINP_MISSES = {0: "none", 1: "array", 2: "top-k", 3: "draw"}
+
+
+def debug_row_minp_misses(smp: "Sampler", batch: int, vocab: int,
+                          stream: Optional[torch.cuda.Stream] = None) -> np.ndarray:
+    """Why the row kernel's min-p finish left each row to the candidate lists'
+    finish in the last ``smp.sample`` call (codes in MINP_MISSES)."""
+    out = np.zeros(batch, np.uint32)
+    check(load().hi_rocm_debug_wide_paths(smp.workspace.data_ptr(), smp.workspace.numel(), batch, vocab,
+                                          out.ctypes.data, _stream_ptr(stream)))
+    return out >> 8
 
 
 def debug_distribution(logits: torch.Tensor, params: torch.Tensor,
@@ -266,4 +280,5 @@ __all__ = [
     "RowSampling", "SamplerError", "HiRocmError", "Sampler", "row_params", "params_to_device",
     "argmax_batched_last_token", "sample_batched_last_token", "select_batched_last_token_per_row",
     "sample_last_row_with_sample", "debug_distribution", "debug_expf", "debug_wide_paths",
+    "debug_row_minp_misses",
 ]

@@ -310,11 +310,14 @@ int hi_rocm_debug_fold(const float* terms, const uint32_t* counts, int runs, flo
                        float* out_start, float* out_final, void* stream);
 
 /* Debug export: how the last hi_rocm_sample call on this workspace
- * finished each top-p row without a top-k bound on its chunked path
- * (u32[batch] to host memory; blocking): 1 = the chunk-parallel wide pass,
- * 2-7 = a named fallback to the general finish, 0 = not such a row.  The
- * batch and vocab must be the call's; any stream, the null one included.
- * No reference counterpart. */
+ * finished each row (u32[batch] to host memory; blocking).  Top-p rows
+ * without a top-k bound on the chunked path: 1 = the chunk-parallel wide
+ * pass, 2-7 = a named fallback to the general finish.  Rows of the row
+ * kernel (batches of 192+ rows without logprobs): 8 = the min-p support
+ * finish, 9 = the candidate lists' finish (bits 8-15: why a min-p row missed
+ * the min-p finish: 1 its support array, 2 its top k not known, 3 the
+ * draw), 10 = the general path.  0 = none of these.  The batch and vocab must be the call's; any stream, the null
+ * one included.  No reference counterpart. */
 int hi_rocm_debug_wide_paths(const void* workspace, size_t workspace_bytes, int batch, int vocab,
                              uint32_t* out_paths, void* stream);
 

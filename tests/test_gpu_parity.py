@@ -43,7 +43,7 @@ def dev(x):
     return torch.from_numpy(x).to("cuda")
 
 
-def run_gpu(w: Workload, token_logprobs=True, repeat=1, paths=None):
+def run_gpu(w: Workload, token_logprobs=True, repeat=1, paths=None, misses=None):
     torch = _torch()
     from hi_amd import sampler as S
     logits = dev(w.logits)
@@ -62,6 +62,8 @@ def run_gpu(w: Workload, token_logprobs=True, repeat=1, paths=None):
         outs.append({k: v.cpu().numpy() for k, v in out.items()})
     if paths is not None:
         paths.append(S.debug_wide_paths(smp, w.batch, w.vocab))
+    if misses is not None:
+        misses.append(S.debug_row_minp_misses(smp, w.batch, w.vocab))
     for o in outs:
         o["tokens"] = o["tokens"].view(np.uint32)
         if "logprob_ids" in o:
@@ -371,6 +373,114 @@ def test_config3_deterministic(hip):
     w = CONFIGS[3]()
     a, b = run_gpu(w, repeat=2)
     assert np.array_equal(a["tokens"], b["tokens"])
+
+
+def test_config3_row_kernel_min_p_path(hip, oracle):
+    """Config 3 as the benchmark runs it (no logprobs: the row kernel), row
+    by row against the oracle; every row is resolved by the min-p support
+    finish (the path the benchmark times), twice in a row."""
+    from hi_amd.sampler import WIDE_PATHS
+    from hi_amd.sampler import MINP_MISSES
+    w = CONFIGS[3]()
+    paths, misses = [], []
+    got = run_gpu(w, token_logprobs=False, repeat=2, paths=paths, misses=misses)
+    assert np.array_equal(got[0]["tokens"], got[1]["tokens"]), "not deterministic"
+    want = run_oracle(oracle, w)
+    compare(w, got[0], want, "c3 row kernel")
+    names = [WIDE_PATHS[int(p)] for p in paths[0]]
+    say(f"row paths: {dict(zip(*np.unique(names, return_counts=True)))}")
+    for b in np.flatnonzero(misses[0]):
+        say(f"  row {b}: min-p miss {MINP_MISSES[int(misses[0][b])]} (T {w.params['temperature'][b]:.3f}, "
+            f"top-k {w.params['top_k'][b]})")
+    assert all(n == "row-minp" for n in names), names
+
+
+def _min_p_workload(rng, V, with_mask):
+    """B=256 rows, all with min-p, for the row kernel's min-p support
+    finish: supports from one token to more than its LDS array holds,
+    top-k below and above the support size, ties of equal logits, distinct
+    logits whose weights round to one value (rank order by index, not by
+    logit), repeated history ids, extreme temperatures, edge uniforms."""
+    from hi_amd.sampler import row_params
+    B = 256
+    x = rng.normal(0, 2.5, (B, V)).astype(F32)
+    x[np.arange(B)[:, None], rng.integers(0, V, (B, 16))] += F32(8.0)
+    p = row_params(B, temperature=0.8, top_p=1.0)
+    p["temperature"] = rng.choice([0.05, 0.3, 0.8, 1.2, 3.0], B)
+    p["top_k"] = rng.choice([1, 3, 20, 64, 100, 256], B)
+    p["top_p"] = rng.choice([1.0, 0.95, 0.8, 0.5, 0.0], B)
+    p["min_p"] = rng.choice([1e-4, 0.01, 0.05, 0.2, 0.9, 1.0], B)
+    p["repetition_penalty"] = rng.choice([1.0, 1.3], B)
+    p["frequency_penalty"] = rng.choice([0.0, 0.2, -0.5], B)
+    p["presence_penalty"] = rng.choice([0.0, 0.3], B)
+    for b in range(0, 24):
+        p["min_p"][b] = 0.05
+        p["top_p"][b] = 0.95
+    x[0, rng.permutation(V)[:40]] = F32(30.0)          # 40 tied maxima: w = 1, order by index
+    p["top_k"][0] = 20
+    x[1, rng.permutation(V)[:300]] = F32(30.0)         # 300 tied maxima: a support above 256
+    p["top_k"][1] = 256
+    base = F32(25.0)
+    ids = rng.permutation(V)[:64]
+    x[2, ids] = base + np.arange(64, dtype=F32) * np.spacing(base)  # 64 distinct logits ...
+    p["temperature"][2] = 3.0                          # ... whose weights collapse to few values
+    p["top_k"][2] = 50
+    x[3] = rng.normal(0, 0.05, V).astype(F32)          # nearly flat: a support of ~V tokens
+    p["min_p"][3] = 0.5
+    x[4, :] = -np.inf
+    x[4, 11] = 2.0                                     # one finite logit
+    x[5, 50:60] = np.inf                               # +inf: the general path
+    x[6, 70] = np.nan
+    for b in (7, 8):
+        p["top_p"][b] = 0.9
+    u = rng.random(B).astype(F32)
+    u[7], u[8] = 0.99999994, 0.0
+    ids_l, cnt_l, offs = [], [], np.zeros(B + 1, np.uint32)
+    for b in range(B):
+        r = np.unique(np.minimum(rng.zipf(1.2, 400) - 1, V + 5))  # ids past V are ignored
+        top = np.argsort(x[b])[-8:]
+        if b % 4 == 1:
+            r = np.union1d(r, top)                     # penalised tokens among the top ones
+        if b % 16 == 3:
+            r = np.concatenate([r, r[:60], r[:10]])    # repeated ids: counts add up (the lists' finish)
+        rng.shuffle(r)
+        ids_l.append(r.astype(np.uint32))
+        cnt_l.append(rng.integers(1, 5, len(r)).astype(np.uint32))
+        offs[b + 1] = offs[b] + len(r)
+    hids, cnts = np.concatenate(ids_l), np.concatenate(cnt_l)
+    mask = None
+    if with_mask:
+        W = (V + 31) // 32
+        off = [rng.integers(0, 2 ** 32, (B, W), dtype=np.uint64) for _ in range(3)]
+        mask = (~(off[0] & off[1] & off[2]) & np.uint64(0xffffffff)).astype(np.uint32)  # 1 in 8 masked
+        mask[9] = 0                                    # fully masked: EOS
+        p["eos_id"][9] = 5
+    return Workload("min-p", x, p, u, offs, hids, cnts, mask, 0)
+
+
+@pytest.mark.parametrize("V,with_mask", [(129280, False), (70000, True)])
+def test_min_p_support_path(hip, oracle, V, with_mask):
+    """The row kernel's min-p support finish against the oracle, with the
+    rows it must hand to the other paths (supports above its array, +inf,
+    nothing finite) still exact."""
+    from hi_amd.sampler import WIDE_PATHS
+    rng = np.random.default_rng(777 + V)
+    w = _min_p_workload(rng, V, with_mask)
+    say(f"min-p rows V={V} mask={with_mask}")
+    from hi_amd.sampler import MINP_MISSES
+    paths, misses = [], []
+    got = run_gpu(w, token_logprobs=False, repeat=2, paths=paths, misses=misses)
+    assert np.array_equal(got[0]["tokens"], got[1]["tokens"]), "not deterministic"
+    want = run_oracle(oracle, w)
+    compare(w, got[0], want, f"min-p V={V} mask={with_mask}")
+    names = np.array([WIDE_PATHS[int(p)] for p in paths[0]])
+    say(f"row paths: {dict(zip(*np.unique(names, return_counts=True)))}")
+    mm = [MINP_MISSES[int(m)] for m in misses[0][names == "row-lists"]]
+    say(f"min-p misses: {dict(zip(*np.unique(mm, return_counts=True)))}")
+    assert names[5] == "row-general"                   # +inf
+    rep = np.arange(256) % 16 == 3
+    assert all(n in ("row-lists", "row-general") for n in names[rep]), names[rep]
+    assert (names == "row-minp").sum() >= 180, names
 
 
 def test_processed_distribution_within_1e5(hip, oracle):

@@ -49,6 +49,7 @@ SIGNATURES = {
     "hi_rocm_launch_select_batched_last_token_per_row_noalloc": (
         _i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "hi_rocm_sampler_reserve": (_i, [_i, _i, _i, _vp]),
+    "hi_rocm_sampler_release": (_i, [_vp]),
     "hi_rocm_launch_moe_topk_router": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "hi_rocm_lm_head_workspace_bytes": (_i, [_i, _i, ctypes.POINTER(_sz)]),
     "hi_rocm_lm_head_logits": (_i, [_vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp]),

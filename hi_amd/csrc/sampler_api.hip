@@ -42,13 +42,30 @@ int api_hip_fail(hipError_t e, const char* where) { return hip_fail(e, where); }
 
 namespace {
 
+// The per-row chunk counters of a workspace start at zero (the kernels
+// leave them so): a fill kernel, not a memset node, so that a call that
+// sets them can be captured in a graph.
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) p[i] = 0u;
+}
+
+hipError_t zero_counters(void* ws, int n, hipStream_t stream) {
+  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     (uint32_t*)ws, n);
+  return hipGetLastError();
+}
+
 // Library-owned workspace for the workspace-free reference mirrors: one
 // buffer per (device, stream), grown on demand, never shrunk, like the
 // reference's thread-local buffer pool (crates/hi-cuda/src/runtime.rs:
-// 218-231).  Calls on one stream are ordered by the stream, so a buffer is
-// never used by two kernels at once; calls on different streams (from any
-// thread) use different buffers.  Growing waits for the buffer's own stream
-// only.
+// 218-231); hi_rocm_sampler_release frees a stream's buffer.  Calls on one
+// stream are ordered by the stream, so a buffer is never used by two
+// kernels at once; calls on different streams (from any thread) use
+// different buffers.  Growing waits for the buffer's own stream only, and
+// is refused while the stream is being captured (like the reference's pool,
+// runtime.rs:238-257, which does not allocate during capture): the caller
+// reserves before capturing.
 struct DeviceWorkspace {
   void* ptr = nullptr;
   size_t bytes = 0;
@@ -63,6 +80,14 @@ int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
   std::lock_guard<std::mutex> lock(g_ws_mutex);
   DeviceWorkspace& ws = g_ws[{dev, (uintptr_t)stream}];
   if (ws.bytes < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(HI_ROCM_ERR_UNSUPPORTED,
+                  "hi-rocm: the stream's sampler workspace would grow to " + std::to_string(bytes) +
+                      " bytes during stream capture (an allocation); call hi_rocm_sampler_reserve with the "
+                      "largest shape before capturing");
     if (ws.ptr) {
       e = hipStreamSynchronize(stream);
       if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
@@ -73,12 +98,34 @@ int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
     }
     e = hipMalloc(&ws.ptr, bytes);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(sampler workspace)");
-    // the per-row chunk counters start at zero; the kernels leave them so
-    e = hipMemsetAsync(ws.ptr, 0, bytes, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync(sampler workspace)");
+    e = zero_counters(ws.ptr, hi_rocm::kDoneRows, stream);
+    if (e != hipSuccess) return hip_fail(e, "sampler workspace counter reset");
     ws.bytes = bytes;
   }
   *out = ws.ptr;
+  return HI_ROCM_OK;
+}
+
+// Frees the calling device's workspace of `stream` after the stream's work.
+int release_workspace(hipStream_t stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  auto it = g_ws.find({dev, (uintptr_t)stream});
+  if (it == g_ws.end()) return HI_ROCM_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(stream, &cs);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(HI_ROCM_ERR_UNSUPPORTED, "hi_rocm_sampler_release: the stream is being captured");
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  if (it->second.ptr) {
+    e = hipFree(it->second.ptr);
+    if (e != hipSuccess) return hip_fail(e, "hipFree");
+  }
+  g_ws.erase(it);
   return HI_ROCM_OK;
 }
 
@@ -287,6 +334,11 @@ int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs, void* stre
   if (max_batch > hi_rocm::kDoneRows) return fail(HI_ROCM_ERR_UNSUPPORTED, "batch above 65536 rows");
   void* ws = nullptr;
   return internal_workspace(hi_rocm::workspace_layout(max_batch, vocab).total, (hipStream_t)stream, &ws);
+}
+
+int hi_rocm_sampler_release(void* stream) {
+  if (stream == nullptr) return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sampler_release: null stream");
+  return release_workspace((hipStream_t)stream);
 }
 
 int hi_rocm_sampler_workspace_bytes(int max_batch, int vocab, int n_logprobs, size_t* out_bytes) {
@@ -502,6 +554,11 @@ extern "C" {
 int hi_rocm_lm_head_workspace_bytes(int batch, int vocab, size_t* out_bytes) {
   if (batch <= 0 || vocab <= 0 || out_bytes == nullptr)
     return fail(HI_ROCM_ERR_ARGS, "hi_rocm_lm_head_workspace_bytes: invalid arguments");
+  // the shapes hi_rocm_sample_lm_head accepts (lm_args)
+  if (batch > hi_rocm::kLmRows)
+    return fail(HI_ROCM_ERR_UNSUPPORTED, "hi_rocm_lm_head_workspace_bytes: batch above 64");
+  if ((vocab + hi_rocm::kLmTile - 1) / hi_rocm::kLmTile > hi_rocm::kLmMaxTiles)
+    return fail(HI_ROCM_ERR_UNSUPPORTED, "hi_rocm_lm_head_workspace_bytes: vocabulary above 524,288");
   *out_bytes = hi_rocm::lm_workspace_bytes(batch, vocab);
   return HI_ROCM_OK;
 }
@@ -556,14 +613,6 @@ constexpr size_t kNoAllocScratchBytes = HI_ROCM_NOALLOC_SCRATCH_BYTES;  // per G
 
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
-// The per-row chunk counters of a call start at zero (the kernels leave
-// them so, but the array keeps whatever the last call left): a fill kernel,
-// not a memset node, so that the call can be captured in a graph.
-__global__ void zero_words_kernel(uint32_t* p, int n) {
-  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (i < n) p[i] = 0u;
-}
-
 std::mutex g_scratch_mutex;
 std::map<int, void*> g_scratch_ptr;  // device -> address of its `scratch`
 
@@ -610,9 +659,9 @@ int hi_rocm_launch_select_batched_last_token_per_row_noalloc(
   rc = scratch_address(&ptr);
   if (rc != HI_ROCM_OK) return rc;
   carve(a, ptr, L);
-  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((batch_count + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, a.done, batch_count);
-  hipError_t e = hipGetLastError();
+  // the per-row counters start at zero (the array keeps whatever the last
+  // call left)
+  hipError_t e = zero_counters(a.done, batch_count, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "scratch counter reset");
   e = hi_rocm::launch_sample(a, (hipStream_t)stream, next_events());
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "sampler launch");

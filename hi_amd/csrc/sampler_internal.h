@@ -154,7 +154,7 @@ struct SampleArgs {
 // that path, or an older call).
 enum WidePath : uint32_t {
   kWideDone = 1,          // finished by the wide pass
-  kWideNoStats = 2,       // a chunk took the select pass's exact path, or no finite logit
+  kWideNoStats = 2,       // a chunk's statistics were not written by this call's pass, or no finite logit
   kWideChunkFull = 3,     // a chunk's table of distinct weights overflowed
   kWideTotal = 4,         // the normaliser is not positive and finite (argmax fallback)
   kWideMergeFull = 5,     // the row's table of distinct weights overflowed

@@ -137,6 +137,7 @@ __device__ __forceinline__ void wide_row_prepare(SelLds& L, const SampleArgs& a,
   for (int c = tid; c < nch; c += NT) {
     mk = max(mk, okey(stats[c].max_l));
     bad |= wst[c].valid ^ 1u;
+    wst[c].valid = 0u;  // so that a chunk this call's pass did not write is seen next time
   }
   unsigned long long* gmass = reinterpret_cast<unsigned long long*>(L.surv[0]);  // kWideGBins entries
   if (tid < kWideGBins) gmass[tid] = 0ull;

@@ -165,6 +165,13 @@ def row_params(batch: int, temperature=0.0, top_p=1.0, top_k=0, min_p=0.0,
     return p
 
 
+def sampler_release(stream: Optional[torch.cuda.Stream] = None) -> None:
+    """Free the library workspace of ``stream`` on the current device
+    (``hi_rocm_sampler_release``); the mirrors allocate it again on demand."""
+    s = stream if stream is not None else torch.cuda.current_stream()
+    check(load().hi_rocm_sampler_release(int(s.cuda_stream)))
+
+
 def params_to_device(params: np.ndarray, device="cuda") -> torch.Tensor:
     raw = np.ascontiguousarray(params, ROW_PARAMS_DTYPE).view(np.uint8)
     return torch.from_numpy(raw.copy()).to(device)
@@ -280,5 +287,5 @@ __all__ = [
     "RowSampling", "SamplerError", "HiRocmError", "Sampler", "row_params", "params_to_device",
     "argmax_batched_last_token", "sample_batched_last_token", "select_batched_last_token_per_row",
     "sample_last_row_with_sample", "debug_distribution", "debug_expf", "debug_wide_paths",
-    "debug_row_minp_misses",
+    "debug_row_minp_misses", "sampler_release",
 ]

@@ -234,12 +234,21 @@ int hi_rocm_launch_select_batched_last_token_per_row_noalloc(const void* logits,
 /* The mirrors above take no workspace, like the reference.  They use a
  * workspace per (device, stream) that the library grows on demand
  * (hipMalloc; growing waits for that stream), so calls on different
- * streams, from any threads, never share one.  Call this once per stream,
- * before any stream capture, with the largest shape to be sampled on it so
- * that no allocation happens afterwards.  No reference counterpart (the
+ * streams, from any threads, never share one.  Growing is refused while the
+ * stream is being captured (status 2, nothing enqueued).  Call this once per
+ * stream, before any stream capture, with the largest shape to be sampled
+ * on it so that no allocation happens afterwards.  No reference counterpart (the
  * reference pre-warms its buffer pool instead,
  * crates/hi-cuda/src/runtime.rs:240-262). */
 int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs, void* stream);
+
+/* Frees the calling device's workspace of `stream` (after waiting for the
+ * stream's work): for a stream that will make no more sampler calls, or
+ * whose buffer should shrink.  A later call on the stream allocates again.
+ * Status 2 while the stream is being captured.  No reference counterpart
+ * (the reference's buffer pool is thread-local and freed with its thread,
+ * crates/hi-cuda/src/runtime.rs:218-231). */
+int hi_rocm_sampler_release(void* stream);
 
 /* ---- extended pipeline (the decode-step API; proposal of the survey's
  *      boundary section, no single reference counterpart) ---- */

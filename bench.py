@@ -26,6 +26,28 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 METRIC = "sampled rows/s @B=256 V=129280; µs/step @B=1; % of HBM peak BW"
 
+# Passes over row-sized data per step, by row class and kernel shape:
+# reads and writes of the logits or of per-logit workspace arrays (4 B per
+# logit), each counted once; everything else a row's finish touches is
+# O(candidates).  "l2" names the passes whose data was written in the same
+# step and is normally re-read from the on-die caches (L2 / the 256 MB
+# Infinity Cache) rather than from HBM.
+PASSES = {
+    "row_kernel (B >= 192 f32, no logprobs; C3)": {
+        "top-k <= 256 (incl. min-p, penalties, mask)": {"reads": 1, "writes": 0},
+        "other classes, or a fallback (general path, 8192-logit chunks)":
+            {"reads": "1 + 1 of s for top-p / temperature-only / top-k > 1024", "writes": "0, or 1 of s",
+             "l2": "the s re-read"},
+    },
+    "select + finish (C1 one launch; C2, C4, C5 two)": {
+        "greedy, top-k <= 1024 (C1, C2's greedy half, C4)": {"reads": 1, "writes": 0},
+        "top-p without top-k (wide pass; C2, C5)": {
+            "reads": "1 (logits) + 1 (s, finish grid) + the refolded chunks' w (a few per row)",
+            "writes": "2 (s by the select pass, w by the finish grid)", "l2": "the s and w re-reads"},
+        "temperature only, top-k > 1024": {"reads": "1 + 1 of s", "writes": "1 of s", "l2": "the s re-read"},
+    },
+}
+
 
 def _dev(torch, x):
     x = np.ascontiguousarray(x)
@@ -88,11 +110,16 @@ def time_large_batch(torch, w, steps, warmup):
     return total_ms / steps, per, wall
 
 
-def time_config(torch, w, steps, warmup):
+def time_config(torch, w, steps, warmup, cfg):
     """One of the other configurations (C2, C4, C5): K eager steps of the
-    whole pipeline on one stream between two HIP events on that stream.
-    Algorithmic bytes per step are the workload's input and output bytes,
-    each counted once; the fraction is of the 8 TB/s HBM peak."""
+    whole pipeline on one stream between two HIP events on that stream, then
+    a second pass with an event after every step for the p50 / p99 spread
+    (those events add a few microseconds to each step).  Algorithmic bytes
+    per step are the workload's input and output bytes, each counted once;
+    the fraction is of the 8 TB/s HBM peak.  `roofline` prices the step's
+    kernels together (the select pass and the finish grid, two launches):
+    the HBM bytes they move per step come from the committed counter
+    summary of this configuration when it was measured on this build."""
     smp, a = _prepare(torch, w)
     stream = torch.cuda.Stream()
     out = None
@@ -108,11 +135,28 @@ def time_config(torch, w, steps, warmup):
         ev1.record(stream)
     torch.cuda.synchronize()
     us = ev0.elapsed_time(ev1) * 1000.0 / steps
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    with torch.cuda.stream(stream):
+        evs[0].record(stream)
+        for i in range(steps):
+            out = _step(smp, a, w, out, stream)
+            evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]) * 1000.0
     alg = w.algorithmic_bytes()
     gbs = alg / (us * 1e-6) / 1e9
+    traffic, tag = traffic_from_profile(f"config{cfg}_hbm_traffic.md")
+    current = traffic is not None and tag == source_hash()
     return {"workload": w.name, "us_per_step": us, "rows_per_s": w.batch / (us * 1e-6),
+            "us_per_step_p50_with_step_events": float(np.percentile(per, 50)),
+            "us_per_step_p99_with_step_events": float(np.percentile(per, 99)),
             "algorithmic_bytes": alg, "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
-            "floor_us": alg / (HBM_PEAK_GBS * 1e9) * 1e6}
+            "floor_us": alg / (HBM_PEAK_GBS * 1e9) * 1e6,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": traffic if current else None,
+                         "traffic_summary": {"file": f"profiles/config{cfg}_hbm_traffic.md", "bytes": traffic,
+                                             "source_hash": tag, "matches_this_build": current},
+                         "kernels": "the step's launches together (select pass + finish grid)"}}
 
 
 def time_parts(torch, w, steps):
@@ -140,9 +184,9 @@ def time_parts(torch, w, steps):
 
 
 def pmc_probe(torch, w, steps, copy_mib=512):
-    """Workload for the rocprofv3 --pmc passes: C3 steps, then one plain
-    device copy of copy_mib MiB whose FETCH_SIZE / WRITE_SIZE calibrate the
-    counters (a copy reads and writes exactly its size)."""
+    """Workload for the rocprofv3 --pmc passes: steps of one configuration,
+    then one plain device copy of copy_mib MiB whose FETCH_SIZE / WRITE_SIZE
+    calibrate the counters (a copy reads and writes exactly its size)."""
     smp, a = _prepare(torch, w)
     stream = torch.cuda.Stream()
     out = None
@@ -173,13 +217,13 @@ def source_hash():
     return h.hexdigest()
 
 
-def traffic_from_profile():
-    """HBM bytes per launch of the C3 step's kernel from the committed
-    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy of
-    known size), with the source hash the summary was measured on.  Returns
-    (bytes or None, summary hash or None): the caller reports the bytes only
-    when the hash is this build's."""
-    path = os.path.join(ROOT, "profiles", "row_kernel_c3_hbm_traffic.md")
+def traffic_from_profile(name="row_kernel_c3_hbm_traffic.md"):
+    """HBM bytes per launch (per step for a configuration summary) from a
+    committed rocprofv3 --pmc summary under profiles/ (FETCH_SIZE +
+    WRITE_SIZE, scaled by a copy of known size), with the source hash the
+    summary was measured on.  Returns (bytes or None, summary hash or None):
+    the caller reports the bytes only when the hash is this build's."""
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None, None
     traffic = tag = None
@@ -441,7 +485,26 @@ def cpu_baseline(w, budget_s=15.0):
         b = (b + 1) % B
     el = time.perf_counter() - t0
     return {"value": rows_done / el, "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": f"{rows_done} rows of {w.name} (oracle, 1 thread, serial rows), {el:.1f} s"}
+            "sample": f"{rows_done} rows of {w.name} (oracle, 1 thread, serial rows), {el:.1f} s",
+            **host_cpu()}
+
+
+def host_cpu():
+    """The host's CPU model and C library, for the CPU baselines' record
+    (the oracle's expf is the host glibc's)."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        libc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        libc = None
+    return {"cpu_model": model, "libc": libc}
 
 
 def host_cores():
@@ -470,7 +533,8 @@ def cpu_baseline_all_cores(w, budget_s=8.0):
         rows_done += w.batch
     el = time.perf_counter() - t0
     return {"value": rows_done / el, "unit": "rows/s", "cores": cores, "kind": "port",
-            "sample": f"{rows_done} rows of {w.name} (oracle, rows split over {cores} threads), {el:.1f} s"}
+            "sample": f"{rows_done} rows of {w.name} (oracle, rows split over {cores} threads), {el:.1f} s",
+            **host_cpu()}
 
 
 def main():
@@ -482,6 +546,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run C3 steps then a plain copy of known size, for rocprofv3 --pmc")
+    ap.add_argument("--pmc-config", type=int, choices=(1, 2, 3, 4, 5),
+                    help="the same probe with configuration N's steps")
     ap.add_argument("--lm-head-only", action="store_true",
                     help="time only the LM-head projection, fused and unfused (for rocprofv3)")
     args = ap.parse_args()
@@ -498,6 +564,10 @@ def main():
     if args.lm_head_only:
         print(json.dumps({"lm_head_fused": time_lm_head(torch),
                           "lm_head_fused_b64": time_lm_head(torch, B=64, rounds=3)}))
+        return
+    if args.pmc_config:
+        from hi_amd.workloads import CONFIGS
+        pmc_probe(torch, CONFIGS[args.pmc_config](), args.steps)
         return
     w3 = config3()
     if args.pmc_probe:
@@ -563,8 +633,9 @@ def main():
                      "algorithmic_bytes_per_launch": alg_bytes},
     }
     from hi_amd.workloads import config2, config4, config5
-    res["other_configs"] = {f"c{i}": time_config(torch, mk(), args.steps, args.warmup)
+    res["other_configs"] = {f"c{i}": time_config(torch, mk(), args.steps, args.warmup, i)
                             for i, mk in ((2, config2), (4, config4), (5, config5))}
+    res["passes"] = PASSES
     res["dsv4_indexer_select"] = time_indexer_select(torch, cpu=not args.no_cpu_baseline)
     res["moe_router"] = time_router(torch, cpu=not args.no_cpu_baseline)
     res["lm_head_fused"] = time_lm_head(torch)

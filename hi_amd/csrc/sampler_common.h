@@ -601,12 +601,15 @@ __device__ __forceinline__ void for_each_candidate(const SampleArgs& a, int row,
 // One compare-exchange step of a descending bitonic sort over element
 // indices i (this value) and i ^ j (the partner's value y / q), in stage k:
 // the lower index of a pair keeps the larger key when (i & k) == 0.
+// The exchange is a select under an all-ones / all-zero mask, with no
+// branch (a conditional exchange compiles to divergent branches per step).
+// Equal keys occur only for the zero padding, whose payloads are equal too.
 __device__ __forceinline__ void bitonic_keep(uint64_t& x, uint32_t& p, uint64_t y, uint32_t q, int i, int j, int k) {
-  const bool keep_max = ((i & k) == 0) == ((i & j) == 0);
-  if (keep_max ? (y > x) : (y < x)) {
-    x = y;
-    p = q;
-  }
+  const uint32_t keep_max = (((i & k) == 0) == ((i & j) == 0)) ? 1u : 0u;
+  const uint32_t gt = y > x ? 1u : 0u;
+  const uint64_t take = 0ull - (uint64_t)(1u ^ gt ^ keep_max);
+  x = (y & take) | (x & ~take);
+  p = (q & (uint32_t)take) | (p & ~(uint32_t)take);
 }
 
 // Descending sort of fs.buf[0..n) carrying fs.pay; n <= kBuf.

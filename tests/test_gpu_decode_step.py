@@ -159,10 +159,12 @@ def test_rng_uniforms_match_stdrng(hip):
         keys[b] = list(k)
         assert keys[b].tolist() == D.stdrng_key_from_seed(s)
     rngs = [D.StdRng(keys[b]) for b in range(B)]
+    raw = [D.StdRng(keys[b]) for b in range(B)]  # the keystream words themselves
     dk = _t(torch, keys.reshape(-1))
     used = torch.zeros(B, dtype=torch.int64, device="cuda")
     used[3] = (1 << 32) * 16 - 2  # crosses the low counter word within the run
     rngs[3] = D.StdRng(keys[3], words_used=(1 << 32) * 16 - 2)
+    raw[3] = D.StdRng(keys[3], words_used=(1 << 32) * 16 - 2)
     ds = torch.from_numpy(sampled).to("cuda")
     out = torch.zeros(B, dtype=torch.float32, device="cuda")
     stream = torch.cuda.Stream()
@@ -174,6 +176,13 @@ def test_rng_uniforms_match_stdrng(hip):
         got = out.cpu().numpy()
         want = np.array([rngs[b].uniform_f32() if sampled[b] else 0.0 for b in range(B)], np.float32)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (step, got, want)
+        # the closed form of gen_range(0.0f32..1.0f32) on the device's values:
+        # u * 2^23 is the integer (w >> 9) of the next keystream word w (the
+        # ChaCha12 core is pinned by RFC 8439's vectors), so 0 <= u < 1
+        for b in range(B):
+            if sampled[b]:
+                w = raw[b].next_u32()
+                assert float(got[b]) * float(1 << 23) == float(w >> 9) and 0.0 <= got[b] < 1.0, (step, b)
     u = used.cpu().numpy()
     assert u[1] == 0 and u[0] == 40 and u[3] == (1 << 32) * 16 - 2 + 40
 

@@ -493,7 +493,7 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     }
   }
   sort_ranked(fs, k);
-  const int pick = wave_draw<kLmMaxK / 64>(fs.buf, k, cfg);
+  const int pick = wg_draw<kLmMaxK / 64>(fs, fs.buf, k, cfg);
   if (tid == 0) a.out_tokens[row] = pick < 0 ? host_argmax : cand_idx(fs.buf[pick]);
 }
 

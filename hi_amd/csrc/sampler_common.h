@@ -574,6 +574,7 @@ struct FinLds {
   uint64_t below;   // largest candidate left out of the selection
   uint32_t wmin;    // bits of the smallest selected weight
   uint64_t thr;     // the selection threshold of a one-wave select
+  int pick;         // wg_draw's result
 };
 constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
 
@@ -1491,30 +1492,6 @@ __device__ __forceinline__ uint64_t wave_select_skip(const uint64_t* items, int 
 constexpr int kLeanChunks = 256;  // chunks per row the lean finish merges
 constexpr int kSpecChunks = 40;   // rows of up to this many chunks load their candidates early
 
-// wave_fold_f32 that stops once a lane at or below the last final one has
-// hit set and p >= cutoff; returns the first such lane (-1: none, all n
-// lanes final).  Lanes past the returned one may hold partial sums.
-__device__ __forceinline__ float wave_fold_f32_until(float v, float start, int n, bool hit, float cutoff,
-                                                     int& first) {
-  const int lane = (int)(threadIdx.x & 63u);
-  const float u = lane == 0 ? start + v : v;
-  float p = u;
-  first = -1;
-  #pragma unroll 1
-  for (int s = 0;; s += 8) {
-    // lanes [0, s] are final
-    const uint64_t m = __ballot(hit && lane <= s && p >= cutoff);
-    if (m != 0ull) {
-      first = __ffsll((unsigned long long)m) - 1;
-      break;
-    }
-    if (s >= n - 1) break;
-    #pragma unroll
-    for (int i = 0; i < 8; ++i) p = wave_fold_u(p) + u;
-  }
-  return p;
-}
-
 // Reference steps 7-10 (gpu.rs:831-899) over the rank order held in
 // registers: entry m * 64 + lane of the rank keys sits in lane `lane` of
 // kr[m], entries [0, k) are the kept ones (k <= 64 * DM).  Returns the
@@ -1558,7 +1535,9 @@ __device__ __forceinline__ int wave_draw_r(const uint64_t (&kr)[DM], int k, cons
   const float total = P;
   if (!(total > 0.f) || !finitef_(total)) return -1;  // argmax_host fallback
   // the nucleus: cum_p over w / total of the positive entries (gpu.rs:843-856),
-  // folded only as far as the first one that reaches the cutoff
+  // folded slot by slot as far as the slot where it reaches the cutoff (a
+  // check per slot, not per step: each check is a round trip through the
+  // scalar unit)
   int cut = -1;  // first positive entry where cum_p reaches the cutoff
   if (cfg.cutoff < 1.f) {
     float Q = 0.f;
@@ -1568,9 +1547,9 @@ __device__ __forceinline__ int wave_draw_r(const uint64_t (&kr)[DM], int k, cons
         const int i = m * 64 + (int)lane;
         const bool pos = i < kp;
         const float fb = pos ? fa[m] / total : 0.f;
-        int first;
-        const float q = wave_fold_f32_until(fb, Q, min(64, kp - m * 64), pos, cfg.cutoff, first);
-        if (first >= 0) cut = m * 64 + first;
+        const float q = wave_fold_f32(fb, Q, min(64, kp - m * 64));
+        const uint64_t hm = __ballot(pos && q >= cfg.cutoff);
+        if (hm != 0ull) cut = m * 64 + __ffsll((unsigned long long)hm) - 1;
         else Q = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(q), min(63, kp - 1 - m * 64)));
       }
     }
@@ -1678,11 +1657,24 @@ __device__ __forceinline__ void wave_sort_desc(uint64_t (&x)[S]) {
   }
 }
 
+// wave_draw by wave 0 alone, the pick handed to every thread: the folds are
+// serial chains, and copies of them in the other waves would only take
+// issue slots from wave 0 on the shared SIMDs.  Ends with a barrier.
+template <int DM>
+__device__ __forceinline__ int wg_draw(FinLds& fs, const uint64_t* keys, int k, const RowCfg& cfg) {
+  if (threadIdx.x < 64u) {
+    const int pick = wave_draw<DM>(keys, k, cfg);
+    if (threadIdx.x == 0u) fs.pick = pick;
+  }
+  __syncthreads();
+  return fs.pick;
+}
+
 // Reference steps 7-10 (gpu.rs:831-899) over the first k <= kBuf entries of
 // the rank order in fs.buf (top-k rows).  Returns the token, or 0xffffffff
 // for "fall back to argmax_host".
 __device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int k) {
-  const int pick = wave_draw<kBuf / 64>(fs.buf, k, cfg);
+  const int pick = wg_draw<kBuf / 64>(fs, fs.buf, k, cfg);
   return pick < 0 ? 0xffffffffu : cand_idx(fs.buf[pick]);
 }
 
@@ -1817,8 +1809,8 @@ __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int
   }
   __syncthreads();
 
-  // 8. the draw, by every wave from registers (gpu.rs:831-899)
-  const int pick = wave_draw<kLeanK / 64>(fs.cbig, min(cfg.k_eff, kk), cfg);
+  // 8. the draw (gpu.rs:831-899)
+  const int pick = wg_draw<kLeanK / 64>(fs, fs.cbig, min(cfg.k_eff, kk), cfg);
   if (pick < 0) return false;  // argmax_host fallback
   const uint32_t token = cand_idx(fs.cbig[pick]);
   if (tid == 0) a.out_tokens[row] = token;

@@ -28,8 +28,10 @@ __device__ __forceinline__ uint32_t dpp32(uint32_t old, uint32_t v) {
 // sums moved one lane up (wave_shr:1 filling lane 0 with zero, which the
 // compiler fuses into the add).  After step s lanes [0, s] hold their
 // final sums and later steps leave them unchanged, so steps run in groups
-// of 8 (n - 1 steps are needed).  No lane's sum is -0 (the terms and
-// `start` are not negative), so 0 + x == x at lane 0.
+// of 32 (n - 1 steps are needed): a taken branch per group costs about as
+// much as five steps, so short groups cost more than the few extra steps.
+// No lane's sum is -0 (the terms and `start` are not negative), so
+// 0 + x == x at lane 0.
 __device__ __forceinline__ float wave_fold_u(float u) {
   return __uint_as_float(dpp32<0x138, 0xf, true>(0u, __float_as_uint(u)));
 }
@@ -37,9 +39,9 @@ __device__ __forceinline__ float wave_fold_f32(float v, float start, int n) {
   const float u = (threadIdx.x & 63u) == 0u ? start + v : v;
   float p = u;
   #pragma unroll 1
-  for (int s = 1; s < n; s += 8) {
+  for (int s = 1; s < n; s += 32) {
     #pragma unroll
-    for (int i = 0; i < 8; ++i) p = wave_fold_u(p) + u;
+    for (int i = 0; i < 32; ++i) p = wave_fold_u(p) + u;
   }
   return p;
 }

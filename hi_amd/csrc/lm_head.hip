@@ -1,6 +1,6 @@
 // hi-rocm: the LM-head projection + bias + softcap, alone (the twin) or fused
 // into the sampler's first pass, and their launchers.
-#include "sampler_common.h"
+#include "sampler_wide.h"
 
 namespace hi_rocm {
 
@@ -16,9 +16,11 @@ namespace hi_rocm {
 // bias, apply the softcap (softcap.h), and keep the tile's processed logits
 // in LDS.  The fused kernel then records, per (row, tile), what the finish
 // needs -- the maximum, both argmaxes and the largest candidate key -- and
-// leaves the tile's logits in the workspace only for top-k rows, whose
-// finish reads back the few tiles that can hold the row's top k (greedy
-// rows write no logits at all).  The twin kernel runs the same code and
+// leaves the tile's logits in the workspace for every row that is not
+// greedy: a top-k row's finish reads back the few tiles that can hold the
+// row's top k, and the rows it cannot resolve (other classes, a cut between
+// distinct logits of equal weight) take the general per-row path over the
+// whole row (greedy rows write no logits at all).  The twin kernel runs the same code and
 // writes every logit instead: the fused path's logits are bit-identical to
 // the twin's by construction (same tiles, same MFMA order, same epilogue).
 //
@@ -232,9 +234,9 @@ __device__ __forceinline__ bool lm_row_ok(const RowCfg& c) {
 __device__ __forceinline__ uint64_t ieee_key(float l, uint32_t e) { return cand_key(okey(l == 0.f ? 0.f : l), e); }
 
 // The fused pass: per (row, tile) records.  Wave w takes the rows w,
-// w + kLmThreads / 64, ... of the tile.  A top-k row also leaves the tile's
-// logits in the workspace, where the finish reads the few tiles that can
-// hold the row's top k (greedy rows leave nothing but the records).
+// w + kLmThreads / 64, ... of the tile.  Every row but a greedy one also
+// leaves the tile's logits in the workspace (greedy rows leave nothing but
+// the records).
 template <int RG>
 __global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(lm_waves_per_eu<RG>(), 8)))
     lm_select_kernel(LmArgs a) {
@@ -242,19 +244,18 @@ __global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu
   float* tile = reinterpret_cast<float*>(lds_raw);
   const int t = blockIdx.x, tile0 = t * kLmTile;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  // lane m holds row m's k (0: greedy or not taken), loaded before the
-  // product so that its latency hides there
-  uint32_t my_k = 0u;
+  // lane m: whether row m keeps its tile logits (every class but greedy),
+  // loaded before the product so that its latency hides there
+  uint32_t keep = 0u;
   if (lane < a.B) {
     const RowCfg cfg = load_cfg(a.pv, lane, a.V, 0, 0);
-    my_k = (cfg.cls == kTopK && cfg.k_eff <= kLmMaxK) ? (uint32_t)cfg.k_eff : 0u;
+    keep = cfg.cls != kGreedy ? 1u : 0u;
   }
   lm_gemm_tile<RG>(a, tile0, tile);
   __syncthreads();
   const int len = min(kLmTile, a.V - tile0);
   constexpr int PER = kLmTile / 64;
   for (int m = wid; m < a.B; m += kLmThreads / 64) {
-    const uint32_t k = (uint32_t)__builtin_amdgcn_readlane((int)my_k, m);
     const float* row = tile + m * kLmTile;
     // the largest candidate key; values that are not finite or are -0 take
     // the exact record path below
@@ -310,27 +311,53 @@ __global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu
     rec.top = top;
     if (lane == 0) a.lm_recs[(int64_t)m * a.n_chunks + t] = rec;
   }
-  // the tile logits of top-k rows, row after row as the twin writes them
-  // (a wave covers half a row, so the row's k is uniform over the wave)
+  // the tile logits of the rows that keep them, row after row as the twin
+  // writes them (a wave covers half a row, so the flag is uniform over it)
   for (int i = threadIdx.x; i < a.B * kLmTile; i += kLmThreads) {
     const int m = i / kLmTile, c = i % kLmTile;
-    const uint32_t k = (uint32_t)__builtin_amdgcn_readlane((int)my_k, m);
-    if (k > 0u && c < len) a.lm_logits[(int64_t)m * a.V + tile0 + c] = tile[i];
+    const uint32_t k = (uint32_t)__builtin_amdgcn_readlane((int)keep, m);
+    if (k != 0u && c < len) a.lm_logits[(int64_t)m * lm_stride(a.V) + tile0 + c] = tile[i];
   }
 }
 
+typedef const __attribute__((address_space(4))) SampleArgs KernargSampleArgs;
+typedef const __attribute__((address_space(4))) char KernargByte;
+
+// The general per-row path (general_row_path) over the row's logits in the
+// workspace, for the rows the fused finish does not resolve.  Not inlined,
+// so that its register demand stays out of the fused finish; `ap` points at
+// the kernel's own LmArgs::gen in the argument segment (a pointer to a local
+// copy would make every workgroup store that copy to scratch on entry).
+__device__ __noinline__ void lm_general(KernargSampleArgs* ap, int row) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  SampleArgs a;
+  {
+    static_assert(sizeof(SampleArgs) % 8 == 0, "copied 8 bytes at a time");
+    typedef const __attribute__((address_space(4))) uint64_t KernargWord;
+    KernargWord* w = (KernargWord*)ap;
+    uint64_t* d = reinterpret_cast<uint64_t*>(&a);
+    #pragma unroll
+    for (int i = 0; i < (int)(sizeof(SampleArgs) / 8); ++i) d[i] = w[i];
+  }
+  general_row_path<false>(a, row, lds_raw);
+}
+
+__device__ __forceinline__ KernargSampleArgs* lm_gen_args() {
+  return (KernargSampleArgs*)((KernargByte*)__builtin_amdgcn_kernarg_segment_ptr() + offsetof(LmArgs, gen));
+}
+
 // The fused finish: one workgroup per row (gpu.rs:753-900 on the row's
-// candidates, as the lean finish does).  out_tokens[row] = 0xffffffff for a
-// row the fused path does not take (its class), 0xfffffffe for a tie it
-// cannot resolve without the logits: the caller samples such a row from the
-// twin's logits.
+// candidates, as the lean finish does).  Rows of other classes, and top-k
+// rows whose cut falls between distinct logits of equal weight, take the
+// general per-row path over the row's logits in the workspace: every row
+// gets its token.
 __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
   const int row = blockIdx.x, tid = threadIdx.x;
   const RowCfg cfg = load_cfg(a.pv, row, a.V, 0, 0);
   if (!lm_row_ok(cfg)) {
-    if (tid == 0) a.out_tokens[row] = 0xffffffffu;
+    lm_general(lm_gen_args(), row);
     return;
   }
   // merge the tile records
@@ -403,7 +430,7 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
   __syncthreads();
   if (tid == 0) fs.counter = 0u;
   __syncthreads();
-  const float* lg = a.lm_logits + (int64_t)row * a.V;
+  const float* lg = a.lm_logits + (int64_t)row * lm_stride(a.V);
   const int n_items = n_list * kLmTile;
   // item i: column i % kLmTile of listed tile i / kLmTile (0 past the
   // vocabulary: below every key)
@@ -488,7 +515,8 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
     __syncthreads();
     const bool lone = xk == S && fs.flag == 0u && !(exact_expf(key_to_s(S - 1u, cfg.t_eff) - M) == w_b);
     if (!lone) {
-      if (tid == 0) a.out_tokens[row] = 0xfffffffeu;
+      __syncthreads();
+      lm_general(lm_gen_args(), row);
       return;
     }
   }
@@ -498,13 +526,18 @@ __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
 }
 
 size_t lm_recs_bytes(int B, int n_tiles) { return ((size_t)B * n_tiles * sizeof(LmTileRec) + 255) & ~(size_t)255; }
+size_t lm_logits_bytes(int B, int V) { return ((size_t)B * lm_stride(V) * sizeof(float) + 255) & ~(size_t)255; }
 size_t lm_workspace_bytes(int B, int V) {
   const int tiles = (V + kLmTile - 1) / kLmTile;
-  return lm_recs_bytes(B, tiles) + (size_t)B * V * sizeof(float);
+  return lm_recs_bytes(B, tiles) + lm_logits_bytes(B, V) + general_layout(B, V).total;
 }
 
 size_t lm_tile_lds(int B) { return (size_t)(B <= 32 ? 32 : kLmRows) * kLmTile * sizeof(float); }
-size_t lm_finish_lds() { return (sizeof(FinLds) + 15) & ~(size_t)15; }
+size_t lm_finish_lds() {
+  const size_t gen = kSelHead;  // general_row_path without a history table
+  const size_t b = sizeof(FinLds) > gen ? sizeof(FinLds) : gen;
+  return (b + 15) & ~(size_t)15;
+}
 
 template <int RG>
 hipError_t launch_lm_logits_rg(const LmArgs& a, hipStream_t stream) {

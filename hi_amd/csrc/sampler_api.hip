@@ -594,6 +594,14 @@ int hi_rocm_sample_lm_head(const void* hidden, const void* weight, const float* 
   a.lm_recs = (hi_rocm::LmTileRec*)workspace;
   a.lm_logits = (float*)((char*)workspace + recs);
   a.out_tokens = out_tokens;
+  // the general per-row path over the workspace's logits, for the rows the
+  // fused finish leaves (no history, mask or logprobs: the entry point takes
+  // none)
+  a.gen = base_args(a.lm_logits, HI_ROCM_DTYPE_F32, batch, vocab, hi_rocm::lm_stride(vocab));
+  a.gen.pv = a.pv;
+  a.gen.out_tokens = out_tokens;
+  carve(a.gen, (char*)workspace + recs + hi_rocm::lm_logits_bytes(batch, vocab),
+        hi_rocm::general_layout(batch, vocab));
   const hipError_t e = hi_rocm::launch_lm_sample(a, (hipStream_t)stream);
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "lm head sample launch");
 }

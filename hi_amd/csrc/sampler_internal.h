@@ -188,22 +188,11 @@ inline int64_t next_pow2_i64(int64_t x) {
   return p;
 }
 
-// Workspace for any call with up to max_batch rows of V logits.
-inline WorkspaceLayout workspace_layout(int max_batch, int V) {
+// The layout with `slots` (row, chunk) records for up to max_batch rows.
+inline WorkspaceLayout workspace_layout_slots(int max_batch, int V, int64_t slots) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   WorkspaceLayout L;
-  L.slots = 0;
-  for (int b = 1; b <= max_batch; ++b) {
-    // records of either pass (streaming select or general scan) at b rows
-    for (int n_lp : {0, kLeanK + 1}) {
-      const int ch = choose_chunk(b, V, n_lp, 1, true);
-      const int64_t s = (int64_t)b * ((V + ch - 1) / ch);
-      if (s > L.slots) L.slots = s;
-    }
-    // the row kernel's general path (8192-logit chunks)
-    const int64_t sg = (int64_t)b * ((V + kRowGeneralChunk - 1) / kRowGeneralChunk);
-    if (sg > L.slots) L.slots = sg;
-  }
+  L.slots = slots;
   L.list_stride = next_pow2_i64(V);
   size_t off = 0;
   // the fused path's per-row counters first, at the same place in every
@@ -221,6 +210,28 @@ inline WorkspaceLayout workspace_layout(int max_batch, int V) {
   L.ws_list = off; off = align(off + (size_t)max_batch * L.list_stride * sizeof(uint64_t));
   L.total = off;
   return L;
+}
+
+// Workspace for any call with up to max_batch rows of V logits.
+inline WorkspaceLayout workspace_layout(int max_batch, int V) {
+  int64_t slots = 0;
+  for (int b = 1; b <= max_batch; ++b) {
+    // records of either pass (streaming select or general scan) at b rows
+    for (int n_lp : {0, kLeanK + 1}) {
+      const int ch = choose_chunk(b, V, n_lp, 1, true);
+      const int64_t s = (int64_t)b * ((V + ch - 1) / ch);
+      if (s > slots) slots = s;
+    }
+    // the row kernel's general path (8192-logit chunks)
+    const int64_t sg = (int64_t)b * ((V + kRowGeneralChunk - 1) / kRowGeneralChunk);
+    if (sg > slots) slots = sg;
+  }
+  return workspace_layout_slots(max_batch, V, slots);
+}
+
+// Workspace of general_row_path alone for up to max_batch rows.
+inline WorkspaceLayout general_layout(int max_batch, int V) {
+  return workspace_layout_slots(max_batch, V, (int64_t)max_batch * ((V + kRowGeneralChunk - 1) / kRowGeneralChunk));
 }
 
 // Measurement hook: when given, the launcher records ev[0] before its first
@@ -264,13 +275,17 @@ struct LmArgs {
   float* out_logits;      // the twin: [B][V]
   ParamsView pv;
   LmTileRec* lm_recs;     // [B][n_chunks]
-  float* lm_logits;       // [B][V]: the tiles of top-k rows
+  float* lm_logits;       // [B][lm_stride(V)]: the tiles of every row but greedy ones
   uint32_t* out_tokens;   // [B]
+  SampleArgs gen;         // general_row_path over lm_logits, for the rows the fused finish leaves
 };
+// Rows of lm_logits start on 16 bytes (the general path's 16-byte loads).
+__host__ __device__ inline int64_t lm_stride(int V) { return ((int64_t)V + 3) & ~(int64_t)3; }
 hipError_t launch_lm_logits(const LmArgs& a, hipStream_t stream);
 hipError_t launch_lm_sample(const LmArgs& a, hipStream_t stream);
 size_t lm_workspace_bytes(int B, int V);
 size_t lm_recs_bytes(int B, int n_tiles);
+size_t lm_logits_bytes(int B, int V);
 
 // Exact top-k block selection of the DSV4 indexer (index_select.hip).
 hipError_t launch_index_select(const float* scores, int n, int top_k, uint8_t* marks, int32_t* sel,

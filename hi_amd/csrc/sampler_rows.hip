@@ -903,18 +903,7 @@ __device__ __noinline__ void row_general(KernargSampleArgs* ap, int row) {
   // registers of 16384-logit ones, which halves the path's spills (its
   // scratch is allocated for every wave of the launch, and costs the
   // launch time even when no row comes here)
-  a.chunk = kRowGeneralChunk;
-  a.n_chunks = (a.V + kRowGeneralChunk - 1) / kRowGeneralChunk;
-  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
-  for (int c = 0; c < a.n_chunks; ++c) {
-    select_chunk<HI_ROCM_DTYPE_F32, kRowGeneralChunk / NT / 4, MASK>(a, row, c, lds_raw);
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) a.diag[row] = kRowPathGeneral;
-  FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
-  if (finish_lean(fs, a, row, cfg)) return;
-  __syncthreads();
-  finish_row(fs, a, row, cfg);
+  general_row_path<MASK>(a, row, lds_raw);
 }
 
 // The row kernel's arguments as its argument segment lays them out: each at

@@ -776,7 +776,26 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   return F.tok;
 }
 
-// The second kernel of the chunked path: one workgroup per (row, chunk),
-// on a 1-D grid whose first B workgroups are chunk 0 of rows 0 .. B-1 and
+// A whole row by one workgroup of NT threads, any row class: the select
+// pass over kRowGeneralChunk-logit chunks in turn, then the chunked path's
+// finish (finish_lean, else finish_row).  The workspace must hold the
+// records of ceil(V / kRowGeneralChunk) chunks per row (general_layout);
+// lds_raw must hold SelLds (plus the history table when a.hoff is given)
+// and FinLds.
+template <bool MASK>
+__device__ __forceinline__ void general_row_path(SampleArgs& a, int row, unsigned char* lds_raw) {
+  a.chunk = kRowGeneralChunk;
+  a.n_chunks = (a.V + kRowGeneralChunk - 1) / kRowGeneralChunk;
+  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
+  for (int c = 0; c < a.n_chunks; ++c) {
+    select_chunk<HI_ROCM_DTYPE_F32, kRowGeneralChunk / NT / 4, MASK>(a, row, c, lds_raw);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) a.diag[row] = kRowPathGeneral;
+  FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
+  if (finish_lean(fs, a, row, cfg)) return;
+  __syncthreads();
+  finish_row(fs, a, row, cfg);
+}
 
 }  // namespace hi_rocm

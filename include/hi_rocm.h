@@ -136,13 +136,15 @@ int hi_rocm_launch_moe_topk_router(const void* scores, void* output_ids, void* o
  *           vocab <= 524288 (status 2 otherwise).
  * hi_rocm_lm_head_logits writes the logits f32[batch][vocab] (the unfused
  * twin).  hi_rocm_sample_lm_head samples from the same logits (bit for bit)
- * without a full logits pass: per-row params as hi_rocm_sample (greedy, or
- * top-k <= 64 with temperature / top-p / min-p; no penalties, mask or
- * logprobs) and one uniform per row; out_tokens[b] = 0xffffffff for a row of
- * another class and 0xfffffffe for a row whose cut falls between distinct
- * logits of equal weight (rare): sample those rows with hi_rocm_sample on
- * the twin's logits.  Workspace (device, hi_rocm_lm_head_workspace_bytes):
- * per-tile records and the tile logits of top-k rows. */
+ * and returns a token for every row: per-row params as hi_rocm_sample (any
+ * class; no penalties, mask or logprobs) and one uniform per row.  Greedy
+ * rows and top-k <= 64 rows (with temperature / top-p / min-p) finish from
+ * per-tile records and the few tiles that can hold the top k; rows of other
+ * classes, and the rare top-k row whose cut falls between distinct logits of
+ * equal weight, take the general per-row path over the row's logits in the
+ * workspace.  Workspace (device, hi_rocm_lm_head_workspace_bytes): per-tile
+ * records, the logits of every row that is not greedy, and the general
+ * path's per-row buffers. */
 int hi_rocm_lm_head_workspace_bytes(int batch, int vocab, size_t* out_bytes);
 int hi_rocm_lm_head_logits(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
                            int hidden_dim, int vocab, float* out_logits, void* stream);

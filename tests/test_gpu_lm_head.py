@@ -7,9 +7,10 @@ gpu.rs:23232-23249 + the sampler).
   operand layout and the epilogue (tolerance: f32 accumulation, 1e-5 of
   the magnitude sum, and the softcap's tanh to 2e-6).
 * The fused tokens against the sampler oracle run on the twin's logits,
-  row by row, bit-exact (the fused pass computes the same logits by
-  construction and never writes them); rows of classes the fused finish
-  does not take report 0xffffffff.
+  row by row, bit-exact, for every row: greedy and top-k <= 64 rows in the
+  fused finish, rows of other classes (top-p only, temperature only,
+  top-k above 64) and cuts between distinct logits of equal weight through
+  the general per-row path over the workspace's copy of the row.
 """
 import ctypes
 
@@ -85,8 +86,12 @@ def test_fused_tokens_match_oracle_on_twin_logits(hip, oracle, B, H, V, cap, see
     params["top_k"] = rng.choice(np.array([1, 5, 20, 40, 64], np.int32), B)
     params["min_p"] = np.where(rng.random(B) < 0.3, F32(0.05), F32(0.0))
     params["temperature"][:4] = 0.0           # greedy
-    params["top_k"][4] = 0                     # top-p only: not taken by the fused finish
+    # rows the fused finish does not take: the general per-row path
+    params["top_k"][4] = 0                     # top-p only
     params["top_p"][4] = 0.9
+    params["top_k"][5], params["top_p"][5], params["min_p"][5] = 0, 1.0, 0.0  # temperature only
+    params["top_k"][6] = 100                   # top-k above the fused finish's 64
+    params["top_k"][7], params["top_p"][7] = 300, 0.8
     u = rng.random(B).astype(F32)
     want = oracle.sample_rows(logits, params, u)["tokens"]
     ws_n = ctypes.c_size_t()
@@ -104,10 +109,7 @@ def test_fused_tokens_match_oracle_on_twin_logits(hip, oracle, B, H, V, cap, see
         s.synchronize()
         got = out.cpu().numpy().view(np.uint32)
         print(f"lm head fused rep {rep}: {got[:8].tolist()}", flush=True)
-        assert got[4] == 0xFFFFFFFF
-        ok = np.arange(B) != 4
-        assert not (got[ok] == 0xFFFFFFFE).any(), "unresolved tie rows"
-        assert np.array_equal(got[ok], want[ok]), (np.flatnonzero(got[ok] != want[ok])[:8])
+        assert np.array_equal(got, want), (np.flatnonzero(got != want)[:8])
 
 
 def test_fused_duplicate_vocabulary_rows(hip, oracle):
@@ -116,8 +118,8 @@ def test_fused_duplicate_vocabulary_rows(hip, oracle):
     exact one-wave select), and top-k cuts inside a run of equal logits (the
     finish resolves them by index, as the reference's (weight, index) rank
     does).  A cut whose next lower logit key weighs the same (small |l/T|,
-    or T > 1) may report 0xfffffffe; every token reported is the oracle's,
-    and most rows resolve."""
+    or T > 1) goes through the general per-row path: every row gets the
+    oracle's token."""
     import torch
     from hi_amd import sampler as S
     from hi_amd._lib import ROW_PARAMS_DTYPE
@@ -151,9 +153,7 @@ def test_fused_duplicate_vocabulary_rows(hip, oracle):
     s.synchronize()
     got = out.cpu().numpy().view(np.uint32)
     print(f"got {got.tolist()}\nwant {want.tolist()}", flush=True)
-    resolved = got != 0xFFFFFFFE
-    assert np.array_equal(got[resolved], want[resolved])
-    assert resolved.sum() >= 8, got
+    assert np.array_equal(got, want), np.flatnonzero(got != want)
 
 
 def test_fused_clustered_tiles(hip, oracle):

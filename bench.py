@@ -292,8 +292,10 @@ def time_indexer_select(torch, shapes=((1162, 512), (65536, 2048)), launches=200
     """DSV4 indexer block selection (hi_rocm_launch_dsv4_indexer_select):
     us per launch over back-to-back launches on one stream, bracketed by HIP
     events on that stream.  Algorithmic bytes per launch: n scores f32 read,
-    n marks u8 and min(k, n) int32 indices written.  One workgroup per
-    launch, so the bound is latency, not HBM.  CPU baseline: the host
+    n marks u8 and min(k, n) int32 indices written.  One workgroup up to
+    8192 scores, else one per 4096 scores in three kernels: the bound is
+    latency (kernel launches and dependent global round trips), not HBM.
+    CPU baseline: the host
     selection the reference's CPU path runs, on the same scores."""
     import ctypes
     from hi_amd import _lib

@@ -70,19 +70,30 @@ struct DeviceWorkspace {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
+// Buffers of a (device, stream): the sampler's, and the DSV4 indexer's
+// (a few KB per 4096 scores; its histogram kept at zero between calls).
+enum WsKind { kWsSampler = 0, kWsIndexer = 1 };
 std::mutex g_ws_mutex;
-std::map<std::pair<int, uintptr_t>, DeviceWorkspace> g_ws;
+std::map<std::tuple<int, uintptr_t, int>, DeviceWorkspace> g_ws;
 
-int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
+// The stream's buffer of `kind`, at least `bytes`, with its first
+// zero_words words zero after a growth.  When it would grow during capture:
+// an error, or with `optional` success and *out = nullptr (the caller takes
+// a path without it).
+int stream_buffer(int kind, size_t bytes, int zero_words, bool optional, hipStream_t stream, void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  DeviceWorkspace& ws = g_ws[{dev, (uintptr_t)stream}];
+  DeviceWorkspace& ws = g_ws[std::make_tuple(dev, (uintptr_t)stream, kind)];
   if (ws.bytes < bytes) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     e = hipStreamIsCapturing(stream, &cs);
     if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone && optional) {
+      *out = nullptr;
+      return HI_ROCM_OK;
+    }
     if (cs != hipStreamCaptureStatusNone)
       return fail(HI_ROCM_ERR_UNSUPPORTED,
                   "hi-rocm: the stream's sampler workspace would grow to " + std::to_string(bytes) +
@@ -98,12 +109,16 @@ int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
     }
     e = hipMalloc(&ws.ptr, bytes);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(sampler workspace)");
-    e = zero_counters(ws.ptr, hi_rocm::kDoneRows, stream);
+    e = zero_counters(ws.ptr, zero_words, stream);
     if (e != hipSuccess) return hip_fail(e, "sampler workspace counter reset");
     ws.bytes = bytes;
   }
   *out = ws.ptr;
   return HI_ROCM_OK;
+}
+
+int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
+  return stream_buffer(kWsSampler, bytes, hi_rocm::kDoneRows, false, stream, out);
 }
 
 // Frees the calling device's workspace of `stream` after the stream's work.
@@ -112,8 +127,9 @@ int release_workspace(hipStream_t stream) {
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  auto it = g_ws.find({dev, (uintptr_t)stream});
-  if (it == g_ws.end()) return HI_ROCM_OK;
+  auto it0 = g_ws.find(std::make_tuple(dev, (uintptr_t)stream, (int)kWsSampler));
+  auto it1 = g_ws.find(std::make_tuple(dev, (uintptr_t)stream, (int)kWsIndexer));
+  if (it0 == g_ws.end() && it1 == g_ws.end()) return HI_ROCM_OK;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   e = hipStreamIsCapturing(stream, &cs);
   if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
@@ -121,11 +137,14 @@ int release_workspace(hipStream_t stream) {
     return fail(HI_ROCM_ERR_UNSUPPORTED, "hi_rocm_sampler_release: the stream is being captured");
   e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-  if (it->second.ptr) {
-    e = hipFree(it->second.ptr);
-    if (e != hipSuccess) return hip_fail(e, "hipFree");
+  for (auto it : {it0, it1}) {
+    if (it == g_ws.end()) continue;
+    if (it->second.ptr) {
+      e = hipFree(it->second.ptr);
+      if (e != hipSuccess) return hip_fail(e, "hipFree");
+    }
+    g_ws.erase(it);
   }
-  g_ws.erase(it);
   return HI_ROCM_OK;
 }
 
@@ -513,9 +532,19 @@ int hi_rocm_launch_dsv4_indexer_select(const void* scores, int n_blocks, int top
   // the kernels' span and loop arithmetic is in int: keep it clear of overflow
   if (n_blocks > INT32_MAX - (1 << 20))
     return fail(HI_ROCM_ERR_UNSUPPORTED, "hi_rocm_launch_dsv4_indexer_select: n_blocks above 2^31 - 2^20");
-  hipError_t e = hi_rocm::launch_index_select((const float*)scores, n_blocks, top_k,
-                                              (uint8_t*)marks, (int32_t*)sel_out,
-                                              (hipStream_t)stream);
+  // above kMultiMinN scores: a workgroup per 4096 of them, with a small
+  // per-stream buffer (one workgroup when that buffer would have to be
+  // allocated during stream capture)
+  const size_t wsb = hi_rocm::index_select_ws_bytes(n_blocks);
+  void* ws = nullptr;
+  if (wsb > 0) {
+    const int rc = stream_buffer(kWsIndexer, wsb, (int)(hi_rocm::kIndexHistBytes / 4), true, (hipStream_t)stream, &ws);
+    if (rc != HI_ROCM_OK) return rc;
+  }
+  hipError_t e = ws ? hi_rocm::launch_index_select_multi((const float*)scores, n_blocks, top_k, (uint8_t*)marks,
+                                                         (int32_t*)sel_out, ws, (hipStream_t)stream)
+                    : hi_rocm::launch_index_select((const float*)scores, n_blocks, top_k, (uint8_t*)marks,
+                                                   (int32_t*)sel_out, (hipStream_t)stream);
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "indexer select launch");
 }
 

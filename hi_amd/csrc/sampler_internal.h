@@ -287,8 +287,17 @@ size_t lm_workspace_bytes(int B, int V);
 size_t lm_recs_bytes(int B, int n_tiles);
 size_t lm_logits_bytes(int B, int V);
 
-// Exact top-k block selection of the DSV4 indexer (index_select.hip).
+// Exact top-k block selection of the DSV4 indexer (index_select.hip): one
+// workgroup (no workspace), or for kMultiMinN < n <= 4096 * 1024 a
+// workgroup per 4096 scores in three kernels, with a workspace of
+// index_select_ws_bytes(n) whose first kIndexHistBytes are zero between
+// calls.
+constexpr int kMultiMinN = 8192;
+constexpr size_t kIndexHistBytes = 4096 * sizeof(uint32_t);
 hipError_t launch_index_select(const float* scores, int n, int top_k, uint8_t* marks, int32_t* sel,
                                hipStream_t stream);
+size_t index_select_ws_bytes(int n);
+hipError_t launch_index_select_multi(const float* scores, int n, int top_k, uint8_t* marks, int32_t* sel,
+                                     void* ws, hipStream_t stream);
 
 }  // namespace hi_rocm

@@ -4,8 +4,9 @@ oracle on the same scores.  Index and mark output must be bit-exact.
 
 Cases: the reference test's own shapes and tie-heavy scores
 (crates/hi-cuda/src/dsv4_gpu.rs:7277-7312), total_cmp special values, all
-scores equal, k >= n, n = 1, and large n (up to 2^18 + 1 with k = 2048),
-with output buffers pre-filled so that a missed or stray write shows."""
+scores equal, k >= n, n = 1, and large n (up to 2^22 with k = 2048) on
+both the one-workgroup and the many-workgroup kernels, with output buffers
+pre-filled so that a missed or stray write shows."""
 import ctypes
 import sys
 
@@ -151,3 +152,48 @@ def test_unaligned_buffers(env):
         assert np.array_equal(d_sel.cpu().numpy(), want_sel)
         m = marks_big.cpu().numpy()
         assert m[0] == 0xAB and np.array_equal(m[1:], want_marks)
+
+
+def test_many_workgroups_ties_and_reuse(env):
+    """The many-workgroup form (n above 8192): every score equal (the
+    boundary bin holds all n, more than the output kernel keeps in LDS, so
+    the threshold is selected over global memory), three levels, and
+    repeated launches of different n and k on one stream (the histogram the
+    calls share must be back at zero after each)."""
+    rng = np.random.default_rng(11)
+    _check(env, np.full(70000, 0.25, np.float32), 1234, "all equal, many workgroups")
+    _check(env, np.full(70000, -3.0, np.float32), 70000, "all equal, many workgroups, k=n")
+    x = rng.integers(0, 3, 50000).astype(np.float32)
+    for k in (1, 4096, 16667, 33334, 49999):
+        _check(env, x, k, "three levels, many workgroups")
+    for n, k in ((65536, 2048), (20000, 2048), (65536, 512), (4194304, 2048), (8193, 8193), (12289, 1)):
+        _check(env, rng.standard_normal(n).astype(np.float32), k, "repeated launches")
+
+
+def test_capture_without_buffer_takes_one_workgroup(env):
+    """A first call on a stream inside graph capture cannot allocate the
+    many-workgroup buffer: it takes the one-workgroup kernel, and the
+    captured graph replays to the oracle's result."""
+    torch, lib, oracle = env
+    rng = np.random.default_rng(13)
+    n, k = 65536, 2048
+    x = rng.standard_normal(n).astype(np.float32)
+    d_x = torch.from_numpy(x).cuda()
+    d_marks = torch.full((n,), 0xAB, dtype=torch.uint8, device="cuda")
+    d_sel = torch.full((k,), -7, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()  # no buffer yet
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    say(f"indexer select: captured on a fresh stream n={n} k={k}")
+    with torch.cuda.graph(g, stream=stream):
+        st = lib.hi_rocm_launch_dsv4_indexer_select(d_x.data_ptr(), n, k, d_marks.data_ptr(), d_sel.data_ptr(),
+                                                    ctypes.c_void_p(stream.cuda_stream))
+    assert st == 0, lib.hi_rocm_last_error()
+    want_sel, want_marks = oracle.indexer_select(x, k)
+    for _ in range(3):
+        d_marks.fill_(0xAB)
+        d_sel.fill_(-7)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(d_sel.cpu().numpy(), want_sel)
+        assert np.array_equal(d_marks.cpu().numpy(), want_marks)

@@ -54,6 +54,8 @@ SIGNATURES = {
     "hi_rocm_lm_head_workspace_bytes": (_i, [_i, _i, ctypes.POINTER(_sz)]),
     "hi_rocm_lm_head_logits": (_i, [_vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp]),
     "hi_rocm_sample_lm_head": (_i, [_vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "hi_rocm_sample_lm_head_ext": (_i, [_vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                        _vp, _i, _vp, _sz, _vp]),
     "hi_rocm_spec_verify_greedy": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hi_rocm_history_append": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _vp]),
     "hi_rocm_history_pack": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp]),

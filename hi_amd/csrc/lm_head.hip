@@ -223,10 +223,16 @@ __global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu
 }
 
 // Whether the fused finish takes a row: greedy, or top-k up to kLmMaxK
-// (with temperature, top-p, min-p), no penalties (the fused entry point
-// takes no history).
-__device__ __forceinline__ bool lm_row_ok(const RowCfg& c) {
-  return c.cls == kGreedy || (c.cls == kTopK && c.k_eff <= kLmMaxK);
+// (with temperature, top-p, min-p), and plain: no mask, no logprobs, and no
+// penalty that changes a logit (the records hold the logits as the
+// projection gives them).
+__device__ __forceinline__ bool lm_plain(const LmArgs& a, int row, const RowCfg& c) {
+  if (a.gen.mask != nullptr || a.gen.n_lp > 0 || a.gen.out_token_lp != nullptr) return false;
+  const bool hist = a.gen.hoff != nullptr && a.gen.hoff[row + 1] > a.gen.hoff[row];
+  return !(hist && (c.rep_on || c.freq != 0.f || c.pres != 0.f));
+}
+__device__ __forceinline__ bool lm_row_ok(const LmArgs& a, int row, const RowCfg& c) {
+  return (c.cls == kGreedy || (c.cls == kTopK && c.k_eff <= kLmMaxK)) && lm_plain(a, row, c);
 }
 
 // IEEE '>' argmax key of a value above -inf: -0 counts as +0 (the two are
@@ -244,12 +250,12 @@ __global__ void __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu
   float* tile = reinterpret_cast<float*>(lds_raw);
   const int t = blockIdx.x, tile0 = t * kLmTile;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  // lane m: whether row m keeps its tile logits (every class but greedy),
-  // loaded before the product so that its latency hides there
+  // lane m: whether row m keeps its tile logits (every row but a plain
+  // greedy one), loaded before the product so that its latency hides there
   uint32_t keep = 0u;
   if (lane < a.B) {
     const RowCfg cfg = load_cfg(a.pv, lane, a.V, 0, 0);
-    keep = cfg.cls != kGreedy ? 1u : 0u;
+    keep = (cfg.cls == kGreedy && lm_plain(a, lane, cfg)) ? 0u : 1u;
   }
   lm_gemm_tile<RG>(a, tile0, tile);
   __syncthreads();
@@ -339,7 +345,8 @@ __device__ __noinline__ void lm_general(KernargSampleArgs* ap, int row) {
     #pragma unroll
     for (int i = 0; i < (int)(sizeof(SampleArgs) / 8); ++i) d[i] = w[i];
   }
-  general_row_path<false>(a, row, lds_raw);
+  if (a.mask) general_row_path<true>(a, row, lds_raw);
+  else general_row_path<false>(a, row, lds_raw);
 }
 
 __device__ __forceinline__ KernargSampleArgs* lm_gen_args() {
@@ -347,16 +354,16 @@ __device__ __forceinline__ KernargSampleArgs* lm_gen_args() {
 }
 
 // The fused finish: one workgroup per row (gpu.rs:753-900 on the row's
-// candidates, as the lean finish does).  Rows of other classes, and top-k
-// rows whose cut falls between distinct logits of equal weight, take the
-// general per-row path over the row's logits in the workspace: every row
-// gets its token.
+// candidates, as the lean finish does).  Rows of other classes, rows with a
+// mask, logprobs or penalties, and top-k rows whose cut falls between
+// distinct logits of equal weight, take the general per-row path over the
+// row's logits in the workspace: every row gets its token.
 __global__ void __launch_bounds__(NT) lm_finish_kernel(LmArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   FinLds& fs = *reinterpret_cast<FinLds*>(lds_raw);
   const int row = blockIdx.x, tid = threadIdx.x;
   const RowCfg cfg = load_cfg(a.pv, row, a.V, 0, 0);
-  if (!lm_row_ok(cfg)) {
+  if (!lm_row_ok(a, row, cfg)) {
     lm_general(lm_gen_args(), row);
     return;
   }
@@ -533,8 +540,8 @@ size_t lm_workspace_bytes(int B, int V) {
 }
 
 size_t lm_tile_lds(int B) { return (size_t)(B <= 32 ? 32 : kLmRows) * kLmTile * sizeof(float); }
-size_t lm_finish_lds() {
-  const size_t gen = kSelHead;  // general_row_path without a history table
+size_t lm_finish_lds(bool hist) {
+  const size_t gen = kSelHead + (hist ? sel_hist_bytes(kRowGeneralChunk) : 0);  // general_row_path
   const size_t b = sizeof(FinLds) > gen ? sizeof(FinLds) : gen;
   return (b + 15) & ~(size_t)15;
 }
@@ -563,7 +570,7 @@ hipError_t launch_lm_sample(const LmArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(lm_select_kernel<2>, dim3((unsigned)a.n_chunks), dim3(kLmThreads), l1, stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t l2 = lm_finish_lds();
+  const size_t l2 = lm_finish_lds(a.gen.hoff != nullptr);
   e = ensure_lds((const void*)lm_finish_kernel, l2);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(lm_finish_kernel, dim3((unsigned)a.B), dim3(NT), l2, stream, a);

@@ -604,17 +604,27 @@ int hi_rocm_lm_head_logits(const void* hidden, const void* weight, const float* 
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "lm head launch");
 }
 
-int hi_rocm_sample_lm_head(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
-                           int hidden_dim, int vocab, const hi_rocm_row_params* params, const float* uniforms,
-                           uint32_t* out_tokens, void* workspace, size_t workspace_bytes, void* stream) {
+int hi_rocm_sample_lm_head_ext(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
+                               int hidden_dim, int vocab, const hi_rocm_row_params* params, const float* uniforms,
+                               const uint32_t* hist_offsets, const uint32_t* hist_ids, const uint32_t* hist_counts,
+                               const uint32_t* mask_words, uint32_t* out_tokens, float* out_logprobs,
+                               uint32_t* out_logprob_ids, float* out_token_logprobs, int n_logprobs, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  static const char* kWhat = "hi_rocm_sample_lm_head";
   hi_rocm::LmArgs a;
-  int rc = lm_args(hidden, weight, bias, softcap, batch, hidden_dim, vocab, "hi_rocm_sample_lm_head", a);
+  int rc = lm_args(hidden, weight, bias, softcap, batch, hidden_dim, vocab, kWhat, a);
   if (rc != HI_ROCM_OK) return rc;
   if (params == nullptr || uniforms == nullptr || out_tokens == nullptr || stream == nullptr)
-    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sample_lm_head: invalid arguments");
+    return fail(HI_ROCM_ERR_ARGS, std::string(kWhat) + ": invalid arguments");
+  if (hist_offsets != nullptr && (hist_ids == nullptr || hist_counts == nullptr))
+    return fail(HI_ROCM_ERR_ARGS, std::string(kWhat) + ": history ids or counts missing");
+  if (n_logprobs < 0 || (n_logprobs > 0 && (out_logprobs == nullptr || out_logprob_ids == nullptr)))
+    return fail(HI_ROCM_ERR_ARGS, std::string(kWhat) + ": logprob outputs missing");
+  if (n_logprobs > hi_rocm::kLeanK)
+    return fail(HI_ROCM_ERR_UNSUPPORTED, std::string(kWhat) + ": n_logprobs above 256");
   const size_t need = hi_rocm::lm_workspace_bytes(batch, vocab);
   if (workspace == nullptr || workspace_bytes < need)
-    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_sample_lm_head: workspace too small");
+    return fail(HI_ROCM_ERR_ARGS, std::string(kWhat) + ": workspace too small");
   a.pv.mode = hi_rocm::kParamsRows;
   a.pv.rows = params;
   a.pv.uniforms = uniforms;
@@ -624,15 +634,31 @@ int hi_rocm_sample_lm_head(const void* hidden, const void* weight, const float* 
   a.lm_logits = (float*)((char*)workspace + recs);
   a.out_tokens = out_tokens;
   // the general per-row path over the workspace's logits, for the rows the
-  // fused finish leaves (no history, mask or logprobs: the entry point takes
-  // none)
+  // fused finish leaves; its penalties, mask and logprobs are the call's
   a.gen = base_args(a.lm_logits, HI_ROCM_DTYPE_F32, batch, vocab, hi_rocm::lm_stride(vocab));
   a.gen.pv = a.pv;
+  a.gen.hoff = hist_offsets;
+  a.gen.hids = hist_ids;
+  a.gen.hcnt = hist_counts;
+  a.gen.mask = mask_words;
+  a.gen.n_lp = n_logprobs;
+  a.gen.need_lse = (n_logprobs > 0 || out_token_logprobs != nullptr) ? 1 : 0;
   a.gen.out_tokens = out_tokens;
+  a.gen.out_lp = out_logprobs;
+  a.gen.out_lp_ids = out_logprob_ids;
+  a.gen.out_token_lp = out_token_logprobs;
   carve(a.gen, (char*)workspace + recs + hi_rocm::lm_logits_bytes(batch, vocab),
         hi_rocm::general_layout(batch, vocab));
   const hipError_t e = hi_rocm::launch_lm_sample(a, (hipStream_t)stream);
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "lm head sample launch");
+}
+
+int hi_rocm_sample_lm_head(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
+                           int hidden_dim, int vocab, const hi_rocm_row_params* params, const float* uniforms,
+                           uint32_t* out_tokens, void* workspace, size_t workspace_bytes, void* stream) {
+  return hi_rocm_sample_lm_head_ext(hidden, weight, bias, softcap, batch, hidden_dim, vocab, params, uniforms,
+                                    nullptr, nullptr, nullptr, nullptr, out_tokens, nullptr, nullptr, nullptr, 0,
+                                    workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

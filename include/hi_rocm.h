@@ -137,7 +137,8 @@ int hi_rocm_launch_moe_topk_router(const void* scores, void* output_ids, void* o
  * hi_rocm_lm_head_logits writes the logits f32[batch][vocab] (the unfused
  * twin).  hi_rocm_sample_lm_head samples from the same logits (bit for bit)
  * and returns a token for every row: per-row params as hi_rocm_sample (any
- * class; no penalties, mask or logprobs) and one uniform per row.  Greedy
+ * class; penalties, mask and logprobs through hi_rocm_sample_lm_head_ext)
+ * and one uniform per row.  Greedy
  * rows and top-k <= 64 rows (with temperature / top-p / min-p) finish from
  * per-tile records and the few tiles that can hold the top k; rows of other
  * classes, and the rare top-k row whose cut falls between distinct logits of
@@ -151,6 +152,16 @@ int hi_rocm_lm_head_logits(const void* hidden, const void* weight, const float* 
 int hi_rocm_sample_lm_head(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
                            int hidden_dim, int vocab, const hi_rocm_row_params* params, const float* uniforms,
                            uint32_t* out_tokens, void* workspace, size_t workspace_bytes, void* stream);
+/* hi_rocm_sample_lm_head with hi_rocm_sample's history (penalties), mask and
+ * logprob arguments (same meaning; n_logprobs <= 256).  Rows with a mask,
+ * logprobs or a penalty that changes a logit take the general per-row path;
+ * the others as hi_rocm_sample_lm_head.  Same workspace. */
+int hi_rocm_sample_lm_head_ext(const void* hidden, const void* weight, const float* bias, float softcap, int batch,
+                               int hidden_dim, int vocab, const hi_rocm_row_params* params, const float* uniforms,
+                               const uint32_t* hist_offsets, const uint32_t* hist_ids, const uint32_t* hist_counts,
+                               const uint32_t* mask_words, uint32_t* out_tokens, float* out_logprobs,
+                               uint32_t* out_logprob_ids, float* out_token_logprobs, int n_logprobs, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* Greedy speculative-decoding verification (gpu.rs:10725-10762
  * speculative_greedy_next_tokens_paged_with_page_table, batched): logits

@@ -207,3 +207,93 @@ def test_twin_rows_do_not_depend_on_the_batch(hip):
     big = _twin(hip, torch, h, w, bias, cap, 40, H, V)
     small = _twin(hip, torch, h[:20].contiguous(), w, bias, cap, 20, H, V)
     assert np.array_equal(big[:20].view(np.uint32), small.view(np.uint32))
+
+
+def test_fused_with_penalties_mask_and_logprobs(hip, oracle):
+    """hi_rocm_sample_lm_head_ext: histories with penalties, an allowed-token
+    mask and logprobs, over mixed row classes (greedy, top-k <= 64, top-p
+    only, top-k 100), against the oracle run on the twin's logits with the
+    same inputs: tokens bit-exact, logprob ids exact, logprobs within 1e-5.
+    Rows 0-3 keep neutral penalties on a history (the fused finish's plain
+    rows would take them, but the call asks for logprobs: the general path),
+    and a second call without mask or logprobs sends only the rows with
+    live penalties there."""
+    import torch
+    from hi_amd import sampler as S
+    from hi_amd._lib import ROW_PARAMS_DTYPE
+    lib = hip.load()
+    B, H, V, cap = 24, 128, 6001, 6.0
+    h, _ = _bf16(torch, (B, H), 1.0, 81)
+    w, _ = _bf16(torch, (V, H), 3.0 / np.sqrt(H), 82)
+    logits = _twin(hip, torch, h, w, None, cap, B, H, V)
+    rng = np.random.default_rng(83)
+    params = np.zeros(B, ROW_PARAMS_DTYPE)
+    params["temperature"] = rng.uniform(0.5, 1.3, B)
+    params["top_p"] = rng.choice(np.array([1.0, 0.9], F32), B)
+    params["top_k"] = rng.choice(np.array([1, 20, 40, 64], np.int32), B)
+    params["min_p"] = np.where(rng.random(B) < 0.3, F32(0.05), F32(0.0))
+    params["repetition_penalty"] = rng.choice(np.array([1.0, 1.2], F32), B)
+    params["frequency_penalty"] = rng.choice(np.array([0.0, 0.3], F32), B)
+    params["presence_penalty"] = rng.choice(np.array([0.0, 0.5], F32), B)
+    params["temperature"][4:7] = 0.0                    # greedy
+    params["top_k"][8], params["top_p"][8] = 0, 0.9      # top-p only
+    params["top_k"][9] = 100                            # above the fused finish's 64
+    params["repetition_penalty"][:4] = 1.0
+    params["frequency_penalty"][:4] = 0.0
+    params["presence_penalty"][:4] = 0.0
+    u = rng.random(B).astype(F32)
+    offs = np.zeros(B + 1, np.uint32)
+    ids_l, cnt_l = [], []
+    for b in range(B):
+        r = np.minimum(rng.zipf(1.3, 40) - 1, V + 3).astype(np.uint32) if b % 5 != 2 else np.zeros(0, np.uint32)
+        ids_l.append(r)
+        cnt_l.append(rng.integers(1, 4, r.size).astype(np.uint32))
+        offs[b + 1] = offs[b] + r.size
+    ids, cnts = np.concatenate(ids_l), np.concatenate(cnt_l)
+    W = (V + 31) // 32
+    mask = np.full((B, W), 0xFFFFFFFF, np.uint32)
+    mask[10:14] = rng.integers(0, 2 ** 32, (4, W), dtype=np.uint64).astype(np.uint32)
+    mask[14] = 0                                         # fully masked: EOS
+    params["eos_id"][14] = 3
+    n_lp = 5
+    want = oracle.sample_rows(logits, params, u, offs, ids, cnts, mask, n_lp, threads=8, want_token_logprobs=True)
+    ws_n = ctypes.c_size_t()
+    hip.check(lib.hi_rocm_lm_head_workspace_bytes(B, V, ctypes.byref(ws_n)))
+    ws = torch.zeros(ws_n.value, dtype=torch.uint8, device="cuda")
+    dp = S.params_to_device(params)
+    dev = lambda x: torch.from_numpy(x.view(np.int32)).cuda()
+    du, doff, dids, dcnt, dmask = torch.from_numpy(u).cuda(), dev(offs), dev(ids), dev(cnts), dev(mask)
+    out = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+    lp = torch.zeros((B, n_lp), dtype=torch.float32, device="cuda")
+    lpi = torch.zeros((B, n_lp), dtype=torch.int32, device="cuda")
+    tlp = torch.zeros(B, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    print(f"lm head fused with penalties, mask and logprobs B={B} H={H} V={V}", flush=True)
+    torch.cuda.synchronize()
+    hip.check(lib.hi_rocm_sample_lm_head_ext(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, dp.data_ptr(),
+                                             du.data_ptr(), doff.data_ptr(), dids.data_ptr(), dcnt.data_ptr(),
+                                             dmask.data_ptr(), out.data_ptr(), lp.data_ptr(), lpi.data_ptr(),
+                                             tlp.data_ptr(), n_lp, ws.data_ptr(), ws_n.value, s.cuda_stream))
+    s.synchronize()
+    got = out.cpu().numpy().view(np.uint32)
+    print(f"got {got.tolist()}\nwant {want['tokens'].tolist()}", flush=True)
+    assert np.array_equal(got, want["tokens"]), np.flatnonzero(got != want["tokens"])
+    assert np.array_equal(lpi.cpu().numpy().view(np.uint32), want["logprob_ids"])
+    gl, wl = lp.cpu().numpy(), want["logprobs"]
+    fin = np.isfinite(wl)
+    assert np.array_equal(fin, np.isfinite(gl))
+    np.testing.assert_allclose(gl[fin], wl[fin], rtol=1e-5, atol=0)
+    gt, wt = tlp.cpu().numpy(), want["token_logprobs"]
+    fin = np.isfinite(wt)
+    np.testing.assert_allclose(gt[fin], wt[fin], rtol=1e-5, atol=0)
+    # no mask, no logprobs: the plain rows finish fused, the penalised ones
+    # through the general path
+    want2 = oracle.sample_rows(logits, params, u, offs, ids, cnts, None, 0, threads=8)
+    out.fill_(-7)
+    hip.check(lib.hi_rocm_sample_lm_head_ext(h.data_ptr(), w.data_ptr(), None, cap, B, H, V, dp.data_ptr(),
+                                             du.data_ptr(), doff.data_ptr(), dids.data_ptr(), dcnt.data_ptr(),
+                                             None, out.data_ptr(), None, None, None, 0, ws.data_ptr(), ws_n.value,
+                                             s.cuda_stream))
+    s.synchronize()
+    got2 = out.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got2, want2["tokens"]), np.flatnonzero(got2 != want2["tokens"])

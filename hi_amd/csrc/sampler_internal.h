@@ -104,15 +104,26 @@ static_assert(sizeof(WideStat) == 144, "WideStat layout");
 // the chunk's weights in the vocabulary-order fold for a start value in
 // binade e0, e0 + 1 or e0 + 2 (exact while the sum stays in that binade),
 // and the number of distinct-weight runs of the nucleus superset it wrote.
+constexpr int kCrossTerms = 48;  // terms of a crossing window
+constexpr int kCrossWins = 2;    // crossing windows a chunk records
 struct ChunkFold {
   uint32_t e0;
   uint32_t nruns;            // superset runs written; kFoldNone: the chunk's table overflowed
   uint32_t has_end;          // chunk 0: `end` is the exact fold of its weights from -0.0
   float end;
-  fold::Map map[3];
+  fold::Map map[3];          // the chunk's terms in binades e0, e0 + 1, e0 + 2
+  // the predicted crossings: nw windows (0: none predicted) around the
+  // terms where the fold leaves a binade; segment s (before window 0,
+  // between the windows, after the last) is folded in binade be[s] by its
+  // map seg[s]; window w holds wn[w] terms, added one by one
+  uint32_t nw;
+  uint32_t be[kCrossWins + 1];
+  uint32_t wn[kCrossWins];
+  fold::Map seg[kCrossWins + 1];
+  float term[kCrossWins][kCrossTerms];
   uint32_t pad[2];
 };
-static_assert(sizeof(ChunkFold) == 48, "ChunkFold layout");
+static_assert(sizeof(ChunkFold) == 480, "ChunkFold layout");
 constexpr uint32_t kFoldNone = 0xffffffffu;
 
 struct SampleArgs {

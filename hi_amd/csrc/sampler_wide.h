@@ -92,11 +92,10 @@ struct WideFinLds {
   uint32_t cnt, fail_c, rsel, csel, tok, fu;
   float acc, acc2;
 };
-// The refold arrays (weights, then fold binades) start after the chain's
-// plans, inside or past the union.
-__host__ __device__ inline size_t wide_fin_w_off() {
-  return (offsetof(WideFinLds, u) + sizeof(ChunkFold) * kWideBatch + 15) & ~(size_t)15;
-}
+// The refold's weights start past the whole struct: the refold runs in the
+// middle of the chain, which still needs the batch of chunk plans and the
+// fields after the union.
+__host__ __device__ inline size_t wide_fin_w_off() { return (sizeof(WideFinLds) + 15) & ~(size_t)15; }
 __host__ __device__ inline size_t wide_fin_lds(int chunk) {
   const size_t r = wide_fin_w_off() + wide_w_bytes(chunk);
   return r > sizeof(WideFinLds) ? r : sizeof(WideFinLds);
@@ -332,7 +331,7 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
   ChunkFold* cf = a.wfold + (int64_t)row * a.n_chunks + chunk;
   if (chunk == 0) {
     const float end = exact_chunk_fold(w, len, -0.0f, L.fl.wmap, &L.fend, L.fl.wcnt);
-    if (tid == 0) { cf->has_end = 1u; cf->end = end; cf->e0 = 1u; }
+    if (tid == 0) { cf->has_end = 1u; cf->end = end; cf->e0 = 1u; cf->nw = 0u; }
   } else {
     const int ep = fold::binade((float)S);
     const int e0 = ep > 1 ? ep - 1 : 1;
@@ -351,8 +350,8 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
     bm[NT + tid] = m1;
     bm[2 * NT + tid] = m2;
     fold::Map t0, t1, t2;
-    block_map_scan(m0, L.fl.wmap, &t0);
-    block_map_scan(m1, L.fl.wmap, &t1);
+    const fold::Map ex0 = block_map_scan(m0, L.fl.wmap, &t0);
+    const fold::Map ex1 = block_map_scan(m1, L.fl.wmap, &t1);
     block_map_scan(m2, L.fl.wmap, &t2);
     if (tid == 0) {
       cf->has_end = 0u;
@@ -361,6 +360,79 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
       cf->map[1] = t1;
       cf->map[2] = t2;
     }
+    // the predicted crossings: from the predicted start, the block, then
+    // the term, where the fold leaves its binade; the chunk records a window
+    // of terms around each (up to kCrossWins) and the maps of the segments
+    // between them, so that the chain crosses with a few real additions
+    // (wide_chain_cross).  The first search reuses the block maps above.
+    const int kx = ep - e0;  // 0 or 1: ep's maps
+    int p0 = 0, ec = ep, nw = 0;
+    uint32_t Ac = fold::to_A((float)S);
+    for (int wdx = 0; wdx < kCrossWins; ++wdx) {
+      // this thread's terms [max(r0, p0), r1) in binade ec, and the exclusive scan
+      const int q0 = max(r0, p0);
+      fold::Map mb, ex;
+      if (wdx == 0) {
+        mb = kx == 0 ? m0 : m1;
+        ex = kx == 0 ? ex0 : ex1;
+      } else {
+        mb = fold::map_identity();
+        for (int r = q0; r < r1; ++r) mb = fold::compose(mb, term_map(w[wide_pad(r)], ec));
+        fold::Map tot;
+        ex = block_map_scan(mb, L.fl.wmap, &tot);
+      }
+      const uint64_t Ab = (uint64_t)Ac + fold::apply(ex, Ac & 1u);
+      int tstar = -1;
+      if (q0 < r1 && Ab < fold::kTop && Ab + fold::apply(mb, (uint32_t)Ab & 1u) >= fold::kTop) {
+        uint32_t A = (uint32_t)Ab;
+        for (int r = q0; r < r1; ++r) {
+          const uint32_t t = fold::apply(term_map(w[wide_pad(r)], ec), A & 1u);
+          if ((uint64_t)A + t >= fold::kTop) { tstar = r; break; }
+          A += t;
+        }
+      }
+      tstar = (int)block_max_u32<NT>((uint32_t)(tstar + 1), L.fl.wcnt) - 1;
+      if (tstar < 0) break;
+      const int ws = max(p0, min(tstar - kCrossTerms / 2, len - kCrossTerms));
+      const int we = min(len, ws + kCrossTerms);
+      // segment [p0, ws) in binade ec
+      fold::Map mp = fold::map_identity();
+      for (int r = q0; r < min(r1, ws); ++r) mp = fold::compose(mp, term_map(w[wide_pad(r)], ec));
+      fold::Map sg;
+      block_map_scan(mp, L.fl.wmap, &sg);
+      if (tid < we - ws) cf->term[wdx][tid] = w[wide_pad(ws + tid)];
+      // the predicted value after the window, and its binade
+      if (tid == 0) {
+        const uint64_t A1 = (uint64_t)Ac + fold::apply(sg, Ac & 1u);
+        float v = A1 < fold::kTop ? fold::from_A((uint32_t)A1, ec) : __builtin_nanf("");
+        for (int r = ws; r < we; ++r) v = fold::fadd(v, w[wide_pad(r)]);
+        L.fend = v;
+        cf->be[wdx] = (uint32_t)ec;
+        cf->wn[wdx] = (uint32_t)(we - ws);
+        cf->seg[wdx] = sg;
+      }
+      __syncthreads();
+      const float v = L.fend;
+      __syncthreads();
+      nw = wdx + 1;
+      p0 = we;
+      ec = fold::binade(v);
+      Ac = fold::to_A(v);
+      if (!finitef_(v)) { nw = 0; break; }  // the prediction left the binade before the window
+    }
+    if (nw > 0) {
+      // the last segment [p0, len) in binade ec
+      const int q0 = max(r0, p0);
+      fold::Map ms = fold::map_identity();
+      for (int r = q0; r < r1; ++r) ms = fold::compose(ms, term_map(w[wide_pad(r)], ec));
+      fold::Map sg;
+      block_map_scan(ms, L.fl.wmap, &sg);
+      if (tid == 0) {
+        cf->be[nw] = (uint32_t)ec;
+        cf->seg[nw] = sg;
+      }
+    }
+    if (tid == 0) cf->nw = (uint32_t)nw;
   }
   // the superset's distinct weights
   constexpr int kLog2 = 11;
@@ -489,6 +561,101 @@ __device__ __forceinline__ float wide_cross_wave(const SampleArgs& a, int row, i
   return x;
 }
 
+// The chain's step over a chunk whose fold leaves the binade it starts in,
+// from the chunk's crossing record (in LDS): x (exact, in binade be[0]),
+// then per window the segment before it by its map and the window's terms
+// as real additions, then the last segment by its map.  False when the
+// record does not apply (x is not in binade be[0], or the fold leaves a
+// binade outside a window, or lands in another binade than predicted).
+// Wave-uniform: every lane of the calling wave gets the same.
+__device__ __forceinline__ bool wide_chain_cross(const ChunkFold& cf, float x, float& y) {
+  const int lane = (int)(threadIdx.x & 63u);
+  const int nw = (int)cf.nw;
+  if (nw == 0 || (uint32_t)fold::binade(x) != cf.be[0]) return false;
+  float v = x;
+  for (int wdx = 0; wdx < nw; ++wdx) {
+    const int e = (int)cf.be[wdx];
+    const uint32_t A = fold::to_A(v);
+    const uint64_t A1 = (uint64_t)A + fold::apply(cf.seg[wdx], A & 1u);
+    if (A1 >= fold::kTop) return false;
+    v = fold::from_A((uint32_t)A1, e);
+    // the window's terms, one per lane, folded onto v in lane order
+    const int n = (int)cf.wn[wdx];
+    const float tl = lane < n ? cf.term[wdx][lane] : 0.f;
+    const float f = wave_fold_f32(tl, v, n);
+    v = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(f), n - 1));
+    if ((uint32_t)fold::binade(v) != cf.be[wdx + 1]) return false;
+  }
+  const uint32_t A = fold::to_A(v);
+  const uint64_t A1 = (uint64_t)A + fold::apply(cf.seg[nw], A & 1u);
+  if (A1 >= fold::kTop) return false;
+  y = fold::from_A((uint32_t)A1, (int)cf.be[nw]);
+  return true;
+}
+
+// The chain over chunks c .. cb + nb - 1 of the batch in LDS (nb <= 64),
+// from the exact value x before chunk c, by one wave, lane i holding chunk
+// c + i.  While the fold stays in one binade e the chunks' maps in e
+// compose, so one scan over the lanes gives the value after every chunk up
+// to the first whose map in e is not stored or leaves e; that chunk steps
+// by its crossing record, and the scan resumes after it in the new binade.
+// Returns the value after the last chunk it could step over and sets fail
+// to the first chunk it could not (0xffffffff: none).
+__device__ __forceinline__ float wide_wave_chain(const ChunkFold* batch, int cb, int nb, int c, float x,
+                                                 uint32_t& fail) {
+  const int lane = (int)(threadIdx.x & 63u);
+  const int hi = c - cb + lane;
+  const bool live = hi < nb;
+  const ChunkFold& h = batch[live ? hi : 0];
+  const int h_e0 = (int)h.e0;
+  const bool h_end = live && h.has_end != 0u;
+  const fold::Map hm0 = h.map[0], hm1 = h.map[1], hm2 = h.map[2];
+  const uint32_t h_endv = __float_as_uint(h.end);
+  fail = 0xffffffffu;
+  int i0 = 0;  // the first lane (chunk c + i0) not yet stepped over
+  const int n = cb + nb - c;
+  while (i0 < n) {
+    if (__builtin_amdgcn_readlane((int)h_end, i0)) {  // chunk 0, from -0.0
+      x = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)h_endv, i0));
+      ++i0;
+      continue;
+    }
+    const int e = fold::binade(x);
+    const uint32_t A = fold::to_A(x);
+    // this lane's map in binade e (saturated: not stored, or past the chunks)
+    const int k = e - h_e0;
+    const bool ok_l = lane >= i0 && lane < n && !h_end && k >= 0 && k < 3;
+    fold::Map m = k == 0 ? hm0 : (k == 1 ? hm1 : hm2);
+    if (!ok_l) m = fold::Map{fold::kSat, fold::kSat};
+    if (lane < i0) m = fold::map_identity();
+    // inclusive scan over the lanes: the increment after each chunk
+    fold::Map inc = m;
+    #pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      fold::Map o;
+      o.t0 = (uint32_t)__shfl_up((int)inc.t0, (unsigned)d, 64);
+      o.t1 = (uint32_t)__shfl_up((int)inc.t1, (unsigned)d, 64);
+      if (lane >= d) inc = fold::compose(o, inc);
+    }
+    const uint64_t Ai = (uint64_t)A + fold::apply(inc, A & 1u);
+    const uint64_t bad = __ballot(lane >= i0 && lane < n && Ai >= fold::kTop);
+    if (bad == 0ull) {
+      const uint32_t Al = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)Ai, n - 1);
+      return fold::from_A(Al, e);
+    }
+    const int f = __ffsll((unsigned long long)bad) - 1;  // the first chunk that does not step in e
+    if (f > i0) x = fold::from_A((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)Ai, f - 1), e);
+    float y = x;
+    if (__builtin_amdgcn_readlane((int)h_end, f) || !wide_chain_cross(batch[c - cb + f], x, y)) {
+      fail = (uint32_t)(c + f);
+      return x;
+    }
+    x = y;
+    i0 = f + 1;
+  }
+  return x;
+}
+
 // Calls f(c, e) for every superset run entry e of chunk c of `row`, in
 // parallel: chunks in blocks of NT, their run counts scanned into offsets.
 template <typename F>
@@ -534,37 +701,38 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   for (int cb = 0; cb < nch; cb += kWideBatch) {
     const int nb = min(kWideBatch, nch - cb);
     {
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(folds + cb);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(F.u.ch.batch);
-      const int words = nb * (int)(sizeof(ChunkFold) / 4);
-      for (int i = tid; i < words; i += NT) dst[i] = src[i];
+      // 16-byte copies, every load of a thread issued before its stores
+      static_assert(sizeof(ChunkFold) % 16 == 0, "ChunkFold in 16-byte pieces");
+      const uint4* src = reinterpret_cast<const uint4*>(folds + cb);
+      uint4* dst = reinterpret_cast<uint4*>(F.u.ch.batch);
+      const int n4 = nb * (int)(sizeof(ChunkFold) / 16);
+      constexpr int kU = 8;
+      for (int base = 0; base < n4; base += kU * NT) {
+        uint4 v[kU];
+        #pragma unroll
+        for (int k = 0; k < kU; ++k) {
+          const int i = base + k * NT + tid;
+          if (i < n4) v[k] = src[i];
+        }
+        #pragma unroll
+        for (int k = 0; k < kU; ++k) {
+          const int i = base + k * NT + tid;
+          if (i < n4) dst[i] = v[k];
+        }
+      }
     }
     __syncthreads();
     for (int i = tid; i < nb; i += NT)
       if (F.u.ch.batch[i].nruns == kFoldNone) ovf = true;
     int c = cb;
     while (c < cb + nb) {
-      if (tid == 0) {
-        float x = acc;
-        uint32_t fail = 0xffffffffu;
-        for (int cc = c; cc < cb + nb; ++cc) {
-          const ChunkFold& cf = F.u.ch.batch[cc - cb];
-          if (cf.has_end) { x = cf.end; continue; }  // chunk 0, from -0.0
-          const int ey = fold::binade(x);
-          const int k = ey - (int)cf.e0;
-          bool ok = k >= 0 && k < 3;
-          float y = x;
-          if (ok) {
-            const uint32_t A = fold::to_A(x);
-            const uint32_t t = fold::apply(cf.map[k], A & 1u);
-            ok = (uint64_t)A + t < fold::kTop;
-            y = fold::from_A(A + t, ey);
-          }
-          if (!ok) { fail = (uint32_t)cc; break; }
-          x = y;
+      if (tid < 64) {
+        uint32_t fail;
+        const float x = wide_wave_chain(F.u.ch.batch, cb, nb, c, acc, fail);
+        if (tid == 0) {
+          F.acc = x;
+          F.fail_c = fail;
         }
-        F.acc = x;
-        F.fail_c = fail;
       }
       __syncthreads();
       acc = F.acc;

@@ -44,10 +44,15 @@ constexpr int kWideRunCap = kWideFinHash;
 constexpr int kWideBatch = 64;         // chunk plans the chain holds in LDS at a time
 constexpr int kWideGBins = 64;         // threshold bins (binades of w below M)
 
-// LDS of a (chunk, row) workgroup; the chunk's weights and fold binades
-// follow at wide_w_off / wide_pe_off.
+// Per-wave slots of the chunk work's workgroup scans and reductions.
+struct WideScanLds {
+  fold::Map wmap[NT / 64];
+  uint32_t wcnt[NT / 64];
+};
+// LDS of a (chunk, row) workgroup; the chunk's weights follow at
+// wide_w_off.
 struct WideChunkLds {
-  fold::WgLds<NT> fl;
+  WideScanLds fl;
   uint32_t hkey[kWideChunkHash];
   uint32_t hcnt[kWideChunkHash];
   uint32_t hmin[kWideChunkHash];
@@ -60,8 +65,7 @@ constexpr size_t kWideChunkHead = (sizeof(WideChunkLds) + 15) & ~(size_t)15;
 __host__ __device__ inline int wide_pad(int i) { return i + (i >> 4); }
 __host__ __device__ inline size_t wide_w_bytes(int chunk) { return (size_t)wide_pad(chunk) * 4 + 16; }
 __host__ __device__ inline size_t wide_w_off(int) { return kWideChunkHead; }
-__host__ __device__ inline size_t wide_pe_off(int chunk) { return kWideChunkHead + wide_w_bytes(chunk); }
-__host__ __device__ inline size_t wide_chunk_lds(int chunk) { return wide_pe_off(chunk) + (size_t)chunk + 16; }
+__host__ __device__ inline size_t wide_chunk_lds(int chunk) { return kWideChunkHead + wide_w_bytes(chunk); }
 
 // LDS of the row finish.  Its phases reuse one union: the chain (chunk
 // plans, and the refold arrays past them), the merge (hash table and sort
@@ -671,14 +675,29 @@ __device__ __forceinline__ void wide_for_each_run(WideFinLds& W, const SampleArg
     W.noff[tid] = off;
     if (tid == 0) W.noff[NT] = tot;
     __syncthreads();
-    for (uint32_t p = (uint32_t)tid; p < tot; p += NT) {
-      int lo = 0, hi = NT - 1;  // the last block whose offset is <= p
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (W.noff[mid] <= p) lo = mid; else hi = mid - 1;
+    // kU entries a thread: every load issued before the first is used
+    constexpr int kU = 8;
+    for (uint32_t base = 0; base < tot; base += kU * NT) {
+      uint64_t v[kU];
+      int cc[kU];
+      #pragma unroll
+      for (int k = 0; k < kU; ++k) {
+        const uint32_t p = base + (uint32_t)(k * NT + tid);
+        cc[k] = -1;
+        if (p < tot) {
+          int lo = 0, hi = NT - 1;  // the last block whose offset is <= p
+          while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (W.noff[mid] <= p) lo = mid; else hi = mid - 1;
+          }
+          const uint64_t* src = a.ws_list + (int64_t)row * a.list_stride + (int64_t)(cb + lo) * a.chunk;
+          cc[k] = cb + lo;
+          v[k] = src[p - W.noff[lo]];
+        }
       }
-      const uint64_t* src = a.ws_list + (int64_t)row * a.list_stride + (int64_t)(cb + lo) * a.chunk;
-      f(cb + lo, src[p - W.noff[lo]]);
+      #pragma unroll
+      for (int k = 0; k < kU; ++k)
+        if (cc[k] >= 0) f(cc[k], v[k]);
     }
     __syncthreads();
   }
@@ -912,31 +931,33 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
     path = kWideDrawFail;
     return 0xffffffffu;
   }
-  // the want-th weight equal to key in chunk csel, in index order
+  // the want-th weight equal to key in chunk csel, in index order: the
+  // chunk's weights (ws_w, written by its chunk work) in blocks of kE
+  // consecutive ones per thread, all loads in flight at once; a thread's
+  // count of matches before it by a scan over the threads
   const int c0 = (int)csel * a.chunk;
   const int len = min(a.chunk, a.V - c0);
-  const float* srow = a.ws_s + (int64_t)row * a.V + c0;
-  const uint32_t wid = (uint32_t)tid >> 6;
-  for (int base = 0; base < len; base += NT) {
-    const int i = base + tid;
-    bool eq = false;
-    if (i < len) {
-      float x = exact_expf(srow[i] - M);
-      x = x < cfg.min_p ? 0.f : x;
-      eq = __float_as_uint(x) == key;
+  const float* wrow = a.ws_w + (int64_t)row * a.V + c0;
+  constexpr int kE = 16;
+  for (int base = 0; base < len; base += kE * NT) {
+    const int i0 = base + tid * kE;
+    uint32_t eqm = 0u;
+    #pragma unroll
+    for (int q = 0; q < kE; ++q) {
+      const int i = i0 + q;
+      const float x = i < len ? wrow[i] : 0.f;
+      eqm |= (i < len && __float_as_uint(x) == key ? 1u : 0u) << q;
     }
-    const uint64_t bm = __ballot(eq);
-    if ((tid & 63) == 0) F.fl.wcnt[wid] = (uint32_t)__popcll(bm);
-    __syncthreads();
-    uint32_t before = F.cnt;
-    for (uint32_t v = 0; v < wid; ++v) before += F.fl.wcnt[v];
-    if (eq && before + lanes_below(bm) + 1u == want) F.tok = (uint32_t)(c0 + i);
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t s = 0u;
-      for (int v = 0; v < NT / 64; ++v) s += F.fl.wcnt[v];
-      F.cnt += s;
+    const uint32_t nm = (uint32_t)__popc(eqm);
+    uint32_t tot;
+    const uint32_t before = F.cnt + block_excl_scan_u32<NT>(nm, F.fl.wcnt, &tot);
+    if (before < want && before + nm >= want) {
+      uint32_t m = eqm;
+      for (uint32_t r = want - before; r > 1u; --r) m &= m - 1u;  // drop the matches before the wanted one
+      F.tok = (uint32_t)(c0 + i0 + __ffs(m) - 1);
     }
+    __syncthreads();
+    if (tid == 0) F.cnt += tot;
     __syncthreads();
     if (F.tok != 0xffffffffu) break;
   }

@@ -160,7 +160,6 @@ void carve(hi_rocm::SampleArgs& a, void* ws, const hi_rocm::WorkspaceLayout& L) 
   a.wstat = (hi_rocm::WideStat*)(base + L.wstat);
   a.wfold = (hi_rocm::ChunkFold*)(base + L.wfold);
   a.wbmap = (hi_rocm::fold::Map*)(base + L.wbmap);
-  a.wrow = (hi_rocm::WideRow*)(base + L.wrow);
   a.diag = (uint32_t*)(base + L.diag);
   a.chunk = hi_rocm::choose_chunk(a.B, a.V, a.n_lp, a.vec_ok, a.hoff != nullptr);
   a.n_chunks = (a.V + a.chunk - 1) / a.chunk;

@@ -73,10 +73,10 @@ __global__ void __launch_bounds__(NT) finish_grid_kernel(SampleArgs a) {
     return;
   }
   WideChunkLds& L = *reinterpret_cast<WideChunkLds*>(lds_raw);
-  const WideRow wr = a.wrow[row];
-  const bool valid = wr.valid != 0u;
-  const float M = wr.M, w_lo = wr.w_lo;
-  if (valid) wide_chunk_work(L, lds_raw, a, row, chunk, cfg, M, w_lo, a.wstat[(int64_t)row * a.n_chunks + chunk].pred);
+  const WideRowStats st = wide_row_stats(L, a, row, chunk, cfg);
+  const bool valid = st.valid != 0u;
+  const float M = st.M, w_lo = st.w_lo;
+  if (valid) wide_chunk_work(L, lds_raw, a, row, chunk, cfg, M, w_lo, st.pred);
   // the last workgroup of the row finishes it (as select_finish_kernel)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -91,6 +91,9 @@ __global__ void __launch_bounds__(NT) finish_grid_kernel(SampleArgs a) {
   }
   __syncthreads();
   if (L.last == 0u) return;
+  // every workgroup of the row has read the chunks' statistics: clear their
+  // valid flags, so that a chunk the next call's pass does not write is seen
+  for (int c = threadIdx.x; c < a.n_chunks; c += NT) a.wstat[(int64_t)row * a.n_chunks + c].valid = 0u;
   uint32_t token = 0xffffffffu;
   uint32_t path = kWideNoStats;
   if (valid) token = wide_finish(lds_raw, a, row, cfg, M, w_lo, path);

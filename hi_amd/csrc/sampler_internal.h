@@ -88,17 +88,9 @@ struct WideStat {
   float ms;                  // the chunk's max scaled logit (the bins' reference)
   uint32_t valid;            // 1: written by this call's select pass
   float hist[kWideBins];
-  double pred;               // predicted fold value before the chunk (written by the row's last chunk)
 };
 
-// Per-row result of the select pass's last workgroup for a top-p row.
-struct WideRow {
-  float M;                   // the row max of s
-  float w_lo;                // the nucleus superset: weights >= w_lo
-  uint32_t valid;            // 0: the row takes the general finish
-  uint32_t pad;
-};
-static_assert(sizeof(WideStat) == 144, "WideStat layout");
+static_assert(sizeof(WideStat) == 136, "WideStat layout");
 
 // Per (row, chunk) result of the wide pass for a top-p row: the maps of
 // the chunk's weights in the vocabulary-order fold for a start value in
@@ -157,7 +149,6 @@ struct SampleArgs {
   WideStat* wstat;     // [B][n_chunks]
   ChunkFold* wfold;    // [B][n_chunks]
   fold::Map* wbmap;    // [B][n_chunks][3][kScanThreads]: per-thread block maps of each ChunkFold binade
-  WideRow* wrow;       // [B]
   uint32_t* diag;      // [B] how the wide pass finished each top-p row (WidePath)
 };
 
@@ -186,7 +177,7 @@ constexpr int kFusedMaxRows = kFusedMaxWorkgroups;
 constexpr int kDoneRows = 65536;
 
 struct WorkspaceLayout {
-  size_t stats, cand, ws_s, ws_w, ws_list, done, wstat, wfold, wbmap, wrow, diag, total;
+  size_t stats, cand, ws_s, ws_w, ws_list, done, wstat, wfold, wbmap, diag, total;
   int64_t slots;       // (row, chunk) records reserved
   int64_t list_stride;
 };
@@ -213,7 +204,6 @@ inline WorkspaceLayout workspace_layout_slots(int max_batch, int V, int64_t slot
   L.wstat = off; off = align(off + (size_t)L.slots * sizeof(WideStat));
   L.wfold = off; off = align(off + (size_t)L.slots * sizeof(ChunkFold));
   L.wbmap = off; off = align(off + (size_t)L.slots * 3 * kScanThreads * sizeof(fold::Map));
-  L.wrow = off; off = align(off + (size_t)max_batch * sizeof(WideRow));
   L.diag = off; off = align(off + (size_t)max_batch * sizeof(uint32_t));
   L.cand = off; off = align(off + (size_t)L.slots * kFast * sizeof(uint64_t));
   L.ws_s = off; off = align(off + (size_t)max_batch * V * sizeof(float));

@@ -1541,7 +1541,5 @@ __device__ __forceinline__ void select_chunk(const SampleArgs& a, int row, int c
   select_exact(L, a, cfg, hv, nd, row, c0, len, slot);
 }
 
-// The wide pass's preparation of a top-p row (sampler_wide.h).
-__device__ __forceinline__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg);
 
 }  // namespace hi_rocm

@@ -10,25 +10,6 @@ __global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const int row = blockIdx.y;
   select_chunk<DT, NL, MASK>(a, row, blockIdx.x, lds_raw);
-  const RowCfg cfg = load_cfg(a.pv, row, a.V, a.n_lp, a.need_lse);
-  if (cfg.cls != kTopP) return;
-  // top-p rows: the last workgroup of the row merges the chunks' maxima and
-  // mass histograms for the wide pass (as select_finish_kernel's counter)
-  SelLds& L = *reinterpret_cast<SelLds*>(lds_raw);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  uint32_t* counter = a.done + row;
-  if (threadIdx.x == 0) {
-    __threadfence();
-    L.wflag[0] = atomicAdd(counter, 1u) == (uint32_t)(a.n_chunks - 1) ? 1u : 0u;
-    if (L.wflag[0]) {
-      __threadfence();
-      *counter = 0u;
-    }
-  }
-  __syncthreads();
-  if (L.wflag[0] == 0u) return;
-  wide_row_prepare(L, a, row, cfg);
 }
 
 template <int DT, int NL, bool MASK>

@@ -16,7 +16,8 @@ namespace hi_rocm {
 // (:843-856), then the candidate total and the inverse CDF (:874-899).  Here
 // the select pass leaves the scaled logits s in ws_s and a mass histogram
 // per chunk (WideStat); then one workgroup per (chunk, row):
-//   1. merges the row's chunk maxima (M) and histograms: a conservative
+//   1. merges the row's chunk maxima (M) and histograms (wide_row_stats,
+//      every workgroup of the row alike): a conservative
 //      weight bound w_lo such that the weights >= w_lo hold at least
 //      cutoff + kWideMargin of the mass (every weight of the nucleus is
 //      >= w_lo unless the f32 folds differ from exact sums by more than the
@@ -53,6 +54,9 @@ struct WideScanLds {
 // wide_w_off.
 struct WideChunkLds {
   WideScanLds fl;
+  unsigned long long gmass[kWideGBins];  // wide_row_stats
+  unsigned long long predfx;
+  float w_lo;
   uint32_t hkey[kWideChunkHash];
   uint32_t hcnt[kWideChunkHash];
   uint32_t hmin[kWideChunkHash];
@@ -127,79 +131,128 @@ __device__ __forceinline__ bool wide_insert(uint32_t* hkey, uint32_t* hcnt, uint
   return false;
 }
 
-// Step 1, once per top-p row, by the select pass's last workgroup of the
-// row: M, the superset bound w_lo and the predicted fold value before each
-// chunk (WideRow, WideStat::pred).  The masses use approximate exp; they
-// only size the superset and predict binades.
-__device__ __forceinline__ void wide_row_prepare(SelLds& L, const SampleArgs& a, int row, const RowCfg& cfg) {
+// Step 1, by every workgroup of a top-p row's chunk work: the row max of s
+// (M), the superset bound w_lo and the predicted fold value before this
+// workgroup's chunk, from the chunks' statistics the select pass wrote
+// (WideStat).  The masses use approximate exp; they only size the superset
+// and predict binades.  valid = 0: a chunk's statistics were not written by
+// this call's pass, or no logit is finite (the row takes finish_row).  The
+// row's finishing workgroup clears the chunks' valid flags afterwards.
+struct WideRowStats {
+  float M, w_lo;
+  uint32_t valid;
+  double pred;
+};
+__device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const SampleArgs& a, int row, int chunk,
+                                                      const RowCfg& cfg) {
   const int tid = threadIdx.x;
   const int nch = a.n_chunks;
   const ChunkStat* stats = a.stats + (int64_t)row * nch;
-  WideStat* wst = a.wstat + (int64_t)row * nch;
+  const WideStat* wst = a.wstat + (int64_t)row * nch;
+  // the loads of the first kU * NT (chunk, bin) items go out with those of
+  // the chunk maxima
+  constexpr int kU = 8;
+  float hv0[kU], ms0[kU];
+  {
+    const int items0 = nch * kWideBins;
+    #pragma unroll
+    for (int k = 0; k < kU; ++k) {
+      const int it = k * NT + tid;
+      hv0[k] = 0.f;
+      ms0[k] = 0.f;
+      if (it < items0) {
+        const WideStat& ws = wst[it / kWideBins];
+        hv0[k] = ws.hist[it % kWideBins];
+        ms0[k] = ws.ms;
+      }
+    }
+  }
   uint32_t mk = 0u, bad = 0u;
   for (int c = tid; c < nch; c += NT) {
     mk = max(mk, okey(stats[c].max_l));
     bad |= wst[c].valid ^ 1u;
-    wst[c].valid = 0u;  // so that a chunk this call's pass did not write is seen next time
   }
-  unsigned long long* gmass = reinterpret_cast<unsigned long long*>(L.surv[0]);  // kWideGBins entries
-  if (tid < kWideGBins) gmass[tid] = 0ull;
-  mk = block_max_u32<NT>(mk, L.redu);
-  bad = block_max_u32<NT>(bad, L.redu);
+  if (tid < kWideGBins) L.gmass[tid] = 0ull;
+  if (tid == 0) L.predfx = 0ull;
+  mk = block_max_u32<NT>(mk, L.fl.wcnt);
+  bad = block_max_u32<NT>(bad, L.fl.wcnt);
   const float ml = okey_inv(mk);
   const float M = finitef_(ml) ? ml / cfg.t_eff : -__builtin_inff();
-  WideRow* wr = a.wrow + row;
-  if (!finitef_(M) || bad) {
-    if (tid == 0) { wr->valid = 0u; wr->M = M; wr->w_lo = 0.f; }
-    return;
-  }
+  if (!finitef_(M) || bad) return WideRowStats{M, 0.f, 0u, 0.0};
   // chunk masses relative to M, in fixed point (2^-32): per binade of their
-  // lower end (for w_lo) and per chunk (for the predictions); one (chunk,
-  // bin) pair per thread step, so the whole workgroup works on every chunk
-  unsigned long long* cmass = reinterpret_cast<unsigned long long*>(L.surv[1]);  // up to kSurvCap chunks at a time
-  double S = 0.0;  // thread 0: the running prediction
-  for (int cb = 0; cb < nch; cb += kSurvCap) {
-    const int nb = min(kSurvCap, nch - cb);
-    for (int i = tid; i < nb; i += NT) cmass[i] = 0ull;
-    __syncthreads();
-    for (int it = tid; it < nb * kWideBins; it += NT) {
-      const int i = it / kWideBins, j = it % kWideBins;
-      const WideStat& ws = wst[cb + i];
-      const float lb = (M - ws.ms) * 1.4426950408889634f;  // log2 of M's weight over the chunk max's
-      const float m = ws.hist[j] * __builtin_amdgcn_exp2f(-lb);
-      if (!(m > 0.f)) continue;
-      const unsigned long long fx = (unsigned long long)((double)m * 4294967296.0);
-      int g = j == kWideBins - 1 ? kWideGBins - 1 : (int)floorf((float)(j + 1) + lb);
-      g = g < kWideGBins ? g : kWideGBins - 1;
-      atomicAdd(&gmass[g], fx);
-      atomicAdd(&cmass[i], fx);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int i = 0; i < nb; ++i) {
-        wst[cb + i].pred = S;
-        S += (double)cmass[i] * (1.0 / 4294967296.0);
+  // lower end (for w_lo) and, for the chunks before this one, their sum
+  // (the prediction); the 32 bins of a chunk are one half of a wave, whose
+  // mass a DPP reduction sums
+  static_assert(kWideBins == 32, "a chunk's bins are one half of a wave");
+  static_assert(kWideGBins == 64, "one bin per lane");
+  const int items = nch * kWideBins;
+  for (int base = 0; base < items; base += kU * NT) {
+    float hv[kU], msv[kU];
+    #pragma unroll
+    for (int k = 0; k < kU; ++k) {
+      const int it = base + k * NT + tid;
+      hv[k] = hv0[k];
+      msv[k] = ms0[k];
+      if (base != 0) {
+        hv[k] = 0.f;
+        if (it < items) {
+          const WideStat& ws = wst[it / kWideBins];
+          hv[k] = ws.hist[it % kWideBins];
+          msv[k] = ws.ms;
+        }
       }
     }
-    __syncthreads();
+    #pragma unroll
+    for (int k = 0; k < kU; ++k) {
+      const int it = base + k * NT + tid;
+      const int j = it % kWideBins;
+      const float lb = (M - msv[k]) * 1.4426950408889634f;  // log2 of M's weight over the chunk max's
+      const float m = hv[k] * __builtin_amdgcn_exp2f(-lb);
+      const bool pos = it < items && m > 0.f;
+      const unsigned long long fx = pos ? (unsigned long long)((double)m * 4294967296.0) : 0ull;
+      if (pos) {
+        int g = j == kWideBins - 1 ? kWideGBins - 1 : (int)floorf((float)(j + 1) + lb);
+        g = g < kWideGBins ? g : kWideGBins - 1;
+        atomicAdd(&L.gmass[g], fx);
+      }
+      unsigned long long cs = fx;
+      #pragma unroll
+      for (int o = 16; o > 0; o >>= 1) {
+        const unsigned long long y = ((unsigned long long)(uint32_t)__shfl_xor((int)(uint32_t)(cs >> 32), o, 64) << 32) |
+                                     (uint32_t)__shfl_xor((int)(uint32_t)cs, o, 64);
+        cs += y;
+      }
+      if (j == 0 && it < items && it / kWideBins < chunk && cs != 0ull) atomicAdd(&L.predfx, cs);
+    }
   }
-  if (tid == 0) {
-    unsigned long long tot = 0ull;
-    for (int g = 0; g < kWideGBins; ++g) tot += gmass[g];
+  __syncthreads();
+  // w_lo: the first binade bin where the masses from the top reach the
+  // cutoff plus the margin (one wave over the 64 bins)
+  if (tid < 64) {
+    const int lane = tid;
+    const unsigned long long v = L.gmass[lane];
+    unsigned long long inc = v;
+    #pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const unsigned long long y = ((unsigned long long)(uint32_t)__shfl_up((int)(uint32_t)(inc >> 32), (unsigned)d, 64) << 32) |
+                                   (uint32_t)__shfl_up((int)(uint32_t)inc, (unsigned)d, 64);
+      if (lane >= d) inc += y;
+    }
+    const unsigned long long tot = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(inc >> 32), 63) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)inc, 63);
     const double frac = (double)cfg.cutoff + (double)kWideMargin;
     float w_lo = 0.f;
     if (cfg.cutoff < 1.f && frac < 1.0) {
       const unsigned long long target = (unsigned long long)(frac * (double)tot);
-      unsigned long long cum = 0ull;
-      for (int g = 0; g < kWideGBins - 1; ++g) {
-        cum += gmass[g];
-        if (cum >= target) { w_lo = __builtin_ldexpf(1.f, -(g + 1)); break; }
-      }
+      const uint64_t hit = __ballot(lane < kWideGBins - 1 && inc >= target);
+      if (hit != 0ull) w_lo = __builtin_ldexpf(1.f, -(__ffsll((unsigned long long)hit)));
     }
-    wr->w_lo = fmaxf(w_lo, cfg.min_p);
-    wr->M = M;
-    wr->valid = 1u;
+    if (lane == 0) L.w_lo = fmaxf(w_lo, cfg.min_p);
   }
+  __syncthreads();
+  const WideRowStats r = WideRowStats{M, L.w_lo, 1u, (double)L.predfx * (1.0 / 4294967296.0)};
+  __syncthreads();  // L is reused by the chunk work
+  return r;
 }
 
 // w[wide_pad(i)] = the weight of scaled logit s[i] (exact expf; min-p

@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(NT) finish_grid_kernel(SampleArgs a) {
   const WideRowStats st = wide_row_stats(L, a, row, chunk, cfg);
   const bool valid = st.valid != 0u;
   const float M = st.M, w_lo = st.w_lo;
-  if (valid) wide_chunk_work(L, lds_raw, a, row, chunk, cfg, M, w_lo, st.pred);
+  if (valid) wide_chunk_work(L, lds_raw, a, row, chunk, cfg, M, w_lo, st.pred, st.mass);
   // the last workgroup of the row finishes it (as select_finish_kernel)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();

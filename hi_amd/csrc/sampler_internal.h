@@ -113,7 +113,8 @@ struct ChunkFold {
   uint32_t wn[kCrossWins];
   fold::Map seg[kCrossWins + 1];
   float term[kCrossWins][kCrossTerms];
-  uint32_t pad[2];
+  uint32_t flags;            // bit k: map[k] holds the chunk's map; bit 3: the block maps are stored
+  uint32_t pad;
 };
 static_assert(sizeof(ChunkFold) == 480, "ChunkFold layout");
 constexpr uint32_t kFoldNone = 0xffffffffu;

@@ -55,7 +55,7 @@ struct WideScanLds {
 struct WideChunkLds {
   WideScanLds fl;
   unsigned long long gmass[kWideGBins];  // wide_row_stats
-  unsigned long long predfx;
+  unsigned long long predfx, ownfx;
   float w_lo;
   uint32_t hkey[kWideChunkHash];
   uint32_t hcnt[kWideChunkHash];
@@ -141,7 +141,8 @@ __device__ __forceinline__ bool wide_insert(uint32_t* hkey, uint32_t* hcnt, uint
 struct WideRowStats {
   float M, w_lo;
   uint32_t valid;
-  double pred;
+  double pred;  // the predicted fold value before the chunk
+  double mass;  // the chunk's predicted mass
 };
 __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const SampleArgs& a, int row, int chunk,
                                                       const RowCfg& cfg) {
@@ -173,12 +174,12 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
     bad |= wst[c].valid ^ 1u;
   }
   if (tid < kWideGBins) L.gmass[tid] = 0ull;
-  if (tid == 0) L.predfx = 0ull;
+  if (tid == 0) { L.predfx = 0ull; L.ownfx = 0ull; }
   mk = block_max_u32<NT>(mk, L.fl.wcnt);
   bad = block_max_u32<NT>(bad, L.fl.wcnt);
   const float ml = okey_inv(mk);
   const float M = finitef_(ml) ? ml / cfg.t_eff : -__builtin_inff();
-  if (!finitef_(M) || bad) return WideRowStats{M, 0.f, 0u, 0.0};
+  if (!finitef_(M) || bad) return WideRowStats{M, 0.f, 0u, 0.0, 0.0};
   // chunk masses relative to M, in fixed point (2^-32): per binade of their
   // lower end (for w_lo) and, for the chunks before this one, their sum
   // (the prediction); the 32 bins of a chunk are one half of a wave, whose
@@ -223,6 +224,7 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
         cs += y;
       }
       if (j == 0 && it < items && it / kWideBins < chunk && cs != 0ull) atomicAdd(&L.predfx, cs);
+      if (j == 0 && it < items && it / kWideBins == chunk) L.ownfx = cs;
     }
   }
   __syncthreads();
@@ -250,7 +252,8 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
     if (lane == 0) L.w_lo = fmaxf(w_lo, cfg.min_p);
   }
   __syncthreads();
-  const WideRowStats r = WideRowStats{M, L.w_lo, 1u, (double)L.predfx * (1.0 / 4294967296.0)};
+  const WideRowStats r = WideRowStats{M, L.w_lo, 1u, (double)L.predfx * (1.0 / 4294967296.0),
+                                      (double)L.ownfx * (1.0 / 4294967296.0)};
   __syncthreads();  // L is reused by the chunk work
   return r;
 }
@@ -364,10 +367,17 @@ __device__ __forceinline__ float exact_chunk_fold(const float* w, int len, float
   return a;
 }
 
-// Steps 2-3 for one (chunk, row), with the row's M, w_lo and the chunk's
-// predicted start S.
+// Whether a chunk predicted to start at S and add `mass` stays well inside
+// the binade of S (0.1% margins, far above the predictions' errors).
+__device__ __forceinline__ bool wide_one_binade(double S, double mass) {
+  const int ep = fold::binade((float)S);
+  return ep > 1 && fold::binade((float)(S * 0.999)) == ep && fold::binade((float)((S + mass) * 1.001)) == ep;
+}
+
+// Steps 2-3 for one (chunk, row), with the row's M, w_lo, the chunk's
+// predicted start S and its predicted mass.
 __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* lds_raw, const SampleArgs& a, int row, int chunk,
-                                const RowCfg& cfg, float M, float w_lo, double S) {
+                                const RowCfg& cfg, float M, float w_lo, double S, double mass) {
   const int tid = threadIdx.x;
   const int c0 = chunk * a.chunk;
   const int len = min(a.chunk, a.V - c0);
@@ -388,7 +398,25 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
   ChunkFold* cf = a.wfold + (int64_t)row * a.n_chunks + chunk;
   if (chunk == 0) {
     const float end = exact_chunk_fold(w, len, -0.0f, L.fl.wmap, &L.fend, L.fl.wcnt);
-    if (tid == 0) { cf->has_end = 1u; cf->end = end; cf->e0 = 1u; cf->nw = 0u; }
+    if (tid == 0) { cf->has_end = 1u; cf->end = end; cf->e0 = 1u; cf->nw = 0u; cf->flags = 0u; }
+  } else if (wide_one_binade(S, mass)) {
+    // predicted start and end well inside one binade ep (0.1% margins): the
+    // chunk's map in ep alone; a chain that finds the start elsewhere, or
+    // the sum leaving ep, refolds the chunk
+    const int ep = fold::binade((float)S);
+    const int J = (len + NT - 1) / NT;
+    const int r0 = min(tid * J, len), r1 = min(r0 + J, len);
+    fold::Map m1 = fold::map_identity();
+    for (int r = r0; r < r1; ++r) m1 = fold::compose(m1, term_map(w[wide_pad(r)], ep));
+    fold::Map t1;
+    block_map_scan(m1, L.fl.wmap, &t1);
+    if (tid == 0) {
+      cf->has_end = 0u;
+      cf->e0 = (uint32_t)(ep - 1);
+      cf->map[1] = t1;
+      cf->flags = 2u;
+      cf->nw = 0u;
+    }
   } else {
     const int ep = fold::binade((float)S);
     const int e0 = ep > 1 ? ep - 1 : 1;
@@ -416,6 +444,7 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
       cf->map[0] = t0;
       cf->map[1] = t1;
       cf->map[2] = t2;
+      cf->flags = 15u;
     }
     // the predicted crossings: from the predicted start, the block, then
     // the term, where the fold leaves its binade; the chunk records a window
@@ -553,6 +582,8 @@ __device__ __forceinline__ float wide_cross_wave(const SampleArgs& a, int row, i
   constexpr int PB = NT / 64;  // blocks per lane
   const int lane = threadIdx.x & 63;
   const ChunkFold cf = a.wfold[(int64_t)row * a.n_chunks + c];
+  ok = (cf.flags & 8u) != 0u;  // a one-binade chunk stores no block maps: refold it
+  if (!ok) return acc;
   const fold::Map* bm = a.wbmap + ((int64_t)row * a.n_chunks + c) * 3 * NT;
   const int c0 = c * a.chunk;
   const int len = min(a.chunk, a.V - c0);
@@ -665,6 +696,7 @@ __device__ __forceinline__ float wide_wave_chain(const ChunkFold* batch, int cb,
   const bool live = hi < nb;
   const ChunkFold& h = batch[live ? hi : 0];
   const int h_e0 = (int)h.e0;
+  const uint32_t h_flags = h.flags;
   const bool h_end = live && h.has_end != 0u;
   const fold::Map hm0 = h.map[0], hm1 = h.map[1], hm2 = h.map[2];
   const uint32_t h_endv = __float_as_uint(h.end);
@@ -681,7 +713,7 @@ __device__ __forceinline__ float wide_wave_chain(const ChunkFold* batch, int cb,
     const uint32_t A = fold::to_A(x);
     // this lane's map in binade e (saturated: not stored, or past the chunks)
     const int k = e - h_e0;
-    const bool ok_l = lane >= i0 && lane < n && !h_end && k >= 0 && k < 3;
+    const bool ok_l = lane >= i0 && lane < n && !h_end && k >= 0 && k < 3 && ((h_flags >> k) & 1u);
     fold::Map m = k == 0 ? hm0 : (k == 1 ? hm1 : hm2);
     if (!ok_l) m = fold::Map{fold::kSat, fold::kSat};
     if (lane < i0) m = fold::map_identity();

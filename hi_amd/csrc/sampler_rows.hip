@@ -204,9 +204,9 @@ __device__ __forceinline__ void row_issue(const SampleArgs& a, int row, RowPipe<
 // processed history logits, those whose key reaches a bound below which no
 // weight can reach min_p whatever the final row max (the bound comes from
 // the largest key seen so far, a lower bound of the row max M), and appends
-// them to L.sbuf.  After the barrier one wave computes the exact weights
-// against M, keeps S, sorts it by (w desc, index asc) in registers, and
-// runs the reference's folds: the kept top-k of the rank order is the first
+// them to L.sbuf.  After the barrier one wave (four for more than 64
+// entries) computes the exact weights against M, keeps S, sorts it by
+// (w desc, index asc) in registers, and runs the reference's folds: the kept top-k of the rank order is the first
 // min(|S|, k) entries of S.  That needs the lists to have dropped nothing
 // that ranks among them: either their thresholds' weights are below min_p
 // (nothing of S was dropped), or the k-th weight of S is above them.
@@ -250,29 +250,6 @@ struct Exp2TabLds {
 // Why the min-p finish left a row to the general finish (0: it did not).
 enum MinpMiss : uint32_t { kMinpOk = 0, kMinpArray = 1, kMinpTopK = 2, kMinpDraw = 3 };
 
-// The wave's sorted support and the draw over its first min(c, k_eff)
-// entries; token gets the drawn index.  Misses: the top k is not known
-// (minp_topk_known), or the reference's argmax fallback (never with a
-// positive row maximum).
-template <int S>
-__device__ __forceinline__ uint32_t minp_draw(uint64_t (&x)[S], int c, const RowCfg& cfg, bool complete, float wT,
-                                              uint32_t& token) {
-  wave_sort_desc<S>(x);
-  if (!minp_topk_known<S>(x, c, cfg.k_eff, complete, wT)) return kMinpTopK;
-  const int pick = wave_draw_r<S>(x, min(c, cfg.k_eff), cfg);
-  if (pick < 0) return kMinpDraw;
-  uint64_t v = 0ull;
-  #pragma unroll
-  for (int m = 0; m < S; ++m)
-    if ((pick >> 6) == m) v = readlane64(x[m], pick & 63);
-  token = cand_idx(v);
-  return kMinpOk;
-}
-
-// The min-p finish on one wave (see above); sc (kRowSCap entries) and hist
-// (256 words) are LDS scratch no other wave uses meanwhile.  Tm is the
-// largest list threshold of the row.  A miss (MinpMiss) sends the row to
-// the candidate lists' finish.
 // The rank (entries above it) of this lane's key among the wave's keys
 // (zero keys count for nothing): over the lanes of km one at a time, or,
 // for many, over all 64 lanes in an unrolled loop of independent compares.
@@ -294,16 +271,18 @@ __device__ __forceinline__ uint32_t wave_rank_desc(uint64_t x, uint64_t km) {
   return (r + r1) + (r2 + r3);
 }
 
-__device__ __forceinline__ uint32_t row_minp_finish(const RowLds& L, const RowCfg& cfg, uint64_t* sc, uint32_t* hist,
-                                                    uint32_t& token) {
+// The min-p finish of a support of at most 64 entries on one wave (see
+// above).  Tm is the largest list threshold of the row.  A miss (MinpMiss)
+// sends the row to the candidate lists' finish.
+__device__ __forceinline__ uint32_t row_minp_finish(const RowLds& L, const RowCfg& cfg, uint32_t& token) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint4 st = *reinterpret_cast<const uint4*>(L.sst);
   const uint32_t ns = st.x, mk = st.y, Tm = st.z;
   if (st.w != 0u || ns == 0u || ns > (uint32_t)kRowSCap || mk <= kKeyNegInf || mk >= kKeyPosInf) return kMinpArray;
   const Exp2TabLds tab{L.exptab};
   const float M = key_to_s(mk, cfg.t_eff);
-  const uint32_t ke = (uint32_t)cfg.k_eff;
-  if (ns <= 64u) {
+  if (ns > 64u) return kMinpArray;  // (row_minp_finish4)
+  {
     // one slot: the support stays where it is
     const uint64_t x = lane < ns ? L.sbuf[lane] : 0ull;
     uint64_t rk = 0ull;
@@ -331,86 +310,99 @@ __device__ __forceinline__ uint32_t row_minp_finish(const RowLds& L, const RowCf
     token = cand_idx(readlane64(y[0], pick));
     return kMinpOk;
   }
+}
+
+// The min-p finish of a support of 65 .. kRowSCap entries on the first four
+// waves (one per SIMD): wave v weighs entries [v * 64S, (v + 1) * 64S) of
+// L.sbuf and sorts them in registers into list v of lst (zero keys, outside
+// the support, last); after a barrier each kept entry's rank is its index in
+// its list plus, for every other list, the number of its keys above it (a
+// binary search), and the entries ranked below k_eff land at their rank in
+// out; after another barrier wave 0 draws from out.  cnt: 4 words.  Called
+// by the four waves alike; the result is wave 0's (the others return kMinpOk
+// and token 0).
+template <int S>
+__device__ __forceinline__ uint32_t row_minp_finish4(const RowLds& L, const RowCfg& cfg, uint32_t ns, uint32_t mk,
+                                                     uint32_t Tm, uint64_t* lst, uint64_t* out, uint32_t* cnt,
+                                                     uint32_t& token) {
+  constexpr int LN = 64 * S;  // entries per list
+  const uint32_t lane = threadIdx.x & 63u;
+  const int v = (int)(threadIdx.x >> 6);
+  const Exp2TabLds tab{L.exptab};
+  const float M = key_to_s(mk, cfg.t_eff);
+  const uint32_t ke = (uint32_t)cfg.k_eff;
+  uint64_t rk[S];
+  #pragma unroll
+  for (int m = 0; m < S; ++m) {
+    const uint32_t i = (uint32_t)(v * LN + m * 64) + lane;
+    rk[m] = 0ull;
+    if (i < ns) {
+      const uint64_t x = L.sbuf[i];
+      const float w = exact_expf_t(key_to_s(cand_skey(x), cfg.t_eff) - M, tab);
+      if (w >= cfg.min_p) rk[m] = rank_key(w, cand_idx(x));
+    }
+  }
+  wave_sort_desc<S>(rk);
+  uint32_t cv = 0u;
+  #pragma unroll
+  for (int m = 0; m < S; ++m) {
+    lst[v * LN + m * 64 + (int)lane] = rk[m];
+    cv += (uint32_t)__popcll(__ballot(rk[m] != 0ull));
+  }
+  if (lane == 0u) cnt[v] = cv;
+  __syncthreads();
+  const uint4 cn = *reinterpret_cast<const uint4*>(cnt);
+  const uint32_t c = cn.x + cn.y + cn.z + cn.w;
+  // the ranks of this wave's entries among the first k_eff (keys are
+  // distinct: ranks of the support are a permutation of [0, c))
+  #pragma unroll
+  for (int m = 0; m < S; ++m) {
+    const uint32_t j = (uint32_t)(m * 64) + lane;
+    if (j < cv && j < ke) {
+      const uint64_t x = rk[m];
+      uint32_t pos[4] = {0u, 0u, 0u, 0u};
+      const uint32_t nu[4] = {cn.x, cn.y, cn.z, cn.w};
+      #pragma unroll
+      for (int st = LN; st >= 1; st >>= 1) {
+        #pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (u == v) continue;
+          const uint32_t q = pos[u] + (uint32_t)st;
+          if (q <= nu[u] && lst[u * LN + (int)q - 1] > x) pos[u] = q;
+        }
+      }
+      const uint32_t r = j + pos[0] + pos[1] + pos[2] + pos[3];
+      if (r < ke) out[r] = x;
+    }
+  }
+  __syncthreads();
+  token = 0u;
+  if (v != 0) return kMinpOk;
   const float wT = Tm > kKeyNegInf ? exact_expf_t(key_to_s(Tm, cfg.t_eff) - M, tab) : 0.f;
   const bool complete = wT < cfg.min_p;
-  constexpr int NS = kRowSCap / 64;
-  uint64_t rk[NS];
-  uint32_t c = 0u;
-  #pragma unroll
-  for (int m = 0; m < NS; ++m) {
-    const uint32_t i = (uint32_t)m * 64u + lane;
-    rk[m] = 0ull;
-    if (m * 64 < (int)ns) {
-      if (i < ns) {
-        const uint64_t x = L.sbuf[i];
-        const float w = exact_expf_t(key_to_s(cand_skey(x), cfg.t_eff) - M, tab);
-        if (w >= cfg.min_p) rk[m] = rank_key(w, cand_idx(x));
-      }
-      c += (uint32_t)__popcll(__ballot(rk[m] != 0ull));
-    }
-  }
-  {
-    // the support gathered into entries [0, c) (every one of them written)
-    uint32_t at = 0u;
+  const uint32_t c2 = min(c, ke);
+  auto draw = [&](auto slots) -> uint32_t {
+    constexpr int D = decltype(slots)::value;
+    uint64_t y[D];
     #pragma unroll
-    for (int m = 0; m < NS; ++m) {
-      if (m * 64 < (int)ns) {
-        const uint64_t bm = __ballot(rk[m] != 0ull);
-        if (rk[m] != 0ull) sc[at + lanes_below(bm)] = rk[m];
-        at += (uint32_t)__popcll(bm);
-      }
+    for (int m = 0; m < D; ++m) {
+      const uint32_t i = (uint32_t)(m * 64) + lane;
+      y[m] = i < c2 ? out[i] : 0ull;
     }
-    wave_lds_sync();
-    #pragma unroll
-    for (int m = 0; m < NS; ++m) {
-      const uint32_t i = (uint32_t)m * 64u + lane;
-      rk[m] = i < c ? sc[i] : 0ull;
-    }
-    wave_lds_sync();
-  }
-  if (c > ke && c > 64u) {
-    // more support than the kept top k: the top k first (a one-wave radix
-    // select over the distinct rank keys: exactly k of them reach thr),
-    // gathered into [0, k)
-    const uint64_t thr = wave_select_skip_f<NS>([&](int i) { return sc[i]; }, (int)c, ke, hist, ~0ull, 0ull);
-    uint32_t at = 0u;
-    wave_lds_sync();
-    #pragma unroll
-    for (int m = 0; m < NS; ++m) {
-      const uint64_t bm = __ballot(rk[m] >= thr);
-      if (rk[m] >= thr) sc[at + lanes_below(bm)] = rk[m];
-      at += (uint32_t)__popcll(bm);
-    }
-    wave_lds_sync();
-    c = ke;
-    #pragma unroll
-    for (int m = 0; m < NS; ++m) {
-      const uint32_t i = (uint32_t)m * 64u + lane;
-      rk[m] = i < c ? sc[i] : 0ull;
-    }
-    wave_lds_sync();
-  }
-  if (c <= 64u) {
-    const uint64_t km = __ballot(rk[0] != 0ull);
-    const uint32_t r = wave_rank_desc(rk[0], km);
-    const int to = rk[0] != 0ull ? (int)(r * 4u) : 63 * 4;
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)(uint32_t)rk[0]);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)(uint32_t)(rk[0] >> 32));
-    uint64_t y[1] = {lane < c ? ((uint64_t)hi << 32) | lo : 0ull};
-    if (!minp_topk_known<1>(y, (int)c, cfg.k_eff, complete, wT)) return kMinpTopK;
-    const int pick = wave_draw_r<1>(y, min((int)c, cfg.k_eff), cfg);
+    if (!minp_topk_known<D>(y, (int)c, cfg.k_eff, complete, wT)) return kMinpTopK;
+    const int pick = wave_draw_r<D>(y, (int)c2, cfg);
     if (pick < 0) return kMinpDraw;
-    token = cand_idx(readlane64(y[0], pick));
+    uint64_t t = 0ull;
+    #pragma unroll
+    for (int m = 0; m < D; ++m)
+      if ((pick >> 6) == m) t = readlane64(y[m], pick & 63);
+    token = cand_idx(t);
     return kMinpOk;
-  }
-  if (c <= 128u) {
-    uint64_t y[2] = {rk[0], rk[1]};
-    return minp_draw<2>(y, (int)c, cfg, complete, wT, token);
-  }
-  // c <= k_eff <= kLeanK here
+  };
   static_assert(kLeanK <= 256, "four slots hold the kept top k");
-  uint64_t y[4] = {rk[0], rk[1], rk[2], rk[3]};
-  return minp_draw<4>(y, (int)c, cfg, complete, wT, token);
+  if (c2 <= 64u) return draw(std::integral_constant<int, 1>{});
+  if (c2 <= 128u) return draw(std::integral_constant<int, 2>{});
+  return draw(std::integral_constant<int, 4>{});
 }
 
 // The fast path of one row, with its first tiles in flight (row_issue);
@@ -759,14 +751,30 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
   //    waves end here (ended waves no longer count at barriers)
   if (wid >= NT / 64) return true;
   if (sp) {
-    // wave 0 runs the min-p finish and publishes whether it resolved the
-    // row: the four waves then take the same path (the general finish
-    // below needs all of them)
-    if (wid == 0) {
+    // the min-p finish (wave 0, or the four waves for a support of more
+    // than 64 entries) publishes whether it resolved the row: the four
+    // waves then take the same path (the general finish below needs all of
+    // them)
+    const uint4 st = *reinterpret_cast<const uint4*>(L.sst);
+    if (st.w == 0u && st.x > 64u && st.x <= (uint32_t)kRowSCap && st.y > kKeyNegInf && st.y < kKeyPosInf) {
+      // a support of more than one wave's slot: the four waves weigh and
+      // sort it (scratch: the tile buffers of waves 0-2)
       uint32_t tok = 0u;
-      // scratch: waves 0 and 1's tile buffers (the other waves wait below)
-      const uint32_t miss = row_minp_finish(L, cfg, reinterpret_cast<uint64_t*>(L.xscr[0]),
-                                            reinterpret_cast<uint32_t*>(L.xscr[1]), tok);
+      uint64_t* lst = reinterpret_cast<uint64_t*>(L.xscr[0]);
+      uint64_t* out = reinterpret_cast<uint64_t*>(L.xscr[1]);
+      uint32_t* cnt = reinterpret_cast<uint32_t*>(L.xscr[2]);
+      const uint32_t miss = st.x <= 256u ? row_minp_finish4<1>(L, cfg, st.x, st.y, st.z, lst, out, cnt, tok)
+                                         : row_minp_finish4<2>(L, cfg, st.x, st.y, st.z, lst, out, cnt, tok);
+      if (tid == 0) {
+        L.sdone = miss;
+        if (miss == kMinpOk) {
+          a.out_tokens[row] = tok;
+          a.diag[row] = kRowPathMinp;
+        }
+      }
+    } else if (wid == 0) {
+      uint32_t tok = 0u;
+      const uint32_t miss = row_minp_finish(L, cfg, tok);
       if (lane == 0u) {
         L.sdone = miss;
         if (miss == kMinpOk) {

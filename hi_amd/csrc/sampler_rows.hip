@@ -360,26 +360,30 @@ __device__ __forceinline__ uint32_t row_minp_finish4(const RowLds& L, const RowC
     const uint32_t j = (uint32_t)(m * 64) + lane;
     if (j < cv && j < ke) {
       const uint64_t x = rk[m];
-      uint32_t pos[4] = {0u, 0u, 0u, 0u};
-      const uint32_t nu[4] = {cn.x, cn.y, cn.z, cn.w};
+      // the keys above x in each other list, by a binary search whose
+      // probes are read unconditionally (one LDS wait per step for the
+      // three lists; zero keys past a list's support never pass)
+      uint32_t pos[3] = {0u, 0u, 0u};
+      int base[3];
+      #pragma unroll
+      for (int t = 0; t < 3; ++t) base[t] = ((v + 1 + t) & 3) * LN;
       #pragma unroll
       for (int st = LN; st >= 1; st >>= 1) {
+        uint64_t pr[3];
         #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (u == v) continue;
-          const uint32_t q = pos[u] + (uint32_t)st;
-          if (q <= nu[u] && lst[u * LN + (int)q - 1] > x) pos[u] = q;
-        }
+        for (int t = 0; t < 3; ++t) pr[t] = lst[base[t] + (int)min(pos[t] + (uint32_t)st, (uint32_t)LN) - 1];
+        #pragma unroll
+        for (int t = 0; t < 3; ++t) pos[t] = (pos[t] + (uint32_t)st <= (uint32_t)LN && pr[t] > x) ? pos[t] + (uint32_t)st : pos[t];
       }
-      const uint32_t r = j + pos[0] + pos[1] + pos[2] + pos[3];
+      const uint32_t r = j + pos[0] + pos[1] + pos[2];
       if (r < ke) out[r] = x;
     }
   }
+  const float wT = Tm > kKeyNegInf ? exact_expf_t(key_to_s(Tm, cfg.t_eff) - M, tab) : 0.f;
+  const bool complete = wT < cfg.min_p;
   __syncthreads();
   token = 0u;
   if (v != 0) return kMinpOk;
-  const float wT = Tm > kKeyNegInf ? exact_expf_t(key_to_s(Tm, cfg.t_eff) - M, tab) : 0.f;
-  const bool complete = wT < cfg.min_p;
   const uint32_t c2 = min(c, ke);
   auto draw = [&](auto slots) -> uint32_t {
     constexpr int D = decltype(slots)::value;

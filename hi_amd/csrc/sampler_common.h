@@ -309,6 +309,19 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   }));
 }
 
+// Orders this wave's LDS accesses (a wave executes its LDS operations in
+// order; this keeps the compiler from moving them across the point).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Number of set bits of m below the calling lane.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 __device__ __forceinline__ uint32_t wave_last_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
@@ -1415,18 +1428,17 @@ __device__ __forceinline__ uint64_t block_select_skip(const uint64_t* items, int
 //
 // kmax > k asks for a threshold that keeps at least k and at most kmax
 // keys (the radix passes stop at the first digit that allows it).
-template <int PER, typename LoadF>
-__device__ __forceinline__ uint64_t wave_select_skip_f(LoadF item, int n, uint32_t k, uint32_t* hist,
+// wave_select_skip_r takes the keys from registers (entry m * 64 + lane in
+// x[m], entries from n on ignored).
+template <int PER>
+__device__ __forceinline__ uint64_t wave_select_skip_r(const uint64_t (&x)[PER], int n, uint32_t k, uint32_t* hist,
                                                        uint64_t lo, uint64_t hi_b, uint32_t kmax = 0u) {
   const int lane = threadIdx.x & 63;
   const uint32_t kcap = kmax > k ? kmax : k;
-  uint64_t x[PER];
   uint64_t mn = ~0ull, mx = 0ull;
   #pragma unroll
   for (int m = 0; m < PER; ++m) {
-    const int i = m * 64 + lane;
-    x[m] = i < n ? item(i) : 0ull;
-    if (i < n) {
+    if (m * 64 + lane < n) {
       mn = x[m] < mn ? x[m] : mn;
       mx = x[m] > mx ? x[m] : mx;
     }
@@ -1482,6 +1494,18 @@ __device__ __forceinline__ uint64_t wave_select_skip_f(LoadF item, int n, uint32
     if (kept <= kcap) break;
   }
   return prefix;
+}
+template <int PER, typename LoadF>
+__device__ __forceinline__ uint64_t wave_select_skip_f(LoadF item, int n, uint32_t k, uint32_t* hist,
+                                                       uint64_t lo, uint64_t hi_b, uint32_t kmax = 0u) {
+  const int lane = threadIdx.x & 63;
+  uint64_t x[PER];
+  #pragma unroll
+  for (int m = 0; m < PER; ++m) {
+    const int i = m * 64 + lane;
+    x[m] = i < n ? item(i) : 0ull;
+  }
+  return wave_select_skip_r<PER>(x, n, k, hist, lo, hi_b, kmax);
 }
 template <int PER>
 __device__ __forceinline__ uint64_t wave_select_skip(const uint64_t* items, int n, uint32_t k, uint32_t* hist,
@@ -1615,6 +1639,27 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// The rank (entries above it) of this lane's key among the wave's keys
+// (zero keys count for nothing): over the lanes of km one at a time, or,
+// for many, over all 64 lanes in an unrolled loop of independent compares.
+__device__ __forceinline__ uint32_t wave_rank_desc(uint64_t x, uint64_t km) {
+  uint32_t r = 0u;
+  if (__popcll(km) <= 16) {
+    for (uint64_t mm = km; mm != 0ull; mm &= mm - 1ull)
+      r += readlane64(x, __builtin_ctzll(mm)) > x ? 1u : 0u;
+    return r;
+  }
+  uint32_t r1 = 0u, r2 = 0u, r3 = 0u;
+  #pragma unroll
+  for (int j = 0; j < 64; j += 4) {
+    r += readlane64(x, j) > x ? 1u : 0u;
+    r1 += readlane64(x, j + 1) > x ? 1u : 0u;
+    r2 += readlane64(x, j + 2) > x ? 1u : 0u;
+    r3 += readlane64(x, j + 3) > x ? 1u : 0u;
+  }
+  return (r + r1) + (r2 + r3);
+}
+
 // Descending sort of the wave's 64 * S keys, entry m * 64 + lane in x[m]:
 // a bitonic network whose compare-exchanges between slots stay in a lane's
 // registers and whose exchanges between lanes are lane_xor64 moves.
@@ -1678,6 +1723,191 @@ __device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int
   return pick < 0 ? 0xffffffffu : cand_idx(fs.buf[pick]);
 }
 
+// finish_core for at most 64 selected candidates (kk <= 64, n <= 64 PER) on
+// wave 0 alone, from registers: the one-wave select, the selection, the
+// weights and tie checks, the rank order by counting and the draw, with no
+// workgroup barrier; meanwhile the other waves add up the candidates'
+// logprob terms.  One barrier at the end publishes the result; the
+// logprobs are then written by every thread.  Same result as the
+// workgroup steps.  The select first bounds the kk-th key by the kk-th
+// largest of the lanes' maxima and, when at most 128 keys reach that bound,
+// selects among them on two slots.
+constexpr int kWavePer = 20;  // candidates per lane of finish_core_wave (n <= 1280)
+
+// The keys of x[0, S) (entry m * 64 + lane in x[m], entries from n on
+// ignored) that reach thr, written to buf[0, min(count, 128)) in lane-major
+// order (a lane's keys together); returns the count.  Every lane writes
+// every slot (the ones left out, and kept ones past 128, to its own word
+// buf[128 + lane]), so the writes take no branch; buf holds 192 keys.
+template <int S>
+__device__ __forceinline__ uint32_t wave_keep_into(const uint64_t (&x)[S], int n, uint64_t thr, uint64_t* buf) {
+  const uint32_t lane = threadIdx.x & 63u;
+  uint32_t c = 0u;
+  #pragma unroll
+  for (int m = 0; m < S; ++m) c += (m * 64 + (int)lane < n && x[m] >= thr) ? 1u : 0u;
+  const uint32_t incl = wave_incl_scan_u32(c);
+  uint32_t at = incl - c;
+  const uint32_t spare = 128u + lane;
+  #pragma unroll
+  for (int m = 0; m < S; ++m) {
+    const bool k = m * 64 + (int)lane < n && x[m] >= thr;
+    buf[k && at < 128u ? at : spare] = x[m];
+    at += k ? 1u : 0u;
+  }
+  return (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+}
+
+// The largest of x[0, S) under thr (0: none).
+template <int S>
+__device__ __forceinline__ uint64_t wave_max_below(const uint64_t (&x)[S], int n, uint64_t thr) {
+  const uint32_t lane = threadIdx.x & 63u;
+  uint64_t b = 0ull;
+  #pragma unroll
+  for (int m = 0; m < S; ++m)
+    if (m * 64 + (int)lane < n && x[m] < thr) b = x[m] > b ? x[m] : b;
+  return wave_max_u64(b);
+}
+
+template <int PER>
+__device__ __forceinline__ bool finish_core_wave(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, int n,
+                                                 float M, uint32_t ub_key, double part, uint32_t above, uint64_t lo,
+                                                 uint64_t hi) {
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const int wid = tid >> 6;
+  const bool want_lp = a.n_lp > 0 || a.out_token_lp != nullptr;
+  const int kk = min(cfg.k_sel, n);
+  if (wid == 0) {
+    uint32_t status = 0u;  // 1: the workgroup finish (finish_row) takes the row
+    uint64_t xr[PER];
+    #pragma unroll
+    for (int m = 0; m < PER; ++m) {
+      const int i = m * 64 + (int)lane;
+      xr[m] = i < n ? fs.cbig[i] : 0ull;
+    }
+    // 4. the top kk by (processed logit desc, index asc) (keys are
+    //    distinct), in lanes [0, kk) of y[0], sorted when `sorted`; below
+    //    is the largest key left out.  A first bound: a key that at least
+    //    kk of the lanes' maxima reach (every lane holds a key when n > kk;
+    //    the maxima are distinct), so at least kk keys reach it; when at
+    //    most 128 do, they are sorted in registers
+    uint64_t y[1] = {0ull};
+    uint64_t below = 0ull;
+    bool sorted = true;
+    if (n <= kk) {
+      y[0] = xr[0];
+      wave_sort_desc<1>(y);
+    } else {
+      uint64_t lmx[1] = {0ull};
+      #pragma unroll
+      for (int m = 0; m < PER; ++m) lmx[0] = xr[m] > lmx[0] ? xr[m] : lmx[0];
+      const uint64_t g = wave_select_skip_r<1>(lmx, 64, (uint32_t)kk, fs.hist, ~0ull, 0ull);
+      const uint32_t n2 = wave_keep_into<PER>(xr, n, g, fs.buf);
+      wave_lds_sync();
+      if (n2 <= 64u) {
+        y[0] = (int)lane < (int)n2 ? fs.buf[lane] : 0ull;
+        wave_sort_desc<1>(y);
+        below = (int)n2 > kk ? readlane64(y[0], kk) : wave_max_below<PER>(xr, n, g);
+      } else if (n2 <= 128u) {
+        uint64_t y2[2];
+        #pragma unroll
+        for (int m = 0; m < 2; ++m) y2[m] = m * 64 + (int)lane < (int)n2 ? fs.buf[m * 64 + lane] : 0ull;
+        wave_sort_desc<2>(y2);
+        y[0] = y2[0];
+        below = kk < 64 ? readlane64(y2[0], kk) : readlane64(y2[1], 0);
+      } else {
+        wave_lds_sync();
+        const uint64_t thr = wave_select_skip_r<PER>(xr, n, (uint32_t)kk, fs.hist, lo, hi);
+        wave_keep_into<PER>(xr, n, thr, fs.buf);
+        below = wave_max_below<PER>(xr, n, thr);
+        wave_lds_sync();
+        y[0] = (int)lane < kk ? fs.buf[lane] : 0ull;
+        sorted = false;
+      }
+    }
+    const uint64_t x = (int)lane < kk ? y[0] : 0ull;
+    const uint64_t thr = sorted ? readlane64(x, kk - 1) : wave_min_u64((int)lane < kk ? x : ~0ull);  // the kk-th key
+    if (n > kk && cand_skey(thr) <= above) status = 1u;
+    // 5. weights and rank keys; the smallest selected weight w_b
+    uint64_t rk = 0ull;
+    uint32_t pk = 0u, wbits = 0xffffffffu;
+    if ((int)lane < kk) {
+      const float sx = key_to_s(cand_skey(x), cfg.t_eff);
+      const float w = exact_expf(sx - M);
+      rk = rank_key(w, cand_idx(x));
+      pk = okey(sx);
+      wbits = __float_as_uint(w);
+    }
+    const float w_b = __uint_as_float(wave_reduce32(wbits, 0xffffffffu, [](uint32_t p, uint32_t q) { return p < q ? p : q; }));
+    // 6. could a logit outside the selection tie with w_b?
+    const uint32_t xk = max(ub_key, below != 0ull ? cand_skey(below) : 0u);
+    if (w_b > 0.f && xk > kKeyNegInf && exact_expf(key_to_s(xk, cfg.t_eff) - M) == w_b) status = 1u;
+    // 7. rank order: weights are monotone in the key, so in key order they
+    //    are the rank order unless two neighbours weigh the same (then, and
+    //    for an unsorted selection, by counting: rank keys are distinct,
+    //    each entry moved to the lane of its rank)
+    uint64_t yr[1] = {rk};
+    uint32_t yp = pk;
+    const uint32_t wprev = dpp32<0x138, 0xf, true>(0u, wbits);  // wave_shr:1: lane l - 1's weight
+    if (!sorted || __ballot(lane >= 1u && (int)lane < kk && wbits == wprev) != 0ull) {
+      const uint64_t km = __ballot((int)lane < kk);
+      const uint32_t r = wave_rank_desc(rk, km);
+      const int to = (int)lane < kk ? (int)(r * 4u) : 63 * 4;  // the other lanes write past kk or nowhere
+      const uint32_t ylo = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)(uint32_t)rk);
+      const uint32_t yhi = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)(uint32_t)(rk >> 32));
+      yp = (uint32_t)__builtin_amdgcn_ds_permute(to, (int)pk);
+      yr[0] = (int)lane < kk ? ((uint64_t)yhi << 32) | ylo : 0ull;
+    }
+    if ((int)lane < kk) {
+      fs.buf[lane] = yr[0];
+      fs.pay[lane] = yp;
+    }
+    // 8. the draw (gpu.rs:831-899)
+    int pick = -1;
+    if (status == 0u) {
+      pick = wave_draw_r<1>(yr, min(cfg.k_eff, kk), cfg);
+      if (pick < 0) status = 1u;  // argmax_host fallback
+    }
+    if (lane == 0u) {
+      if (status == 0u) a.out_tokens[row] = cand_idx(readlane64(yr[0], pick));
+      fs.flag = status;
+      fs.pick = pick;
+    }
+  } else if (want_lp) {
+    // the candidates' share of the logprob normaliser, in double
+    for (int j = tid - 64; j < n; j += NT - 64) {
+      const uint32_t kv = cand_skey(fs.cbig[j]);
+      if (kv > kKeyNegInf) part += exp((double)key_to_s(kv, cfg.t_eff) - (double)M);
+    }
+  }
+  if (want_lp) {
+    part = wave_sum_f64(part);
+    if (lane == 0u) fs.redd[wid] = part;
+  }
+  __syncthreads();
+  if (fs.flag != 0u) return false;
+  if (!want_lp) return true;
+  // 9. logprobs of the processed distribution (extension)
+  double tot = 0.0;
+  #pragma unroll
+  for (int v = 0; v < NT / 64; ++v) tot += fs.redd[v];
+  const double log_sum = log(tot);
+  const int N = a.n_lp;
+  for (int j = tid; j < N; j += NT) {
+    float lp = -__builtin_inff();
+    uint32_t id = 0xffffffffu;
+    if (j < kk) {
+      id = cand_idx(fs.buf[j]);
+      lp = (float)(((double)okey_inv(fs.pay[j]) - (double)M) - log_sum);
+    }
+    a.out_lp_ids[(int64_t)row * N + j] = id;
+    a.out_lp[(int64_t)row * N + j] = lp;
+  }
+  if (a.out_token_lp && tid == 0)
+    a.out_token_lp[row] = (float)(((double)okey_inv(fs.pay[fs.pick]) - (double)M) - log_sum);
+  return true;
+}
+
 // Steps 4-9 of the lean finish over the candidates fs.cbig[0, n) of `row`
 // (candidate keys, any order; n >= 1).  M is the row max of s; ub_key bounds
 // the processed-logit keys of the row's logits that are not candidates (0:
@@ -1689,6 +1919,8 @@ __device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int
 __device__ __forceinline__ bool finish_core(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, int n,
                                             float M, uint32_t ub_key, double part, uint32_t above = 0u,
                                             uint64_t lo = ~0ull, uint64_t hi = 0ull, bool one_wave_select = true) {
+  if (one_wave_select && min(cfg.k_sel, n) <= 64 && n <= 64 * kWavePer)
+    return finish_core_wave<kWavePer>(fs, a, row, cfg, n, M, ub_key, part, above, lo, hi);
   const int tid = threadIdx.x;
   const uint32_t lane = (uint32_t)tid & 63u;
   const bool want_lp = a.n_lp > 0 || a.out_token_lp != nullptr;

@@ -250,27 +250,6 @@ struct Exp2TabLds {
 // Why the min-p finish left a row to the general finish (0: it did not).
 enum MinpMiss : uint32_t { kMinpOk = 0, kMinpArray = 1, kMinpTopK = 2, kMinpDraw = 3 };
 
-// The rank (entries above it) of this lane's key among the wave's keys
-// (zero keys count for nothing): over the lanes of km one at a time, or,
-// for many, over all 64 lanes in an unrolled loop of independent compares.
-__device__ __forceinline__ uint32_t wave_rank_desc(uint64_t x, uint64_t km) {
-  uint32_t r = 0u;
-  if (__popcll(km) <= 16) {
-    for (uint64_t mm = km; mm != 0ull; mm &= mm - 1ull)
-      r += readlane64(x, __builtin_ctzll(mm)) > x ? 1u : 0u;
-    return r;
-  }
-  uint32_t r1 = 0u, r2 = 0u, r3 = 0u;
-  #pragma unroll
-  for (int j = 0; j < 64; j += 4) {
-    r += readlane64(x, j) > x ? 1u : 0u;
-    r1 += readlane64(x, j + 1) > x ? 1u : 0u;
-    r2 += readlane64(x, j + 2) > x ? 1u : 0u;
-    r3 += readlane64(x, j + 3) > x ? 1u : 0u;
-  }
-  return (r + r1) + (r2 + r3);
-}
-
 // The min-p finish of a support of at most 64 entries on one wave (see
 // above).  Tm is the largest list threshold of the row.  A miss (MinpMiss)
 // sends the row to the candidate lists' finish.

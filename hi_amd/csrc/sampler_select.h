@@ -212,19 +212,6 @@ __device__ __forceinline__ void block_tail3(uint64_t& mn, uint32_t& mx, float& s
 // Wave-level helpers
 // ==========================================================================
 
-// Orders this wave's LDS accesses (a wave executes its LDS operations in
-// order; this keeps the compiler from moving them across the point).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Number of set bits of m below the calling lane.
-__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
-  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-}
-
 // The largest key prefix with the low 12 bits clear that at least `need`
 // of the wave's group-maximum keys (four per lane) reach, or 0 when none
 // does: it is the need-th largest key with its low 12 bits cleared.  For

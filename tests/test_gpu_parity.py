@@ -871,3 +871,35 @@ def test_workspace_reuse_across_batch_sizes(hip, oracle):
         torch.cuda.synchronize()
         want = run_oracle(oracle, w)
         assert np.array_equal(out["tokens"].cpu().numpy().view(np.uint32), want["tokens"]), B
+
+
+@pytest.mark.parametrize("n_lp", [0, 64])
+def test_lean_finish_one_wave_select(hip, oracle, n_lp):
+    """The chunked finish's one-wave path (at most 64 selected candidates):
+    its select bounds the k-th key by the k-th largest of the lanes' maxima,
+    keeps the candidates that reach it, and ranks them among themselves when
+    at most 128 do (top-k 1: exactly k reach it; top-k 40: a few more;
+    top-k 64 on flat rows: too many, the full select); rows with tied
+    logits (equal weights, rank by index), with fewer candidates than k
+    (a short vocabulary), and with the top k in one chunk."""
+    from hi_amd.sampler import row_params
+    rng = np.random.default_rng(9100 + n_lp)
+    for V in (151936, 3000):
+        B = 10
+        x = rng.normal(0, 3.0, (B, V)).astype(F32)
+        x[1] = rng.normal(0, 0.02, V).astype(F32)          # nearly flat
+        x[2, rng.permutation(V)[:90]] = F32(9.5)            # 90 tied maxima
+        x[3, :] = np.round(x[3, :] * 4) / 4                # many equal logits
+        x[4, 300:340] += F32(25.0)                          # the top 40 in one chunk
+        x[5, rng.permutation(V)[:8]] += F32(12.0)
+        p = row_params(B, temperature=0.7, top_p=0.9, top_k=40)
+        p["top_k"] = [1, 64, 40, 63, 40, 2, 64, 40, 17, 50]
+        p["temperature"][6] = 3.0
+        p["top_p"][7] = 1.0
+        u = rng.random(B).astype(F32)
+        u[8] = 0.0
+        w = Workload(f"one-wave V={V} n_lp={n_lp}", x, p, u, n_logprobs=n_lp)
+        say(w.name)
+        got = run_gpu(w)
+        want = run_oracle(oracle, w)
+        compare(w, got, want, w.name)

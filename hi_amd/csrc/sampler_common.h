@@ -588,6 +588,8 @@ struct FinLds {
   uint32_t wmin;    // bits of the smallest selected weight
   uint64_t thr;     // the selection threshold of a one-wave select
   int pick;         // wg_draw's result
+  uint32_t nparts;  // finish_core_wave: waves that added their logprob share
+  double lsum;      // finish_core_wave: log of the logprob normaliser
 };
 constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
 
@@ -1801,7 +1803,8 @@ __device__ __forceinline__ bool finish_core_wave(FinLds& fs, const SampleArgs& a
       uint64_t lmx[1] = {0ull};
       #pragma unroll
       for (int m = 0; m < PER; ++m) lmx[0] = xr[m] > lmx[0] ? xr[m] : lmx[0];
-      const uint64_t g = wave_select_skip_r<1>(lmx, 64, (uint32_t)kk, fs.hist, ~0ull, 0ull);
+      wave_sort_desc<1>(lmx);
+      const uint64_t g = readlane64(lmx[0], kk - 1);
       const uint32_t n2 = wave_keep_into<PER>(xr, n, g, fs.buf);
       wave_lds_sync();
       if (n2 <= 64u) {
@@ -1874,24 +1877,30 @@ __device__ __forceinline__ bool finish_core_wave(FinLds& fs, const SampleArgs& a
       fs.pick = pick;
     }
   } else if (want_lp) {
-    // the candidates' share of the logprob normaliser, in double
+    // the candidates' share of the logprob normaliser, in double, added to
+    // the caller's share (wave 1's lanes); the last of these waves to end
+    // takes the log of the sum (fs.nparts is zero on entry)
     for (int j = tid - 64; j < n; j += NT - 64) {
       const uint32_t kv = cand_skey(fs.cbig[j]);
       if (kv > kKeyNegInf) part += exp((double)key_to_s(kv, cfg.t_eff) - (double)M);
     }
-  }
-  if (want_lp) {
     part = wave_sum_f64(part);
-    if (lane == 0u) fs.redd[wid] = part;
+    if (lane == 0u) {
+      fs.redd[wid] = part;
+      const uint32_t done = __hip_atomic_fetch_add(&fs.nparts, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (done == (uint32_t)(NT / 64 - 2)) {
+        double tot = 0.0;
+        #pragma unroll
+        for (int v = 1; v < NT / 64; ++v) tot += __hip_atomic_load(&fs.redd[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        fs.lsum = log(tot);
+      }
+    }
   }
   __syncthreads();
   if (fs.flag != 0u) return false;
   if (!want_lp) return true;
   // 9. logprobs of the processed distribution (extension)
-  double tot = 0.0;
-  #pragma unroll
-  for (int v = 0; v < NT / 64; ++v) tot += fs.redd[v];
-  const double log_sum = log(tot);
+  const double log_sum = fs.lsum;
   const int N = a.n_lp;
   for (int j = tid; j < N; j += NT) {
     float lp = -__builtin_inff();
@@ -2156,7 +2165,7 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   }
   const float M = finitef_(mx) ? mx / cfg.t_eff : -__builtin_inff();
   if (eos || !finitef_(M)) return false;
-  if (want_lp && tid < 64) {
+  if (want_lp && tid >= 64 && tid < 128) {  // wave 1 (finish_core_wave's first adder)
     #pragma unroll
     for (int q = 0; q < CQ; ++q) {
       const int c = q * 64 + (int)lane;
@@ -2180,17 +2189,25 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   if (tid < 64) {
     #pragma unroll
     for (int q = 0; q < CQ; ++q) if (q * 64 + (int)lane < nch) fs.aux[q * 64 + lane] = offq[q];
-    if (lane == 0u) fs.aux[nch] = n_total;
+    if (lane == 0u) {
+      fs.aux[nch] = n_total;
+      fs.nparts = 0u;
+    }
   }
   __syncthreads();
 
   // 2. the candidates into LDS (chunk-major): all loads first
   if (spec) {
+    // (every wave holds every chunk's offset and count: lane c of offq[0]
+    // and cnt[0], nch <= 64)
+    static_assert(kSpecChunks <= 64, "the early chunks' offsets sit in one register");
+    const int w0 = __builtin_amdgcn_readfirstlane(tid >> 6);
     #pragma unroll
     for (int i = 0; i < kSpecPer; ++i) {
-      const int c = (tid >> 6) + (NT / 64) * i;
+      const int c = w0 + (NT / 64) * i;
       if (c < nch) {
-        const uint32_t o = fs.aux[c], nc = fs.aux[c + 1] - o;
+        const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)offq[0], c);
+        const uint32_t nc = (uint32_t)__builtin_amdgcn_readlane((int)cnt[0], c);
         if (lane < nc) fs.cbig[o + lane] = sp[i];
         for (uint32_t j = 64u + lane; j < nc; j += 64u) fs.cbig[o + j] = cand[(int64_t)c * kFast + j];
       }

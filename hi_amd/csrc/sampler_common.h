@@ -567,6 +567,14 @@ struct ScanLds {
   // hash counts[kHashCap] follow
 };
 
+// exact_expf's table read from an LDS copy: in the tail of a launch a load
+// from global memory waits behind the other workgroups' streams, and after
+// an acquire fence it misses the emptied L2.
+struct Exp2TabLds {
+  const uint64_t* p;
+  __device__ uint64_t operator()(uint32_t i) const { return p[i]; }
+};
+
 struct FinLds {
   uint64_t cbig[kGather];     // gathered candidates (32 KiB) -- also a fold tile
   uint64_t buf[kBuf];         // selected candidates / rank keys
@@ -590,6 +598,7 @@ struct FinLds {
   int pick;         // wg_draw's result
   uint32_t nparts;  // finish_core_wave: waves that added their logprob share
   double lsum;      // finish_core_wave: log of the logprob normaliser
+  uint64_t exptab[32];  // finish_core_wave: exact_expf's table (finish_lean copies it)
 };
 constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
 
@@ -1733,7 +1742,8 @@ __device__ __forceinline__ uint32_t draw_topk(FinLds& fs, const RowCfg& cfg, int
 // logprobs are then written by every thread.  Same result as the
 // workgroup steps.  The select first bounds the kk-th key by the kk-th
 // largest of the lanes' maxima and, when at most 128 keys reach that bound,
-// selects among them on two slots.
+// sorts them in registers.  On entry fs.nparts is zero and fs.exptab holds
+// exact_expf's table (finish_lean sets both).
 constexpr int kWavePer = 20;  // candidates per lane of finish_core_wave (n <= 1280)
 
 // The keys of x[0, S) (entry m * 64 + lane in x[m], entries from n on
@@ -1834,9 +1844,10 @@ __device__ __forceinline__ bool finish_core_wave(FinLds& fs, const SampleArgs& a
     // 5. weights and rank keys; the smallest selected weight w_b
     uint64_t rk = 0ull;
     uint32_t pk = 0u, wbits = 0xffffffffu;
+    const Exp2TabLds tab{fs.exptab};
     if ((int)lane < kk) {
       const float sx = key_to_s(cand_skey(x), cfg.t_eff);
-      const float w = exact_expf(sx - M);
+      const float w = exact_expf_t(sx - M, tab);
       rk = rank_key(w, cand_idx(x));
       pk = okey(sx);
       wbits = __float_as_uint(w);
@@ -1844,7 +1855,7 @@ __device__ __forceinline__ bool finish_core_wave(FinLds& fs, const SampleArgs& a
     const float w_b = __uint_as_float(wave_reduce32(wbits, 0xffffffffu, [](uint32_t p, uint32_t q) { return p < q ? p : q; }));
     // 6. could a logit outside the selection tie with w_b?
     const uint32_t xk = max(ub_key, below != 0ull ? cand_skey(below) : 0u);
-    if (w_b > 0.f && xk > kKeyNegInf && exact_expf(key_to_s(xk, cfg.t_eff) - M) == w_b) status = 1u;
+    if (w_b > 0.f && xk > kKeyNegInf && exact_expf_t(key_to_s(xk, cfg.t_eff) - M, tab) == w_b) status = 1u;
     // 7. rank order: weights are monotone in the key, so in key order they
     //    are the rank order unless two neighbours weigh the same (then, and
     //    for an unsorted selection, by counting: rank keys are distinct,
@@ -1879,7 +1890,7 @@ __device__ __forceinline__ bool finish_core_wave(FinLds& fs, const SampleArgs& a
   } else if (want_lp) {
     // the candidates' share of the logprob normaliser, in double, added to
     // the caller's share (wave 1's lanes); the last of these waves to end
-    // takes the log of the sum (fs.nparts is zero on entry)
+    // takes the log of the sum
     for (int j = tid - 64; j < n; j += NT - 64) {
       const uint32_t kv = cand_skey(fs.cbig[j]);
       if (kv > kKeyNegInf) part += exp((double)key_to_s(kv, cfg.t_eff) - (double)M);
@@ -2097,6 +2108,7 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
   //    slots are candidates
   constexpr int kSpecPer = kSpecChunks / (NT / 64);
   const bool spec = nch <= kSpecChunks;
+  const uint64_t et = tid < 32 ? exp2_tab32((uint32_t)tid) : 0ull;  // for fs.exptab
   uint64_t sp[kSpecPer];
   if (spec) {
     #pragma unroll
@@ -2193,6 +2205,7 @@ __device__ __forceinline__ bool finish_lean(FinLds& fs, const SampleArgs& a, int
       fs.aux[nch] = n_total;
       fs.nparts = 0u;
     }
+    if (lane < 32u) fs.exptab[lane] = et;
   }
   __syncthreads();
 

@@ -240,13 +240,6 @@ __device__ __forceinline__ bool minp_topk_known(const uint64_t (&x)[S], int c, i
   return rank_w(v) > wT;
 }
 
-// exact_expf's table read from an LDS copy: in the tail of a launch a load
-// from global memory waits behind the other workgroups' streams.
-struct Exp2TabLds {
-  const uint64_t* p;
-  __device__ uint64_t operator()(uint32_t i) const { return p[i]; }
-};
-
 // Why the min-p finish left a row to the general finish (0: it did not).
 enum MinpMiss : uint32_t { kMinpOk = 0, kMinpArray = 1, kMinpTopK = 2, kMinpDraw = 3 };
 

@@ -376,6 +376,34 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
   return s;
 }
 
+// The 64-bit value of lane (lane ^ j), j a power of two below 64: DPP moves
+// within a 16-lane row for j <= 8 (quad_perm; row_shl/row_shr:4 and a
+// select; row_ror:8), ds_swizzle's xor mode across the rows of a 32-lane
+// half for j = 16, ds_bpermute across the halves for j = 32.  j is a
+// constant once the caller's loops are unrolled, so the switch folds.
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t v, int j) {
+  switch (j) {
+    case 1: return dpp32<kDppXor1>(v, v);
+    case 2: return dpp32<kDppXor2>(v, v);
+    case 4: {
+      const uint32_t up = dpp32<0x104>(v, v);  // row_shl:4: lane l gets lane l + 4
+      const uint32_t dn = dpp32<0x114>(v, v);  // row_shr:4: lane l gets lane l - 4
+      return (threadIdx.x & 4u) ? dn : up;
+    }
+    case 8: return dpp32<0x128>(v, v);         // row_ror:8: lane l gets lane (l + 8) mod 16 of its row
+    case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401f);  // and 0x1f, xor 0x10
+    default: return (uint32_t)__shfl_xor((int)v, 32, 64);
+  }
+}
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v, int j) {
+  return ((uint64_t)lane_xor32((uint32_t)(v >> 32), j) << 32) | lane_xor32((uint32_t)v, j);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
   const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
   const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
@@ -598,7 +626,7 @@ struct FinLds {
   int pick;         // wg_draw's result
   uint32_t nparts;  // finish_core_wave: waves that added their logprob share
   double lsum;      // finish_core_wave: log of the logprob normaliser
-  uint64_t exptab[32];  // finish_core_wave: exact_expf's table (finish_lean copies it)
+  uint64_t exptab[32];  // exact_expf's table (finish_lean and rank_candidates copy it)
 };
 constexpr int kTileFloats = kGather * 2;  // floats of the fold tile (cbig)
 
@@ -686,8 +714,8 @@ __device__ __forceinline__ void sort_ranked(FinLds& fs, int n) {
         const int o = j >> 2;  // partner lane: lane ^ o (same wave: 4 * 64 = 256 elements)
         #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint64_t y = shfl_xor_u64(x[r], o);
-          const uint32_t q = (uint32_t)__shfl_xor((int)p[r], o, 64);
+          const uint64_t y = lane_xor64(x[r], o);  // DPP within rows of 16 lanes
+          const uint32_t q = lane_xor32(p[r], o);
           bitonic_keep(x[r], p[r], y, q, 4 * tid + r, j, k);
         }
       } else {
@@ -766,25 +794,41 @@ __device__ __forceinline__ uint64_t row_select_exact(FinLds& fs, const SampleArg
 }
 
 // Number of candidates the chunks of `row` wrote.
-__device__ __forceinline__ int candidate_count(const SampleArgs& a, int row) {
-  const ChunkStat* stats = a.stats + (int64_t)row * a.n_chunks;
-  int n = 0;
-  for (int c = 0; c < a.n_chunks; ++c) n += (int)stats[c].n_cand;
-  return n;
-}
-
 // The exact first `kk` entries of the reference rank order (weight desc,
 // index asc) of `row`.  On return fs.buf[0..kk) holds rank keys in order and
 // fs.pay[0..kk) the scaled-logit keys; returns kk.  M is the row max of s.
+// *n_lds (when given) gets the number of the row's candidates when all of
+// them are in fs.cbig[0, n) in chunk order, else -1.
 __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg,
-                               int kk_req, float M) {
+                               int kk_req, float M, int* n_lds = nullptr) {
   const int tid = threadIdx.x;
   const int nch = a.n_chunks;
   const ChunkStat* stats = a.stats + (int64_t)row * nch;
-  const int n_total = candidate_count(a, row);
+  if (n_lds) *n_lds = -1;
+  // the chunks' candidate offsets, fs.aux[0, nch] when they fit (the chunk
+  // records are read once, all at a time)
+  const bool offs = nch < kBins;
+  uint32_t run = 0u;
+  for (int cb = 0; cb < nch; cb += NT) {
+    const int c = cb + tid;
+    const uint32_t n = c < nch ? stats[c].n_cand : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan_u32<NT>(n, fs.redu, &tot);
+    if (offs && c < nch) fs.aux[c] = run + ex;
+    run += tot;
+  }
+  if (offs && tid == 0) fs.aux[nch] = run;
+  __syncthreads();
+  const int n_total = (int)run;
   int kk = min(kk_req, n_total);
   if (kk <= 0) return 0;
   auto s_of = [&](uint64_t x) { return key_to_s(cand_skey(x), cfg.t_eff); };
+  // exact_expf's table from an LDS copy (after the finish's acquire fence a
+  // load of the constant table misses the emptied L2); the barrier after
+  // step 1 publishes it
+  if (tid < 32) fs.exptab[tid] = exp2_tab32((uint32_t)tid);
+  const Exp2TabLds et{fs.exptab};
+  auto wexp = [&](float x) { return exact_expf_t(x, et); };
   // 1. candidates into LDS: all of them when they fit, else those at or above
   //    t0, the largest chunk cut (the kk-th composite is at least every
   //    truncated chunk's smallest kept composite)
@@ -792,9 +836,32 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
   uint64_t below_max = 0;  // largest candidate left out of LDS
   int n_u;
   bool in_lds = true;
-  if (n_total <= kGather) {
+  if (n_total <= kGather && !offs) {
     for_each_candidate(a, row, [&](uint64_t x, int pos) { fs.cbig[pos] = x; });
     n_u = n_total;
+    if (n_lds) *n_lds = n_total;
+  } else if (n_total <= kGather) {
+    // every candidate, all loads issued before the stores
+    constexpr int kPer = kGather / NT;
+    const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
+    uint64_t v[kPer];
+    int c = 0;
+    #pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int i = tid + r * NT;
+      v[r] = 0ull;
+      if (i < n_total) {
+        while ((int)fs.aux[c + 1] <= i) ++c;
+        v[r] = cand[(int64_t)c * kFast + (i - (int)fs.aux[c])];
+      }
+    }
+    #pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int i = tid + r * NT;
+      if (i < n_total) fs.cbig[i] = v[r];
+    }
+    n_u = n_total;
+    if (n_lds) *n_lds = n_total;
   } else {
     for (int c = tid; c < nch; c += NT)
       if (stats[c].trunc && stats[c].min_kept > t0) t0 = stats[c].min_kept;
@@ -864,6 +931,7 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
     mn = block_min_u64<NT>(mn, fs.red64);
     const uint64_t kth = kk < n_total ? thr : mn;
     if (ub != 0u && cand_skey(kth) <= ub) {
+      if (n_lds) *n_lds = -1;  // (row_select_exact uses fs.cbig)
       kk = min(kk_req, a.V);
       uint64_t bm;
       thr = row_select_exact(fs, a, row, cfg, kk, &bm);
@@ -877,7 +945,7 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
   for (int i = tid; i < kk; i += NT) {
     const uint64_t x = fs.buf[i];
     const float sx = s_of(x);
-    const float w = exact_expf(sx - M);
+    const float w = wexp(sx - M);
     fs.buf[i] = rank_key(w, cand_idx(x));
     fs.pay[i] = okey(sx);
     wmin_bits = min(wmin_bits, __float_as_uint(w));
@@ -897,13 +965,13 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
   if (w_b > 0.f) {
     // (a) unselected candidates: weights are monotone in the key, so only if
     //     the largest of them ties
-    if (below_max != 0 && exact_expf(s_of(below_max) - M) == w_b) {
+    if (below_max != 0 && wexp(s_of(below_max) - M) == w_b) {
       if (in_lds) {
         for (int i = tid; i < n_u; i += NT) {
           const uint64_t x = fs.cbig[i];
           if (x >= thr) continue;
           const float sx = s_of(x);
-          const float w = exact_expf(sx - M);
+          const float w = wexp(sx - M);
           if (w == w_b) add_ext(w, cand_idx(x), sx);
         }
       }
@@ -911,7 +979,7 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
         for_each_candidate(a, row, [&](uint64_t x, int) {
           if (x >= thr || (in_lds && x >= t0)) return;  // selected, or seen in LDS
           const float sx = s_of(x);
-          const float w = exact_expf(sx - M);
+          const float w = wexp(sx - M);
           if (w == w_b) add_ext(w, cand_idx(x), sx);
         });
       }
@@ -925,7 +993,7 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
         const int c = cb + tid;
         if (c < nch) {
           const ChunkStat cs = stats[c];
-          if (cs.trunc && exact_expf(key_to_s(cs.unkept_key, cfg.t_eff) - M) == w_b)
+          if (cs.trunc && wexp(key_to_s(cs.unkept_key, cfg.t_eff) - M) == w_b)
             fs.aux[atomicAdd(&fs.counter, 1u)] = (uint32_t)c;
         }
       }
@@ -948,7 +1016,7 @@ __device__ __forceinline__ int rank_candidates(FinLds& fs, const SampleArgs& a, 
           const uint64_t ck = cand_key(kl, (uint32_t)e);
           if (ck >= cs.min_kept || ck >= thr) continue;  // a candidate, or selected
           const float sx = key_to_s(kl, cfg.t_eff);
-          const float w = exact_expf(sx - M);
+          const float w = wexp(sx - M);
           if (w == w_b) add_ext(w, (uint32_t)e, sx);
         }
       }
@@ -1228,7 +1296,38 @@ __device__ __forceinline__ uint32_t row_argmax_total(FinLds& fs, const SampleArg
 }
 
 __device__ __forceinline__ void finish_logprobs(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t token,
-                                float M, bool eos, int ranked_k);
+                                float M, bool eos, int ranked_k, double log_sum_known = __builtin_nan(""));
+
+template <int DM>
+__device__ __forceinline__ int wave_draw(const uint64_t* keys, int k, const RowCfg& cfg);
+
+// This thread's share of the logprob normaliser relative to M, threads t0,
+// t0 + nt, ... of the row's work: the candidates of every chunk in double
+// (from fs.cbig[0, n_lds) when they are all there, n_lds >= 0, else from
+// the workspace), the other logits from each chunk's mass.
+__device__ __forceinline__ double logprob_part(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, float M,
+                                              int n_lds, int t0, int nt) {
+  double part = 0.0;
+  auto add = [&](uint64_t x) {
+    if (cand_skey(x) > kKeyNegInf) part += exp((double)key_to_s(cand_skey(x), cfg.t_eff) - (double)M);
+  };
+  const int nch = a.n_chunks;
+  const ChunkStat* stats = a.stats + (int64_t)row * nch;
+  if (n_lds >= 0) {
+    for (int i = t0; i < n_lds; i += nt) add(fs.cbig[i]);
+  } else {
+    const uint64_t* cand = a.cand + (int64_t)row * nch * kFast;
+    for (int c = 0; c < nch; ++c) {
+      const int n = (int)stats[c].n_cand;
+      for (int j = t0; j < n; j += nt) add(cand[(int64_t)c * kFast + j]);
+    }
+  }
+  for (int c = t0; c < nch; c += nt) {
+    const ChunkStat cs = stats[c];
+    if (cs.lse_sum > 0.f) part += (double)cs.lse_sum * exp((double)cs.lse_m - (double)M);
+  }
+  return part;
+}
 
 __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg) {
   const int tid = threadIdx.x;
@@ -1243,8 +1342,10 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
   const float u = cfg.u;
 
   const bool eos = a.mask && !rs.any_finite;
+  const bool want_lp = a.n_lp > 0 || a.out_token_lp != nullptr;
   uint32_t token;
   int ranked_k = 0;  // entries of fs.buf in rank order
+  double log_sum = __builtin_nan("");  // the logprob normaliser's log, once known
   if (eos) {
     token = cfg.eos;
   } else if (cfg.cls == kGreedy) {
@@ -1252,8 +1353,28 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
   } else if (!finitef_(M)) {
     token = cfg.cls == kTempOnly ? am_fin : row_argmax_total(fs, a, row, cfg);
   } else if (cfg.cls == kTopK && !cfg.store_s) {
-    ranked_k = rank_candidates(fs, a, row, cfg, cfg.k_sel, M);
-    token = draw_topk(fs, cfg, min(cfg.k_eff, ranked_k));
+    int n_lds = -1;
+    ranked_k = rank_candidates(fs, a, row, cfg, cfg.k_sel, M, &n_lds);
+    // the draw on wave 0 (gpu.rs:831-899); meanwhile the other waves add up
+    // the logprob normaliser
+    int pick = -1;
+    if (tid < 64) {
+      pick = wave_draw<kBuf / 64>(fs.buf, min(cfg.k_eff, ranked_k), cfg);
+      if (tid == 0) fs.pick = pick;
+    } else if (want_lp) {
+      double part = logprob_part(fs, a, row, cfg, M, n_lds, tid - 64, NT - 64);
+      part = wave_sum_f64(part);
+      if ((tid & 63) == 0) fs.redd[tid >> 6] = part;
+    }
+    __syncthreads();
+    pick = fs.pick;
+    if (want_lp) {
+      double tot = 0.0;
+      #pragma unroll
+      for (int v = 1; v < NT / 64; ++v) tot += fs.redd[v];
+      log_sum = log(tot);
+    }
+    token = pick < 0 ? 0xffffffffu : cand_idx(fs.buf[pick]);
     if (token == 0xffffffffu) token = row_argmax_total(fs, a, row, cfg);
   } else if (cfg.cls == kTempOnly) {
     token = draw_temp_only(fs, a, row, M, u, am_fin);
@@ -1262,9 +1383,9 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
     if (token == 0xffffffffu) token = row_argmax_total(fs, a, row, cfg);
   }
   if (tid == 0) a.out_tokens[row] = token;
-  if (a.n_lp <= 0 && !a.out_token_lp) return;
+  if (!want_lp) return;
   __syncthreads();
-  finish_logprobs(fs, a, row, cfg, token, M, eos, ranked_k);
+  finish_logprobs(fs, a, row, cfg, token, M, eos, ranked_k, log_sum);
 }
 
 // Logprobs of the processed distribution (extension) once the row's token
@@ -1273,7 +1394,7 @@ __device__ __forceinline__ void finish_row(FinLds& fs, const SampleArgs& a, int 
 // order (0: none yet).  The normaliser sums the candidates of every chunk
 // in double and the other logits from each chunk's mass.
 __device__ __forceinline__ void finish_logprobs(FinLds& fs, const SampleArgs& a, int row, const RowCfg& cfg, uint32_t token,
-                                float M, bool eos, int ranked_k) {
+                                float M, bool eos, int ranked_k, double log_sum_known) {
   const int tid = threadIdx.x;
   const int V = a.V;
   const int N = a.n_lp;
@@ -1286,17 +1407,9 @@ __device__ __forceinline__ void finish_logprobs(FinLds& fs, const SampleArgs& a,
     return;
   }
   if (N > 0 && ranked_k < N) ranked_k = rank_candidates(fs, a, row, cfg, N, M);
-  // log of the normaliser relative to M: the candidates of every chunk in
-  // double, the other logits from each chunk's mass
-  double part = 0.0;
-  for_each_candidate(a, row, [&](uint64_t x, int) {
-    if (cand_skey(x) > kKeyNegInf) part += exp((double)key_to_s(cand_skey(x), cfg.t_eff) - (double)M);
-  });
-  for (int c = tid; c < a.n_chunks; c += NT) {
-    const ChunkStat cs = a.stats[(int64_t)row * a.n_chunks + c];
-    if (cs.lse_sum > 0.f) part += (double)cs.lse_sum * exp((double)cs.lse_m - (double)M);
-  }
-  const double log_sum = log(block_sum_f64<NT>(part, fs.redd));
+  const double log_sum = log_sum_known == log_sum_known
+                             ? log_sum_known
+                             : log(block_sum_f64<NT>(logprob_part(fs, a, row, cfg, M, -1, tid, NT), fs.redd));
   for (int j = tid; j < N; j += NT) {
     float lp = -__builtin_inff();
     uint32_t id = 0xffffffffu;
@@ -1622,33 +1735,6 @@ __device__ __forceinline__ int wave_draw(const uint64_t* keys, int k, const RowC
   return wave_draw_r<DM>(kr, k, cfg);
 }
 
-// The 64-bit value of lane (lane ^ j), j a power of two below 64: DPP moves
-// within a 16-lane row for j <= 8 (quad_perm; row_shl/row_shr:4 and a
-// select; row_ror:8), ds_swizzle's xor mode across the rows of a 32-lane
-// half for j = 16, ds_bpermute across the halves for j = 32.  j is a
-// constant once the caller's loops are unrolled, so the switch folds.
-__device__ __forceinline__ uint32_t lane_xor32(uint32_t v, int j) {
-  switch (j) {
-    case 1: return dpp32<kDppXor1>(v, v);
-    case 2: return dpp32<kDppXor2>(v, v);
-    case 4: {
-      const uint32_t up = dpp32<0x104>(v, v);  // row_shl:4: lane l gets lane l + 4
-      const uint32_t dn = dpp32<0x114>(v, v);  // row_shr:4: lane l gets lane l - 4
-      return (threadIdx.x & 4u) ? dn : up;
-    }
-    case 8: return dpp32<0x128>(v, v);         // row_ror:8: lane l gets lane (l + 8) mod 16 of its row
-    case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401f);  // and 0x1f, xor 0x10
-    default: return (uint32_t)__shfl_xor((int)v, 32, 64);
-  }
-}
-__device__ __forceinline__ uint64_t lane_xor64(uint64_t v, int j) {
-  return ((uint64_t)lane_xor32((uint32_t)(v >> 32), j) << 32) | lane_xor32((uint32_t)v, j);
-}
-__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
-  return ((uint64_t)hi << 32) | lo;
-}
 
 // The rank (entries above it) of this lane's key among the wave's keys
 // (zero keys count for nothing): over the lanes of km one at a time, or,

@@ -54,6 +54,7 @@ struct WideScanLds {
 // wide_w_off.
 struct WideChunkLds {
   WideScanLds fl;
+  uint64_t exptab[32];                   // exact_expf's table (wide_row_stats copies it)
   unsigned long long gmass[kWideGBins];  // wide_row_stats
   unsigned long long predfx, ownfx;
   float w_lo;
@@ -175,6 +176,7 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
   }
   if (tid < kWideGBins) L.gmass[tid] = 0ull;
   if (tid == 0) { L.predfx = 0ull; L.ownfx = 0ull; }
+  if (tid < 32) L.exptab[tid] = exp2_tab32((uint32_t)tid);
   mk = block_max_u32<NT>(mk, L.fl.wcnt);
   bad = block_max_u32<NT>(bad, L.fl.wcnt);
   const float ml = okey_inv(mk);
@@ -258,10 +260,12 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
   return r;
 }
 
-// w[wide_pad(i)] = the weight of scaled logit s[i] (exact expf; min-p
-// zeros it), i < len: all of a thread's loads of a block are issued before
-// any is used.
-__device__ __forceinline__ void wide_weights(const float* s, int len, float M, float min_p, float* w) {
+// w[wide_pad(i)] = the weight of scaled logit s[i] (exact expf, its table
+// read from LDS; min-p zeros it), i < len: all of a thread's loads of a
+// block are issued before any is used.
+__device__ __forceinline__ void wide_weights(const float* s, int len, float M, float min_p, float* w,
+                                             const uint64_t* tab) {
+  const Exp2TabLds et{tab};
   constexpr int kB = 8;
   for (int base = 0; base < len; base += kB * NT) {
     float v[kB];
@@ -273,7 +277,7 @@ __device__ __forceinline__ void wide_weights(const float* s, int len, float M, f
     #pragma unroll
     for (int k = 0; k < kB; ++k) {
       const int i = base + k * NT + (int)threadIdx.x;
-      const float x = exact_expf(v[k] - M);
+      const float x = exact_expf_t(v[k] - M, et);
       if (i < len) w[wide_pad(i)] = x < min_p ? 0.f : x;  // min-p: excluded like a zero weight
     }
   }
@@ -383,7 +387,7 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
   const int len = min(a.chunk, a.V - c0);
   float* w = reinterpret_cast<float*>(lds_raw + wide_w_off(a.chunk));
   const float* srow = a.ws_s + (int64_t)row * a.V + c0;
-  wide_weights(srow, len, M, cfg.min_p, w);
+  wide_weights(srow, len, M, cfg.min_p, w, L.exptab);
   for (int h = tid; h < kWideChunkHash; h += NT) { L.hkey[h] = 0u; L.hcnt[h] = 0u; L.hmin[h] = 0xffffffffu; }
   if (tid == 0) { L.nrun = 0u; L.ovf = 0u; }
   __syncthreads();

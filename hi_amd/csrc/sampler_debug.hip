@@ -98,7 +98,9 @@ __global__ void __launch_bounds__(NT) debug_processed_kernel(SampleArgs a, float
   for (int e = c0 + tid; e < c1; e += NT) {
     float l = load_raw(a.logits, a.dtype, rbase + e);
     if (!allowed(a, row, (uint32_t)e)) l = -__builtin_inff();
-    if (pen) l = apply_penalties(l, cnt[e - c0], cfg);
+    // the form the row kernel uses (the branch-free one without a
+    // repetition penalty), so that the check covers both
+    if (pen) l = cfg.rep_on ? apply_penalties(l, cnt[e - c0], cfg) : apply_penalties_norep(l, cnt[e - c0], cfg);
     out_proc[(int64_t)row * V + e] = l;
     const float s = finitef_(l) ? l / cfg.t_eff : -__builtin_inff();
     st.max_l = fmaxf(st.max_l, s);

@@ -630,36 +630,51 @@ __device__ __forceinline__ bool row_stream(RowLds& L, const SampleArgs& a, int r
     if (MASK) hmw[r] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ms, (int)((hid[r] >> 5) * 4u), 0, 0);
   }
 
-  // 5. the rest of the row, tiles 2, 3, ... (the last pass may run past it)
-  const int npass = (ntiles + 1) / 2;
-  for (int p = 1; p < npass; ++p) {
-    step(Slot0{}, 2 * p, false);
-    step(Slot1{}, 2 * p + 1, false);
-  }
-  if (lane == 0u) {
-    L.wthr[wid] = T;
-    L.wbad[wid] = bad ? 1u : 0u;
-    L.wcnt[wid] = wn;
-  }
+  // the penalties of this thread's history entries held in registers
+  // (their logits and mask words arrive behind tiles 2 and 3, so applying
+  // them after the first pass below waits for nothing the stream needs)
   uint32_t hk[kRowHistPer];  // processed keys of this thread's history entries
   #pragma unroll
   for (int r = 0; r < kRowHistPer; ++r) hk[r] = kKeyNegInf;
-  if (hist) {
-    auto put = [&](uint32_t id, uint32_t raw) {
-      const uint2 h = hw[id >> 5];
-      const uint32_t rank = h.y + (uint32_t)__popc(h.x & ((1u << (id & 31u)) - 1u));
-      const float l = __uint_as_float(raw);
-      const uint32_t c = L.ob_cnt[rank];
-      const uint32_t k = lkey(cfg.rep_on ? apply_penalties(l, c, cfg) : apply_penalties_norep(l, c, cfg));
-      L.ob_raw[rank] = k;
-      return k;
-    };
-    constexpr uint32_t kNegInfBits = 0xff800000u;
+  auto put = [&](uint32_t id, uint32_t raw) {
+    const uint2 h = hw[id >> 5];
+    const uint32_t rank = h.y + (uint32_t)__popc(h.x & ((1u << (id & 31u)) - 1u));
+    const float l = __uint_as_float(raw);
+    const uint32_t c = L.ob_cnt[rank];
+    const uint32_t k = lkey(cfg.rep_on ? apply_penalties(l, c, cfg) : apply_penalties_norep(l, c, cfg));
+    L.ob_raw[rank] = k;
+    return k;
+  };
+  constexpr uint32_t kNegInfBits = 0xff800000u;
+  auto put_registers = [&]() {
+    if (!hist) return;
     #pragma unroll
     for (int r = 0; r < kRowHistPer; ++r) {
       if (hid[r] < (uint32_t)V)
         hk[r] = put(hid[r], MASK && !((hmw[r] >> (hid[r] & 31u)) & 1u) ? kNegInfBits : hraw[r]);
     }
+  };
+
+  // 5. the rest of the row, tiles 2, 3, ... (the last pass may run past
+  //    it); the first pass is peeled so that the history entries' wait
+  //    names exactly the loads before them
+  const int npass = (ntiles + 1) / 2;
+  if (npass > 1) {
+    step(Slot0{}, 2, false);
+    step(Slot1{}, 3, false);
+    put_registers();
+  }
+  for (int p = 2; p < npass; ++p) {
+    step(Slot0{}, 2 * p, false);
+    step(Slot1{}, 2 * p + 1, false);
+  }
+  if (npass <= 1) put_registers();
+  if (lane == 0u) {
+    L.wthr[wid] = T;
+    L.wbad[wid] = bad ? 1u : 0u;
+    L.wcnt[wid] = wn;
+  }
+  if (hist) {
     for (uint32_t h = h0 + kFirst + (uint32_t)tid; h < h1; h += kRowThreads) {
       const uint32_t id = a.hids[h];
       if (id < (uint32_t)V) {

@@ -1885,9 +1885,9 @@ __device__ __forceinline__ bool finish_core_wave(FinLds& fs, const SampleArgs& a
     }
     // 4. the top kk by (processed logit desc, index asc) (keys are
     //    distinct), in lanes [0, kk) of y[0], sorted when `sorted`; below
-    //    is the largest key left out.  A first bound: a key that at least
-    //    kk of the lanes' maxima reach (every lane holds a key when n > kk;
-    //    the maxima are distinct), so at least kk keys reach it; when at
+    //    is the largest key left out.  A first bound: the kk-th largest of
+    //    the lanes' maxima (more than kk lanes hold a key when n > kk, and
+    //    their maxima are distinct), so at least kk keys reach it; when at
     //    most 128 do, they are sorted in registers
     uint64_t y[1] = {0ull};
     uint64_t below = 0ull;

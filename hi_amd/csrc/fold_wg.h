@@ -23,9 +23,48 @@
 #include <stdint.h>
 
 #include "exact_fold.h"
+#include "wave_ops.h"
 
 namespace hi_rocm {
 namespace fold {
+
+// Lane moves of a map or a double by a DPP control (wave_ops.h): a lane
+// with no source lane (or outside ROW_MASK) gets all-zero bits, which are
+// the identity map, a zero count and +0.0.
+template <int CTRL, int RM, bool BC>
+__device__ __forceinline__ Map dpp_map(Map m) {
+  return Map{dpp32<CTRL, RM, BC>(0u, m.t0), dpp32<CTRL, RM, BC>(0u, m.t1)};
+}
+template <int CTRL, int RM, bool BC>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint64_t r = ((uint64_t)dpp32<CTRL, RM, BC>(0u, (uint32_t)(b >> 32)) << 32) | dpp32<CTRL, RM, BC>(0u, (uint32_t)b);
+  return __longlong_as_double((long long)r);
+}
+// Inclusive scan in lane order (lane l: m_0, then m_1, ..., then m_l): four
+// row shifts within the 16-lane rows, then the row broadcasts of lanes 15
+// and 31; each step composes the lower lanes' part first.
+__device__ __forceinline__ Map wave_map_scan(Map m) {
+  m = compose(dpp_map<kDppShr1, 0xf, true>(m), m);
+  m = compose(dpp_map<kDppShr1 + 1, 0xf, true>(m), m);
+  m = compose(dpp_map<kDppShr1 + 3, 0xf, true>(m), m);
+  m = compose(dpp_map<kDppShr1 + 7, 0xf, true>(m), m);
+  m = compose(dpp_map<kDppBcast15, 0xa, false>(m), m);
+  m = compose(dpp_map<kDppBcast31, 0xc, false>(m), m);
+  return m;
+}
+// The value of the lane below (wave_shr:1; the identity at lane 0).
+__device__ __forceinline__ Map wave_map_prev(Map m) { return dpp_map<0x138, 0xf, true>(m); }
+// Inclusive prefix sum of doubles in lane order.
+__device__ __forceinline__ double wave_scan_f64(double v) {
+  v += dpp_f64<kDppShr1, 0xf, true>(v);
+  v += dpp_f64<kDppShr1 + 1, 0xf, true>(v);
+  v += dpp_f64<kDppShr1 + 3, 0xf, true>(v);
+  v += dpp_f64<kDppShr1 + 7, 0xf, true>(v);
+  v += dpp_f64<kDppBcast15, 0xa, false>(v);
+  v += dpp_f64<kDppBcast31, 0xc, false>(v);
+  return v;
+}
 
 constexpr int kWgSeg = 256;  // segments of one plan: a monotone prefix has <= 254 binades
 
@@ -50,7 +89,12 @@ struct WgLds {
   float acc;                // chain result
 };
 
-__device__ __forceinline__ double shfl_up_f64(double v, int d) { return __shfl_up(v, (unsigned)d, 64); }
+// A DPP control as a type (for the generic steps of a scan).
+template <int C, int RM, bool BC>
+struct DppStep {
+  static constexpr int c = C, rm = RM;
+  static constexpr bool bc = BC;
+};
 
 // Segmented combine: (f1, m1) then (f2, m2).
 __device__ __forceinline__ void seg_combine(uint32_t f1, Map m1, uint32_t& f2, Map& m2) {
@@ -96,12 +140,7 @@ __device__ __forceinline__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, i
   // 1. predicted binades from a prefix sum in double
   double my = 0.0;
   for (int r = r0; r < r1; ++r) my += (double)mult(r) * (double)term(r);
-  double inc = my;
-  #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const double o = shfl_up_f64(inc, d);
-    if (lane >= d) inc += o;
-  }
+  double inc = wave_scan_f64(my);
   if (lane == 63) L.dsum[wid] = inc;
   __syncthreads();
   double before = 0.0, all = 0.0;
@@ -123,12 +162,7 @@ __device__ __forceinline__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, i
   //     exact sum passes it, which would mispredict every later boundary)
   my = 0.0;
   for (int r = r0; r < r1; ++r) my += rounded_inc(term(r), mult(r), pe[r]);
-  inc = my;
-  #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const double o = shfl_up_f64(inc, d);
-    if (lane >= d) inc += o;
-  }
+  inc = wave_scan_f64(my);
   __syncthreads();
   if (lane == 63) L.dsum[wid] = inc;
   __syncthreads();
@@ -179,37 +213,39 @@ __device__ __forceinline__ void fold_plan(WgLds<NTH>& L, uint8_t* pe, int pos, i
   Map m = nbt ? tail : head;
   Map ma = nbt ? tail_a : head_a;
   uint32_t cnt = nbt;
-  #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t of = (uint32_t)__shfl_up((int)f, (unsigned)d, 64);
-    const Map om = Map{(uint32_t)__shfl_up((int)m.t0, (unsigned)d, 64), (uint32_t)__shfl_up((int)m.t1, (unsigned)d, 64)};
-    Map oa = map_identity();
-    if (ALT) oa = Map{(uint32_t)__shfl_up((int)ma.t0, (unsigned)d, 64), (uint32_t)__shfl_up((int)ma.t1, (unsigned)d, 64)};
-    const uint32_t oc = (uint32_t)__shfl_up((int)cnt, (unsigned)d, 64);
-    if (lane >= d) {
-      if (ALT && !f) ma = compose(oa, ma);
-      seg_combine(of, om, f, m);
-      cnt += oc;
+  // (DPP steps: a lane with no lane below combines with zero flags, the
+  // identity map and a zero count, which changes nothing)
+  auto step = [&](auto ctl) {
+    constexpr int C = decltype(ctl)::c, RM = decltype(ctl)::rm;
+    constexpr bool BC = decltype(ctl)::bc;
+    const uint32_t of = dpp32<C, RM, BC>(0u, f);
+    const Map om = dpp_map<C, RM, BC>(m);
+    const uint32_t oc = dpp32<C, RM, BC>(0u, cnt);
+    if (ALT) {
+      const Map oa = dpp_map<C, RM, BC>(ma);
+      if (!f) ma = compose(oa, ma);
     }
-  }
+    seg_combine(of, om, f, m);
+    cnt += oc;
+  };
+  step(DppStep<kDppShr1, 0xf, true>{});
+  step(DppStep<kDppShr1 + 1, 0xf, true>{});
+  step(DppStep<kDppShr1 + 3, 0xf, true>{});
+  step(DppStep<kDppShr1 + 7, 0xf, true>{});
+  step(DppStep<kDppBcast15, 0xa, false>{});
+  step(DppStep<kDppBcast31, 0xc, false>{});
   if (lane == 63) {
     L.wflag[wid] = f;
     L.wmap[wid] = m;
     if (ALT) L.walt[wid] = ma;
     L.wcnt[wid] = cnt;
   }
-  // exclusive: the inclusive value of the lane below
-  uint32_t ef = (uint32_t)__shfl_up((int)f, 1u, 64);
-  Map em = Map{(uint32_t)__shfl_up((int)m.t0, 1u, 64), (uint32_t)__shfl_up((int)m.t1, 1u, 64)};
+  // exclusive: the inclusive value of the lane below (zero at lane 0)
+  uint32_t ef = dpp32<0x138, 0xf, true>(0u, f);
+  Map em = wave_map_prev(m);
   Map ea = map_identity();
-  if (ALT) ea = Map{(uint32_t)__shfl_up((int)ma.t0, 1u, 64), (uint32_t)__shfl_up((int)ma.t1, 1u, 64)};
-  uint32_t ec = (uint32_t)__shfl_up((int)cnt, 1u, 64);
-  if (lane == 0) {
-    ef = 0u;
-    em = map_identity();
-    ea = map_identity();
-    ec = 0u;
-  }
+  if (ALT) ea = wave_map_prev(ma);
+  uint32_t ec = dpp32<0x138, 0xf, true>(0u, cnt);
   __syncthreads();
   uint32_t cf = 0u, cc = 0u, tot = 0u;
   Map cm = map_identity(), ca = map_identity();

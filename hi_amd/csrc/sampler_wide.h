@@ -220,11 +220,7 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
       }
       unsigned long long cs = fx;
       #pragma unroll
-      for (int o = 16; o > 0; o >>= 1) {
-        const unsigned long long y = ((unsigned long long)(uint32_t)__shfl_xor((int)(uint32_t)(cs >> 32), o, 64) << 32) |
-                                     (uint32_t)__shfl_xor((int)(uint32_t)cs, o, 64);
-        cs += y;
-      }
+      for (int o = 16; o > 0; o >>= 1) cs += lane_xor64(cs, o);
       if (j == 0 && it < items && it / kWideBins < chunk && cs != 0ull) atomicAdd(&L.predfx, cs);
       if (j == 0 && it < items && it / kWideBins == chunk) L.ownfx = cs;
     }
@@ -234,14 +230,20 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
   // cutoff plus the margin (one wave over the 64 bins)
   if (tid < 64) {
     const int lane = tid;
-    const unsigned long long v = L.gmass[lane];
-    unsigned long long inc = v;
-    #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const unsigned long long y = ((unsigned long long)(uint32_t)__shfl_up((int)(uint32_t)(inc >> 32), (unsigned)d, 64) << 32) |
-                                   (uint32_t)__shfl_up((int)(uint32_t)inc, (unsigned)d, 64);
-      if (lane >= d) inc += y;
-    }
+    // inclusive prefix sum over the lanes (DPP row shifts and broadcasts;
+    // lanes with no source add zero)
+    unsigned long long inc = L.gmass[lane];
+    auto up = [&](auto ctl) {
+      constexpr int C = decltype(ctl)::c, RM = decltype(ctl)::rm;
+      constexpr bool BC = decltype(ctl)::bc;
+      inc += ((unsigned long long)dpp32<C, RM, BC>(0u, (uint32_t)(inc >> 32)) << 32) | dpp32<C, RM, BC>(0u, (uint32_t)inc);
+    };
+    up(fold::DppStep<kDppShr1, 0xf, true>{});
+    up(fold::DppStep<kDppShr1 + 1, 0xf, true>{});
+    up(fold::DppStep<kDppShr1 + 3, 0xf, true>{});
+    up(fold::DppStep<kDppShr1 + 7, 0xf, true>{});
+    up(fold::DppStep<kDppBcast15, 0xa, false>{});
+    up(fold::DppStep<kDppBcast31, 0xc, false>{});
     const unsigned long long tot = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(inc >> 32), 63) << 32) |
                                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)inc, 63);
     const double frac = (double)cfg.cutoff + (double)kWideMargin;
@@ -260,11 +262,11 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
   return r;
 }
 
-// w[wide_pad(i)] = the weight of scaled logit s[i] (exact expf, its table
-// read from LDS; min-p zeros it), i < len: all of a thread's loads of a
-// block are issued before any is used.
+// w[wide_pad(i)] = wg[i] = the weight of scaled logit s[i] (exact expf, its
+// table read from LDS; min-p zeros it), i < len: all of a thread's loads of
+// a block are issued before any is used.
 __device__ __forceinline__ void wide_weights(const float* s, int len, float M, float min_p, float* w,
-                                             const uint64_t* tab) {
+                                             const uint64_t* tab, float* wg) {
   const Exp2TabLds et{tab};
   constexpr int kB = 8;
   for (int base = 0; base < len; base += kB * NT) {
@@ -277,8 +279,12 @@ __device__ __forceinline__ void wide_weights(const float* s, int len, float M, f
     #pragma unroll
     for (int k = 0; k < kB; ++k) {
       const int i = base + k * NT + (int)threadIdx.x;
-      const float x = exact_expf_t(v[k] - M, et);
-      if (i < len) w[wide_pad(i)] = x < min_p ? 0.f : x;  // min-p: excluded like a zero weight
+      float x = exact_expf_t(v[k] - M, et);
+      x = x < min_p ? 0.f : x;  // min-p: excluded like a zero weight
+      if (i < len) {
+        w[wide_pad(i)] = x;
+        wg[i] = x;
+      }
     }
   }
 }
@@ -295,22 +301,28 @@ __device__ __forceinline__ fold::Map term_map(float x, int e) {
   return m;
 }
 
+// f(x) for the terms x = w[wide_pad(r)], r in [r0, r1), in order.  The LDS
+// loads of 16 terms are issued together (a loop of single loads waits out
+// the LDS latency on every term).  Past r1 the terms read as -0.0, which a
+// fold and a map treat as no term at all: x + -0.0 == x for every x, and
+// term_map(-0.0, e) is the identity.
+template <typename F>
+__device__ __forceinline__ void wide_terms(const float* w, int r0, int r1, F f) {
+  for (int g = r0; g < r1; g += 16) {
+    float t[16];
+    #pragma unroll
+    for (int k = 0; k < 16; ++k) t[k] = g + k < r1 ? w[wide_pad(g + k)] : -0.0f;
+    #pragma unroll
+    for (int k = 0; k < 16; ++k) f(t[k]);
+  }
+}
+
 // Exclusive scan of maps over the workgroup in thread order; *tot gets the
 // composition of all.  Two barriers.
 __device__ __forceinline__ fold::Map block_map_scan(fold::Map m, fold::Map* wm, fold::Map* tot) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  fold::Map inc = m;
-  #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    fold::Map o;
-    o.t0 = (uint32_t)__shfl_up((int)inc.t0, (unsigned)d, 64);
-    o.t1 = (uint32_t)__shfl_up((int)inc.t1, (unsigned)d, 64);
-    if (lane >= d) inc = fold::compose(o, inc);
-  }
-  fold::Map ex;
-  ex.t0 = (uint32_t)__shfl_up((int)inc.t0, 1u, 64);
-  ex.t1 = (uint32_t)__shfl_up((int)inc.t1, 1u, 64);
-  if (lane == 0) ex = fold::map_identity();
+  const fold::Map inc = fold::wave_map_scan(m);
+  const fold::Map ex = fold::wave_map_prev(inc);
   __syncthreads();
   if (lane == 63) wm[wid] = inc;
   __syncthreads();
@@ -343,8 +355,7 @@ __device__ __forceinline__ float exact_chunk_fold(const float* w, int len, float
     const int e = fold::binade(a);
     const uint32_t A = fold::to_A(a);
     fold::Map m = fold::map_identity();
-    if (tid >= pos)
-      for (int r = r0; r < r1; ++r) m = fold::compose(m, term_map(w[wide_pad(r)], e));
+    if (tid >= pos) wide_terms(w, r0, r1, [&](float x) { m = fold::compose(m, term_map(x, e)); });
     fold::Map tot;
     const fold::Map ex = block_map_scan(m, wm, &tot);
     const uint32_t p = A & 1u;
@@ -360,7 +371,7 @@ __device__ __forceinline__ float exact_chunk_fold(const float* w, int len, float
       // At < kTop: the blocks before this one stayed in the binade
       float x = fold::from_A((uint32_t)At, e);
       const int stop = min(len, (tid + kSeqBlocks) * J);
-      for (int r = r0; r < stop; ++r) x = fold::fadd(x, w[wide_pad(r)]);
+      wide_terms(w, r0, stop, [&](float t) { x = fold::fadd(x, t); });
       shf[0] = x;
     }
     __syncthreads();
@@ -387,15 +398,11 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
   const int len = min(a.chunk, a.V - c0);
   float* w = reinterpret_cast<float*>(lds_raw + wide_w_off(a.chunk));
   const float* srow = a.ws_s + (int64_t)row * a.V + c0;
-  wide_weights(srow, len, M, cfg.min_p, w, L.exptab);
+  // the weights, in LDS and (for the finish's exact refolds) in ws_w
+  wide_weights(srow, len, M, cfg.min_p, w, L.exptab, a.ws_w + (int64_t)row * a.V + c0);
   for (int h = tid; h < kWideChunkHash; h += NT) { L.hkey[h] = 0u; L.hcnt[h] = 0u; L.hmin[h] = 0xffffffffu; }
   if (tid == 0) { L.nrun = 0u; L.ovf = 0u; }
   __syncthreads();
-  // the weights for the finish's exact refolds
-  {
-    float* wg = a.ws_w + (int64_t)row * a.V + c0;
-    for (int i = tid; i < len; i += NT) wg[i] = w[wide_pad(i)];
-  }
   // the chunk's part of the vocabulary-order fold: chunk 0 starts from the
   // known -0.0 and folds exactly; the others give their maps in the
   // binades around the predicted start
@@ -411,7 +418,7 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
     const int J = (len + NT - 1) / NT;
     const int r0 = min(tid * J, len), r1 = min(r0 + J, len);
     fold::Map m1 = fold::map_identity();
-    for (int r = r0; r < r1; ++r) m1 = fold::compose(m1, term_map(w[wide_pad(r)], ep));
+    wide_terms(w, r0, r1, [&](float x) { m1 = fold::compose(m1, term_map(x, ep)); });
     fold::Map t1;
     block_map_scan(m1, L.fl.wmap, &t1);
     if (tid == 0) {
@@ -427,12 +434,11 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
     const int J = (len + NT - 1) / NT;
     const int r0 = min(tid * J, len), r1 = min(r0 + J, len);
     fold::Map m0 = fold::map_identity(), m1 = m0, m2 = m0;
-    for (int r = r0; r < r1; ++r) {
-      const float x = w[wide_pad(r)];
+    wide_terms(w, r0, r1, [&](float x) {
       m0 = fold::compose(m0, term_map(x, e0));
       m1 = fold::compose(m1, term_map(x, e0 + 1));
       m2 = fold::compose(m2, term_map(x, e0 + 2));
-    }
+    });
     // each thread's block maps, for the finish's crossing search
     fold::Map* bm = a.wbmap + ((int64_t)row * a.n_chunks + chunk) * 3 * NT;
     bm[tid] = m0;
@@ -467,7 +473,7 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
         ex = kx == 0 ? ex0 : ex1;
       } else {
         mb = fold::map_identity();
-        for (int r = q0; r < r1; ++r) mb = fold::compose(mb, term_map(w[wide_pad(r)], ec));
+        wide_terms(w, q0, r1, [&](float x) { mb = fold::compose(mb, term_map(x, ec)); });
         fold::Map tot;
         ex = block_map_scan(mb, L.fl.wmap, &tot);
       }
@@ -475,11 +481,13 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
       int tstar = -1;
       if (q0 < r1 && Ab < fold::kTop && Ab + fold::apply(mb, (uint32_t)Ab & 1u) >= fold::kTop) {
         uint32_t A = (uint32_t)Ab;
-        for (int r = q0; r < r1; ++r) {
-          const uint32_t t = fold::apply(term_map(w[wide_pad(r)], ec), A & 1u);
-          if ((uint64_t)A + t >= fold::kTop) { tstar = r; break; }
-          A += t;
-        }
+        int r = q0;
+        wide_terms(w, q0, r1, [&](float x) {
+          const uint32_t t = fold::apply(term_map(x, ec), A & 1u);
+          if (tstar < 0 && (uint64_t)A + t >= fold::kTop) tstar = r;
+          A += tstar < 0 ? t : 0u;
+          ++r;
+        });
       }
       tstar = (int)block_max_u32<NT>((uint32_t)(tstar + 1), L.fl.wcnt) - 1;
       if (tstar < 0) break;
@@ -487,7 +495,7 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
       const int we = min(len, ws + kCrossTerms);
       // segment [p0, ws) in binade ec
       fold::Map mp = fold::map_identity();
-      for (int r = q0; r < min(r1, ws); ++r) mp = fold::compose(mp, term_map(w[wide_pad(r)], ec));
+      wide_terms(w, q0, min(r1, ws), [&](float x) { mp = fold::compose(mp, term_map(x, ec)); });
       fold::Map sg;
       block_map_scan(mp, L.fl.wmap, &sg);
       if (tid < we - ws) cf->term[wdx][tid] = w[wide_pad(ws + tid)];
@@ -495,7 +503,7 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
       if (tid == 0) {
         const uint64_t A1 = (uint64_t)Ac + fold::apply(sg, Ac & 1u);
         float v = A1 < fold::kTop ? fold::from_A((uint32_t)A1, ec) : __builtin_nanf("");
-        for (int r = ws; r < we; ++r) v = fold::fadd(v, w[wide_pad(r)]);
+        wide_terms(w, ws, we, [&](float t) { v = fold::fadd(v, t); });
         L.fend = v;
         cf->be[wdx] = (uint32_t)ec;
         cf->wn[wdx] = (uint32_t)(we - ws);
@@ -514,7 +522,7 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
       // the last segment [p0, len) in binade ec
       const int q0 = max(r0, p0);
       fold::Map ms = fold::map_identity();
-      for (int r = q0; r < r1; ++r) ms = fold::compose(ms, term_map(w[wide_pad(r)], ec));
+      wide_terms(w, q0, r1, [&](float x) { ms = fold::compose(ms, term_map(x, ec)); });
       fold::Map sg;
       block_map_scan(ms, L.fl.wmap, &sg);
       if (tid == 0) {
@@ -528,10 +536,19 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
   constexpr int kLog2 = 11;
   static_assert((1 << kLog2) == kWideChunkHash, "hash size");
   bool full = false;
-  for (int i = tid; i < len; i += NT) {
-    const float x = w[wide_pad(i)];
-    if (x > 0.f && x >= w_lo)
-      full |= !wide_insert(L.hkey, L.hcnt, L.hmin, kLog2, __float_as_uint(x), 1u, (uint32_t)i);
+  for (int base = 0; base < len; base += 16 * NT) {
+    float v[16];
+    #pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int i = base + k * NT + tid;
+      v[k] = i < len ? w[wide_pad(i)] : 0.f;
+    }
+    #pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int i = base + k * NT + tid;
+      if (v[k] > 0.f && v[k] >= w_lo)
+        full |= !wide_insert(L.hkey, L.hcnt, L.hmin, kLog2, __float_as_uint(v[k]), 1u, (uint32_t)i);
+    }
   }
   if (full) L.ovf = 1u;
   __syncthreads();
@@ -609,18 +626,8 @@ __device__ __forceinline__ float wide_cross_wave(const SampleArgs& a, int row, i
       bl[q] = b >= bstart ? bm[k * NT + b] : fold::map_identity();
       mine = fold::compose(mine, bl[q]);
     }
-    fold::Map inc = mine;
-    #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      fold::Map o;
-      o.t0 = (uint32_t)__shfl_up((int)inc.t0, (unsigned)d, 64);
-      o.t1 = (uint32_t)__shfl_up((int)inc.t1, (unsigned)d, 64);
-      if (lane >= d) inc = fold::compose(o, inc);
-    }
-    fold::Map ex;
-    ex.t0 = (uint32_t)__shfl_up((int)inc.t0, 1u, 64);
-    ex.t1 = (uint32_t)__shfl_up((int)inc.t1, 1u, 64);
-    if (lane == 0) ex = fold::map_identity();
+    const fold::Map inc = fold::wave_map_scan(mine);
+    const fold::Map ex = fold::wave_map_prev(inc);
     const uint32_t A = fold::to_A(x), p = A & 1u;
     const uint64_t cross = __ballot((uint64_t)A + fold::apply(inc, p) >= fold::kTop);
     if (cross == 0ull) {
@@ -722,14 +729,7 @@ __device__ __forceinline__ float wide_wave_chain(const ChunkFold* batch, int cb,
     if (!ok_l) m = fold::Map{fold::kSat, fold::kSat};
     if (lane < i0) m = fold::map_identity();
     // inclusive scan over the lanes: the increment after each chunk
-    fold::Map inc = m;
-    #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      fold::Map o;
-      o.t0 = (uint32_t)__shfl_up((int)inc.t0, (unsigned)d, 64);
-      o.t1 = (uint32_t)__shfl_up((int)inc.t1, (unsigned)d, 64);
-      if (lane >= d) inc = fold::compose(o, inc);
-    }
+    const fold::Map inc = fold::wave_map_scan(m);
     const uint64_t Ai = (uint64_t)A + fold::apply(inc, A & 1u);
     const uint64_t bad = __ballot(lane >= i0 && lane < n && Ai >= fold::kTop);
     if (bad == 0ull) {

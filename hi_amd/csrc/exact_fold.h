@@ -94,25 +94,24 @@ struct Inc {
   uint32_t n;
   uint32_t cls;
 };
+// Both cases are computed and one is selected (no branches): d <= 0 is an
+// integer number of ulps (X < 2^24, so three shifts reach kSat and X << 3
+// stays below 2^27); for d >= 1 the shift is clamped to 25, where X >> 25
+// is 0 and the remainder X is below the half 2^24 (a term below a quarter
+// ulp adds nothing).
 HRF_HD Inc classify(float x, int e) {
   const uint32_t b = fbits(x) & 0x7fffffffu;
   const int ex = (int)(b >> 23);
   const uint32_t X = ex ? ((b & 0x7fffffu) | 0x800000u) : b;
   const int d = e - (ex ? ex : 1);
+  const int sh = d >= 0 ? 0 : (-d > 3 ? 3 : -d);
+  const uint32_t up = X << sh;
+  const int ds = d < 1 ? 1 : (d > 25 ? 25 : d);
+  const uint32_t rem = X & ((1u << ds) - 1u);
+  const uint32_t half = 1u << (ds - 1);
   Inc r;
-  if (d <= 0) {  // an integer number of ulps (X < 2^24: three shifts saturate)
-    const int sh = -d > 3 ? 3 : -d;
-    r.n = sat((uint64_t)X << sh);
-    r.cls = 0u;
-  } else if (d >= 25) {  // below a quarter ulp
-    r.n = 0u;
-    r.cls = 0u;
-  } else {
-    r.n = X >> d;
-    const uint32_t rem = X & ((1u << d) - 1u);
-    const uint32_t half = 1u << (d - 1);
-    r.cls = rem < half ? 0u : (rem == half ? 1u : 2u);
-  }
+  r.n = d <= 0 ? (up > kSat ? kSat : up) : X >> ds;
+  r.cls = d <= 0 ? 0u : (rem < half ? 0u : (rem == half ? 1u : 2u));
   return r;
 }
 
@@ -140,11 +139,15 @@ HRF_HD Map run_map(Inc c, uint32_t m) {
   r.t1 = c.cls == 1u ? ((c.n & 1u) ? sat(base - 1u) : sat(base + 1u)) : r.t0;
   return r;
 }
-// f, then g.
+// f, then g.  Map values are at most kSat + 2 (term maps add at most two
+// to a saturated count, every composition saturates), so the sums stay
+// below 2^28 in 32 bits.
 HRF_HD Map compose(Map f, Map g) {
   Map h;
-  h.t0 = sat((uint64_t)f.t0 + ((f.t0 & 1u) ? g.t1 : g.t0));
-  h.t1 = sat((uint64_t)f.t1 + ((f.t1 & 1u) ? g.t0 : g.t1));
+  const uint32_t a0 = f.t0 + ((f.t0 & 1u) ? g.t1 : g.t0);
+  const uint32_t a1 = f.t1 + ((f.t1 & 1u) ? g.t0 : g.t1);
+  h.t0 = a0 > kSat ? kSat : a0;
+  h.t1 = a1 > kSat ? kSat : a1;
   return h;
 }
 HRF_HD uint32_t apply(Map f, uint32_t p) { return p ? f.t1 : f.t0; }

@@ -737,6 +737,58 @@ __device__ __forceinline__ void sort_ranked(FinLds& fs, int n) {
   __syncthreads();
 }
 
+// Descending bitonic sort of the keys buf[0..n), n <= PER * NT, keys only
+// (zero pads them and sorts last; equal keys are equal values).  PER
+// consecutive elements per thread in registers: distances below PER inside
+// the thread, up to 32 * PER across the lanes of a wave (DPP, swizzle and
+// bpermute lane moves), 64 * PER and more through buf with barriers.  buf
+// has room for PER * NT keys; all of them are written.
+template <int PER>
+__device__ __forceinline__ void block_sort_desc(uint64_t* buf, int n) {
+  const int tid = threadIdx.x;
+  uint64_t x[PER];
+  #pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int i = PER * tid + r;
+    x[r] = i < n ? buf[i] : 0ull;
+  }
+  auto keep = [](uint64_t& v, uint64_t y, int i, int j, int k) {
+    const bool keep_max = ((i & k) == 0) == ((i & j) == 0);
+    const uint64_t hi = y > v ? y : v, lo = y > v ? v : y;
+    v = keep_max ? hi : lo;
+  };
+  #pragma unroll
+  for (int k = 2; k <= PER * NT; k <<= 1) {
+    #pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= 64 * PER) {
+        __syncthreads();
+        #pragma unroll
+        for (int r = 0; r < PER; ++r) buf[PER * tid + r] = x[r];
+        __syncthreads();
+        #pragma unroll
+        for (int r = 0; r < PER; ++r) {
+          const int i = PER * tid + r;
+          keep(x[r], buf[i ^ j], i, j, k);
+        }
+      } else if (j >= PER) {
+        #pragma unroll
+        for (int r = 0; r < PER; ++r) keep(x[r], lane_xor64(x[r], j / PER), PER * tid + r, j, k);
+      } else {
+        uint64_t y[PER];
+        #pragma unroll
+        for (int r = 0; r < PER; ++r) y[r] = x[r ^ j];
+        #pragma unroll
+        for (int r = 0; r < PER; ++r) keep(x[r], y[r], PER * tid + r, j, k);
+      }
+    }
+  }
+  __syncthreads();
+  #pragma unroll
+  for (int r = 0; r < PER; ++r) buf[PER * tid + r] = x[r];
+  __syncthreads();
+}
+
 // Calls f(key) with the candidate key (processed-logit key, index) of every
 // logit of `row` this thread owns, recomputing the processed logits: tiles
 // of 2048 logits with an LDS count table of the row's history (cnt has

@@ -769,19 +769,28 @@ __device__ __forceinline__ void wide_for_each_run(WideFinLds& W, const SampleArg
     for (uint32_t base = 0; base < tot; base += kU * NT) {
       uint64_t v[kU];
       int cc[kU];
+      // the last block whose offset is <= p, by a search of fixed steps
+      // (the kU searches interleave; a data-dependent loop would run them
+      // one after another, each step an LDS round trip)
+      int lo[kU];
+      #pragma unroll
+      for (int k = 0; k < kU; ++k) lo[k] = 0;
+      #pragma unroll
+      for (int st = NT / 2; st >= 1; st >>= 1) {
+        #pragma unroll
+        for (int k = 0; k < kU; ++k) {
+          const uint32_t p = base + (uint32_t)(k * NT + tid);
+          lo[k] = W.noff[lo[k] + st] <= p ? lo[k] + st : lo[k];
+        }
+      }
       #pragma unroll
       for (int k = 0; k < kU; ++k) {
         const uint32_t p = base + (uint32_t)(k * NT + tid);
         cc[k] = -1;
         if (p < tot) {
-          int lo = 0, hi = NT - 1;  // the last block whose offset is <= p
-          while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (W.noff[mid] <= p) lo = mid; else hi = mid - 1;
-          }
-          const uint64_t* src = a.ws_list + (int64_t)row * a.list_stride + (int64_t)(cb + lo) * a.chunk;
-          cc[k] = cb + lo;
-          v[k] = src[p - W.noff[lo]];
+          const uint64_t* src = a.ws_list + (int64_t)row * a.list_stride + (int64_t)(cb + lo[k]) * a.chunk;
+          cc[k] = cb + lo[k];
+          v[k] = src[p - W.noff[lo[k]]];
         }
       }
       #pragma unroll
@@ -888,15 +897,35 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   });
   if (__syncthreads_or(full)) return 0xffffffffu;
   path = kWideDrawFail;
-  // d. distinct weights, descending
-  for (int h = tid; h < kWideFinHash; h += NT) {
-    const uint32_t k = F.u.mg.hkey[h];
-    if (k != 0u) F.u.mg.sortk[atomicAdd(&F.cnt, 1u)] = ((uint64_t)k << 32) | (uint64_t)h;
+  // d. distinct weights, descending: the table's used slots compacted in
+  //    order of (thread, slot) (thread t holds slots q * NT + t: their
+  //    count, then a block scan of the counts), then ranked
+  {
+    constexpr int kSl = kWideFinHash / NT;
+    uint32_t hk[kSl];
+    uint32_t nu = 0u;
+    #pragma unroll
+    for (int q = 0; q < kSl; ++q) {
+      hk[q] = F.u.mg.hkey[q * NT + tid];
+      nu += hk[q] != 0u ? 1u : 0u;
+    }
+    uint32_t tot;
+    uint32_t o = block_excl_scan_u32<NT>(nu, F.fl.wcnt, &tot);
+    #pragma unroll
+    for (int q = 0; q < kSl; ++q)
+      if (hk[q] != 0u) F.u.mg.sortk[o++] = ((uint64_t)hk[q] << 32) | (uint64_t)(q * NT + tid);
+    if (tid == 0) F.cnt = tot;
   }
   __syncthreads();
   const int R = (int)F.cnt;
   if (R == 0) return 0xffffffffu;
-  {
+  if (R <= NT) {
+    block_sort_desc<1>(F.u.mg.sortk, R);
+  } else if (R <= 2 * NT) {
+    block_sort_desc<2>(F.u.mg.sortk, R);
+  } else if (R <= 4 * NT) {
+    block_sort_desc<4>(F.u.mg.sortk, R);
+  } else {
     const int n2 = next_pow2(R);
     for (int i = R + tid; i < n2; i += NT) F.u.mg.sortk[i] = 0ull;
     __syncthreads();
@@ -1003,16 +1032,30 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   wide_for_each_run(F, a, row, [&](int c, uint64_t e) {
     if ((uint32_t)(e >> 32) == key) F.u.cntc[c] = (uint32_t)(e >> 16) & 0xffffu;
   });
-  if (tid == 0) {
-    uint32_t seen = 0u;
-    F.csel = 0xffffffffu;
-    for (int c = 0; c < nch; ++c) {
-      const uint32_t k = F.u.cntc[c];
-      if (k != 0u && seen + k >= cp) { F.csel = (uint32_t)c; F.rsel = cp - seen; break; }
-      seen += k;
+  if (tid < 64) {
+    // the chunk holding the cp-th match: an inclusive scan of the chunks'
+    // match counts over the lanes, 64 chunks at a time
+    uint32_t seen = 0u, csel = 0xffffffffu, rsel = 0u;
+    for (int cb = 0; cb < nch; cb += 64) {
+      const int c = cb + tid;
+      const uint32_t k = c < nch ? F.u.cntc[c] : 0u;
+      const uint32_t inc = wave_incl_scan_u32(k);
+      const uint64_t hit = __ballot(k != 0u && seen + inc >= cp);
+      if (hit != 0ull) {
+        const int l = __ffsll((unsigned long long)hit) - 1;
+        const uint32_t before = seen + (uint32_t)__builtin_amdgcn_readlane((int)(inc - k), l);
+        csel = (uint32_t)(cb + l);
+        rsel = cp - before;
+        break;
+      }
+      seen += (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
     }
-    F.tok = 0xffffffffu;
-    F.cnt = 0u;
+    if (tid == 0) {
+      F.csel = csel;
+      F.rsel = rsel;
+      F.tok = 0xffffffffu;
+      F.cnt = 0u;
+    }
   }
   __syncthreads();
   const uint32_t csel = F.csel, want = F.rsel;

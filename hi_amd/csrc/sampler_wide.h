@@ -49,6 +49,7 @@ constexpr int kWideGBins = 64;         // threshold bins (binades of w below M)
 struct WideScanLds {
   fold::Map wmap[NT / 64];
   uint32_t wcnt[NT / 64];
+  fold::Map wmap3[3][NT / 64];  // block_map_scan3
 };
 // LDS of a (chunk, row) workgroup; the chunk's weights follow at
 // wide_w_off.
@@ -61,8 +62,10 @@ struct WideChunkLds {
   uint32_t hkey[kWideChunkHash];
   uint32_t hcnt[kWideChunkHash];
   uint32_t hmin[kWideChunkHash];
+  fold::Map exm[NT];  // the full path's block maps before each block, in the predicted binade
   uint32_t nrun, ovf, last, fu;
   float fend;
+  int x_ws, x_we;  // window 0 of the full path
 };
 constexpr size_t kWideChunkHead = (sizeof(WideChunkLds) + 15) & ~(size_t)15;
 // Weights sit in LDS with one pad word per 16, so that threads reading
@@ -336,6 +339,38 @@ __device__ __forceinline__ fold::Map block_map_scan(fold::Map m, fold::Map* wm, 
   return fold::compose(before, ex);
 }
 
+// block_map_scan of three maps at once (one pair of barriers); returns the
+// exclusive scans of m0 and m1, and the totals of all three.
+__device__ __forceinline__ void block_map_scan3(fold::Map m0, fold::Map m1, fold::Map m2, fold::Map (*wm)[NT / 64],
+                                                fold::Map& ex0, fold::Map& ex1, fold::Map* tot) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const fold::Map i0 = fold::wave_map_scan(m0), i1 = fold::wave_map_scan(m1), i2 = fold::wave_map_scan(m2);
+  const fold::Map e0 = fold::wave_map_prev(i0), e1 = fold::wave_map_prev(i1);
+  __syncthreads();
+  if (lane == 63) {
+    wm[0][wid] = i0;
+    wm[1][wid] = i1;
+    wm[2][wid] = i2;
+  }
+  __syncthreads();
+  fold::Map b0 = fold::map_identity(), b1 = b0, a0 = b0, a1 = b0, a2 = b0;
+  #pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    if (w < wid) {
+      b0 = fold::compose(b0, wm[0][w]);
+      b1 = fold::compose(b1, wm[1][w]);
+    }
+    a0 = fold::compose(a0, wm[0][w]);
+    a1 = fold::compose(a1, wm[1][w]);
+    a2 = fold::compose(a2, wm[2][w]);
+  }
+  tot[0] = a0;
+  tot[1] = a1;
+  tot[2] = a2;
+  ex0 = fold::compose(b0, e0);
+  ex1 = fold::compose(b1, e1);
+}
+
 // The exact sequential f32 fold of w[wide_pad(0 .. len)) (LDS) from a0, by
 // the workgroup.  Thread t holds a block of consecutive terms; in the
 // current binade every block is one map, so a scan gives each block's
@@ -444,90 +479,174 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
     bm[tid] = m0;
     bm[NT + tid] = m1;
     bm[2 * NT + tid] = m2;
-    fold::Map t0, t1, t2;
-    const fold::Map ex0 = block_map_scan(m0, L.fl.wmap, &t0);
-    const fold::Map ex1 = block_map_scan(m1, L.fl.wmap, &t1);
-    block_map_scan(m2, L.fl.wmap, &t2);
+    if (tid == 0) L.x_ws = -1;
+    fold::Map tt[3], ex0, ex1;
+    block_map_scan3(m0, m1, m2, L.fl.wmap3, ex0, ex1, tt);
     if (tid == 0) {
       cf->has_end = 0u;
       cf->e0 = (uint32_t)e0;
-      cf->map[0] = t0;
-      cf->map[1] = t1;
-      cf->map[2] = t2;
+      cf->map[0] = tt[0];
+      cf->map[1] = tt[1];
+      cf->map[2] = tt[2];
       cf->flags = 15u;
     }
     // the predicted crossings: from the predicted start, the block, then
     // the term, where the fold leaves its binade; the chunk records a window
     // of terms around each (up to kCrossWins) and the maps of the segments
     // between them, so that the chain crosses with a few real additions
-    // (wide_chain_cross).  The first search reuses the block maps above.
+    // (wide_chain_cross).
     const int kx = ep - e0;  // 0 or 1: ep's maps
+    {
+      const fold::Map ex = kx == 0 ? ex0 : ex1;
+      L.exm[tid] = ex;
+    }
+    __syncthreads();
     int p0 = 0, ec = ep, nw = 0;
     uint32_t Ac = fold::to_A((float)S);
-    for (int wdx = 0; wdx < kCrossWins; ++wdx) {
-      // this thread's terms [max(r0, p0), r1) in binade ec, and the exclusive scan
-      const int q0 = max(r0, p0);
-      fold::Map mb, ex;
-      if (wdx == 0) {
-        mb = kx == 0 ? m0 : m1;
-        ex = kx == 0 ? ex0 : ex1;
-      } else {
-        mb = fold::map_identity();
-        wide_terms(w, q0, r1, [&](float x) { mb = fold::compose(mb, term_map(x, ec)); });
-        fold::Map tot;
-        ex = block_map_scan(mb, L.fl.wmap, &tot);
-      }
+    // window 0, all of it by the wave holding the one block that leaves ep
+    // (the predicted values rise, so only one block can): the term that
+    // leaves (the block's terms one a lane, a scan of their maps), the
+    // window around it, the map of the segment before the window (the scan
+    // up to the window's block, then that block's terms before the window,
+    // again one a lane) and the predicted value after the window (a DPP
+    // chain of real additions)
+    {
+      const fold::Map mb = kx == 0 ? m0 : m1;
+      const fold::Map ex = L.exm[tid];
       const uint64_t Ab = (uint64_t)Ac + fold::apply(ex, Ac & 1u);
-      int tstar = -1;
-      if (q0 < r1 && Ab < fold::kTop && Ab + fold::apply(mb, (uint32_t)Ab & 1u) >= fold::kTop) {
-        uint32_t A = (uint32_t)Ab;
-        int r = q0;
-        wide_terms(w, q0, r1, [&](float x) {
-          const uint32_t t = fold::apply(term_map(x, ec), A & 1u);
-          if (tstar < 0 && (uint64_t)A + t >= fold::kTop) tstar = r;
-          A += tstar < 0 ? t : 0u;
-          ++r;
-        });
-      }
-      tstar = (int)block_max_u32<NT>((uint32_t)(tstar + 1), L.fl.wcnt) - 1;
-      if (tstar < 0) break;
-      const int ws = max(p0, min(tstar - kCrossTerms / 2, len - kCrossTerms));
-      const int we = min(len, ws + kCrossTerms);
-      // segment [p0, ws) in binade ec
-      fold::Map mp = fold::map_identity();
-      wide_terms(w, q0, min(r1, ws), [&](float x) { mp = fold::compose(mp, term_map(x, ec)); });
-      fold::Map sg;
-      block_map_scan(mp, L.fl.wmap, &sg);
-      if (tid < we - ws) cf->term[wdx][tid] = w[wide_pad(ws + tid)];
-      // the predicted value after the window, and its binade
-      if (tid == 0) {
+      const uint64_t bal = __ballot(r0 < r1 && Ab < fold::kTop && Ab + fold::apply(mb, (uint32_t)Ab & 1u) >= fold::kTop);
+      if (bal != 0ull) {
+        static_assert(kSelChunkLarge / NT <= 64, "a block's terms fit one wave");
+        const int lane = tid & 63;
+        const int l = __ffsll((unsigned long long)bal) - 1;
+        const int rc0 = ((tid & ~63) + l) * J;
+        const int nc = min(rc0 + J, len) - rc0;
+        const uint32_t Ablk = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)Ab, l);
+        const fold::Map mt = lane < nc ? term_map(w[wide_pad(rc0 + lane)], ec) : fold::map_identity();
+        const fold::Map it = fold::wave_map_scan(mt);
+        const uint64_t cr = __ballot(lane < nc && (uint64_t)Ablk + fold::apply(it, Ablk & 1u) >= fold::kTop);
+        const int tstar = rc0 + __ffsll((unsigned long long)cr) - 1;  // (cr != 0: the block leaves ep)
+        const int ws = max(0, min(tstar - kCrossTerms / 2, len - kCrossTerms));
+        const int we = min(len, ws + kCrossTerms);
+        const int tb = ws / J;
+        const int np = ws - tb * J;  // the window block's terms before the window
+        const fold::Map mp = lane < np ? term_map(w[wide_pad(tb * J + lane)], ec) : fold::map_identity();
+        const fold::Map ip = fold::wave_map_scan(mp);
+        const fold::Map head = fold::Map{(uint32_t)__builtin_amdgcn_readlane((int)ip.t0, 63),
+                                         (uint32_t)__builtin_amdgcn_readlane((int)ip.t1, 63)};
+        const fold::Map sg = fold::compose(L.exm[tb], head);
         const uint64_t A1 = (uint64_t)Ac + fold::apply(sg, Ac & 1u);
-        float v = A1 < fold::kTop ? fold::from_A((uint32_t)A1, ec) : __builtin_nanf("");
-        wide_terms(w, ws, we, [&](float t) { v = fold::fadd(v, t); });
-        L.fend = v;
-        cf->be[wdx] = (uint32_t)ec;
-        cf->wn[wdx] = (uint32_t)(we - ws);
-        cf->seg[wdx] = sg;
+        const float v0 = A1 < fold::kTop ? fold::from_A((uint32_t)A1, ec) : __builtin_nanf("");
+        const int nw0 = we - ws;
+        const float tl = lane < nw0 ? w[wide_pad(ws + lane)] : 0.f;
+        const float f = wave_fold_f32(tl, v0, nw0);
+        const float v = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(f), nw0 - 1));
+        if (lane == 0) {
+          L.fend = v;
+          L.x_ws = ws;
+          L.x_we = we;
+          cf->be[0] = (uint32_t)ec;
+          cf->wn[0] = (uint32_t)nw0;
+          cf->seg[0] = sg;
+        }
       }
-      __syncthreads();
-      const float v = L.fend;
-      __syncthreads();
-      nw = wdx + 1;
-      p0 = we;
-      ec = fold::binade(v);
-      Ac = fold::to_A(v);
-      if (!finitef_(v)) { nw = 0; break; }  // the prediction left the binade before the window
     }
-    if (nw > 0) {
-      // the last segment [p0, len) in binade ec
+    __syncthreads();
+    {
+      const int ws = L.x_ws;
+      if (ws >= 0) {
+        const int we = L.x_we;
+        if (tid < we - ws) cf->term[0][tid] = w[wide_pad(ws + tid)];
+        const float v = L.fend;
+        nw = 1;
+        p0 = we;
+        ec = fold::binade(v);
+        Ac = fold::to_A(v);
+        if (!finitef_(v)) nw = 0;  // the prediction left the binade before the window
+      }
+    }
+    // the rest of the chunk from p0 in binade ec: the threads' maps of
+    // their terms from p0 on, and their scan.  The total is the last
+    // segment, unless the fold leaves ec again: then window 1 (found as
+    // window 0, by the wave holding the block that leaves) and the last
+    // segment after it.
+    if (nw == 1) {
       const int q0 = max(r0, p0);
-      fold::Map ms = fold::map_identity();
-      wide_terms(w, q0, r1, [&](float x) { ms = fold::compose(ms, term_map(x, ec)); });
-      fold::Map sg;
-      block_map_scan(ms, L.fl.wmap, &sg);
-      if (tid == 0) {
-        cf->be[nw] = (uint32_t)ec;
-        cf->seg[nw] = sg;
+      fold::Map mb = fold::map_identity();
+      wide_terms(w, q0, r1, [&](float x) { mb = fold::compose(mb, term_map(x, ec)); });
+      fold::Map tot;
+      const fold::Map ex = block_map_scan(mb, L.fl.wmap, &tot);
+      if ((uint64_t)Ac + fold::apply(tot, Ac & 1u) < fold::kTop) {
+        if (tid == 0) {
+          cf->be[1] = (uint32_t)ec;
+          cf->seg[1] = tot;
+        }
+      } else {
+        if (tid == 0) L.x_ws = -1;
+        L.exm[tid] = ex;  // (window 0's reads of exm ended at the barrier after it)
+        __syncthreads();
+        const uint64_t Ab = (uint64_t)Ac + fold::apply(ex, Ac & 1u);
+        const uint64_t bal = __ballot(q0 < r1 && Ab < fold::kTop && Ab + fold::apply(mb, (uint32_t)Ab & 1u) >= fold::kTop);
+        if (bal != 0ull) {
+          const int lane = tid & 63;
+          const int l = __ffsll((unsigned long long)bal) - 1;
+          const int tc = (tid & ~63) + l;
+          const int rc0 = max(tc * J, p0);
+          const int nc = min(tc * J + J, len) - rc0;
+          const uint32_t Ablk = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)Ab, l);
+          const fold::Map mt = lane < nc ? term_map(w[wide_pad(rc0 + lane)], ec) : fold::map_identity();
+          const fold::Map it = fold::wave_map_scan(mt);
+          const uint64_t cr = __ballot(lane < nc && (uint64_t)Ablk + fold::apply(it, Ablk & 1u) >= fold::kTop);
+          const int tstar = rc0 + __ffsll((unsigned long long)cr) - 1;
+          const int ws = max(p0, min(tstar - kCrossTerms / 2, len - kCrossTerms));
+          const int we = min(len, ws + kCrossTerms);
+          const int tb = ws / J;
+          const int hb = max(tb * J, p0);  // the window block's first term from p0 on
+          const int np = ws - hb;
+          const fold::Map mp = lane < np ? term_map(w[wide_pad(hb + lane)], ec) : fold::map_identity();
+          const fold::Map ip = fold::wave_map_scan(mp);
+          const fold::Map head = fold::Map{(uint32_t)__builtin_amdgcn_readlane((int)ip.t0, 63),
+                                           (uint32_t)__builtin_amdgcn_readlane((int)ip.t1, 63)};
+          const fold::Map sg = fold::compose(L.exm[tb], head);
+          const uint64_t A1 = (uint64_t)Ac + fold::apply(sg, Ac & 1u);
+          const float v0 = A1 < fold::kTop ? fold::from_A((uint32_t)A1, ec) : __builtin_nanf("");
+          const int nw1 = we - ws;
+          const float tl = lane < nw1 ? w[wide_pad(ws + lane)] : 0.f;
+          const float f = wave_fold_f32(tl, v0, nw1);
+          const float v = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(f), nw1 - 1));
+          if (lane == 0) {
+            L.fend = v;
+            L.x_ws = ws;
+            L.x_we = we;
+            cf->be[1] = (uint32_t)ec;
+            cf->wn[1] = (uint32_t)nw1;
+            cf->seg[1] = sg;
+          }
+        }
+        __syncthreads();
+        const int ws = L.x_ws;
+        nw = 0;  // (no block leaves: not reached, the total leaves ec)
+        if (ws >= 0) {
+          const int we = L.x_we;
+          if (tid < we - ws) cf->term[1][tid] = w[wide_pad(ws + tid)];
+          const float v = L.fend;
+          nw = finitef_(v) ? 2 : 0;  // (not finite: the prediction left the binade before the window)
+          p0 = we;
+          ec = fold::binade(v);
+          Ac = fold::to_A(v);
+        }
+        if (nw == 2) {
+          // the last segment [p0, len) in binade ec
+          const int q2 = max(r0, p0);
+          fold::Map ms = fold::map_identity();
+          wide_terms(w, q2, r1, [&](float x) { ms = fold::compose(ms, term_map(x, ec)); });
+          fold::Map sg;
+          block_map_scan(ms, L.fl.wmap, &sg);
+          if (tid == 0) {
+            cf->be[2] = (uint32_t)ec;
+            cf->seg[2] = sg;
+          }
+        }
       }
     }
     if (tid == 0) cf->nw = (uint32_t)nw;

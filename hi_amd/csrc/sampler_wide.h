@@ -572,8 +572,13 @@ __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* 
     // segment after it.
     if (nw == 1) {
       const int q0 = max(r0, p0);
+      // a block wholly after p0 in one of the three binades: its map above
+      const int kc = ec - e0;
       fold::Map mb = fold::map_identity();
-      wide_terms(w, q0, r1, [&](float x) { mb = fold::compose(mb, term_map(x, ec)); });
+      if (r0 >= p0 && kc >= 0 && kc < 3)
+        mb = kc == 0 ? m0 : (kc == 1 ? m1 : m2);
+      else
+        wide_terms(w, q0, r1, [&](float x) { mb = fold::compose(mb, term_map(x, ec)); });
       fold::Map tot;
       const fold::Map ex = block_map_scan(mb, L.fl.wmap, &tot);
       if ((uint64_t)Ac + fold::apply(tot, Ac & 1u) < fold::kTop) {

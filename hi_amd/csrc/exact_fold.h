@@ -159,8 +159,8 @@ HRF_HD uint32_t cross_copy(uint32_t A, Inc c) {
   const int64_t need = (int64_t)kTop - (int64_t)A - delta(c, A & 1u);  // cc * s >= need
   if (need <= (int64_t)s) return 1u;
   if (s == 0u) return kNone;
-  const uint64_t cc = ((uint64_t)need + s - 1u) / s;
-  return cc >= kNone ? kNone : (uint32_t)cc;
+  // need <= kTop + 1 and s <= kSat + 1: the quotient is taken in 32 bits
+  return ((uint32_t)need + (uint32_t)s - 1u) / (uint32_t)s;
 }
 // A after c >= 0 copies, all inside the binade.
 HRF_HD uint32_t after_copies(uint32_t A, Inc c, uint32_t cnt) {

@@ -628,8 +628,8 @@ constexpr int kWideCopies = 8;             // copies of the mass histogram (lane
 struct SelLds {
   uint64_t surv[NT / 64][kSurvCap];
   uint32_t hist[256];
-  float whist[kWideBins * kWideCopies];  // top-p rows: the chunk's mass histogram (WideStat),
-                                         // kWideCopies interleaved copies
+  uint32_t whist[kWideBins * kWideCopies];  // top-p rows: the chunk's mass histogram (WideStat),
+                                            // copy c of bin j at j * kWideCopies + c
   uint32_t sel[4];
   uint32_t hw[NT / 64];       // history tokens among each wave's logits
   uint32_t wcnt[NT / 64];
@@ -843,26 +843,42 @@ __device__ __forceinline__ SelNeeds sel_needs(const SampleArgs& a, const RowCfg&
 }
 
 // Adds one processed logit v (NaN: absent) to a top-p row's chunk mass
-// histogram: w' = exp((v - m) / T) = 2^r, bin floor(-r), clamped.  Lane l
-// adds to copy l % kWideCopies: the lanes of a wave that hit one bin (a
-// row's logits fill a few bins) then conflict kWideCopies times less.  The
-// masses are approximate (the wide pass keeps a margin), so the order of
-// the additions does not matter.
-__device__ __forceinline__ void wide_hist_add(float* whist, float v, float m, float a2) {
+// histogram: w' = exp((v - m) / T) = 2^r, bin j = floor(-r), clamped.
+// The bins hold integers, w' * 2^(j + 16) (in [2^15, 2^16] inside a bin;
+// the clamped last bin drops what lies below 2^-47), because LDS float
+// atomics are slow on this part: with ds_add_f32 C2's select pass took
+// 41-44 us (with 8 or 64 copies of the bins alike), with ds_add_u32 20 us,
+// the same as with no histogram.  Thread t adds to copy t % kWideCopies.
+// A copy takes the terms of NT / kWideCopies threads, at most 64 + kSelOb a
+// thread, each at most 2^16: below 2^28.  The masses are approximate (the
+// wide pass keeps a margin), so the order of the additions does not
+// matter.
+__device__ __forceinline__ void wide_hist_add(uint32_t* whist, float v, float m, float a2) {
   if (!finitef_(v)) return;
   const float r = (v - m) * a2;
   const int j = -r < (float)(kWideBins - 1) ? (int)(-r) : kWideBins - 1;
-  atomicAdd(&whist[j * kWideCopies + (int)(threadIdx.x & (kWideCopies - 1))], __builtin_amdgcn_exp2f(r));
+  const uint32_t fx = (uint32_t)__builtin_amdgcn_exp2f(r + (float)(j + 16));
+  atomicAdd(&whist[j * kWideCopies + (int)(threadIdx.x & (kWideCopies - 1))], fx);
 }
-__device__ __forceinline__ void wide_hist_clear(float* whist) {
-  for (int i = threadIdx.x; i < kWideBins * kWideCopies; i += NT) whist[i] = 0.f;
+__device__ __forceinline__ void wide_hist_clear(uint32_t* whist) {
+  for (int i = threadIdx.x; i < kWideBins * kWideCopies; i += NT) whist[i] = 0u;
 }
-// Bin b (b < kWideBins) summed over the copies.
-__device__ __forceinline__ float wide_hist_bin(const float* whist, int b) {
-  float s = 0.f;
+// The bins' masses (relative to the chunk maximum) summed over their
+// copies into out[0 .. kWideBins), by all NT threads: thread t adds copies
+// 8 (t & 7) .. + 7 of bin t / 8 (two 16-byte reads), then the eight
+// threads of a bin add up (DPP).
+__device__ __forceinline__ void wide_hist_store(const uint32_t* whist, float* out) {
+  static_assert(kWideBins * 8 == NT && kWideCopies % 8 == 0, "eight threads a bin");
+  constexpr int kPer = kWideCopies / 8;
+  const int t = threadIdx.x;
+  const uint32_t* p = whist + (t >> 3) * kWideCopies + (t & 7) * kPer;
+  uint32_t u = 0u;
   #pragma unroll
-  for (int c = 0; c < kWideCopies; ++c) s += whist[b * kWideCopies + c];
-  return s;
+  for (int c = 0; c < kPer; ++c) u += p[c];
+  float s = (float)u * __builtin_ldexpf(1.f, -(t >> 3) - 16);
+  #pragma unroll
+  for (int o = 1; o < 8; o <<= 1) s += __uint_as_float(lane_xor32(__float_as_uint(s), o));
+  if ((t & 7) == 0) out[t >> 3] = s;
 }
 
 // Exact pass over the chunk from global memory, element by element.  Used
@@ -952,7 +968,7 @@ __device__ __forceinline__ void select_exact(SelLds& L, const SampleArgs& a, con
   if (nd.whist) {
     __syncthreads();
     WideStat* ws = a.wstat + slot;
-    if (tid < kWideBins) ws->hist[tid] = wide_hist_bin(L.whist, tid);
+    wide_hist_store(L.whist, ws->hist);
     if (tid == 0) {
       ws->ms = finitef_(lmax) ? lmax / cfg.t_eff : lmax;
       ws->valid = 1u;
@@ -1356,6 +1372,8 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
   #pragma unroll
   for (int w = 0; w < NT / 64; ++w) { n += L.wcnt[w]; rare |= L.wcnt[w] > (uint32_t)kSurvCap ? 1u : 0u; }
   if (rare) return false;
+  // (every wave's atomics are in: the barrier above)
+  if (nd.whist) wide_hist_store(L.whist, a.wstat[slot].hist);
   if (wid != 0) return true;
 
   // wave 0: the chunk's top k_sel of the survivors, argmaxes, record
@@ -1424,7 +1442,6 @@ __device__ __forceinline__ bool select_wide(SelLds& L, const SampleArgs& a, cons
   }
   if (nd.whist) {
     WideStat* ws = a.wstat + slot;
-    if (lane < (uint32_t)kWideBins) ws->hist[lane] = wide_hist_bin(L.whist, (int)lane);
     if (lane == 0u) {
       ws->ms = m / cfg.t_eff;
       ws->valid = 1u;

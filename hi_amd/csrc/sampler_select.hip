@@ -4,9 +4,13 @@
 
 namespace hi_rocm {
 
-// The streaming select pass: workgroup (chunk, row).
+// The streaming select pass: workgroup (chunk, row).  At most 128 VGPRs
+// (four waves per SIMD): the 16384-logit chunks' kernels need ~160 and then
+// run three workgroups per CU; held to 128 they spill ~150 bytes a lane and
+// still take C4's select pass from 38.6 to 36.6 us (the 4096-logit ones
+// need under 70 either way).
 template <int DT, int NL, bool MASK>
-__global__ void __launch_bounds__(NT) select_kernel(SampleArgs a) {
+__global__ void __launch_bounds__(NT, 4) select_kernel(SampleArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   const int row = blockIdx.y;
   select_chunk<DT, NL, MASK>(a, row, blockIdx.x, lds_raw);

@@ -74,6 +74,7 @@ SIGNATURES = {
     "hi_rocm_debug_expf": (_i, [_vp, _vp, _i64, _vp]),
     "hi_rocm_debug_fold": (_i, [_vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp]),
     "hi_rocm_debug_wide_paths": (_i, [_vp, _sz, _i, _i, _vp, _vp]),
+    "hi_rocm_debug_wide_totals": (_i, [_vp, _sz, _i, _i, _vp, _vp]),
     "hi_rocm_last_error": (ctypes.c_char_p, []),
     "hi_rocm_version": (ctypes.c_char_p, []),
     # include/hi_rocm_host.h

@@ -161,6 +161,7 @@ void carve(hi_rocm::SampleArgs& a, void* ws, const hi_rocm::WorkspaceLayout& L) 
   a.wfold = (hi_rocm::ChunkFold*)(base + L.wfold);
   a.wbmap = (hi_rocm::fold::Map*)(base + L.wbmap);
   a.diag = (uint32_t*)(base + L.diag);
+  a.wtot = (float*)(base + L.wtot);
   a.chunk = hi_rocm::choose_chunk(a.B, a.V, a.n_lp, a.vec_ok, a.hoff != nullptr);
   a.n_chunks = (a.V + a.chunk - 1) / a.chunk;
 }
@@ -514,6 +515,19 @@ int hi_rocm_debug_wide_paths(const void* workspace, size_t workspace_bytes, int 
                                 hipMemcpyDeviceToHost, (hipStream_t)stream);
   if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
   return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug wide paths copy");
+}
+
+int hi_rocm_debug_wide_totals(const void* workspace, size_t workspace_bytes, int batch, int vocab,
+                              float* out_totals, void* stream) {
+  if (workspace == nullptr || out_totals == nullptr || batch <= 0 || vocab <= 0 || batch > hi_rocm::kDoneRows ||
+      !vocab_ok(vocab))
+    return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_wide_totals: invalid arguments");
+  const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(batch, vocab);
+  if (workspace_bytes < L.total) return fail(HI_ROCM_ERR_ARGS, "hi_rocm_debug_wide_totals: workspace too small");
+  hipError_t e = hipMemcpyAsync(out_totals, (const char*)workspace + L.wtot, (size_t)batch * 2 * sizeof(float),
+                                hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "debug wide totals copy");
 }
 
 int hi_rocm_debug_expf(const float* x, float* y, int64_t n, void* stream) {

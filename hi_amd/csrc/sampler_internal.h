@@ -151,6 +151,7 @@ struct SampleArgs {
   ChunkFold* wfold;    // [B][n_chunks]
   fold::Map* wbmap;    // [B][n_chunks][3][kScanThreads]: per-thread block maps of each ChunkFold binade
   uint32_t* diag;      // [B] how the wide pass finished each top-p row (WidePath)
+  float* wtot;         // [B][2] the wide pass's normaliser and candidate total (debug export)
 };
 
 // diag values for top-p rows of the chunked path (0: not a top-p row of
@@ -178,7 +179,7 @@ constexpr int kFusedMaxRows = kFusedMaxWorkgroups;
 constexpr int kDoneRows = 65536;
 
 struct WorkspaceLayout {
-  size_t stats, cand, ws_s, ws_w, ws_list, done, wstat, wfold, wbmap, diag, total;
+  size_t stats, cand, ws_s, ws_w, ws_list, done, wstat, wfold, wbmap, diag, wtot, total;
   int64_t slots;       // (row, chunk) records reserved
   int64_t list_stride;
 };
@@ -206,6 +207,7 @@ inline WorkspaceLayout workspace_layout_slots(int max_batch, int V, int64_t slot
   L.wfold = off; off = align(off + (size_t)L.slots * sizeof(ChunkFold));
   L.wbmap = off; off = align(off + (size_t)L.slots * 3 * kScanThreads * sizeof(fold::Map));
   L.diag = off; off = align(off + (size_t)max_batch * sizeof(uint32_t));
+  L.wtot = off; off = align(off + (size_t)max_batch * 2 * sizeof(float));
   L.cand = off; off = align(off + (size_t)L.slots * kFast * sizeof(uint64_t));
   L.ws_s = off; off = align(off + (size_t)max_batch * V * sizeof(float));
   L.ws_w = off; off = align(off + (size_t)max_batch * V * sizeof(float));

@@ -998,6 +998,7 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   }
   ovf = __syncthreads_or(ovf);
   const float total = acc;
+  if (tid == 0) a.wtot[2 * row] = total;
   path = kWideTotal;
   if (!(total > 0.f) || !finitef_(total)) return 0xffffffffu;  // argmax_host fallback (finish_row)
   path = kWideChunkFull;
@@ -1125,6 +1126,7 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   const float ct = fold::fold_runs<NT>(F.fl, F.pe, rstar + 1, -0.0f, [&](int r) { return F.u.fo.rx[r]; }, m2_of,
                                        [&](int r, float v) { F.u.fo.st2[r] = v; });
   __syncthreads();
+  if (tid == 0) a.wtot[2 * row + 1] = ct;
   if (!(ct > 0.f) || !finitef_(ct)) return 0xffffffffu;
   // g. the inverse CDF: the first rank whose running weight passes target
   const float target = clamp_uniform(cfg.u) * ct;

@@ -245,6 +245,17 @@ def debug_wide_paths(smp: "Sampler", batch: int, vocab: int,
     return out & 0xff
 
 
+def debug_wide_totals(smp: "Sampler", batch: int, vocab: int,
+                      stream: Optional[torch.cuda.Stream] = None) -> np.ndarray:
+    """The wide pass's normaliser and candidate total of each top-p row it
+    finished in the last ``smp.sample`` call (float32[batch][2];
+    ``hi_rocm_debug_wide_totals``; other rows hold stale values)."""
+    out = np.zeros((batch, 2), np.float32)
+    check(load().hi_rocm_debug_wide_totals(smp.workspace.data_ptr(), smp.workspace.numel(), batch, vocab,
+                                           out.ctypes.data, _stream_ptr(stream)))
+    return out
+
+
 MINP_MISSES = {0: "none", 1: "array", 2: "top-k", 3: "draw"}
 
 

@@ -343,6 +343,17 @@ int hi_rocm_debug_fold(const float* terms, const uint32_t* counts, int runs, flo
 int hi_rocm_debug_wide_paths(const void* workspace, size_t workspace_bytes, int batch, int vocab,
                              uint32_t* out_paths, void* stream);
 
+/* Debug export: for the last call on `workspace`, the wide pass's two f32
+ * sums of each top-p row it finished (rows whose hi_rocm_debug_wide_paths
+ * code is 1): the normaliser (the vocabulary-order sum of the weights) and
+ * the candidate total, as float[batch][2] to host memory (blocking).
+ * Entries of other rows are left from earlier calls.  The batch and vocab
+ * must be the call's; any stream.  No reference counterpart: the sums are
+ * gpu.rs:837's `total` and :874's `candidate_total`, which the parity tests
+ * compare with the oracle's bit for bit. */
+int hi_rocm_debug_wide_totals(const void* workspace, size_t workspace_bytes, int batch, int vocab,
+                              float* out_totals, void* stream);
+
 /* Debug export: y[i] = the device weight function exp(x[i]) for n floats
  * (device arrays).  Bit-identical to host glibc expf.  No reference
  * counterpart; the reference's closest check is crates/hi-cuda/src/

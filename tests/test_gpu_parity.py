@@ -43,7 +43,7 @@ def dev(x):
     return torch.from_numpy(x).to("cuda")
 
 
-def run_gpu(w: Workload, token_logprobs=True, repeat=1, paths=None, misses=None):
+def run_gpu(w: Workload, token_logprobs=True, repeat=1, paths=None, misses=None, totals=None):
     torch = _torch()
     from hi_amd import sampler as S
     logits = dev(w.logits)
@@ -64,6 +64,8 @@ def run_gpu(w: Workload, token_logprobs=True, repeat=1, paths=None, misses=None)
         paths.append(S.debug_wide_paths(smp, w.batch, w.vocab))
     if misses is not None:
         misses.append(S.debug_row_minp_misses(smp, w.batch, w.vocab))
+    if totals is not None:
+        totals.append(S.debug_wide_totals(smp, w.batch, w.vocab))
     for o in outs:
         o["tokens"] = o["tokens"].view(np.uint32)
         if "logprob_ids" in o:
@@ -367,6 +369,72 @@ def test_config_parity(hip, oracle, cfg):
         got_paths = [WIDE_PATHS[int(p)] for p in paths[0][topp]]
         say(f"wide paths: {dict(zip(*np.unique(got_paths, return_counts=True)))}")
         assert all(p == "wide" for p in got_paths), got_paths
+
+
+def _crossing_rows(rng, B, V):
+    """Top-p rows whose vocabulary-order sums cross many binades inside
+    chunks: tiny weights first and large ones later, a few huge logits
+    among tiny ones, long runs of equal logits, a ramp, and noise."""
+    x = np.empty((B, V), np.float32)
+    for b in range(B):
+        kind = b % 6
+        if kind == 0:    # rising: the sum crosses a binade every few chunks
+            x[b] = np.linspace(-30.0, 0.0, V).astype(np.float32) + rng.normal(0, 0.05, V).astype(np.float32)
+        elif kind == 1:  # spikes on a flat floor
+            x[b] = rng.normal(-12.0, 0.5, V).astype(np.float32)
+            x[b, rng.choice(V, 24, replace=False)] = rng.uniform(-1.0, 0.0, 24).astype(np.float32)
+        elif kind == 2:  # runs of equal logits (equal weights in every chunk)
+            x[b] = np.repeat(rng.integers(-40, 1, V // 64 + 1), 64)[:V].astype(np.float32) / 8.0
+        elif kind == 3:  # falling
+            x[b] = np.linspace(0.0, -25.0, V).astype(np.float32)
+        elif kind == 4:  # bf16-like quantised normal
+            x[b] = np.round(rng.normal(0.0, 3.0, V) * 4.0).astype(np.float32) / 4.0
+        else:            # tiny weights, then one block of large ones mid-row
+            x[b] = rng.normal(-20.0, 1.0, V).astype(np.float32)
+            s0 = int(rng.integers(0, V - 5000))
+            x[b, s0:s0 + 5000] = rng.normal(0.0, 1.0, 5000).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("case", ["c2", "c5", "crossings"])
+def test_wide_pass_sums_equal_oracle(hip, oracle, case):
+    """The wide pass's normaliser (the vocabulary-order f32 sum of the
+    weights, gpu.rs:837) and candidate total (:874) equal the oracle's bit
+    for bit on every top-p row it finishes: this pins the chunk maps, the
+    crossing records and windows, the chain and the rank-order folds, which
+    the tokens alone check only where a sum decides a cut."""
+    if case == "crossings":
+        rng = np.random.default_rng(77)
+        B, V = 24, 151936
+        from hi_amd.sampler import row_params
+        p = row_params(B, temperature=1.0, top_p=0.9)
+        p["temperature"] = rng.uniform(0.5, 1.5, B).astype(np.float32)
+        p["top_p"] = rng.uniform(0.5, 0.99, B).astype(np.float32)
+        w = Workload("crossings", _crossing_rows(rng, B, V), p, rng.random(B).astype(np.float32))
+    else:
+        w = CONFIGS[int(case[1])]()
+    totals, paths = [], []
+    run_gpu(w, totals=totals, paths=paths)
+    tot, path = totals[0], paths[0]
+    raw = bf16_bits_to_f32(w.logits) if w.is_bf16 else w.logits
+    checked = 0
+    for b in range(w.batch):
+        if path[b] != 1:
+            continue
+        l, _ = oracle.process_row(raw[b], w.params[b], None, None,
+                                  None if w.mask_words is None else w.mask_words[b])
+        pr = w.params[b]
+        tk = int(pr["top_k"])
+        _, info = oracle.ranked_sample(l, float(pr["temperature"]), float(pr["top_p"]), tk if tk > 0 else None,
+                                       float(w.uniforms[b]), float(pr["min_p"]), info=True)
+        got_t, got_c = tot[b]
+        assert np.float32(got_t).view(np.uint32) == np.float32(info["total"]).view(np.uint32), \
+            (case, b, float(got_t), info["total"])
+        assert np.float32(got_c).view(np.uint32) == np.float32(info["candidate_total"]).view(np.uint32), \
+            (case, b, float(got_c), info["candidate_total"])
+        checked += 1
+    say(f"{case}: {checked} wide rows, sums bit-exact")
+    assert checked >= (8 if case == "crossings" else 16), checked
 
 
 def test_config3_deterministic(hip):

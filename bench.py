@@ -1,6 +1,6 @@
 """Benchmark of the hi-rocm batched token sampler on one MI355X.
 
-Headline (BASELINE.json metric): sampled rows/s for the full pipeline at
+Headline metric: sampled rows/s for the full pipeline at
 B=256, V=129280 fp32 (config 3: penalties + top-k + top-p + min-p + draw),
 plus µs/step at B=1 (config 1, hipGraph-captured) and the fraction of the
 HBM roofline.  A "step" is one sampler call over one batch of synthetic

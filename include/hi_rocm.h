@@ -263,8 +263,9 @@ int hi_rocm_sampler_reserve(int max_batch, int vocab, int n_logprobs, void* stre
  * crates/hi-cuda/src/runtime.rs:218-231). */
 int hi_rocm_sampler_release(void* stream);
 
-/* ---- extended pipeline (the decode-step API; proposal of the survey's
- *      boundary section, no single reference counterpart) ---- */
+/* ---- extended pipeline (the decode-step API: per-row parameters, history,
+ *      mask, logprobs and bf16 in one call; no single reference
+ *      counterpart) ---- */
 
 /* Workspace bytes hi_rocm_sample needs for up to max_batch rows of `vocab`. */
 int hi_rocm_sampler_workspace_bytes(int max_batch, int vocab, int n_logprobs,

@@ -186,12 +186,14 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
   const float M = finitef_(ml) ? ml / cfg.t_eff : -__builtin_inff();
   if (!finitef_(M) || bad) return WideRowStats{M, 0.f, 0u, 0.0, 0.0};
   // chunk masses relative to M, in fixed point (2^-32): per binade of their
-  // lower end (for w_lo) and, for the chunks before this one, their sum
-  // (the prediction); the 32 bins of a chunk are one half of a wave, whose
-  // mass a DPP reduction sums
+  // lower end (for w_lo) and, for the chunks before this one and for this
+  // one, their sums (the prediction): each thread adds its bins' shares,
+  // then one wave reduction and an atomic per wave (integer sums, exact in
+  // any order)
   static_assert(kWideBins == 32, "a chunk's bins are one half of a wave");
   static_assert(kWideGBins == 64, "one bin per lane");
   const int items = nch * kWideBins;
+  unsigned long long pre = 0ull, own = 0ull;
   for (int base = 0; base < items; base += kU * NT) {
     float hv[kU], msv[kU];
     #pragma unroll
@@ -221,12 +223,16 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
         g = g < kWideGBins ? g : kWideGBins - 1;
         atomicAdd(&L.gmass[g], fx);
       }
-      unsigned long long cs = fx;
-      #pragma unroll
-      for (int o = 16; o > 0; o >>= 1) cs += lane_xor64(cs, o);
-      if (j == 0 && it < items && it / kWideBins < chunk && cs != 0ull) atomicAdd(&L.predfx, cs);
-      if (j == 0 && it < items && it / kWideBins == chunk) L.ownfx = cs;
+      const int c = it / kWideBins;
+      pre += c < chunk ? fx : 0ull;
+      own += c == chunk ? fx : 0ull;
     }
+  }
+  pre = wave_reduce64(pre, 0ull, [](uint64_t x, uint64_t y) { return x + y; });
+  own = wave_reduce64(own, 0ull, [](uint64_t x, uint64_t y) { return x + y; });
+  if ((tid & 63) == 0) {
+    if (pre != 0ull) atomicAdd(&L.predfx, pre);
+    if (own != 0ull) atomicAdd(&L.ownfx, own);
   }
   __syncthreads();
   // w_lo: the first binade bin where the masses from the top reach the

@@ -73,10 +73,11 @@ __global__ void __launch_bounds__(NT) finish_grid_kernel(SampleArgs a) {
     return;
   }
   WideChunkLds& L = *reinterpret_cast<WideChunkLds*>(lds_raw);
-  const WideRowStats st = wide_row_stats(L, a, row, chunk, cfg);
+  float pre[kWidePre];
+  const WideRowStats st = wide_row_stats(L, a, row, chunk, cfg, pre);
   const bool valid = st.valid != 0u;
   const float M = st.M, w_lo = st.w_lo;
-  if (valid) wide_chunk_work(L, lds_raw, a, row, chunk, cfg, M, w_lo, st.pred, st.mass);
+  if (valid) wide_chunk_work(L, lds_raw, a, row, chunk, cfg, M, w_lo, st.pred, st.mass, pre);
   // the last workgroup of the row finishes it (as select_finish_kernel)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();

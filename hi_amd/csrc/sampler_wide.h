@@ -135,6 +135,18 @@ __device__ __forceinline__ bool wide_insert(uint32_t* hkey, uint32_t* hcnt, uint
   return false;
 }
 
+// The first kWidePre * NT scaled logits of a chunk (the whole of a
+// 4096-logit chunk), loaded by wide_row_stats behind its own loads, so that
+// their latency hides behind the statistics.
+constexpr int kWidePre = 16;
+__device__ __forceinline__ void wide_preload(const float* s, int len, float (&pre)[kWidePre]) {
+  #pragma unroll
+  for (int k = 0; k < kWidePre; ++k) {
+    const int i = k * NT + (int)threadIdx.x;
+    pre[k] = i < len ? s[i] : -__builtin_inff();
+  }
+}
+
 // Step 1, by every workgroup of a top-p row's chunk work: the row max of s
 // (M), the superset bound w_lo and the predicted fold value before this
 // workgroup's chunk, from the chunks' statistics the select pass wrote
@@ -149,7 +161,7 @@ struct WideRowStats {
   double mass;  // the chunk's predicted mass
 };
 __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const SampleArgs& a, int row, int chunk,
-                                                      const RowCfg& cfg) {
+                                                      const RowCfg& cfg, float (&pre)[kWidePre]) {
   const int tid = threadIdx.x;
   const int nch = a.n_chunks;
   const ChunkStat* stats = a.stats + (int64_t)row * nch;
@@ -172,8 +184,22 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
       }
     }
   }
-  uint32_t mk = 0u, bad = 0u;
-  for (int c = tid; c < nch; c += NT) {
+  // the chunk maxima and valid flags (chunks tid, tid + NT, ...): the first
+  // round goes out with the loads above; then the chunk's scaled logits,
+  // behind all of them, so that waiting for the statistics' loads does not
+  // wait for these
+  float ml0 = 0.f;
+  uint32_t v0 = 1u;
+  if (tid < nch) {
+    ml0 = stats[tid].max_l;
+    v0 = wst[tid].valid;
+  }
+  {
+    const int c0 = chunk * a.chunk;
+    wide_preload(a.ws_s + (int64_t)row * a.V + c0, min(a.chunk, a.V - c0), pre);
+  }
+  uint32_t mk = tid < nch ? okey(ml0) : 0u, bad = tid < nch ? v0 ^ 1u : 0u;
+  for (int c = tid + NT; c < nch; c += NT) {
     mk = max(mk, okey(stats[c].max_l));
     bad |= wst[c].valid ^ 1u;
   }
@@ -193,7 +219,7 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
   static_assert(kWideBins == 32, "a chunk's bins are one half of a wave");
   static_assert(kWideGBins == 64, "one bin per lane");
   const int items = nch * kWideBins;
-  unsigned long long pre = 0ull, own = 0ull;
+  unsigned long long bef = 0ull, own = 0ull;
   for (int base = 0; base < items; base += kU * NT) {
     float hv[kU], msv[kU];
     #pragma unroll
@@ -224,14 +250,14 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
         atomicAdd(&L.gmass[g], fx);
       }
       const int c = it / kWideBins;
-      pre += c < chunk ? fx : 0ull;
+      bef += c < chunk ? fx : 0ull;
       own += c == chunk ? fx : 0ull;
     }
   }
-  pre = wave_reduce64(pre, 0ull, [](uint64_t x, uint64_t y) { return x + y; });
+  bef = wave_reduce64(bef, 0ull, [](uint64_t x, uint64_t y) { return x + y; });
   own = wave_reduce64(own, 0ull, [](uint64_t x, uint64_t y) { return x + y; });
   if ((tid & 63) == 0) {
-    if (pre != 0ull) atomicAdd(&L.predfx, pre);
+    if (bef != 0ull) atomicAdd(&L.predfx, bef);
     if (own != 0ull) atomicAdd(&L.ownfx, own);
   }
   __syncthreads();
@@ -272,13 +298,24 @@ __device__ __forceinline__ WideRowStats wide_row_stats(WideChunkLds& L, const Sa
 }
 
 // w[wide_pad(i)] = wg[i] = the weight of scaled logit s[i] (exact expf, its
-// table read from LDS; min-p zeros it), i < len: all of a thread's loads of
-// a block are issued before any is used.
+// table read from LDS; min-p zeros it), i < len; the first kWidePre * NT
+// come in `pre`, the rest are loaded here (all of a thread's loads of a
+// block issued before any is used).
 __device__ __forceinline__ void wide_weights(const float* s, int len, float M, float min_p, float* w,
-                                             const uint64_t* tab, float* wg) {
+                                             const uint64_t* tab, float* wg, const float (&pre)[kWidePre]) {
   const Exp2TabLds et{tab};
+  #pragma unroll
+  for (int k = 0; k < kWidePre; ++k) {
+    const int i = k * NT + (int)threadIdx.x;
+    float x = exact_expf_t(pre[k] - M, et);
+    x = x < min_p ? 0.f : x;  // min-p: excluded like a zero weight
+    if (i < len) {
+      w[wide_pad(i)] = x;
+      wg[i] = x;
+    }
+  }
   constexpr int kB = 8;
-  for (int base = 0; base < len; base += kB * NT) {
+  for (int base = kWidePre * NT; base < len; base += kB * NT) {
     float v[kB];
     #pragma unroll
     for (int k = 0; k < kB; ++k) {
@@ -433,14 +470,15 @@ __device__ __forceinline__ bool wide_one_binade(double S, double mass) {
 // Steps 2-3 for one (chunk, row), with the row's M, w_lo, the chunk's
 // predicted start S and its predicted mass.
 __device__ __forceinline__ void wide_chunk_work(WideChunkLds& L, unsigned char* lds_raw, const SampleArgs& a, int row, int chunk,
-                                const RowCfg& cfg, float M, float w_lo, double S, double mass) {
+                                const RowCfg& cfg, float M, float w_lo, double S, double mass,
+                                const float (&pre)[kWidePre]) {
   const int tid = threadIdx.x;
   const int c0 = chunk * a.chunk;
   const int len = min(a.chunk, a.V - c0);
   float* w = reinterpret_cast<float*>(lds_raw + wide_w_off(a.chunk));
   const float* srow = a.ws_s + (int64_t)row * a.V + c0;
   // the weights, in LDS and (for the finish's exact refolds) in ws_w
-  wide_weights(srow, len, M, cfg.min_p, w, L.exptab, a.ws_w + (int64_t)row * a.V + c0);
+  wide_weights(srow, len, M, cfg.min_p, w, L.exptab, a.ws_w + (int64_t)row * a.V + c0, pre);
   for (int h = tid; h < kWideChunkHash; h += NT) { L.hkey[h] = 0u; L.hcnt[h] = 0u; L.hmin[h] = 0xffffffffu; }
   if (tid == 0) { L.nrun = 0u; L.ovf = 0u; }
   __syncthreads();

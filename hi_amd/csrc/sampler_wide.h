@@ -918,20 +918,25 @@ __device__ __forceinline__ float wide_wave_chain(const ChunkFold* batch, int cb,
 }
 
 // Calls f(c, e) for every superset run entry e of chunk c of `row`, in
-// parallel: chunks in blocks of NT, their run counts scanned into offsets.
+// parallel: chunks in blocks of NT, their run counts scanned into offsets
+// (a row of at most NT chunks whose offsets noff already holds passes their
+// total as `ready_tot`, and the scan is skipped).
 template <typename F>
-__device__ __forceinline__ void wide_for_each_run(WideFinLds& W, const SampleArgs& a, int row, F f) {
+__device__ __forceinline__ void wide_for_each_run(WideFinLds& W, const SampleArgs& a, int row, F f,
+                                                  int ready_tot = -1) {
   const int tid = threadIdx.x;
   const int nch = a.n_chunks;
   const ChunkFold* folds = a.wfold + (int64_t)row * nch;
   for (int cb = 0; cb < nch; cb += NT) {
-    const int c = cb + tid;
-    const uint32_t n = c < nch ? folds[c].nruns : 0u;
-    uint32_t tot;
-    const uint32_t off = block_excl_scan_u32<NT>(n, W.fl.wcnt, &tot);
-    W.noff[tid] = off;
-    if (tid == 0) W.noff[NT] = tot;
-    __syncthreads();
+    uint32_t tot = (uint32_t)ready_tot;
+    if (ready_tot < 0) {
+      const int c = cb + tid;
+      const uint32_t n = c < nch ? folds[c].nruns : 0u;
+      const uint32_t off = block_excl_scan_u32<NT>(n, W.fl.wcnt, &tot);
+      W.noff[tid] = off;
+      if (tid == 0) W.noff[NT] = tot;
+      __syncthreads();
+    }
     // kU entries a thread: every load issued before the first is used
     constexpr int kU = 8;
     for (uint32_t base = 0; base < tot; base += kU * NT) {
@@ -978,6 +983,53 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   const int tid = threadIdx.x;
   const int nch = a.n_chunks;
   const ChunkFold* folds = a.wfold + (int64_t)row * nch;
+
+  // the merge's input (every chunk's superset runs, step c), loaded before
+  // the chain so that its latency hides behind it: rows of more than kPreMin
+  // entries a thread and up to kPreU (C2's bf16 rows: 3.6K entries; the merge
+  // 11.6 -> 5 us), each with its chunk (a search of fixed steps over the
+  // chunks' offsets in noff, which the chain leaves alone); rows of fewer
+  // entries merge after the chain, where the early loads would delay the
+  // chain's own more than they save
+  constexpr int kPreU = 16, kPreMin = 4;
+  uint64_t pv[kPreU];
+  int pc[kPreU];
+  bool pre_ok = nch <= NT;
+  int ready_tot = -1;  // noff's total, when the merge can reuse it
+  if (pre_ok) {
+    uint32_t n = tid < nch ? folds[tid].nruns : 0u;
+    n = n == kFoldNone ? 0u : n;  // (the row fails on the chunk's overflow below)
+    uint32_t tot;
+    const uint32_t off = block_excl_scan_u32<NT>(n, F.fl.wcnt, &tot);
+    F.noff[tid] = off;
+    if (tid == 0) F.noff[NT] = tot;
+    __syncthreads();
+    ready_tot = (int)tot;
+    pre_ok = tot > (uint32_t)(kPreMin * NT) && tot <= (uint32_t)(kPreU * NT);
+    if (pre_ok) {
+      int lo[kPreU];
+      #pragma unroll
+      for (int k = 0; k < kPreU; ++k) lo[k] = 0;
+      #pragma unroll
+      for (int st = NT / 2; st >= 1; st >>= 1) {
+        #pragma unroll
+        for (int k = 0; k < kPreU; ++k) {
+          const uint32_t p = (uint32_t)(k * NT + tid);
+          lo[k] = F.noff[lo[k] + st] <= p ? lo[k] + st : lo[k];
+        }
+      }
+      #pragma unroll
+      for (int k = 0; k < kPreU; ++k) {
+        const uint32_t p = (uint32_t)(k * NT + tid);
+        pc[k] = -1;
+        pv[k] = 0ull;
+        if (p < tot) {
+          pc[k] = lo[k];
+          pv[k] = a.ws_list[(int64_t)row * a.list_stride + (int64_t)lo[k] * a.chunk + (p - F.noff[lo[k]])];
+        }
+      }
+    }
+  }
 
   // a. the normaliser: the chunk plans chained in vocabulary order
   //    (Rust's Sum folds from -0.0)
@@ -1060,10 +1112,17 @@ __device__ __forceinline__ uint32_t wide_finish(unsigned char* lds_raw, const Sa
   if (tid == 0) F.cnt = 0u;
   __syncthreads();
   bool full = false;
-  wide_for_each_run(F, a, row, [&](int c, uint64_t e) {
+  auto insert = [&](int c, uint64_t e) {
     full |= !wide_insert(F.u.mg.hkey, F.u.mg.hcnt, F.u.mg.hmin, kLog2, (uint32_t)(e >> 32),
                          (uint32_t)(e >> 16) & 0xffffu, (uint32_t)(c * a.chunk) + ((uint32_t)e & 0xffffu));
-  });
+  };
+  if (pre_ok) {
+    #pragma unroll
+    for (int k = 0; k < kPreU; ++k)
+      if (pc[k] >= 0) insert(pc[k], pv[k]);
+  } else {
+    wide_for_each_run(F, a, row, insert, ready_tot);
+  }
   if (__syncthreads_or(full)) return 0xffffffffu;
   path = kWideDrawFail;
   // d. distinct weights, descending: the table's used slots compacted in

@@ -9,6 +9,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
@@ -725,22 +726,42 @@ int hi_rocm_launch_select_batched_last_token_per_row_noalloc(
                         cols, stream, kWhat, a);
   if (rc != HI_ROCM_OK) return rc;
   if (batch_count > hi_rocm::kDoneRows) return fail(HI_ROCM_ERR_UNSUPPORTED, "batch above 65536 rows");
-  const hi_rocm::WorkspaceLayout L = hi_rocm::workspace_layout(batch_count, cols);
-  if (L.total > kNoAllocScratchBytes)
+  // Rows are independent, so a batch whose workspace exceeds the array runs
+  // in groups of as many rows as fit (15 at vocabulary 151,936), one after
+  // another on the stream, each group reusing the array; only a vocabulary
+  // of which one row does not fit is rejected.
+  const size_t one = hi_rocm::workspace_layout(1, cols).total;
+  if (one > kNoAllocScratchBytes)
     return fail(HI_ROCM_ERR_UNSUPPORTED,
-                std::string(kWhat) + ": batch " + std::to_string(batch_count) + " x vocab " + std::to_string(cols) +
-                    " needs " + std::to_string(L.total) + " bytes of workspace, above the " +
+                std::string(kWhat) + ": one row of vocab " + std::to_string(cols) + " needs " +
+                    std::to_string(one) + " bytes of workspace, above the " +
                     std::to_string(kNoAllocScratchBytes) + "-byte static scratch");
+  int lo = 1, hi = batch_count;  // the largest group that fits
+  while (lo < hi) {
+    const int mid = lo + (hi - lo + 1) / 2;
+    if (hi_rocm::workspace_layout(mid, cols).total <= kNoAllocScratchBytes) lo = mid;
+    else hi = mid - 1;
+  }
+  const int group = lo;
   void* ptr = nullptr;
   rc = scratch_address(&ptr);
   if (rc != HI_ROCM_OK) return rc;
-  carve(a, ptr, L);
-  // the per-row counters start at zero (the array keeps whatever the last
-  // call left)
-  hipError_t e = zero_counters(a.done, batch_count, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "scratch counter reset");
-  e = hi_rocm::launch_sample(a, (hipStream_t)stream, next_events());
-  return e == hipSuccess ? HI_ROCM_OK : hip_fail(e, "sampler launch");
+  for (int r0 = 0; r0 < batch_count; r0 += group) {
+    const int n = std::min(group, batch_count - r0);
+    hi_rocm::SampleArgs g;
+    rc = per_row_args((const float*)logits + (int64_t)r0 * seq_len * cols, (uint32_t*)output_tokens + r0,
+                      (const float*)samples + r0, (const float*)temperatures + r0, (const float*)top_ps + r0,
+                      (const int*)top_ks + r0, n, seq_len, cols, stream, kWhat, g);
+    if (rc != HI_ROCM_OK) return rc;
+    carve(g, ptr, hi_rocm::workspace_layout(n, cols));
+    // the per-row counters start at zero (the array keeps whatever the
+    // last call or group left)
+    hipError_t e = zero_counters(g.done, n, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "scratch counter reset");
+    e = hi_rocm::launch_sample(g, (hipStream_t)stream, next_events());
+    if (e != hipSuccess) return hip_fail(e, "sampler launch");
+  }
+  return HI_ROCM_OK;
 }
 
 }  // extern "C"

@@ -231,9 +231,11 @@ int hi_rocm_debug_chacha_block(const uint32_t* key, const uint32_t* words12_15, 
  * (code under stream capture, serving loops that forbid hipMalloc).  Same
  * arguments, checks and results as the mirror above; its workspace is a
  * static device array of HI_ROCM_NOALLOC_SCRATCH_BYTES per GPU (held by
- * every GPU the library runs on until the process ends), so shapes whose
- * workspace (hi_rocm_sampler_workspace_bytes) exceeds it are rejected with
- * HI_ROCM_ERR_UNSUPPORTED -- e.g. up to 15 rows at vocabulary 151,936.
+ * every GPU the library runs on until the process ends).  A batch whose
+ * workspace (hi_rocm_sampler_workspace_bytes) exceeds it runs in groups of
+ * as many rows as fit (15 at vocabulary 151,936), one launch sequence a
+ * group; a vocabulary of which one row does not fit is rejected with
+ * HI_ROCM_ERR_UNSUPPORTED.
  * Every call on a GPU shares that GPU's array: calls that overlap on one
  * GPU (several streams or threads) race and must be serialised. */
 #define HI_ROCM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)

@@ -415,7 +415,30 @@ def test_wide_pass_sums_equal_oracle(hip, oracle, case):
         w = CONFIGS[int(case[1])]()
     totals, paths = [], []
     run_gpu(w, totals=totals, paths=paths)
-    tot, path = totals[0], paths[0]
+    checked = _check_wide_sums(oracle, w, totals[0], paths[0], case)
+    say(f"{case}: {checked} wide rows, sums bit-exact")
+    assert checked >= (8 if case == "crossings" else 16), checked
+
+
+@pytest.mark.parametrize("cfg,seed", [(2, 21), (2, 22), (5, 23), (5, 24)])
+def test_wide_pass_other_seeds(hip, oracle, cfg, seed):
+    """C2's and C5's workloads drawn from other seeds: tokens equal to the
+    oracle's, every top-p row finished by the wide pass, and its two sums
+    bit-exact.  C2's bf16 rows list thousands of superset runs (their merge
+    input loads before the chain), C5's masked rows fewer (after it)."""
+    w = CONFIGS[cfg](seed=seed)
+    say(f"config {cfg} seed {seed}: B={w.batch} V={w.vocab}")
+    totals, paths = [], []
+    got = run_gpu(w, totals=totals, paths=paths)
+    compare(w, got, run_oracle(oracle, w), f"{w.name} seed {seed}")
+    checked = _check_wide_sums(oracle, w, totals[0], paths[0], f"c{cfg}/{seed}")
+    say(f"config {cfg} seed {seed}: {checked} wide rows, sums bit-exact")
+    assert checked >= 16, checked
+
+
+def _check_wide_sums(oracle, w, tot, path, case):
+    """Compares the wide pass's normaliser and candidate total with the
+    oracle's on every row it finished (path 1); returns how many."""
     raw = bf16_bits_to_f32(w.logits) if w.is_bf16 else w.logits
     checked = 0
     for b in range(w.batch):
@@ -433,8 +456,7 @@ def test_wide_pass_sums_equal_oracle(hip, oracle, case):
         assert np.float32(got_c).view(np.uint32) == np.float32(info["candidate_total"]).view(np.uint32), \
             (case, b, float(got_c), info["candidate_total"])
         checked += 1
-    say(f"{case}: {checked} wide rows, sums bit-exact")
-    assert checked >= (8 if case == "crossings" else 16), checked
+    return checked
 
 
 def test_config3_deterministic(hip):

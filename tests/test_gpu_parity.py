@@ -371,6 +371,17 @@ def test_config_parity(hip, oracle, cfg):
         assert all(p == "wide" for p in got_paths), got_paths
 
 
+@pytest.mark.parametrize("cfg,seed", [(1, 31), (1, 32), (3, 33), (3, 34), (4, 35), (4, 36)])
+def test_config_parity_other_seeds(hip, oracle, cfg, seed):
+    """C1's, C3's and C4's workloads drawn from other seeds (C3 is the
+    headline's row kernel, C4 the select + finish pair of top-k 1024 rows):
+    tokens (and C1's logprobs) equal to the oracle's."""
+    w = CONFIGS[cfg](seed=seed)
+    say(f"config {cfg} seed {seed}: {w.name} B={w.batch} V={w.vocab}")
+    got = run_gpu(w)
+    compare(w, got, run_oracle(oracle, w), f"{w.name} seed {seed}")
+
+
 def _crossing_rows(rng, B, V):
     """Top-p rows whose vocabulary-order sums cross many binades inside
     chunks: tiny weights first and large ones later, a few huge logits
